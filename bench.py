@@ -1,0 +1,294 @@
+#!/usr/bin/env python
+"""Benchmark of the MI355X Qwen3.6 MoE decode layer (and the DeltaNet step).
+
+Headline (the JSON `value`): microseconds per MoE layer decode step at batch
+16, bf16 weights, weights resident in HBM.
+Extra sub-results on the same line: batch 1 (config 0), batch 128 with the
+Zipf router bias (config 2) and the Gated DeltaNet step at batch 1 and 8
+(config 3).
+
+Method: every step is one MoE layer (router + top-k + routing tables +
+experts + residual) issued through the C ABI from a preallocated plan.  K
+steps are captured in one HIP graph and replayed once between two HIP events
+on the capture stream, after W eager warmup steps and one untimed replay.
+Steps cycle through R independent weight sets (each 1.6 GB) so one step's
+57.7 MB does not stay in the 256 MB last-level cache.  The expert stage
+(gate/up + down kernels, 98% of the bytes) is timed the same way on its own
+to give the roofline entry.  The CPU baseline is the oracle (a CPU
+restatement of the reference's PyTorch path) on the same inputs.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+METRIC = "µs per MoE layer decode step at batch 1/16/128; achieved HBM TB/s vs peak"
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+REFERENCE_A100_T1_US = 181.5  # real_moe_ms 0.1815 ms, A100 (reference docs/modal.md:1053)
+
+
+def parse_args() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=64)
+    p.add_argument("--warmup", type=int, default=8)
+    p.add_argument("--tokens", type=int, default=16, help="batch of the headline workload")
+    p.add_argument("--weight-sets", type=int, default=8)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
+    p.add_argument("--no-extra", action="store_true", help="skip the batch-1/128 and DeltaNet sub-results")
+    p.add_argument("--only", choices=["moe", "experts", "deltanet"], default=None,
+                   help="run a single timing loop (for profilers) and print its line")
+    return p.parse_args()
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU: this build has no multi-GPU path (requested --gpus {args.gpus}). "
+            "Run with --gpus 1.",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from fastkernels_amd import workloads as wl
+    from fastkernels_amd.plan import DeltaNetStepPlan, MoeLayerPlan
+    from fastkernels_amd.spec import qwen36_35b_a3b_spec
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    spec = qwen36_35b_a3b_spec()
+    H, E, I, K = spec.hidden_size, spec.num_experts, spec.expert_intermediate_size, spec.num_routed_experts
+    stream = torch.cuda.Stream(dev)
+
+    # -- weight sets, generated on the device (seeded) ------------------------
+    def moe_set(r: int) -> dict:
+        g = torch.Generator(device=dev).manual_seed(1000 + r)
+
+        def rnd(*shape):
+            return (torch.randn(*shape, generator=g, device=dev, dtype=torch.float32) * wl.WEIGHT_SCALE).to(torch.bfloat16)
+
+        def rnd_big(*shape):
+            out = torch.empty(shape, device=dev, dtype=torch.bfloat16)
+            for s in range(0, shape[0], 32):
+                out[s : s + 32] = rnd(min(32, shape[0] - s), *shape[1:])
+            return out
+
+        return {
+            "norm_weight": torch.zeros(H, device=dev, dtype=torch.bfloat16),
+            "router_weight": rnd(E, H),
+            "expert_gate_up_weight": rnd_big(E, 2 * I, H),
+            "expert_down_weight": rnd_big(E, H, I),
+            "shared_gate_up_weight": rnd(2 * I, H),
+            "shared_down_weight": rnd(H, I),
+            "shared_expert_gate_weight": rnd(H),
+        }
+
+    R = max(1, args.weight_sets)
+    log(f"generating {R} MoE weight sets on {torch.cuda.get_device_name(0)}")
+    sets = [moe_set(r) for r in range(R)]
+    torch.cuda.synchronize()
+
+    def timed_graph(fns, steps: int, warmup: int) -> float:
+        """ms per step over exactly `steps` graph-captured steps."""
+
+        with torch.cuda.stream(stream):
+            for i in range(warmup):
+                fns[i % len(fns)](stream)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                fns[i % len(fns)](stream)
+        graph.replay()  # upload + warm
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        end.synchronize()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
+
+    def moe_plans(tokens: int, bias=None, nsets: int = R) -> list:
+        plans = []
+        for r in range(nsets):
+            p = MoeLayerPlan(sets[r], tokens, top_k=K, router_bias=bias)
+            p.hidden.copy_(wl.make_hidden(tokens, H, seed=1 + r, dtype=torch.bfloat16).to(dev))
+            plans.append(p)
+        return plans
+
+    def distinct(plans) -> list[int]:
+        torch.cuda.synchronize()
+        return [int((torch.bincount(p.ids.reshape(-1), minlength=E) > 0).sum()) for p in plans]
+
+    def moe_result(tokens: int, bias=None, nsets: int = R, steps: int = args.steps) -> dict:
+        plans = moe_plans(tokens, bias, nsets)
+        fns = [p.run for p in plans]
+        ms_layer = timed_graph(fns, steps, args.warmup)
+        u = distinct(plans)
+        ms_experts = timed_graph([p.run_experts for p in plans], steps, 2)
+        ms_router = timed_graph([p.run_router for p in plans], steps, 2)
+        per_step_u = [u[i % len(u)] for i in range(steps)]
+        layer_bytes = sum(wl.moe_layer_bytes(tokens, x, spec) for x in per_step_u) / steps
+        expert_bytes = sum(
+            (x + 1) * 3 * H * I * 2 + H * 2 + tokens * H * 2 + 2 * tokens * H * 4 for x in per_step_u
+        ) / steps
+        us = ms_layer * 1e3
+        return {
+            "tokens": tokens,
+            "us_per_layer_step": round(us, 3),
+            "distinct_experts_mean": round(sum(per_step_u) / steps, 2),
+            "algorithmic_bytes_per_step": int(layer_bytes),
+            "achieved_tbs": round(layer_bytes / (ms_layer * 1e-3) / 1e12, 3),
+            "hbm_frac": round(layer_bytes / (ms_layer * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+            "expert_stage_us": round(ms_experts * 1e3, 3),
+            "expert_stage_bytes": int(expert_bytes),
+            "expert_stage_tbs": round(expert_bytes / (ms_experts * 1e-3) / 1e12, 3),
+            "router_stage_us": round(ms_router * 1e3, 3),
+            "weight_sets": nsets,
+            "_plans": plans,
+        }
+
+    if args.only == "moe":
+        res = moe_result(args.tokens)
+        res.pop("_plans")
+        print(json.dumps(res))
+        return 0
+
+    # -- headline: MoE layer at batch `tokens` ---------------------------------
+    log(f"timing MoE layer T={args.tokens}")
+    main_res = moe_result(args.tokens)
+    plans = main_res.pop("_plans")
+    ms_per_step = main_res["us_per_layer_step"] / 1e3
+
+    sub = {}
+    if not args.no_extra:
+        log("timing MoE layer T=1")
+        r1 = moe_result(1)
+        r1.pop("_plans")
+        r1["reference_a100_us"] = REFERENCE_A100_T1_US
+        sub["moe_t1"] = r1
+        log("timing MoE layer T=128 (Zipf router bias)")
+        bias = wl.zipf_router_bias(E, seed=0).to(dev)
+        r128 = moe_result(128, bias=bias, nsets=min(R, 4), steps=min(args.steps, 32))
+        p128 = r128.pop("_plans")
+        torch.cuda.synchronize()
+        counts = torch.bincount(p128[0].ids.reshape(-1), minlength=E)
+        r128["hottest_expert_tokens"] = int(counts.max())
+        r128["zipf_alpha"] = wl.ZIPF_ALPHA
+        sub["moe_t128_zipf"] = r128
+        del p128
+        log("timing Gated DeltaNet step T=1 and T=8")
+        dn_sets = [wl.make_deltanet_weights(spec, seed=2000 + r, device=dev) for r in range(R)]
+        for tokens in (1, 8):
+            dplans = []
+            for r in range(R):
+                dp = DeltaNetStepPlan(dn_sets[r], tokens, spec)
+                dp.hidden.copy_(wl.make_hidden(tokens, H, seed=50 + r).to(dev))
+                dplans.append(dp)
+            ms = timed_graph([p.run for p in dplans], args.steps, args.warmup)
+            nbytes = wl.deltanet_step_bytes(tokens, spec)
+            sub[f"deltanet_t{tokens}"] = {
+                "tokens": tokens,
+                "us_per_step": round(ms * 1e3, 3),
+                "algorithmic_bytes_per_step": nbytes,
+                "achieved_tbs": round(nbytes / (ms * 1e-3) / 1e12, 3),
+                "hbm_frac": round(nbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+            }
+        del dn_sets
+
+    # -- CPU baseline (oracle on the host cores, bounded sample) ----------------
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("CPU baseline (oracle restatement of the reference PyTorch MoE path)")
+        import oracle
+
+        torch.set_num_threads(os.cpu_count() or 1)
+        w_cpu = {k: v.cpu() for k, v in sets[0].items()}
+        x_cpu = plans[0].hidden.cpu()
+        args_cpu = (w_cpu["norm_weight"], w_cpu["router_weight"], w_cpu["expert_gate_up_weight"],
+                    w_cpu["expert_down_weight"], w_cpu["shared_gate_up_weight"], w_cpu["shared_down_weight"],
+                    w_cpu["shared_expert_gate_weight"])
+        oracle.moe_layer(x_cpu, *args_cpu, top_k=K)  # warmup
+        n, t0 = 0, time.perf_counter()
+        while True:
+            oracle.moe_layer(x_cpu, *args_cpu, top_k=K)
+            n += 1
+            if n >= 2 and time.perf_counter() - t0 > args.cpu_seconds:
+                break
+        cpu_us = (time.perf_counter() - t0) / n * 1e6
+        cpu = {
+            "value": round(cpu_us, 1),
+            "unit": "us per layer step",
+            "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"MoE layer T={args.tokens} (weight set 0, same bytes as the GPU run), {n} iterations after 1 warmup",
+            "cpu_model": platform.processor() or platform.machine(),
+            "os_cpu_count": os.cpu_count(),
+        }
+        del w_cpu
+
+    expert_frac = main_res["expert_stage_tbs"] * 1e12 / (HBM_PEAK_GBS * 1e9)
+    line = {
+        "metric": METRIC,
+        "value": main_res["us_per_layer_step"],
+        "unit": "us",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"moe_layer_t{args.tokens}",
+            "tokens": args.tokens,
+            "hidden": H,
+            "experts": E,
+            "top_k": K,
+            "intermediate": I,
+            "shared_expert": "sigmoid-gated",
+            "weight_sets": R,
+            "parallelism": "single-gpu",
+        },
+        "roofline": {
+            "kernel": "moe_gateup_kernel + moe_down_kernel (expert stage)",
+            "bound": "hbm",
+            "achieved": round(main_res["expert_stage_tbs"] * 1e3, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(expert_frac, 4),
+            "traffic": None,
+        },
+        "layer": main_res,
+        "sub_results": sub,
+        "cpu_baseline": cpu,
+        "device": torch.cuda.get_device_name(0),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

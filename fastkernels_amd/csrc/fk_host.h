@@ -1,0 +1,31 @@
+// Host-side helpers shared by the C-ABI translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/fastkernels_hip.h"
+
+namespace fk {
+
+// Records a formatted reason for the calling thread's last failure and
+// returns `status`, so call sites read `return fail(FK_ERR_INVALID, "...")`.
+int fail(int status, const char* fmt, ...);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline bool is_float_dtype(int dt) { return dt == FK_DTYPE_F32 || dt == FK_DTYPE_BF16; }
+inline bool is_index_dtype(int dt) { return dt == FK_DTYPE_I32 || dt == FK_DTYPE_I64; }
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Checks the launch that was just enqueued.
+inline int check_launch(const char* what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess) return fail(FK_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(err));
+  return FK_OK;
+}
+
+}  // namespace fk

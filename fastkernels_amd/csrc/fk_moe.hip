@@ -1,0 +1,832 @@
+// Qwen3.6 MoE decode layer for gfx950: router + top-k + routing tables,
+// gate/up + SwiGLU, down-projection + weighted accumulate + residual.
+//
+// Data layout in HBM (all row-major, as the reference packs them,
+// models/qwen36_weights.py:26-37):
+//   router_weight  [E, H]          one 4 KB row per expert at H=2048 (bf16)
+//   gate_up        [E, 2I, H]      gate rows 0..I-1, up rows I..2I-1
+//   down           [E, H, I]       one 1 KB row per output feature at I=512
+//   shared_gate_up [2I, H], shared_down [H, I], shared_gate [H]
+// Workspace (fk_moe_workspace_bytes): counters, routing tables and the fp32
+// SwiGLU activations act[(T*K + T), I], indexed by the permuted position of a
+// routed (token, slot) pair, followed by one row per token for the shared
+// expert.
+//
+// Launch structure (one stream, no host synchronisation):
+//   1. moe_router_kernel   grid ceil(E/4) x 256 threads.  One wavefront per
+//      expert row; the last workgroup to arrive (atomic ticket) runs softmax,
+//      top-k and the routing tables for every token.
+//   2. moe_gateup_kernel   grid (slots) x (I/8); a slot is one active expert
+//      or the shared expert; each workgroup streams 8 gate + 8 up rows of its
+//      expert once and applies them to every pair routed there.
+//   3. moe_down_kernel     grid H/8; each workgroup owns 8 output features and
+//      streams those 8 rows of every active expert's down matrix, so each
+//      output element is accumulated by exactly one lane in a fixed order
+//      (deterministic, no atomics).
+#include "fk_common.h"
+#include "fk_host.h"
+
+namespace fk {
+
+constexpr int kMaxPairs = 4096;    // T*K handled by the routing-table builder
+constexpr int kMaxExperts = 1024;  // matches the reference router limit
+constexpr int kGateUpRows = 8;     // intermediates per gate/up workgroup (2 per wave)
+constexpr int kDownRows = 8;       // output features per down workgroup (2 per wave)
+
+struct MoeWs {
+  uint32_t* tickets;    // [16] self-resetting arrival counters
+  int32_t* counts;      // [E]
+  int32_t* offsets;     // [E+1] exclusive prefix of counts
+  int32_t* perm;        // [P] permuted position -> pair index t*K+k
+  int32_t* inverse;     // [P] pair index -> permuted position
+  int32_t* active;      // [E] ids of experts with count > 0, ascending
+  int32_t* num_active;  // [1]
+  int32_t* ids32;       // [P] clamped expert ids
+  float* wts;           // [P] routing weights (fp32)
+  float* sgate;         // [T] shared-expert gate sigmoid(w_g . x)
+  float* act;           // [(P + T), I] SwiGLU activations
+};
+
+static size_t moe_ws_layout(int T, int K, int E, int I, char* base, MoeWs* ws) {
+  const size_t P = (size_t)T * K;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = off;
+    off = align_up(off + bytes, 256);
+    return base ? base + at : nullptr;
+  };
+  ws->tickets = reinterpret_cast<uint32_t*>(take(16 * sizeof(uint32_t)));
+  ws->counts = reinterpret_cast<int32_t*>(take((size_t)E * 4));
+  ws->offsets = reinterpret_cast<int32_t*>(take((size_t)(E + 1) * 4));
+  ws->perm = reinterpret_cast<int32_t*>(take(P * 4));
+  ws->inverse = reinterpret_cast<int32_t*>(take(P * 4));
+  ws->active = reinterpret_cast<int32_t*>(take((size_t)E * 4));
+  ws->num_active = reinterpret_cast<int32_t*>(take(4));
+  ws->ids32 = reinterpret_cast<int32_t*>(take(P * 4));
+  ws->wts = reinterpret_cast<float*>(take(P * 4));
+  ws->sgate = reinterpret_cast<float*>(take((size_t)T * 4));
+  ws->act = reinterpret_cast<float*>(take((P + T) * (size_t)I * 4));
+  return off;
+}
+
+// ---------------------------------------------------------------------------
+// Routing tables (histogram, offsets, stable permutation, active experts).
+// Runs inside one 256-thread workgroup; `s_ids` holds the P clamped ids.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    int o = __shfl_up(v, d, kWave);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+__device__ void build_routing_tables(const int* s_ids, int P, int E, MoeWs ws, int* s_cnt, int* s_off) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ int s_wtot[4][2];
+  for (int e = tid; e < E; e += 256) s_cnt[e] = 0;
+  __syncthreads();
+  for (int j = tid; j < P; j += 256) atomicAdd(&s_cnt[s_ids[j]], 1);
+  __syncthreads();
+
+  const int per = (E + 255) / 256;  // bins per thread (<= 4)
+  const int base = tid * per;
+  int sum = 0, nz = 0;
+  for (int q = 0; q < per; ++q) {
+    int e = base + q;
+    if (e < E) {
+      sum += s_cnt[e];
+      nz += s_cnt[e] > 0;
+    }
+  }
+  int isum = wave_incl_scan(sum, lane);
+  int inz = wave_incl_scan(nz, lane);
+  if (lane == 63) {
+    s_wtot[wave][0] = isum;
+    s_wtot[wave][1] = inz;
+  }
+  __syncthreads();
+  int psum = 0, pnz = 0;
+  for (int w = 0; w < wave; ++w) {
+    psum += s_wtot[w][0];
+    pnz += s_wtot[w][1];
+  }
+  int run = psum + isum - sum;
+  int runnz = pnz + inz - nz;
+  for (int q = 0; q < per; ++q) {
+    int e = base + q;
+    if (e < E) {
+      int c = s_cnt[e];
+      s_off[e] = run;
+      ws.offsets[e] = run;
+      ws.counts[e] = c;
+      if (c > 0) ws.active[runnz++] = e;
+      run += c;
+    }
+  }
+  if (tid == 0) {
+    ws.offsets[E] = P;
+    ws.num_active[0] = s_wtot[0][1] + s_wtot[1][1] + s_wtot[2][1] + s_wtot[3][1];
+  }
+  __syncthreads();
+  // Stable permutation: the thread owning expert e walks the pairs in
+  // (token, slot) order and appends the ones routed to e.
+  for (int e = tid; e < E; e += 256) {
+    int c = s_cnt[e];
+    int r = s_off[e];
+    for (int j = 0; j < P && c > 0; ++j) {
+      if (s_ids[j] == e) {
+        ws.perm[r] = j;
+        ws.inverse[j] = r;
+        ++r;
+        --c;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 1. Router
+// ---------------------------------------------------------------------------
+struct RouterArgs {
+  const void* x;
+  const void* nw;
+  const void* W;
+  const void* bias;
+  int nw_dt, bias_dt;
+  int T, H, E, K;
+  float eps, off;
+  float* logits;
+  int64_t* ids_out;
+  float* w_out;
+  MoeWs ws;
+};
+
+template <bool BFW, bool BFX, int NJ>
+__global__ __launch_bounds__(256) void moe_router_kernel(RouterArgs a) {
+  __shared__ int s_ids[kMaxPairs];
+  __shared__ int s_cnt[kMaxExperts];
+  __shared__ int s_off[kMaxExperts];
+  __shared__ int s_last;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.x * 4 + wave;
+  const int nch = a.H >> 3;
+
+  if (e < a.E) {
+    // Fold (norm_offset + w) into this expert's row once; the RMS scale is a
+    // per-token scalar applied after the dot product.
+    float wn[NJ][8];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = lane + kWave * j;
+      if (c < nch) {
+        float w8[8];
+        load8_f32<BFW>(a.W, (size_t)e * a.H + (size_t)c * 8, w8);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) wn[j][q] = w8[q] * (a.off + load_scalar(a.nw, a.nw_dt, (size_t)c * 8 + q));
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) wn[j][q] = 0.f;
+      }
+    }
+    const float bias = a.bias ? load_scalar(a.bias, a.bias_dt, e) : 0.f;
+    for (int t = 0; t < a.T; ++t) {
+      float ss = 0.f, d = 0.f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int c = lane + kWave * j;
+        if (c < nch) {
+          float x8[8];
+          load8_f32<BFX>(a.x, (size_t)t * a.H + (size_t)c * 8, x8);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            ss = fmaf(x8[q], x8[q], ss);
+            d = fmaf(x8[q], wn[j][q], d);
+          }
+        }
+      }
+      ss = wave_sum(ss);
+      d = wave_sum(d);
+      if (lane == 0) a.logits[(size_t)t * a.E + e] = d * rsqrtf(ss / (float)a.H + a.eps) + bias;
+    }
+  }
+
+  // Arrival: the last workgroup sees every logit.
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = (atomicAdd(&a.ws.tickets[0], 1u) == gridDim.x - 1);
+  __syncthreads();
+  if (!s_last) return;
+  __threadfence();
+
+  // Softmax + top-k per token, one wavefront per token.
+  for (int t = wave; t < a.T; t += 4) {
+    float p[16];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int ex = lane + kWave * j;
+      p[j] = ex < a.E ? __builtin_nontemporal_load(a.logits + (size_t)t * a.E + ex) : -INFINITY;
+      m = fmaxf(m, p[j]);
+    }
+    m = wave_max(m);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int ex = lane + kWave * j;
+      p[j] = ex < a.E ? expf(p[j] - m) : 0.f;
+      s += p[j];
+    }
+    s = wave_sum(s);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) p[j] = p[j] / s;
+
+    uint32_t taken = 0;
+    float denom = 0.f;
+    int my_id = 0;
+    float my_v = 0.f;
+    for (int k = 0; k < a.K; ++k) {
+      // Key orders by probability (non-negative floats compare as uints),
+      // then by the lower expert id.
+      uint64_t best = 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int ex = lane + kWave * j;
+        if (ex < a.E && !((taken >> j) & 1u)) {
+          uint64_t key = ((uint64_t)__float_as_uint(p[j]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)ex);
+          best = key > best ? key : best;
+        }
+      }
+      best = wave_max_u64(best);
+      const int sel = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+      const float v = __uint_as_float((uint32_t)(best >> 32));
+      if ((sel & 63) == lane) taken |= 1u << (sel >> 6);
+      denom += v;
+      if (lane == k) {
+        my_id = sel;
+        my_v = v;
+      }
+    }
+    if (lane < a.K) {
+      const size_t o = (size_t)t * a.K + lane;
+      const float w = my_v / denom;
+      a.ids_out[o] = my_id;
+      a.w_out[o] = w;
+      a.ws.ids32[o] = my_id;
+      a.ws.wts[o] = w;
+      s_ids[o] = my_id;
+    }
+  }
+  __syncthreads();
+  build_routing_tables(s_ids, a.T * a.K, a.E, a.ws, s_cnt, s_off);
+  if (threadIdx.x == 0) a.ws.tickets[0] = 0u;  // ready for the next call
+}
+
+// Routing tables from caller-supplied ids (single workgroup).
+struct AlignArgs {
+  const void* ids;
+  int ids_dt;
+  const void* w;
+  int w_dt;
+  int T, K, E;
+  MoeWs ws;
+  int32_t* counts_out;
+  int32_t* offsets_out;
+  int32_t* perm_out;
+  int32_t* inverse_out;
+};
+
+__global__ __launch_bounds__(256) void moe_align_kernel(AlignArgs a) {
+  __shared__ int s_ids[kMaxPairs];
+  __shared__ int s_cnt[kMaxExperts];
+  __shared__ int s_off[kMaxExperts];
+  const int P = a.T * a.K;
+  for (int j = threadIdx.x; j < P; j += 256) {
+    long long v = a.ids_dt == FK_DTYPE_I64 ? reinterpret_cast<const long long*>(a.ids)[j]
+                                           : (long long)reinterpret_cast<const int*>(a.ids)[j];
+    int e = (int)(v < 0 ? 0 : (v >= a.E ? a.E - 1 : v));
+    s_ids[j] = e;
+    a.ws.ids32[j] = e;
+    a.ws.wts[j] = a.w ? load_scalar(a.w, a.w_dt, j) : 0.f;
+  }
+  __syncthreads();
+  build_routing_tables(s_ids, P, a.E, a.ws, s_cnt, s_off);
+  __syncthreads();
+  // Optional copies of the tables for callers that inspect them.
+  for (int e = threadIdx.x; e < a.E; e += 256) {
+    if (a.counts_out) a.counts_out[e] = s_cnt[e];
+    if (a.offsets_out) a.offsets_out[e] = s_off[e];
+  }
+  if (threadIdx.x == 0 && a.offsets_out) a.offsets_out[a.E] = P;
+  if (a.perm_out || a.inverse_out) {
+    __threadfence_block();
+    __syncthreads();
+    for (int j = threadIdx.x; j < P; j += 256) {
+      if (a.perm_out) a.perm_out[j] = a.ws.perm[j];
+      if (a.inverse_out) a.inverse_out[j] = a.ws.inverse[j];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2./3. Expert stage
+// ---------------------------------------------------------------------------
+struct ExpertArgs {
+  const void* x;
+  int x_dt;
+  const void* gu;
+  const void* dn;
+  const void* sgu;
+  const void* sdn;
+  const void* sg;
+  int sg_dt;
+  int T, H, I, E, K;
+  int has_shared;
+  float* out;
+  float* layer_out;
+  MoeWs ws;
+};
+
+template <bool BFW, bool BFX, int NJ>
+__global__ __launch_bounds__(256) void moe_gateup_kernel(ExpertArgs a) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int chunks = a.I / kGateUpRows;
+  int slot = blockIdx.x / chunks;
+  const int chunk = blockIdx.x - slot * chunks;
+  const int P = a.T * a.K;
+  const size_t esz = BFW ? 2 : 4;
+
+  const char* W;
+  bool shared = false;
+  int pos0, npairs;
+  if (a.has_shared && slot == 0) {
+    W = reinterpret_cast<const char*>(a.sgu);
+    shared = true;
+    pos0 = P;
+    npairs = a.T;
+  } else {
+    if (a.has_shared) slot -= 1;
+    if (slot >= a.ws.num_active[0]) return;
+    const int e = a.ws.active[slot];
+    W = reinterpret_cast<const char*>(a.gu) + (size_t)e * 2 * a.I * a.H * esz;
+    pos0 = a.ws.offsets[e];
+    npairs = a.ws.counts[e];
+  }
+
+  const int nch = a.H >> 3;
+  const int i0 = chunk * kGateUpRows + wave * 2;  // this wave's two intermediates
+  const size_t rows[4] = {(size_t)i0, (size_t)i0 + 1, (size_t)a.I + i0, (size_t)a.I + i0 + 1};
+
+  // Stream the four rows (gate i0, gate i0+1, up i0, up i0+1) once.
+  Raw8<BFW> wr[4][NJ];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = lane + kWave * j;
+      if (c < nch) wr[r][j] = load_raw8_stream<BFW>(W, rows[r] * a.H + (size_t)c * 8);
+    }
+  }
+
+  for (int pp = 0; pp < npairs; ++pp) {
+    const int pos = pos0 + pp;
+    const int t = shared ? pp : a.ws.perm[pos] / a.K;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = lane + kWave * j;
+      if (c < nch) {
+        float x8[8];
+        load8_f32<BFX>(a.x, (size_t)t * a.H + (size_t)c * 8, x8);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float w8[8];
+          raw8_to_f32<BFW>(wr[r][j], w8);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[r] = fmaf(w8[q], x8[q], acc[r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] = wave_sum(acc[r]);
+    if (lane == 0) {
+      float2 v = make_float2(silu(acc[0]) * acc[2], silu(acc[1]) * acc[3]);
+      *reinterpret_cast<float2*>(a.ws.act + (size_t)pos * a.I + i0) = v;
+    }
+  }
+
+  // Shared-expert gate sigmoid(w_g . x_t), once per token.
+  if (shared && chunk == 0 && a.sg) {
+    for (int t = wave; t < a.T; t += 4) {
+      float d = 0.f;
+      for (int c = lane; c < nch; c += kWave) {
+        float x8[8];
+        load8_f32<BFX>(a.x, (size_t)t * a.H + (size_t)c * 8, x8);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) d = fmaf(x8[q], load_scalar(a.sg, a.sg_dt, (size_t)c * 8 + q), d);
+      }
+      d = wave_sum(d);
+      if (lane == 0) a.ws.sgate[t] = sigmoid(d);
+    }
+  }
+}
+
+// Down projection.  SINGLE (T == 1): each lane keeps its partial sums across
+// all slots and reduces once per output feature.  Otherwise every
+// (feature, pair) dot is reduced and lane 0 accumulates it per token in LDS,
+// in slot order (shared first, then ascending expert id, pairs in (token,
+// slot) order).
+template <bool BFW, int NJI, bool SINGLE>
+__global__ __launch_bounds__(256) void moe_down_kernel(ExpertArgs a) {
+  extern __shared__ float s_acc[];  // [4 waves][2 rows][T] (multi-token path)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r0 = blockIdx.x * kDownRows + wave * 2;
+  const int nci = a.I >> 3;
+  const int P = a.T * a.K;
+  const size_t esz = BFW ? 2 : 4;
+  const int U = a.ws.num_active[0];
+  const int nslots = U + (a.has_shared ? 1 : 0);
+  const bool row_ok[2] = {r0 < a.H, r0 + 1 < a.H};
+  const float gate_default = 1.f;
+
+  auto slot_info = [&](int s, const char*& W, int& pos0, int& npairs, bool& shared) {
+    if (a.has_shared && s == 0) {
+      W = reinterpret_cast<const char*>(a.sdn);
+      pos0 = P;
+      npairs = a.T;
+      shared = true;
+    } else {
+      const int e = a.ws.active[s - (a.has_shared ? 1 : 0)];
+      W = reinterpret_cast<const char*>(a.dn) + (size_t)e * a.H * a.I * esz;
+      pos0 = a.ws.offsets[e];
+      npairs = a.ws.counts[e];
+      shared = false;
+    }
+  };
+
+  if constexpr (SINGLE) {
+    float acc[2] = {0.f, 0.f};
+    constexpr int B = 4;  // slots in flight per wave
+    for (int s0 = 0; s0 < nslots; s0 += B) {
+      Raw8<BFW> wr[B][2][NJI];
+      float av[B][NJI][8];
+      float wt[B];
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        const int s = s0 + b;
+        wt[b] = 0.f;
+        if (s < nslots) {
+          const char* W;
+          int pos0, npairs;
+          bool shared;
+          slot_info(s, W, pos0, npairs, shared);
+          wt[b] = shared ? (a.sg ? a.ws.sgate[0] : gate_default) : a.ws.wts[a.ws.perm[pos0]];
+#pragma unroll
+          for (int r = 0; r < 2; ++r)
+#pragma unroll
+            for (int j = 0; j < NJI; ++j) {
+              const int c = lane + kWave * j;
+              if (c < nci && row_ok[r]) wr[b][r][j] = load_raw8_stream<BFW>(W, (size_t)(r0 + r) * a.I + (size_t)c * 8);
+            }
+#pragma unroll
+          for (int j = 0; j < NJI; ++j) {
+            const int c = lane + kWave * j;
+            if (c < nci) load8_act(a.ws.act, (size_t)pos0 * a.I + (size_t)c * 8, av[b][j]);
+          }
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < B; ++b) {
+        if (s0 + b < nslots) {
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            float d = 0.f;
+#pragma unroll
+            for (int j = 0; j < NJI; ++j) {
+              const int c = lane + kWave * j;
+              if (c < nci && row_ok[r]) {
+                float w8[8];
+                raw8_to_f32<BFW>(wr[b][r][j], w8);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) d = fmaf(w8[q], av[b][j][q], d);
+              }
+            }
+            acc[r] = fmaf(wt[b], d, acc[r]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const float v = wave_sum(acc[r]);
+      if (lane == 0 && row_ok[r]) {
+        a.out[r0 + r] = v;
+        if (a.layer_out) a.layer_out[r0 + r] = load_scalar(a.x, a.x_dt, r0 + r) + v;
+      }
+    }
+  } else {
+    float* my_acc = s_acc + (size_t)wave * 2 * a.T;
+    for (int i = lane; i < 2 * a.T; i += kWave) my_acc[i] = 0.f;
+    __syncthreads();
+    for (int s = 0; s < nslots; ++s) {
+      const char* W;
+      int pos0, npairs;
+      bool shared;
+      slot_info(s, W, pos0, npairs, shared);
+      Raw8<BFW> wr[2][NJI];
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int j = 0; j < NJI; ++j) {
+          const int c = lane + kWave * j;
+          if (c < nci && row_ok[r]) wr[r][j] = load_raw8_stream<BFW>(W, (size_t)(r0 + r) * a.I + (size_t)c * 8);
+        }
+      for (int pp = 0; pp < npairs; ++pp) {
+        const int pos = pos0 + pp;
+        int t;
+        float wt;
+        if (shared) {
+          t = pp;
+          wt = a.sg ? a.ws.sgate[t] : gate_default;
+        } else {
+          const int pair = a.ws.perm[pos];
+          t = pair / a.K;
+          wt = a.ws.wts[pair];
+        }
+        float d[2] = {0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NJI; ++j) {
+          const int c = lane + kWave * j;
+          if (c < nci) {
+            float av[8];
+            load8_act(a.ws.act, (size_t)pos * a.I + (size_t)c * 8, av);
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+              if (row_ok[r]) {
+                float w8[8];
+                raw8_to_f32<BFW>(wr[r][j], w8);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) d[r] = fmaf(w8[q], av[q], d[r]);
+              }
+            }
+          }
+        }
+        d[0] = wave_sum(d[0]);
+        d[1] = wave_sum(d[1]);
+        if (lane == 0) {
+          my_acc[t] = fmaf(wt, d[0], my_acc[t]);
+          my_acc[a.T + t] = fmaf(wt, d[1], my_acc[a.T + t]);
+        }
+      }
+    }
+    __syncthreads();
+    for (int r = 0; r < 2; ++r) {
+      if (!row_ok[r]) continue;
+      for (int t = lane; t < a.T; t += kWave) {
+        const float v = my_acc[r * a.T + t];
+        const size_t o = (size_t)t * a.H + r0 + r;
+        a.out[o] = v;
+        if (a.layer_out) a.layer_out[o] = load_scalar(a.x, a.x_dt, o) + v;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers
+// ---------------------------------------------------------------------------
+static int check_ws(void* ws, size_t bytes, int T, int K, int E, int I, MoeWs* out) {
+  size_t need = moe_ws_layout(T, K, E, I, nullptr, out);
+  if (!ws) return fail(FK_ERR_WORKSPACE, "workspace is NULL (need %zu bytes)", need);
+  if (bytes < need) return fail(FK_ERR_WORKSPACE, "workspace has %zu bytes, need %zu", bytes, need);
+  if (!aligned16(ws)) return fail(FK_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
+  moe_ws_layout(T, K, E, I, reinterpret_cast<char*>(ws), out);
+  return FK_OK;
+}
+
+#define FK_DISPATCH_BOOL(cond, NAME, ...) \
+  if (cond) {                             \
+    constexpr bool NAME = true;           \
+    __VA_ARGS__                           \
+  } else {                                \
+    constexpr bool NAME = false;          \
+    __VA_ARGS__                           \
+  }
+
+static int launch_router(const RouterArgs& ra, int router_dt, int hidden_dt, hipStream_t stream) {
+  const int grid = (ra.E + 3) / 4;
+  const bool bfw = router_dt == FK_DTYPE_BF16, bfx = hidden_dt == FK_DTYPE_BF16;
+  const bool wide = ra.H > 2048;
+  FK_DISPATCH_BOOL(bfw, BW, FK_DISPATCH_BOOL(bfx, BX, {
+    if (wide) {
+      hipLaunchKernelGGL((moe_router_kernel<BW, BX, 8>), dim3(grid), dim3(256), 0, stream, ra);
+    } else {
+      hipLaunchKernelGGL((moe_router_kernel<BW, BX, 4>), dim3(grid), dim3(256), 0, stream, ra);
+    }
+  }))
+  return check_launch("moe_router_kernel");
+}
+
+static int launch_experts(const ExpertArgs& ea, int expert_dt, hipStream_t stream) {
+  const bool bfw = expert_dt == FK_DTYPE_BF16, bfx = ea.x_dt == FK_DTYPE_BF16;
+  const bool wide = ea.H > 2048;
+  const int max_active = ea.T * ea.K < ea.E ? ea.T * ea.K : ea.E;
+  const int slots = max_active + (ea.has_shared ? 1 : 0);
+  const int gu_grid = slots * (ea.I / kGateUpRows);
+  FK_DISPATCH_BOOL(bfw, BW, FK_DISPATCH_BOOL(bfx, BX, {
+    if (wide) {
+      hipLaunchKernelGGL((moe_gateup_kernel<BW, BX, 8>), dim3(gu_grid), dim3(256), 0, stream, ea);
+    } else {
+      hipLaunchKernelGGL((moe_gateup_kernel<BW, BX, 4>), dim3(gu_grid), dim3(256), 0, stream, ea);
+    }
+  }))
+  int st = check_launch("moe_gateup_kernel");
+  if (st) return st;
+
+  const int dn_grid = (ea.H + kDownRows - 1) / kDownRows;
+  const bool wide_i = ea.I > 512;
+  const size_t shm = ea.T == 1 ? 0 : (size_t)4 * 2 * ea.T * sizeof(float);
+  FK_DISPATCH_BOOL(bfw, BW, {
+    if (ea.T == 1) {
+      if (wide_i) hipLaunchKernelGGL((moe_down_kernel<BW, 2, true>), dim3(dn_grid), dim3(256), 0, stream, ea);
+      else hipLaunchKernelGGL((moe_down_kernel<BW, 1, true>), dim3(dn_grid), dim3(256), 0, stream, ea);
+    } else {
+      if (wide_i) hipLaunchKernelGGL((moe_down_kernel<BW, 2, false>), dim3(dn_grid), dim3(256), shm, stream, ea);
+      else hipLaunchKernelGGL((moe_down_kernel<BW, 1, false>), dim3(dn_grid), dim3(256), shm, stream, ea);
+    }
+  })
+  return check_launch("moe_down_kernel");
+}
+
+static int validate_common(int T, int H, int E, int K) {
+  if (T < 1) return fail(FK_ERR_INVALID, "tokens must be positive (got %d)", T);
+  if (H < 8 || H % 8) return fail(FK_ERR_ALIGNMENT, "hidden_size must be a positive multiple of 8 (got %d)", H);
+  if (H > 4096) return fail(FK_ERR_UNSUPPORTED, "hidden_size must be <= 4096 (got %d)", H);
+  if (E < 1 || E > kMaxExperts) return fail(FK_ERR_UNSUPPORTED, "num_experts must be in [1, %d] (got %d)", kMaxExperts, E);
+  if (K < 1 || K > 8 || K > E) return fail(FK_ERR_INVALID, "top_k must be in [1, min(8, num_experts)] (got %d)", K);
+  if ((long long)T * K > kMaxPairs) return fail(FK_ERR_UNSUPPORTED, "tokens * top_k must be <= %d", kMaxPairs);
+  return FK_OK;
+}
+
+static int validate_experts(const void* hidden, int hidden_dt, const void* gu, const void* dn, int expert_dt,
+                            const void* sgu, const void* sdn, const void* sg, int sg_dt, int T, int H, int I,
+                            int E, int K) {
+  int st = validate_common(T, H, E, K);
+  if (st) return st;
+  if (!is_float_dtype(hidden_dt) || !is_float_dtype(expert_dt)) return fail(FK_ERR_DTYPE, "hidden/expert dtype must be f32 or bf16");
+  if (sg && !is_float_dtype(sg_dt)) return fail(FK_ERR_DTYPE, "shared_gate dtype must be f32 or bf16");
+  if (I < 8 || I % 8) return fail(FK_ERR_ALIGNMENT, "intermediate must be a positive multiple of 8 (got %d)", I);
+  if (I > 1024) return fail(FK_ERR_UNSUPPORTED, "intermediate must be <= 1024 (got %d)", I);
+  if (!hidden || !gu || !dn) return fail(FK_ERR_INVALID, "hidden and expert weights must be non-NULL");
+  if ((sgu == nullptr) != (sdn == nullptr)) return fail(FK_ERR_INVALID, "shared_gate_up and shared_down must both be set or both NULL");
+  if (!aligned16(hidden) || !aligned16(gu) || !aligned16(dn) || (sgu && !aligned16(sgu)) || (sdn && !aligned16(sdn)))
+    return fail(FK_ERR_ALIGNMENT, "hidden and expert weights must be 16-byte aligned");
+  return FK_OK;
+}
+
+static ExpertArgs make_expert_args(const void* hidden, int hidden_dt, const void* gu, const void* dn,
+                                   const void* sgu, const void* sdn, const void* sg, int sg_dt, int T, int H,
+                                   int I, int E, int K, float* out, float* layer_out, const MoeWs& ws) {
+  ExpertArgs ea;
+  ea.x = hidden;
+  ea.x_dt = hidden_dt;
+  ea.gu = gu;
+  ea.dn = dn;
+  ea.sgu = sgu;
+  ea.sdn = sdn;
+  ea.sg = sgu ? sg : nullptr;
+  ea.sg_dt = sg_dt;
+  ea.T = T;
+  ea.H = H;
+  ea.I = I;
+  ea.E = E;
+  ea.K = K;
+  ea.has_shared = sgu != nullptr;
+  ea.out = out;
+  ea.layer_out = layer_out;
+  ea.ws = ws;
+  return ea;
+}
+
+}  // namespace fk
+
+using namespace fk;
+
+extern "C" {
+
+size_t fk_moe_workspace_bytes(int tokens, int top_k, int num_experts, int intermediate) {
+  if (tokens < 1 || top_k < 1 || num_experts < 1 || intermediate < 1) return 0;
+  MoeWs ws;
+  return moe_ws_layout(tokens, top_k, num_experts, intermediate, nullptr, &ws);
+}
+
+int fk_moe_router(const void* hidden, int hidden_dtype, const void* norm_weight, int norm_dtype,
+                  const void* router_weight, int router_dtype, const void* router_bias, int bias_dtype,
+                  int tokens, int hidden_size, int num_experts, int top_k, float eps, float norm_offset,
+                  float* logits, int64_t* topk_ids, float* topk_weights, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  int st = validate_common(tokens, hidden_size, num_experts, top_k);
+  if (st) return st;
+  if (!is_float_dtype(hidden_dtype) || !is_float_dtype(norm_dtype) || !is_float_dtype(router_dtype) ||
+      (router_bias && !is_float_dtype(bias_dtype)))
+    return fail(FK_ERR_DTYPE, "router inputs must be f32 or bf16");
+  if (!hidden || !norm_weight || !router_weight || !logits || !topk_ids || !topk_weights)
+    return fail(FK_ERR_INVALID, "router pointers must be non-NULL");
+  if (!aligned16(hidden) || !aligned16(router_weight)) return fail(FK_ERR_ALIGNMENT, "hidden and router_weight must be 16-byte aligned");
+  MoeWs ws;
+  // The router only needs the routing tables; size them for any intermediate.
+  st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, 0, &ws);
+  if (st) return st;
+  RouterArgs ra;
+  ra.x = hidden;
+  ra.nw = norm_weight;
+  ra.W = router_weight;
+  ra.bias = router_bias;
+  ra.nw_dt = norm_dtype;
+  ra.bias_dt = bias_dtype;
+  ra.T = tokens;
+  ra.H = hidden_size;
+  ra.E = num_experts;
+  ra.K = top_k;
+  ra.eps = eps;
+  ra.off = norm_offset;
+  ra.logits = logits;
+  ra.ids_out = topk_ids;
+  ra.w_out = topk_weights;
+  ra.ws = ws;
+  return launch_router(ra, router_dtype, hidden_dtype, as_stream(stream));
+}
+
+int fk_moe_align(const void* topk_ids, int ids_dtype, const void* topk_weights, int weights_dtype, int tokens,
+                 int top_k, int num_experts, void* workspace, size_t workspace_bytes, int32_t* counts_out,
+                 int32_t* offsets_out, int32_t* perm_out, int32_t* inverse_out, void* stream) {
+  if (tokens < 1 || top_k < 1 || top_k > 8) return fail(FK_ERR_INVALID, "need tokens >= 1 and 1 <= top_k <= 8");
+  if (num_experts < 1 || num_experts > kMaxExperts) return fail(FK_ERR_UNSUPPORTED, "num_experts must be in [1, %d]", kMaxExperts);
+  if ((long long)tokens * top_k > kMaxPairs) return fail(FK_ERR_UNSUPPORTED, "tokens * top_k must be <= %d", kMaxPairs);
+  if (!is_index_dtype(ids_dtype)) return fail(FK_ERR_DTYPE, "topk_ids must be int32 or int64");
+  if (topk_weights && !is_float_dtype(weights_dtype)) return fail(FK_ERR_DTYPE, "topk_weights must be f32 or bf16");
+  if (!topk_ids) return fail(FK_ERR_INVALID, "topk_ids must be non-NULL");
+  MoeWs ws;
+  int st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, 0, &ws);
+  if (st) return st;
+  AlignArgs aa;
+  aa.ids = topk_ids;
+  aa.ids_dt = ids_dtype;
+  aa.w = topk_weights;
+  aa.w_dt = weights_dtype;
+  aa.T = tokens;
+  aa.K = top_k;
+  aa.E = num_experts;
+  aa.ws = ws;
+  aa.counts_out = counts_out;
+  aa.offsets_out = offsets_out;
+  aa.perm_out = perm_out;
+  aa.inverse_out = inverse_out;
+  hipLaunchKernelGGL(moe_align_kernel, dim3(1), dim3(256), 0, as_stream(stream), aa);
+  return check_launch("moe_align_kernel");
+}
+
+int fk_moe_experts(const void* hidden, int hidden_dtype, const void* gate_up, const void* down, int expert_dtype,
+                   const void* shared_gate_up, const void* shared_down, const void* shared_gate,
+                   int shared_gate_dtype, int tokens, int hidden_size, int intermediate, int num_experts,
+                   int top_k, float* out, float* layer_out, void* workspace, size_t workspace_bytes,
+                   void* stream) {
+  int st = validate_experts(hidden, hidden_dtype, gate_up, down, expert_dtype, shared_gate_up, shared_down,
+                            shared_gate, shared_gate_dtype, tokens, hidden_size, intermediate, num_experts, top_k);
+  if (st) return st;
+  if (!out) return fail(FK_ERR_INVALID, "out must be non-NULL");
+  MoeWs ws;
+  st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, intermediate, &ws);
+  if (st) return st;
+  ExpertArgs ea = make_expert_args(hidden, hidden_dtype, gate_up, down, shared_gate_up, shared_down, shared_gate,
+                                   shared_gate_dtype, tokens, hidden_size, intermediate, num_experts, top_k, out,
+                                   layer_out, ws);
+  return launch_experts(ea, expert_dtype, as_stream(stream));
+}
+
+int fk_moe_layer(const void* hidden, int hidden_dtype, const void* norm_weight, int norm_dtype,
+                 const void* router_weight, int router_dtype, const void* router_bias, int bias_dtype,
+                 const void* gate_up, const void* down, int expert_dtype, const void* shared_gate_up,
+                 const void* shared_down, const void* shared_gate, int shared_gate_dtype, int tokens,
+                 int hidden_size, int intermediate, int num_experts, int top_k, float eps, float norm_offset,
+                 float* logits, int64_t* topk_ids, float* topk_weights, float* moe_out, float* layer_out,
+                 void* workspace, size_t workspace_bytes, void* stream) {
+  int st = validate_experts(hidden, hidden_dtype, gate_up, down, expert_dtype, shared_gate_up, shared_down,
+                            shared_gate, shared_gate_dtype, tokens, hidden_size, intermediate, num_experts, top_k);
+  if (st) return st;
+  if (!moe_out) return fail(FK_ERR_INVALID, "moe_out must be non-NULL");
+  MoeWs ws;
+  st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, intermediate, &ws);
+  if (st) return st;
+  st = fk_moe_router(hidden, hidden_dtype, norm_weight, norm_dtype, router_weight, router_dtype, router_bias,
+                     bias_dtype, tokens, hidden_size, num_experts, top_k, eps, norm_offset, logits, topk_ids,
+                     topk_weights, workspace, workspace_bytes, stream);
+  if (st) return st;
+  ExpertArgs ea = make_expert_args(hidden, hidden_dtype, gate_up, down, shared_gate_up, shared_down, shared_gate,
+                                   shared_gate_dtype, tokens, hidden_size, intermediate, num_experts, top_k,
+                                   moe_out, layer_out, ws);
+  return launch_experts(ea, expert_dtype, as_stream(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,352 @@
+// Small standalone operators: expert histogram, fused SwiGLU, residual add,
+// and the single-workgroup synthetic (tiny-spec) MoE and DeltaNet blocks used
+// by the --moe-impl / --deltanet-impl switch of the synthetic decode bench.
+#include "fk_common.h"
+#include "fk_host.h"
+
+namespace fk {
+
+__device__ __forceinline__ long long load_index(const void* p, int dtype, size_t i) {
+  return dtype == FK_DTYPE_I64 ? reinterpret_cast<const long long*>(p)[i]
+                               : (long long)reinterpret_cast<const int*>(p)[i];
+}
+
+__global__ void fill_i32_kernel(int32_t* p, int n, int32_t v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+__global__ void histogram_kernel(const void* ids, int ids_dt, long long n, int E, int32_t* counts) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const long long e = load_index(ids, ids_dt, (size_t)i);
+  if (e >= 0 && e < E) atomicAdd(&counts[e], 1);
+}
+
+__global__ void swiglu_kernel(const void* gu, int dt, long long rows, int I, void* out) {
+  const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * I) return;
+  const long long r = idx / I, i = idx - r * I;
+  const float g = load_scalar(gu, dt, (size_t)(r * 2 * I + i));
+  const float u = load_scalar(gu, dt, (size_t)(r * 2 * I + I + i));
+  store_scalar(out, dt, (size_t)idx, silu(g) * u);
+}
+
+__global__ void residual_add_kernel(const void* x, int x_dt, const float* u, long long n, float* out) {
+  const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) out[i] = load_scalar(x, x_dt, (size_t)i) + u[i];
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic MoE (one token, one workgroup).  Semantics of
+// reference_qwen36_moe_decode (reference/qwen36_decode.py:212-224): router on
+// x * rsqrt(mean x^2 + eps) * w (plain weight), softmax top-k renormalised,
+// routed experts + ungated shared expert on the raw x, plus the residual.
+// ---------------------------------------------------------------------------
+constexpr int kSynMax = 1024;
+
+struct SynMoeArgs {
+  const void* x;
+  int x_dt;
+  const void* nw;
+  const void* rw;
+  const void* gu;
+  const void* dn;
+  const void* sgu;
+  const void* sdn;
+  int w_dt;
+  int H, E, I, K;
+  float eps;
+  void* out;
+  int out_dt;
+};
+
+__global__ __launch_bounds__(256) void synthetic_moe_kernel(SynMoeArgs a) {
+  __shared__ float s_x[kSynMax], s_n[kSynMax], s_logit[kSynMax], s_act[kSynMax], s_acc[kSynMax];
+  __shared__ float s_red[4];
+  __shared__ int s_sel[8];
+  __shared__ float s_w[8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  float ss = 0.f;
+  for (int h = tid; h < a.H; h += 256) {
+    const float v = load_scalar(a.x, a.x_dt, h);
+    s_x[h] = v;
+    ss = fmaf(v, v, ss);
+    s_acc[h] = 0.f;
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) s_red[wave] = ss;
+  __syncthreads();
+  const float rs = rsqrtf((s_red[0] + s_red[1] + s_red[2] + s_red[3]) / (float)a.H + a.eps);
+  for (int h = tid; h < a.H; h += 256) s_n[h] = s_x[h] * rs * load_scalar(a.nw, a.w_dt, h);
+  __syncthreads();
+  for (int e = tid; e < a.E; e += 256) {
+    float d = 0.f;
+    for (int h = 0; h < a.H; ++h) d = fmaf(s_n[h], load_scalar(a.rw, a.w_dt, (size_t)e * a.H + h), d);
+    s_logit[e] = d;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float p[16];
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int e = lane + kWave * j;
+      p[j] = e < a.E ? s_logit[e] : -INFINITY;
+      m = fmaxf(m, p[j]);
+    }
+    m = wave_max(m);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int e = lane + kWave * j;
+      p[j] = e < a.E ? expf(p[j] - m) : 0.f;
+      s += p[j];
+    }
+    s = wave_sum(s);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) p[j] = p[j] / s;
+    uint32_t taken = 0;
+    float denom = 0.f;
+    for (int k = 0; k < a.K; ++k) {
+      uint64_t best = 0;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int e = lane + kWave * j;
+        if (e < a.E && !((taken >> j) & 1u)) {
+          const uint64_t key = ((uint64_t)__float_as_uint(p[j]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)e);
+          best = key > best ? key : best;
+        }
+      }
+      best = wave_max_u64(best);
+      const int sel = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
+      const float v = __uint_as_float((uint32_t)(best >> 32));
+      if ((sel & 63) == lane) taken |= 1u << (sel >> 6);
+      denom += v;
+      if (lane == 0) {
+        s_sel[k] = sel;
+        s_w[k] = v;
+      }
+    }
+    if (lane == 0)
+      for (int k = 0; k < a.K; ++k) s_w[k] /= denom;
+  }
+  __syncthreads();
+  const size_t esz = a.w_dt == FK_DTYPE_BF16 ? 2 : 4;
+  for (int k = 0; k <= a.K; ++k) {
+    const bool shared = k == a.K;
+    const char* gu = shared ? reinterpret_cast<const char*>(a.sgu)
+                            : reinterpret_cast<const char*>(a.gu) + (size_t)s_sel[k] * 2 * a.I * a.H * esz;
+    const char* dn = shared ? reinterpret_cast<const char*>(a.sdn)
+                            : reinterpret_cast<const char*>(a.dn) + (size_t)s_sel[k] * a.H * a.I * esz;
+    const float wk = shared ? 1.f : s_w[k];
+    for (int i = tid; i < a.I; i += 256) {
+      float g = 0.f, u = 0.f;
+      for (int h = 0; h < a.H; ++h) {
+        g = fmaf(load_scalar(gu, a.w_dt, (size_t)i * a.H + h), s_x[h], g);
+        u = fmaf(load_scalar(gu, a.w_dt, (size_t)(a.I + i) * a.H + h), s_x[h], u);
+      }
+      s_act[i] = silu(g) * u;
+    }
+    __syncthreads();
+    for (int h = tid; h < a.H; h += 256) {
+      float d = 0.f;
+      for (int i = 0; i < a.I; ++i) d = fmaf(load_scalar(dn, a.w_dt, (size_t)h * a.I + i), s_act[i], d);
+      s_acc[h] = fmaf(wk, d, s_acc[h]);
+    }
+    __syncthreads();
+  }
+  for (int h = tid; h < a.H; h += 256) store_scalar(a.out, a.out_dt, h, s_x[h] + s_acc[h]);
+}
+
+// ---------------------------------------------------------------------------
+// Synthetic DeltaNet (one token, one workgroup).  Semantics of
+// reference_qwen36_deltanet_decode (reference/qwen36_decode.py:155-171).
+// ---------------------------------------------------------------------------
+struct SynDnArgs {
+  const void* x;
+  int x_dt;
+  const void* state;
+  int s_dt;
+  const void* nw;
+  const void* qw;
+  const void* kw;
+  const void* vw;
+  const void* gw;
+  const void* ow;
+  int w_dt;
+  int H, Hk, D, Vd;
+  float eps;
+  void* x_out;
+  void* s_out;
+};
+
+__global__ __launch_bounds__(256) void synthetic_deltanet_kernel(SynDnArgs a) {
+  __shared__ float s_x[kSynMax], s_xn[kSynMax], s_q[kSynMax], s_k[kSynMax], s_v[kSynMax], s_g[kSynMax], s_r[kSynMax];
+  __shared__ float s_red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int QW = a.Hk * a.D, VW = a.Hk * a.Vd;
+  float ss = 0.f;
+  for (int h = tid; h < a.H; h += 256) {
+    const float v = load_scalar(a.x, a.x_dt, h);
+    s_x[h] = v;
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) s_red[wave] = ss;
+  __syncthreads();
+  const float rs = rsqrtf((s_red[0] + s_red[1] + s_red[2] + s_red[3]) / (float)a.H + a.eps);
+  for (int h = tid; h < a.H; h += 256) s_xn[h] = s_x[h] * rs * load_scalar(a.nw, a.w_dt, h);
+  __syncthreads();
+  for (int r = tid; r < QW; r += 256) {
+    float q = 0.f, k = 0.f;
+    for (int h = 0; h < a.H; ++h) {
+      q = fmaf(load_scalar(a.qw, a.w_dt, (size_t)r * a.H + h), s_xn[h], q);
+      k = fmaf(load_scalar(a.kw, a.w_dt, (size_t)r * a.H + h), s_xn[h], k);
+    }
+    s_q[r] = q;
+    s_k[r] = k;
+  }
+  for (int r = tid; r < VW; r += 256) {
+    float v = 0.f, g = 0.f;
+    for (int h = 0; h < a.H; ++h) {
+      v = fmaf(load_scalar(a.vw, a.w_dt, (size_t)r * a.H + h), s_xn[h], v);
+      g = fmaf(load_scalar(a.gw, a.w_dt, (size_t)r * a.H + h), s_xn[h], g);
+    }
+    s_v[r] = v;
+    s_g[r] = sigmoid(g);
+  }
+  __syncthreads();
+  // New state and the gated read-out, one thread per (head, value column).
+  for (int hv = tid; hv < VW; hv += 256) {
+    const int hh = hv / a.Vd, vv = hv - hh * a.Vd;
+    float r = 0.f;
+    for (int d = 0; d < a.D; ++d) {
+      const size_t si = ((size_t)hh * a.D + d) * a.Vd + vv;
+      const float ns = 0.95f * load_scalar(a.state, a.s_dt, si) + s_k[hh * a.D + d] * s_v[hv];
+      store_scalar(a.s_out, a.s_dt, si, ns);
+      r = fmaf(s_q[hh * a.D + d], ns, r);
+    }
+    s_r[hv] = r * s_g[hv];
+  }
+  __syncthreads();
+  for (int h = tid; h < a.H; h += 256) {
+    float d = 0.f;
+    for (int j = 0; j < VW; ++j) d = fmaf(load_scalar(a.ow, a.w_dt, (size_t)h * VW + j), s_r[j], d);
+    store_scalar(a.x_out, a.x_dt, h, s_x[h] + d);
+  }
+}
+
+}  // namespace fk
+
+using namespace fk;
+
+extern "C" {
+
+int fk_expert_histogram(const void* ids, int ids_dtype, int64_t n, int num_experts, int32_t* counts, void* stream) {
+  if (!is_index_dtype(ids_dtype)) return fail(FK_ERR_DTYPE, "ids must be int32 or int64");
+  if (num_experts < 1) return fail(FK_ERR_INVALID, "num_experts must be positive");
+  if (n < 0) return fail(FK_ERR_INVALID, "n must be >= 0");
+  if (!counts || (n > 0 && !ids)) return fail(FK_ERR_INVALID, "ids/counts must be non-NULL");
+  hipStream_t s = as_stream(stream);
+  hipLaunchKernelGGL(fill_i32_kernel, dim3((num_experts + 255) / 256), dim3(256), 0, s, counts, num_experts, 0);
+  int st = check_launch("fill_i32_kernel");
+  if (st || n == 0) return st;
+  hipLaunchKernelGGL(histogram_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ids, ids_dtype,
+                     (long long)n, num_experts, counts);
+  return check_launch("histogram_kernel");
+}
+
+int fk_fused_swiglu(const void* gate_up, int dtype, int64_t rows, int intermediate, void* out, void* stream) {
+  if (!is_float_dtype(dtype)) return fail(FK_ERR_DTYPE, "gate_up must be f32 or bf16");
+  if (rows < 0 || intermediate < 1) return fail(FK_ERR_INVALID, "rows must be >= 0 and intermediate positive");
+  const long long n = (long long)rows * intermediate;
+  if (n == 0) return FK_OK;
+  if (!gate_up || !out) return fail(FK_ERR_INVALID, "gate_up/out must be non-NULL");
+  hipLaunchKernelGGL(swiglu_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream), gate_up,
+                     dtype, (long long)rows, intermediate, out);
+  return check_launch("swiglu_kernel");
+}
+
+int fk_residual_add(const void* hidden, int hidden_dtype, const float* update, int64_t n, float* out, void* stream) {
+  if (!is_float_dtype(hidden_dtype)) return fail(FK_ERR_DTYPE, "hidden must be f32 or bf16");
+  if (n < 0) return fail(FK_ERR_INVALID, "n must be >= 0");
+  if (n == 0) return FK_OK;
+  if (!hidden || !update || !out) return fail(FK_ERR_INVALID, "pointers must be non-NULL");
+  hipLaunchKernelGGL(residual_add_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream), hidden,
+                     hidden_dtype, update, (long long)n, out);
+  return check_launch("residual_add_kernel");
+}
+
+int fk_synthetic_moe(const void* hidden, int hidden_dtype, const void* norm_weight, const void* router_weight,
+                     const void* gate_up, const void* down, const void* shared_gate_up, const void* shared_down,
+                     int weight_dtype, int hidden_size, int num_experts, int intermediate, int top_k, float eps,
+                     void* out, int out_dtype, void* stream) {
+  if (!is_float_dtype(hidden_dtype) || !is_float_dtype(weight_dtype) || !is_float_dtype(out_dtype))
+    return fail(FK_ERR_DTYPE, "synthetic MoE tensors must be f32 or bf16");
+  if (hidden_size < 1 || hidden_size > kSynMax || intermediate < 1 || intermediate > kSynMax)
+    return fail(FK_ERR_UNSUPPORTED, "synthetic MoE supports hidden/intermediate in [1, %d]", kSynMax);
+  if (num_experts < 1 || num_experts > kSynMax) return fail(FK_ERR_UNSUPPORTED, "num_experts must be in [1, %d]", kSynMax);
+  if (top_k < 1 || top_k > 8 || top_k > num_experts) return fail(FK_ERR_INVALID, "top_k must be in [1, min(8, experts)]");
+  if (!hidden || !norm_weight || !router_weight || !gate_up || !down || !shared_gate_up || !shared_down || !out)
+    return fail(FK_ERR_INVALID, "synthetic MoE pointers must be non-NULL");
+  SynMoeArgs sa;
+  sa.x = hidden;
+  sa.x_dt = hidden_dtype;
+  sa.nw = norm_weight;
+  sa.rw = router_weight;
+  sa.gu = gate_up;
+  sa.dn = down;
+  sa.sgu = shared_gate_up;
+  sa.sdn = shared_down;
+  sa.w_dt = weight_dtype;
+  sa.H = hidden_size;
+  sa.E = num_experts;
+  sa.I = intermediate;
+  sa.K = top_k;
+  sa.eps = eps;
+  sa.out = out;
+  sa.out_dt = out_dtype;
+  hipLaunchKernelGGL(synthetic_moe_kernel, dim3(1), dim3(256), 0, as_stream(stream), sa);
+  return check_launch("synthetic_moe_kernel");
+}
+
+int fk_synthetic_deltanet(const void* hidden, int hidden_dtype, const void* state, int state_dtype,
+                          const void* norm_weight, const void* q_weight, const void* k_weight, const void* v_weight,
+                          const void* gate_weight, const void* out_weight, int weight_dtype, int hidden_size,
+                          int qk_heads, int head_dim, int value_dim_per_head, float eps, void* hidden_out,
+                          void* state_out, void* stream) {
+  if (!is_float_dtype(hidden_dtype) || !is_float_dtype(state_dtype) || !is_float_dtype(weight_dtype))
+    return fail(FK_ERR_DTYPE, "synthetic DeltaNet tensors must be f32 or bf16");
+  if (hidden_size < 1 || qk_heads < 1 || head_dim < 1 || value_dim_per_head < 1)
+    return fail(FK_ERR_INVALID, "synthetic DeltaNet sizes must be positive");
+  if (hidden_size > kSynMax || qk_heads * head_dim > kSynMax || qk_heads * value_dim_per_head > kSynMax)
+    return fail(FK_ERR_UNSUPPORTED, "synthetic DeltaNet widths must be <= %d", kSynMax);
+  if (!hidden || !state || !norm_weight || !q_weight || !k_weight || !v_weight || !gate_weight || !out_weight ||
+      !hidden_out || !state_out)
+    return fail(FK_ERR_INVALID, "synthetic DeltaNet pointers must be non-NULL");
+  SynDnArgs da;
+  da.x = hidden;
+  da.x_dt = hidden_dtype;
+  da.state = state;
+  da.s_dt = state_dtype;
+  da.nw = norm_weight;
+  da.qw = q_weight;
+  da.kw = k_weight;
+  da.vw = v_weight;
+  da.gw = gate_weight;
+  da.ow = out_weight;
+  da.w_dt = weight_dtype;
+  da.H = hidden_size;
+  da.Hk = qk_heads;
+  da.D = head_dim;
+  da.Vd = value_dim_per_head;
+  da.eps = eps;
+  da.x_out = hidden_out;
+  da.s_out = state_out;
+  hipLaunchKernelGGL(synthetic_deltanet_kernel, dim3(1), dim3(256), 0, as_stream(stream), da);
+  return check_launch("synthetic_deltanet_kernel");
+}
+
+}  // extern "C"

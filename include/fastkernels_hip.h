@@ -1,0 +1,239 @@
+/*
+ * fastkernels_hip.h - C ABI of libfastkernels_hip.so, the MI355X (gfx950)
+ * kernels behind fastkernels_amd.kernels.hip.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor arguments are device pointers to contiguous, row-major
+ *     storage.  Rows that the kernels stream with vector loads (weights,
+ *     hidden rows) must start on a 16-byte boundary and hold a multiple of 8
+ *     elements; violations return FK_ERR_ALIGNMENT before any launch.
+ *   - `*_dtype` arguments take FK_DTYPE_* codes.  Arithmetic is fp32.
+ *   - `stream` is a hipStream_t passed as void*; NULL means the legacy
+ *     default stream.  Calls only enqueue work: no host synchronisation, no
+ *     device allocation.  Outputs and workspaces are caller-owned.
+ *   - Workspaces hold self-resetting counters and must be zero-filled once
+ *     when first allocated; after that they can be reused by consecutive calls
+ *     on one stream.  Calls that overlap on different streams need separate
+ *     workspaces.
+ *   - Every function returns FK_OK (0) or an FK_ERR_* status;
+ *     fk_last_error_detail() gives a human-readable reason for the calling
+ *     thread's last failure.
+ *
+ * Each declaration cites the reference operator it replaces
+ * (suryavanshi/fastkernels, src/fastkernels/kernels/triton/...).
+ */
+#ifndef FASTKERNELS_HIP_H
+#define FASTKERNELS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FK_ABI_VERSION 1
+
+enum {
+  FK_DTYPE_F32 = 0,
+  FK_DTYPE_BF16 = 1,
+  FK_DTYPE_I32 = 2,
+  FK_DTYPE_I64 = 3
+};
+
+enum {
+  FK_OK = 0,
+  FK_ERR_INVALID = 1,     /* bad rank/shape/size argument */
+  FK_ERR_DTYPE = 2,       /* unsupported dtype code */
+  FK_ERR_WORKSPACE = 3,   /* workspace missing or too small */
+  FK_ERR_LAUNCH = 4,      /* hipLaunchKernel / runtime error */
+  FK_ERR_UNSUPPORTED = 5, /* shape outside the kernels' limits */
+  FK_ERR_ALIGNMENT = 6    /* pointer or row length breaks 16-byte vector loads */
+};
+
+int fk_abi_version(void);
+const char* fk_status_string(int status);
+const char* fk_last_error_detail(void);
+
+/* ------------------------------------------------------------------------ */
+/* MoE decode layer                                                          */
+/* ------------------------------------------------------------------------ */
+
+/* Bytes of workspace needed by fk_moe_router / fk_moe_align / fk_moe_experts
+ * / fk_moe_layer for this problem size (routing tables, counters, the fp32
+ * SwiGLU activations of every routed (token, slot) pair and shared token). */
+size_t fk_moe_workspace_bytes(int tokens, int top_k, int num_experts, int intermediate);
+
+/* Router: n = RMSNorm(x) * (norm_offset + w); logits = n . W^T (+ bias);
+ * softmax; top-k ordered by (probability desc, expert id asc); weights
+ * renormalised to sum 1.  Also writes the routing tables consumed by
+ * fk_moe_experts into `workspace`.
+ * Replaces triton_qwen36_moe_router_decode (qwen36_router.py:193-257) and
+ * triton_qwen36_batched_moe_router_decode (qwen36_router.py:260-319).
+ * `router_bias` (nullable, length num_experts) has no reference counterpart:
+ * it is added to the logits (and so appears in `logits`). */
+int fk_moe_router(const void* hidden, int hidden_dtype,
+                  const void* norm_weight, int norm_dtype,
+                  const void* router_weight, int router_dtype,
+                  const void* router_bias, int bias_dtype,
+                  int tokens, int hidden_size, int num_experts, int top_k,
+                  float eps, float norm_offset,
+                  float* logits, int64_t* topk_ids, float* topk_weights,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Routing tables from caller-supplied ids/weights: expert histogram,
+ * exclusive offsets, the stable permutation of (token, slot) pairs sorted by
+ * (expert, token, slot), and its inverse.  Out-of-range ids are clamped to
+ * [0, num_experts-1] as the reference expert kernels do
+ * (qwen36_expert.py:146).  The four outputs are optional copies of the tables
+ * kept in `workspace`.  `topk_weights` may be NULL (histogram-only use).
+ * Replaces triton_expert_histogram (moe.py:87-102); the permutation has no
+ * reference counterpart (the reference re-streams weights per pair,
+ * qwen36_expert.py:456-537). */
+int fk_moe_align(const void* topk_ids, int ids_dtype,
+                 const void* topk_weights, int weights_dtype,
+                 int tokens, int top_k, int num_experts,
+                 void* workspace, size_t workspace_bytes,
+                 int32_t* counts_out, int32_t* offsets_out,
+                 int32_t* perm_out, int32_t* inverse_out, void* stream);
+
+/* Expert stage for the routing tables in `workspace`: per routed pair
+ * a = silu(W_gu[e,:I] x) * (W_gu[e,I:] x), y += w * (W_d[e] a); optional
+ * shared expert (same shapes, un-indexed) scaled by sigmoid(w_g . x) when
+ * `shared_gate` is non-NULL.  Experts read the un-normalised hidden x.
+ * out (f32[T,H]) = moe update; layer_out (nullable) = x + out.
+ * shared_gate_up == NULL && shared_down == NULL selects routed-only.
+ * Replaces triton_qwen36_routed_experts_decode (qwen36_expert.py:889-966),
+ * triton_qwen36_routed_shared_experts_decode (:969-1093),
+ * triton_qwen36_batched_routed_experts_decode (:1096-1178),
+ * triton_qwen36_batched_routed_shared_experts_decode (:1181-1309) and
+ * triton_qwen36_single_expert_mlp_decode (:817-886, one expert, K=1). */
+int fk_moe_experts(const void* hidden, int hidden_dtype,
+                   const void* gate_up, const void* down, int expert_dtype,
+                   const void* shared_gate_up, const void* shared_down,
+                   const void* shared_gate, int shared_gate_dtype,
+                   int tokens, int hidden_size, int intermediate,
+                   int num_experts, int top_k,
+                   float* out, float* layer_out,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* Router + expert stage in one call (the full MoE block plus residual).
+ * Replaces triton_qwen36_moe_decode (qwen36_expert.py:1312-1350),
+ * triton_qwen36_batched_moe_decode (:1353-1387) and
+ * triton_qwen36_batched_moe_layer_decode (qwen36_layer.py:55-106). */
+int fk_moe_layer(const void* hidden, int hidden_dtype,
+                 const void* norm_weight, int norm_dtype,
+                 const void* router_weight, int router_dtype,
+                 const void* router_bias, int bias_dtype,
+                 const void* gate_up, const void* down, int expert_dtype,
+                 const void* shared_gate_up, const void* shared_down,
+                 const void* shared_gate, int shared_gate_dtype,
+                 int tokens, int hidden_size, int intermediate,
+                 int num_experts, int top_k, float eps, float norm_offset,
+                 float* logits, int64_t* topk_ids, float* topk_weights,
+                 float* moe_out, float* layer_out,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* counts[e] = #{i : ids[i] == e} over n ids (int32 or int64); ids outside
+ * [0, num_experts) are ignored.  counts is overwritten.
+ * Replaces triton_expert_histogram (moe.py:87-102) as a standalone op. */
+int fk_expert_histogram(const void* ids, int ids_dtype, int64_t n,
+                        int num_experts, int32_t* counts, void* stream);
+
+/* out[r, i] = silu(gu[r, i]) * gu[r, I + i]; out has the dtype of gu.
+ * Replaces triton_fused_swiglu (moe.py:67-84). */
+int fk_fused_swiglu(const void* gate_up, int dtype, int64_t rows,
+                    int intermediate, void* out, void* stream);
+
+/* out = float(hidden) + update over n elements.
+ * Replaces the residual-add kernel of qwen36_layer.py:37-52. */
+int fk_residual_add(const void* hidden, int hidden_dtype, const float* update,
+                    int64_t n, float* out, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Gated DeltaNet decode step                                                */
+/* ------------------------------------------------------------------------ */
+
+/* xn = RMSNorm(x) * (norm_offset + w); mixed_qkv = xn W_qkv^T, z = xn W_z^T,
+ * a = xn W_a^T, b = xn W_b^T (all f32 outputs).
+ * Replaces triton_qwen36_batched_deltanet_project (qwen36_deltanet.py:403-457). */
+int fk_deltanet_project(const void* hidden, int hidden_dtype,
+                        const void* norm_weight, int norm_dtype,
+                        const void* w_qkv, const void* w_z,
+                        const void* w_a, const void* w_b, int weight_dtype,
+                        int tokens, int hidden_size, int qkv_rows, int z_rows,
+                        int ab_rows, float eps, float norm_offset,
+                        float* mixed_qkv, float* z, float* a_logits,
+                        float* b_logits, void* stream);
+
+/* Causal depthwise conv over [conv_state | mixed^T] per channel, SiLU, and
+ * the rolled state (last kernel_size columns, stored in state_dtype).
+ * Replaces triton_qwen36_batched_deltanet_conv (qwen36_deltanet.py:534-584). */
+int fk_deltanet_conv(const void* mixed, int mixed_dtype,
+                     const void* conv_state, int state_dtype,
+                     const void* conv_weight, int weight_dtype,
+                     int tokens, int channels, int kernel_size,
+                     float* conv_out, void* next_state, void* stream);
+
+/* Bytes of workspace for fk_deltanet_recurrent_output. */
+size_t fk_deltanet_workspace_bytes(int tokens, int value_heads, int head_dim);
+
+/* Gated delta rule over `tokens` consecutive rows through one recurrent
+ * state, per-head gated RMSNorm (plain weight) and the output projection.
+ * update (f32[T,hidden]) = core W_out^T; next_state has state_dtype.
+ * residual/residual_out (both nullable) add: residual_out = residual + update.
+ * `tensor_dtypes` holds the dtypes of, in order: mixed_qkv, z, a_logits,
+ * b_logits, recurrent_state, out_proj_weight, linear_norm_weight, a_log,
+ * dt_bias, residual.
+ * Replaces triton_qwen36_batched_deltanet_recurrent_output
+ * (qwen36_deltanet.py:744-863). */
+int fk_deltanet_recurrent_output(const void* mixed_qkv, const void* z,
+                                 const void* a_logits, const void* b_logits,
+                                 const void* recurrent_state,
+                                 const void* out_proj_weight,
+                                 const void* linear_norm_weight,
+                                 const void* a_log, const void* dt_bias,
+                                 const void* residual,
+                                 const int32_t* tensor_dtypes,
+                                 int tokens, int qk_heads, int value_heads,
+                                 int head_dim, int hidden_size, float eps,
+                                 float* update, void* next_state,
+                                 float* residual_out,
+                                 void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Synthetic (tiny-spec) decode blocks behind the --moe-impl/--deltanet-impl  */
+/* switch of bench/qwen36_decode_reference.py                                */
+/* ------------------------------------------------------------------------ */
+
+/* One-token MoE with plain-weight RMSNorm router, softmax top-k (ties to the
+ * lower id) with renormalisation, routed + ungated shared expert, residual;
+ * output in out_dtype.  Limits: hidden, intermediate <= 1024, experts <= 1024.
+ * Replaces triton_synthetic_qwen36_moe_decode (qwen36_moe.py:362-444). */
+int fk_synthetic_moe(const void* hidden, int hidden_dtype,
+                     const void* norm_weight, const void* router_weight,
+                     const void* gate_up, const void* down,
+                     const void* shared_gate_up, const void* shared_down,
+                     int weight_dtype, int hidden_size, int num_experts,
+                     int intermediate, int top_k, float eps,
+                     void* out, int out_dtype, void* stream);
+
+/* One-token toy DeltaNet: S' = 0.95 S + k (x) v per qk head,
+ * out = x + W_o ((q . S') * sigmoid(W_g xn)), xn = RMSNorm(x) * w.
+ * hidden_out has hidden_dtype, state_out has state_dtype.
+ * Replaces triton_synthetic_qwen36_deltanet_decode (qwen36_deltanet.py:966-1041). */
+int fk_synthetic_deltanet(const void* hidden, int hidden_dtype,
+                          const void* state, int state_dtype,
+                          const void* norm_weight, const void* q_weight,
+                          const void* k_weight, const void* v_weight,
+                          const void* gate_weight, const void* out_weight,
+                          int weight_dtype, int hidden_size, int qk_heads,
+                          int head_dim, int value_dim_per_head, float eps,
+                          void* hidden_out, void* state_out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FASTKERNELS_HIP_H */
