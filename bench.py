@@ -44,7 +44,7 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     p.add_argument("--no-extra", action="store_true", help="skip the batch-1/128 and DeltaNet sub-results")
-    p.add_argument("--only", choices=["moe", "experts", "deltanet"], default=None,
+    p.add_argument("--only", choices=["moe", "deltanet"], default=None,
                    help="run a single timing loop (for profilers) and print its line")
     return p.parse_args()
 
@@ -103,7 +103,7 @@ def main() -> int:
 
     R = max(1, args.weight_sets)
     log(f"generating {R} MoE weight sets on {torch.cuda.get_device_name(0)}")
-    sets = [moe_set(r) for r in range(R)]
+    sets = [] if args.only == "deltanet" else [moe_set(r) for r in range(R)]
     torch.cuda.synchronize()
 
     def timed_graph(fns, steps: int, warmup: int) -> float:
@@ -117,13 +117,15 @@ def main() -> int:
         with torch.cuda.graph(graph, stream=stream):
             for i in range(steps):
                 fns[i % len(fns)](stream)
-        graph.replay()  # upload + warm
-        torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        graph.replay()
-        end.record(stream)
+        # replay() launches on the current stream: make it the timed stream.
+        with torch.cuda.stream(stream):
+            graph.replay()  # upload + warm
+            stream.synchronize()
+            start.record(stream)
+            graph.replay()
+            end.record(stream)
         end.synchronize()
         torch.cuda.synchronize()
         return start.elapsed_time(end) / steps
@@ -168,10 +170,30 @@ def main() -> int:
             "_plans": plans,
         }
 
+    def deltanet_result(tokens: int, nsets: int = R) -> dict:
+        dn_sets = [wl.make_deltanet_weights(spec, seed=2000 + r, device=dev) for r in range(nsets)]
+        dplans = []
+        for r in range(nsets):
+            dp = DeltaNetStepPlan(dn_sets[r], tokens, spec)
+            dp.hidden.copy_(wl.make_hidden(tokens, H, seed=50 + r).to(dev))
+            dplans.append(dp)
+        ms = timed_graph([p.run for p in dplans], args.steps, args.warmup)
+        nbytes = wl.deltanet_step_bytes(tokens, spec)
+        return {
+            "tokens": tokens,
+            "us_per_step": round(ms * 1e3, 3),
+            "algorithmic_bytes_per_step": nbytes,
+            "achieved_tbs": round(nbytes / (ms * 1e-3) / 1e12, 3),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+        }
+
     if args.only == "moe":
         res = moe_result(args.tokens)
         res.pop("_plans")
         print(json.dumps(res))
+        return 0
+    if args.only == "deltanet":
+        print(json.dumps(deltanet_result(args.tokens)))
         return 0
 
     # -- headline: MoE layer at batch `tokens` ---------------------------------
@@ -198,23 +220,8 @@ def main() -> int:
         sub["moe_t128_zipf"] = r128
         del p128
         log("timing Gated DeltaNet step T=1 and T=8")
-        dn_sets = [wl.make_deltanet_weights(spec, seed=2000 + r, device=dev) for r in range(R)]
         for tokens in (1, 8):
-            dplans = []
-            for r in range(R):
-                dp = DeltaNetStepPlan(dn_sets[r], tokens, spec)
-                dp.hidden.copy_(wl.make_hidden(tokens, H, seed=50 + r).to(dev))
-                dplans.append(dp)
-            ms = timed_graph([p.run for p in dplans], args.steps, args.warmup)
-            nbytes = wl.deltanet_step_bytes(tokens, spec)
-            sub[f"deltanet_t{tokens}"] = {
-                "tokens": tokens,
-                "us_per_step": round(ms * 1e3, 3),
-                "algorithmic_bytes_per_step": nbytes,
-                "achieved_tbs": round(nbytes / (ms * 1e-3) / 1e12, 3),
-                "hbm_frac": round(nbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
-            }
-        del dn_sets
+            sub[f"deltanet_t{tokens}"] = deltanet_result(tokens)
 
     # -- CPU baseline (oracle on the host cores, bounded sample) ----------------
     cpu = None

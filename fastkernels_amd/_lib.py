@@ -35,7 +35,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "fk_abi_version": (c_int, []),
     "fk_status_string": (c_char_p, [I]),
     "fk_last_error_detail": (c_char_p, []),
-    "fk_moe_workspace_bytes": (c_size_t, [I, I, I, I]),
+    "fk_moe_workspace_bytes": (c_size_t, [I, I, I, I, I]),
     "fk_moe_router": (
         c_int,
         [P, I, P, I, P, I, P, I, I, I, I, I, c_float, c_float, P, P, P, P, c_size_t, P],
@@ -62,7 +62,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, c_float, P, P, P, P, c_size_t, P],
     ),
-    "fk_synthetic_moe": (c_int, [P, I, P, P, P, P, P, P, I, I, I, I, I, c_float, P, I, P]),
+    "fk_deltanet_step_workspace_bytes": (c_size_t, [I, I, I, I]),
+    "fk_deltanet_step": (
+        c_int,
+        [P, P, P, P, P, P, P, P, P, P, P, P, P, P, I, I, I, I, I, I, c_float, P, P, P, P, P, c_size_t, P],
+    ),
+    "fk_synthetic_moe":(c_int, [P, I, P, P, P, P, P, P, I, I, I, I, I, c_float, P, I, P]),
     "fk_synthetic_deltanet": (
         c_int,
         [P, I, P, I, P, P, P, P, P, P, I, I, I, I, I, c_float, P, P, P],

@@ -119,6 +119,17 @@ __device__ __forceinline__ void load8_f32(const void* base, size_t elem_index, f
   raw8_to_f32<BF16>(load_raw8<BF16>(base, elem_index), out);
 }
 
+// Eight consecutive elements of a tensor whose dtype is a run-time code
+// (uniform branch; both arms are 16-byte vector loads).  Needs 16-byte
+// alignment of `base` and an element index that is a multiple of 8.
+__device__ __forceinline__ void load8_any(const void* base, int dtype, size_t elem_index, float out[8]) {
+  if (dtype == FK_DTYPE_BF16) {
+    load8_f32<true>(base, elem_index, out);
+  } else {
+    load8_f32<false>(base, elem_index, out);
+  }
+}
+
 // fp32 activations (8 consecutive floats, 32 bytes).
 __device__ __forceinline__ void load8_act(const float* base, size_t elem_index, float out[8]) {
   const float4* p = reinterpret_cast<const float4*>(base + elem_index);
@@ -129,38 +140,135 @@ __device__ __forceinline__ void load8_act(const float* base, size_t elem_index, 
 }
 
 // ---------------------------------------------------------------------------
-// Wavefront reductions (64 lanes).  Butterfly order is fixed, so results are
-// bitwise reproducible run to run.
+// Wavefront all-reductions (64 lanes) built from DPP lane permutes, one
+// ds_swizzle and v_permlane32_swap instead of six ds_bpermute round trips.
+// Every lane ends with the full result; the combine order is fixed, so
+// results are bitwise reproducible run to run.
+//   step 1  quad_perm [1,0,3,2]    partner = lane ^ 1
+//   step 2  quad_perm [2,3,0,1]    partner = lane ^ 2
+//   step 3  row_half_mirror        partner = 7 - lane within 8 (other quad)
+//   step 4  row_mirror             partner = 15 - lane within 16 (other 8)
+//   step 5  ds_swizzle xor 16      partner = lane ^ 16
+//   step 6  v_permlane32_swap      partner = lane ^ 32
+// Steps 3 and 4 are not xor partners, but after steps 1-2 (resp. 1-3) all
+// lanes of the source group hold the same partial, so any lane of the other
+// group is an equivalent partner.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+constexpr int kDppQuadXor1 = 0xB1;
+constexpr int kDppQuadXor2 = 0x4E;
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kSwizzleXor16 = 0x401F;  // bit mode: and 0x1f, or 0, xor 0x10
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+
+__device__ __forceinline__ uint32_t xor16_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, kSwizzleXor16);
+}
+
+// Value held by lane ^ 32.
+__device__ __forceinline__ uint32_t xor32_u32(uint32_t v) {
+  auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (__lane_id() < 32) ? (uint32_t)r[1] : (uint32_t)r[0];
+}
+
+template <typename Op>
+__device__ __forceinline__ float wave_allreduce_f32(float v, Op op) {
+  v = op(v, __uint_as_float(dpp_u32<kDppQuadXor1>(__float_as_uint(v))));
+  v = op(v, __uint_as_float(dpp_u32<kDppQuadXor2>(__float_as_uint(v))));
+  v = op(v, __uint_as_float(dpp_u32<kDppRowHalfMirror>(__float_as_uint(v))));
+  v = op(v, __uint_as_float(dpp_u32<kDppRowMirror>(__float_as_uint(v))));
+  v = op(v, __uint_as_float(xor16_u32(__float_as_uint(v))));
+  v = op(v, __uint_as_float(xor32_u32(__float_as_uint(v))));
   return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  return wave_allreduce_f32(v, [](float a, float b) { return a + b; });
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
-  return v;
+  return wave_allreduce_f32(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
-// Sum over aligned groups of `G` lanes (G a power of two <= 64).
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int m = G / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-  return v;
-}
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    uint32_t lo = __shfl_xor((uint32_t)(v & 0xffffffffu), m, kWave);
-    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m, kWave);
-    uint64_t o = ((uint64_t)hi << 32) | lo;
-    v = o > v ? o : v;
-  }
+  auto step = [&](uint32_t lo, uint32_t hi) { v = max_u64(v, ((uint64_t)hi << 32) | lo); };
+  step(dpp_u32<kDppQuadXor1>((uint32_t)v), dpp_u32<kDppQuadXor1>((uint32_t)(v >> 32)));
+  step(dpp_u32<kDppQuadXor2>((uint32_t)v), dpp_u32<kDppQuadXor2>((uint32_t)(v >> 32)));
+  step(dpp_u32<kDppRowHalfMirror>((uint32_t)v), dpp_u32<kDppRowHalfMirror>((uint32_t)(v >> 32)));
+  step(dpp_u32<kDppRowMirror>((uint32_t)v), dpp_u32<kDppRowMirror>((uint32_t)(v >> 32)));
+  step(xor16_u32((uint32_t)v), xor16_u32((uint32_t)(v >> 32)));
+  step(xor32_u32((uint32_t)v), xor32_u32((uint32_t)(v >> 32)));
   return v;
+}
+
+// ---------------------------------------------------------------------------
+// Cross-workgroup publication without cache-wide fences.
+//
+// A device-scope fence costs a chip-wide L2 write-back/invalidate (measured
+// on MI355X: ~60 ns per workgroup, serialised).  Small values that other
+// workgroups must read are instead written with device-scope atomic stores
+// (write-through, `sc1`) and read with device-scope atomic loads (`sc1`,
+// served from the coherent level); `publish_wait()` makes the storing
+// wavefront wait until its stores are acknowledged before it signals with a
+// device-scope atomic RMW.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent(int* p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int load_coherent(const int* p) {
+  return __hip_atomic_load(const_cast<int*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish_wait() { __builtin_amdgcn_s_waitcnt(0); }
+__device__ __forceinline__ uint32_t ticket_add(uint32_t* p) {
+  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t load_coherent(const uint32_t* p) {
+  return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Grid-wide barrier for kernels whose grid the host has capped at the number
+// of co-resident workgroups.  Called by one thread per workgroup after the
+// workgroup's publishing stores have been waited for.  The wait is bounded:
+// after `kSpinLimit` polls the workgroup records FK_DEVICE_ERR_BARRIER in
+// `*error` and continues, so a broken launch configuration can produce wrong
+// results but never a hang.
+constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr uint32_t FK_DEVICE_ERR_BARRIER = 1u;
+
+__device__ __forceinline__ void grid_arrive_and_wait(uint32_t* counter, uint32_t target, uint32_t* error) {
+  ticket_add(counter);
+  for (uint32_t i = 0; i < kSpinLimit; ++i) {
+    if (load_coherent(counter) >= target) return;
+    __builtin_amdgcn_s_sleep(2);
+  }
+  __hip_atomic_fetch_or(error, FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Integer wave all-reductions (same lane schedule as wave_allreduce_f32).
+template <typename Op>
+__device__ __forceinline__ int wave_allreduce_i32(int v, Op op) {
+  v = op(v, (int)dpp_u32<kDppQuadXor1>((uint32_t)v));
+  v = op(v, (int)dpp_u32<kDppQuadXor2>((uint32_t)v));
+  v = op(v, (int)dpp_u32<kDppRowHalfMirror>((uint32_t)v));
+  v = op(v, (int)dpp_u32<kDppRowMirror>((uint32_t)v));
+  v = op(v, (int)xor16_u32((uint32_t)v));
+  v = op(v, (int)xor32_u32((uint32_t)v));
+  return v;
+}
+__device__ __forceinline__ int wave_min_i32(int v) {
+  return wave_allreduce_i32(v, [](int a, int b) { return a < b ? a : b; });
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }

@@ -7,22 +7,24 @@
 //   gate_up        [E, 2I, H]      gate rows 0..I-1, up rows I..2I-1
 //   down           [E, H, I]       one 1 KB row per output feature at I=512
 //   shared_gate_up [2I, H], shared_down [H, I], shared_gate [H]
-// Workspace (fk_moe_workspace_bytes): counters, routing tables and the fp32
-// SwiGLU activations act[(T*K + T), I], indexed by the permuted position of a
-// routed (token, slot) pair, followed by one row per token for the shared
-// expert.
+// Workspace (fk_moe_workspace_bytes): counters, routing tables, the fp32
+// SwiGLU activations act[(T*K + T), I] and the per-pair down-projection
+// outputs y[(T*K + T), H].  Rows are indexed by the permuted position of a
+// routed (token, slot) pair; the last T rows belong to the shared expert.
 //
 // Launch structure (one stream, no host synchronisation):
 //   1. moe_router_kernel   grid ceil(E/4) x 256 threads.  One wavefront per
-//      expert row; the last workgroup to arrive (atomic ticket) runs softmax,
-//      top-k and the routing tables for every token.
-//   2. moe_gateup_kernel   grid (slots) x (I/8); a slot is one active expert
-//      or the shared expert; each workgroup streams 8 gate + 8 up rows of its
+//      expert row (weights folded with the norm weight, held in registers,
+//      tokens in batches of 4); the last workgroup to arrive (atomic ticket,
+//      no cache-wide fence) runs softmax, top-k and the routing tables.
+//   2. moe_gateup_kernel   grid slots x (I/8); a slot is one active expert or
+//      the shared expert; each workgroup streams 8 gate + 8 up rows of its
 //      expert once and applies them to every pair routed there.
-//   3. moe_down_kernel     grid H/8; each workgroup owns 8 output features and
-//      streams those 8 rows of every active expert's down matrix, so each
-//      output element is accumulated by exactly one lane in a fixed order
-//      (deterministic, no atomics).
+//   3. moe_down_kernel     grid slots x (H/32); each workgroup streams 32
+//      contiguous down rows (32 KB at I=512) of one expert and writes
+//      y[pair, rows] for every pair routed there.
+//   4. moe_combine_kernel  out[t] = sum_k w[t,k] y[pos(t,k)] + g_t y[shared t]
+//      in slot order, and layer_out = x + out (deterministic, no atomics).
 #include "fk_common.h"
 #include "fk_host.h"
 
@@ -31,7 +33,8 @@ namespace fk {
 constexpr int kMaxPairs = 4096;    // T*K handled by the routing-table builder
 constexpr int kMaxExperts = 1024;  // matches the reference router limit
 constexpr int kGateUpRows = 8;     // intermediates per gate/up workgroup (2 per wave)
-constexpr int kDownRows = 8;       // output features per down workgroup (2 per wave)
+constexpr int kDownRowsPerWave = 8; // down rows per wavefront
+constexpr int kDownRows = 4 * kDownRowsPerWave;  // down rows per workgroup
 
 struct MoeWs {
   uint32_t* tickets;    // [16] self-resetting arrival counters
@@ -45,9 +48,10 @@ struct MoeWs {
   float* wts;           // [P] routing weights (fp32)
   float* sgate;         // [T] shared-expert gate sigmoid(w_g . x)
   float* act;           // [(P + T), I] SwiGLU activations
+  float* y;             // [(P + T), H] per-pair down-projection outputs
 };
 
-static size_t moe_ws_layout(int T, int K, int E, int I, char* base, MoeWs* ws) {
+static size_t moe_ws_layout(int T, int K, int E, int I, int H, char* base, MoeWs* ws) {
   const size_t P = (size_t)T * K;
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -66,6 +70,7 @@ static size_t moe_ws_layout(int T, int K, int E, int I, char* base, MoeWs* ws) {
   ws->wts = reinterpret_cast<float*>(take(P * 4));
   ws->sgate = reinterpret_cast<float*>(take((size_t)T * 4));
   ws->act = reinterpret_cast<float*>(take((P + T) * (size_t)I * 4));
+  ws->y = reinterpret_cast<float*>(take((P + T) * (size_t)H * 4));
   return off;
 }
 
@@ -82,12 +87,56 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
   return v;
 }
 
-__device__ void build_routing_tables(const int* s_ids, int P, int E, MoeWs ws, int* s_cnt, int* s_off) {
+// Deterministic, parallel stable counting sort of the P pairs by expert.
+// Wave w owns the contiguous pair segment [w*seg, (w+1)*seg); it walks it in
+// chunks of 64 (one pair per lane), ranks each pair among equal experts of
+// the chunk by scanning the 64 ids through readlane broadcasts, and keeps
+// running per-expert counts of its segment in s_wcnt[w][e].  A pair's
+// permuted position is offsets[e] + (pairs of e in earlier segments) +
+// (its rank inside its own segment), which preserves (token, slot) order.
+// LDS: s_ids[P] ids, s_rank[P], s_wcnt[4*E], s_cnt[E], s_off[E].
+__device__ void build_routing_tables(const int* s_ids, int P, int E, MoeWs ws, int* s_cnt, int* s_off, int* s_rank,
+                                     int* s_wcnt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   __shared__ int s_wtot[4][2];
-  for (int e = tid; e < E; e += 256) s_cnt[e] = 0;
+  for (int i = tid; i < 4 * E; i += 256) s_wcnt[i] = 0;
   __syncthreads();
-  for (int j = tid; j < P; j += 256) atomicAdd(&s_cnt[s_ids[j]], 1);
+
+  const int seg = (P + 3) / 4;
+  const int j0 = min(P, wave * seg), j1 = min(P, j0 + seg);
+  int* wc = s_wcnt + wave * E;
+  for (int c0 = j0; c0 < j1; c0 += kWave) {
+    const int j = c0 + lane;
+    const bool valid = j < j1;
+    const int e = valid ? s_ids[j] : -1;
+    const int n = min(kWave, j1 - c0);
+    int below = 0, total = 0;
+    for (int src = 0; src < n; ++src) {
+      const int v = __builtin_amdgcn_readlane(e, src);
+      below += (v == e) & (src < lane);
+      total += (v == e);
+    }
+    int before = 0;
+    if (valid) {
+      before = wc[e];
+      s_rank[j] = before + below;
+    }
+    // One lane per expert of the chunk (its last occurrence) advances the
+    // running count; LDS operations of one wavefront complete in order.
+    if (valid && below == total - 1) wc[e] = before + total;
+  }
+  __syncthreads();
+
+  // Per-expert totals, and per-wave exclusive prefixes in place.
+  for (int e = tid; e < E; e += 256) {
+    int run = 0;
+    for (int w = 0; w < 4; ++w) {
+      const int c = s_wcnt[w * E + e];
+      s_wcnt[w * E + e] = run;
+      run += c;
+    }
+    s_cnt[e] = run;
+  }
   __syncthreads();
 
   const int per = (E + 255) / 256;  // bins per thread (<= 4)
@@ -130,19 +179,12 @@ __device__ void build_routing_tables(const int* s_ids, int P, int E, MoeWs ws, i
     ws.num_active[0] = s_wtot[0][1] + s_wtot[1][1] + s_wtot[2][1] + s_wtot[3][1];
   }
   __syncthreads();
-  // Stable permutation: the thread owning expert e walks the pairs in
-  // (token, slot) order and appends the ones routed to e.
-  for (int e = tid; e < E; e += 256) {
-    int c = s_cnt[e];
-    int r = s_off[e];
-    for (int j = 0; j < P && c > 0; ++j) {
-      if (s_ids[j] == e) {
-        ws.perm[r] = j;
-        ws.inverse[j] = r;
-        ++r;
-        --c;
-      }
-    }
+  for (int j = tid; j < P; j += 256) {
+    const int w = j / seg;
+    const int e = s_ids[j];
+    const int r = s_off[e] + s_wcnt[w * E + e] + s_rank[j];
+    ws.perm[r] = j;
+    ws.inverse[j] = r;
   }
 }
 
@@ -163,124 +205,193 @@ struct RouterArgs {
   MoeWs ws;
 };
 
-template <bool BFW, bool BFX, int NJ>
+// Softmax + top-k of one token by one wavefront.  Lane l owns experts
+// l + 64 j; each lane keeps its best remaining candidate (its "head": highest
+// probability, lowest id on ties) and every round takes the wave maximum of
+// the heads, breaking probability ties toward the lowest expert id.  Weights
+// are renormalised by the sum of the selected probabilities in selection
+// order.
+template <int NJE>
+__device__ void router_topk_token(const RouterArgs& a, int t, int lane) {
+  float p[NJE];
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NJE; ++j) {
+    const int ex = lane + kWave * j;
+    p[j] = ex < a.E ? load_coherent(a.logits + (size_t)t * a.E + ex) : -INFINITY;
+    m = fmaxf(m, p[j]);
+  }
+  m = wave_max(m);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJE; ++j) {
+    const int ex = lane + kWave * j;
+    p[j] = ex < a.E ? expf(p[j] - m) : 0.f;
+    s += p[j];
+  }
+  s = wave_sum(s);
+#pragma unroll
+  for (int j = 0; j < NJE; ++j) p[j] = lane + kWave * j < a.E ? p[j] / s : -1.f;  // -1: no expert
+
+  uint32_t taken = 0;
+  float hv = -1.f;
+  int hj = 0;
+  auto refresh_head = [&]() {
+    hv = -1.f;
+    hj = 0;
+#pragma unroll
+    for (int j = 0; j < NJE; ++j)
+      if (!((taken >> j) & 1u) && p[j] > hv) {
+        hv = p[j];
+        hj = j;
+      }
+  };
+  refresh_head();
+  float denom = 0.f;
+  int my_id = 0;
+  float my_v = 0.f;
+  for (int k = 0; k < a.K; ++k) {
+    const float mv = wave_max(hv);
+    const unsigned long long tied = __ballot(hv == mv);
+    int sel_lane;
+    if (__popcll(tied) == 1) {
+      sel_lane = __ffsll(tied) - 1;
+    } else {
+      const int cand = hv == mv ? lane + kWave * hj : 0x7fffffff;
+      sel_lane = wave_min_i32(cand) & (kWave - 1);
+    }
+    const int sel = __shfl(lane + kWave * hj, sel_lane, kWave);
+    if (lane == sel_lane) {
+      taken |= 1u << hj;
+      refresh_head();
+    }
+    denom += mv;
+    if (lane == k) {
+      my_id = sel;
+      my_v = mv;
+    }
+  }
+  if (lane < a.K) {
+    const size_t o = (size_t)t * a.K + lane;
+    const float w = my_v / denom;
+    a.ids_out[o] = my_id;
+    a.w_out[o] = w;
+    store_coherent(a.ws.ids32 + o, my_id);
+    a.ws.wts[o] = w;
+  }
+}
+
+// Router.  Grid (ceil(E/4), token tiles), capped by the host at the number
+// of co-resident workgroups.  Phase 1: one wavefront per expert row (weights
+// folded with the norm weight, in registers) over the tile's tokens in
+// batches of 4.  Grid barrier.  Phase 2: one wavefront per token runs
+// softmax/top-k.  Phase 3: the last workgroup to finish builds the routing
+// tables.  Cross-workgroup data moves through coherent stores/loads and
+// device-scope tickets (no cache-wide fences).
+template <bool BFW, bool BFX, int NJ, int NJE>
 __global__ __launch_bounds__(256) void moe_router_kernel(RouterArgs a) {
   __shared__ int s_ids[kMaxPairs];
+  __shared__ int s_rank[kMaxPairs];
+  __shared__ int s_wcnt[4 * kMaxExperts];
   __shared__ int s_cnt[kMaxExperts];
   __shared__ int s_off[kMaxExperts];
   __shared__ int s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int e = blockIdx.x * 4 + wave;
   const int nch = a.H >> 3;
+  const int tile = (a.T + gridDim.y - 1) / gridDim.y;
+  const int tb = blockIdx.y * tile;
+  const int te = min(a.T, tb + tile);
 
-  if (e < a.E) {
-    // Fold (norm_offset + w) into this expert's row once; the RMS scale is a
-    // per-token scalar applied after the dot product.
+  if (e < a.E && tb < te) {
     float wn[NJ][8];
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int c = lane + kWave * j;
       if (c < nch) {
-        float w8[8];
+        float w8[8], n8[8];
         load8_f32<BFW>(a.W, (size_t)e * a.H + (size_t)c * 8, w8);
+        load8_any(a.nw, a.nw_dt, (size_t)c * 8, n8);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) wn[j][q] = w8[q] * (a.off + load_scalar(a.nw, a.nw_dt, (size_t)c * 8 + q));
+        for (int q = 0; q < 8; ++q) wn[j][q] = w8[q] * (a.off + n8[q]);
       } else {
 #pragma unroll
         for (int q = 0; q < 8; ++q) wn[j][q] = 0.f;
       }
     }
     const float bias = a.bias ? load_scalar(a.bias, a.bias_dt, e) : 0.f;
-    for (int t = 0; t < a.T; ++t) {
-      float ss = 0.f, d = 0.f;
+    // Lane (t - tb) keeps token t's logit and all lanes store once at the end:
+    // write-through stores inside the loop would hold up the next batch's
+    // loads (the vector-memory counter retires in order).
+    const bool defer = te - tb <= kWave;
+    float mine = 0.f;
+    constexpr int TB = 4;  // tokens per batch: independent loads and reductions
+    for (int t0 = tb; t0 < te; t0 += TB) {
+      float ss[TB], d[TB];
 #pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int c = lane + kWave * j;
-        if (c < nch) {
-          float x8[8];
-          load8_f32<BFX>(a.x, (size_t)t * a.H + (size_t)c * 8, x8);
+      for (int tt = 0; tt < TB; ++tt) {
+        ss[tt] = 0.f;
+        d[tt] = 0.f;
+        const int t = t0 + tt;
+        if (t < te) {
 #pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            ss = fmaf(x8[q], x8[q], ss);
-            d = fmaf(x8[q], wn[j][q], d);
+          for (int j = 0; j < NJ; ++j) {
+            const int c = lane + kWave * j;
+            if (c < nch) {
+              float x8[8];
+              load8_f32<BFX>(a.x, (size_t)t * a.H + (size_t)c * 8, x8);
+#pragma unroll
+              for (int q = 0; q < 8; ++q) {
+                ss[tt] = fmaf(x8[q], x8[q], ss[tt]);
+                d[tt] = fmaf(x8[q], wn[j][q], d[tt]);
+              }
+            }
           }
         }
       }
-      ss = wave_sum(ss);
-      d = wave_sum(d);
-      if (lane == 0) a.logits[(size_t)t * a.E + e] = d * rsqrtf(ss / (float)a.H + a.eps) + bias;
-    }
-  }
-
-  // Arrival: the last workgroup sees every logit.
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = (atomicAdd(&a.ws.tickets[0], 1u) == gridDim.x - 1);
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-
-  // Softmax + top-k per token, one wavefront per token.
-  for (int t = wave; t < a.T; t += 4) {
-    float p[16];
-    float m = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int ex = lane + kWave * j;
-      p[j] = ex < a.E ? __builtin_nontemporal_load(a.logits + (size_t)t * a.E + ex) : -INFINITY;
-      m = fmaxf(m, p[j]);
-    }
-    m = wave_max(m);
-    float s = 0.f;
+      for (int tt = 0; tt < TB; ++tt) {
+        ss[tt] = wave_sum(ss[tt]);
+        d[tt] = wave_sum(d[tt]);
+      }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int ex = lane + kWave * j;
-      p[j] = ex < a.E ? expf(p[j] - m) : 0.f;
-      s += p[j];
-    }
-    s = wave_sum(s);
-#pragma unroll
-    for (int j = 0; j < 16; ++j) p[j] = p[j] / s;
-
-    uint32_t taken = 0;
-    float denom = 0.f;
-    int my_id = 0;
-    float my_v = 0.f;
-    for (int k = 0; k < a.K; ++k) {
-      // Key orders by probability (non-negative floats compare as uints),
-      // then by the lower expert id.
-      uint64_t best = 0;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int ex = lane + kWave * j;
-        if (ex < a.E && !((taken >> j) & 1u)) {
-          uint64_t key = ((uint64_t)__float_as_uint(p[j]) << 32) | (uint64_t)(0xffffffffu - (uint32_t)ex);
-          best = key > best ? key : best;
+      for (int tt = 0; tt < TB; ++tt) {
+        const int t = t0 + tt;
+        if (t >= te) continue;
+        const float logit = d[tt] * rsqrtf(ss[tt] / (float)a.H + a.eps) + bias;
+        if (defer) {
+          mine = lane == t - tb ? logit : mine;
+        } else if (lane == 0) {
+          store_coherent(a.logits + (size_t)t * a.E + e, logit);
         }
       }
-      best = wave_max_u64(best);
-      const int sel = (int)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
-      const float v = __uint_as_float((uint32_t)(best >> 32));
-      if ((sel & 63) == lane) taken |= 1u << (sel >> 6);
-      denom += v;
-      if (lane == k) {
-        my_id = sel;
-        my_v = v;
-      }
     }
-    if (lane < a.K) {
-      const size_t o = (size_t)t * a.K + lane;
-      const float w = my_v / denom;
-      a.ids_out[o] = my_id;
-      a.w_out[o] = w;
-      a.ws.ids32[o] = my_id;
-      a.ws.wts[o] = w;
-      s_ids[o] = my_id;
-    }
+    if (defer && lane < te - tb) store_coherent(a.logits + (size_t)(tb + lane) * a.E + e, mine);
   }
+
+  const uint32_t G = gridDim.x * gridDim.y;
+  publish_wait();
   __syncthreads();
-  build_routing_tables(s_ids, a.T * a.K, a.E, a.ws, s_cnt, s_off);
-  if (threadIdx.x == 0) a.ws.tickets[0] = 0u;  // ready for the next call
+  if (threadIdx.x == 0) grid_arrive_and_wait(&a.ws.tickets[0], G, &a.ws.tickets[15]);
+  __syncthreads();
+
+  const int gw = (blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave;
+  for (int t = gw; t < a.T; t += (int)G * 4) router_topk_token<NJE>(a, t, lane);
+
+  publish_wait();
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = ticket_add(&a.ws.tickets[1]) == G - 1;
+  __syncthreads();
+  if (!s_last) return;
+  const int P = a.T * a.K;
+  for (int j = threadIdx.x; j < P; j += 256) s_ids[j] = load_coherent(a.ws.ids32 + j);
+  __syncthreads();
+  build_routing_tables(s_ids, P, a.E, a.ws, s_cnt, s_off, s_rank, s_wcnt);
+  if (threadIdx.x == 0) {
+    // Every workgroup has passed the barrier (it counted into ticket 1).
+    a.ws.tickets[0] = 0u;
+    a.ws.tickets[1] = 0u;
+  }
 }
 
 // Routing tables from caller-supplied ids (single workgroup).
@@ -299,6 +410,8 @@ struct AlignArgs {
 
 __global__ __launch_bounds__(256) void moe_align_kernel(AlignArgs a) {
   __shared__ int s_ids[kMaxPairs];
+  __shared__ int s_rank[kMaxPairs];
+  __shared__ int s_wcnt[4 * kMaxExperts];
   __shared__ int s_cnt[kMaxExperts];
   __shared__ int s_off[kMaxExperts];
   const int P = a.T * a.K;
@@ -311,7 +424,7 @@ __global__ __launch_bounds__(256) void moe_align_kernel(AlignArgs a) {
     a.ws.wts[j] = a.w ? load_scalar(a.w, a.w_dt, j) : 0.f;
   }
   __syncthreads();
-  build_routing_tables(s_ids, P, a.E, a.ws, s_cnt, s_off);
+  build_routing_tables(s_ids, P, a.E, a.ws, s_cnt, s_off, s_rank, s_wcnt);
   __syncthreads();
   // Optional copies of the tables for callers that inspect them.
   for (int e = threadIdx.x; e < a.E; e += 256) {
@@ -432,176 +545,109 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(ExpertArgs a) {
   }
 }
 
-// Down projection.  SINGLE (T == 1): each lane keeps its partial sums across
-// all slots and reduces once per output feature.  Otherwise every
-// (feature, pair) dot is reduced and lane 0 accumulates it per token in LDS,
-// in slot order (shared first, then ascending expert id, pairs in (token,
-// slot) order).
-template <bool BFW, int NJI, bool SINGLE>
+// Down projection, expert-major.  Workgroup (slot, row chunk) streams 32
+// contiguous rows of the slot's down matrix (8 per wavefront, one 16-byte
+// load per lane per row at I=512, all issued before use) and, for every pair
+// routed to the slot, writes y[pos, row] = W_d[e][row] . act[pos].
+template <bool BFW, int NJI>
 __global__ __launch_bounds__(256) void moe_down_kernel(ExpertArgs a) {
-  extern __shared__ float s_acc[];  // [4 waves][2 rows][T] (multi-token path)
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r0 = blockIdx.x * kDownRows + wave * 2;
-  const int nci = a.I >> 3;
+  const int chunks = (a.H + kDownRows - 1) / kDownRows;
+  int slot = blockIdx.x / chunks;
+  const int chunk = blockIdx.x - slot * chunks;
   const int P = a.T * a.K;
   const size_t esz = BFW ? 2 : 4;
-  const int U = a.ws.num_active[0];
-  const int nslots = U + (a.has_shared ? 1 : 0);
-  const bool row_ok[2] = {r0 < a.H, r0 + 1 < a.H};
-  const float gate_default = 1.f;
-
-  auto slot_info = [&](int s, const char*& W, int& pos0, int& npairs, bool& shared) {
-    if (a.has_shared && s == 0) {
-      W = reinterpret_cast<const char*>(a.sdn);
-      pos0 = P;
-      npairs = a.T;
-      shared = true;
-    } else {
-      const int e = a.ws.active[s - (a.has_shared ? 1 : 0)];
-      W = reinterpret_cast<const char*>(a.dn) + (size_t)e * a.H * a.I * esz;
-      pos0 = a.ws.offsets[e];
-      npairs = a.ws.counts[e];
-      shared = false;
-    }
-  };
-
-  if constexpr (SINGLE) {
-    float acc[2] = {0.f, 0.f};
-    constexpr int B = 4;  // slots in flight per wave
-    for (int s0 = 0; s0 < nslots; s0 += B) {
-      Raw8<BFW> wr[B][2][NJI];
-      float av[B][NJI][8];
-      float wt[B];
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        const int s = s0 + b;
-        wt[b] = 0.f;
-        if (s < nslots) {
-          const char* W;
-          int pos0, npairs;
-          bool shared;
-          slot_info(s, W, pos0, npairs, shared);
-          wt[b] = shared ? (a.sg ? a.ws.sgate[0] : gate_default) : a.ws.wts[a.ws.perm[pos0]];
-#pragma unroll
-          for (int r = 0; r < 2; ++r)
-#pragma unroll
-            for (int j = 0; j < NJI; ++j) {
-              const int c = lane + kWave * j;
-              if (c < nci && row_ok[r]) wr[b][r][j] = load_raw8_stream<BFW>(W, (size_t)(r0 + r) * a.I + (size_t)c * 8);
-            }
-#pragma unroll
-          for (int j = 0; j < NJI; ++j) {
-            const int c = lane + kWave * j;
-            if (c < nci) load8_act(a.ws.act, (size_t)pos0 * a.I + (size_t)c * 8, av[b][j]);
-          }
-        }
-      }
-#pragma unroll
-      for (int b = 0; b < B; ++b) {
-        if (s0 + b < nslots) {
-#pragma unroll
-          for (int r = 0; r < 2; ++r) {
-            float d = 0.f;
-#pragma unroll
-            for (int j = 0; j < NJI; ++j) {
-              const int c = lane + kWave * j;
-              if (c < nci && row_ok[r]) {
-                float w8[8];
-                raw8_to_f32<BFW>(wr[b][r][j], w8);
-#pragma unroll
-                for (int q = 0; q < 8; ++q) d = fmaf(w8[q], av[b][j][q], d);
-              }
-            }
-            acc[r] = fmaf(wt[b], d, acc[r]);
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      const float v = wave_sum(acc[r]);
-      if (lane == 0 && row_ok[r]) {
-        a.out[r0 + r] = v;
-        if (a.layer_out) a.layer_out[r0 + r] = load_scalar(a.x, a.x_dt, r0 + r) + v;
-      }
-    }
+  const char* W;
+  int pos0, npairs;
+  if (a.has_shared && slot == 0) {
+    W = reinterpret_cast<const char*>(a.sdn);
+    pos0 = P;
+    npairs = a.T;
   } else {
-    float* my_acc = s_acc + (size_t)wave * 2 * a.T;
-    for (int i = lane; i < 2 * a.T; i += kWave) my_acc[i] = 0.f;
-    __syncthreads();
-    for (int s = 0; s < nslots; ++s) {
-      const char* W;
-      int pos0, npairs;
-      bool shared;
-      slot_info(s, W, pos0, npairs, shared);
-      Raw8<BFW> wr[2][NJI];
+    if (a.has_shared) slot -= 1;
+    if (slot >= a.ws.num_active[0]) return;
+    const int e = a.ws.active[slot];
+    W = reinterpret_cast<const char*>(a.dn) + (size_t)e * a.H * a.I * esz;
+    pos0 = a.ws.offsets[e];
+    npairs = a.ws.counts[e];
+  }
+  const int nci = a.I >> 3;
+  const int r0 = chunk * kDownRows + wave * kDownRowsPerWave;
+  constexpr int R = kDownRowsPerWave;
+
+  Raw8<BFW> wr[R][NJI];
 #pragma unroll
-      for (int r = 0; r < 2; ++r)
+  for (int r = 0; r < R; ++r)
 #pragma unroll
-        for (int j = 0; j < NJI; ++j) {
-          const int c = lane + kWave * j;
-          if (c < nci && row_ok[r]) wr[r][j] = load_raw8_stream<BFW>(W, (size_t)(r0 + r) * a.I + (size_t)c * 8);
-        }
-      for (int pp = 0; pp < npairs; ++pp) {
-        const int pos = pos0 + pp;
-        int t;
-        float wt;
-        if (shared) {
-          t = pp;
-          wt = a.sg ? a.ws.sgate[t] : gate_default;
-        } else {
-          const int pair = a.ws.perm[pos];
-          t = pair / a.K;
-          wt = a.ws.wts[pair];
-        }
-        float d[2] = {0.f, 0.f};
+    for (int j = 0; j < NJI; ++j) {
+      const int c = lane + kWave * j;
+      if (c < nci && r0 + r < a.H) wr[r][j] = load_raw8_stream<BFW>(W, (size_t)(r0 + r) * a.I + (size_t)c * 8);
+    }
+
+  for (int pp = 0; pp < npairs; ++pp) {
+    const int pos = pos0 + pp;
+    float d[R];
 #pragma unroll
-        for (int j = 0; j < NJI; ++j) {
-          const int c = lane + kWave * j;
-          if (c < nci) {
-            float av[8];
-            load8_act(a.ws.act, (size_t)pos * a.I + (size_t)c * 8, av);
+    for (int r = 0; r < R; ++r) d[r] = 0.f;
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-              if (row_ok[r]) {
-                float w8[8];
-                raw8_to_f32<BFW>(wr[r][j], w8);
+    for (int j = 0; j < NJI; ++j) {
+      const int c = lane + kWave * j;
+      if (c < nci) {
+        float av[8];
+        load8_act(a.ws.act, (size_t)pos * a.I + (size_t)c * 8, av);
 #pragma unroll
-                for (int q = 0; q < 8; ++q) d[r] = fmaf(w8[q], av[q], d[r]);
-              }
-            }
+        for (int r = 0; r < R; ++r) {
+          if (r0 + r < a.H) {
+            float w8[8];
+            raw8_to_f32<BFW>(wr[r][j], w8);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) d[r] = fmaf(w8[q], av[q], d[r]);
           }
         }
-        d[0] = wave_sum(d[0]);
-        d[1] = wave_sum(d[1]);
-        if (lane == 0) {
-          my_acc[t] = fmaf(wt, d[0], my_acc[t]);
-          my_acc[a.T + t] = fmaf(wt, d[1], my_acc[a.T + t]);
-        }
       }
     }
-    __syncthreads();
-    for (int r = 0; r < 2; ++r) {
-      if (!row_ok[r]) continue;
-      for (int t = lane; t < a.T; t += kWave) {
-        const float v = my_acc[r * a.T + t];
-        const size_t o = (size_t)t * a.H + r0 + r;
-        a.out[o] = v;
-        if (a.layer_out) a.layer_out[o] = load_scalar(a.x, a.x_dt, o) + v;
-      }
+    float mine = 0.f;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(d[r]);
+      mine = lane == r ? v : mine;
     }
+    if (lane < R && r0 + lane < a.H) a.ws.y[(size_t)pos * a.H + r0 + lane] = mine;
   }
+}
+
+// out[t, h] = sum_k w[t,k] * y[pos(t,k), h]  (slot order k = 0..K-1)
+//             + g_t * y[P + t, h]            (shared expert, g_t = sigmoid(w_g . x_t) or 1)
+// layer_out = x + out.
+__global__ __launch_bounds__(256) void moe_combine_kernel(ExpertArgs a) {
+  const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const size_t total = (size_t)a.T * a.H;
+  if (idx >= total) return;
+  const int t = (int)(idx / a.H);
+  const int h = (int)(idx - (size_t)t * a.H);
+  const int P = a.T * a.K;
+  float acc = 0.f;
+  for (int k = 0; k < a.K; ++k) {
+    const int pair = t * a.K + k;
+    acc += a.ws.wts[pair] * a.ws.y[(size_t)a.ws.inverse[pair] * a.H + h];
+  }
+  if (a.has_shared) {
+    const float g = a.sg ? a.ws.sgate[t] : 1.f;
+    acc += g * a.ws.y[(size_t)(P + t) * a.H + h];
+  }
+  a.out[idx] = acc;
+  if (a.layer_out) a.layer_out[idx] = load_scalar(a.x, a.x_dt, idx) + acc;
 }
 
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
-static int check_ws(void* ws, size_t bytes, int T, int K, int E, int I, MoeWs* out) {
-  size_t need = moe_ws_layout(T, K, E, I, nullptr, out);
+static int check_ws(void* ws, size_t bytes, int T, int K, int E, int I, int H, MoeWs* out) {
+  size_t need = moe_ws_layout(T, K, E, I, H, nullptr, out);
   if (!ws) return fail(FK_ERR_WORKSPACE, "workspace is NULL (need %zu bytes)", need);
   if (bytes < need) return fail(FK_ERR_WORKSPACE, "workspace has %zu bytes, need %zu", bytes, need);
   if (!aligned16(ws)) return fail(FK_ERR_ALIGNMENT, "workspace must be 16-byte aligned");
-  moe_ws_layout(T, K, E, I, reinterpret_cast<char*>(ws), out);
+  moe_ws_layout(T, K, E, I, H, reinterpret_cast<char*>(ws), out);
   return FK_OK;
 }
 
@@ -614,18 +660,43 @@ static int check_ws(void* ws, size_t bytes, int T, int K, int E, int I, MoeWs* o
     __VA_ARGS__                           \
   }
 
-static int launch_router(const RouterArgs& ra, int router_dt, int hidden_dt, hipStream_t stream) {
-  const int grid = (ra.E + 3) / 4;
-  const bool bfw = router_dt == FK_DTYPE_BF16, bfx = hidden_dt == FK_DTYPE_BF16;
-  const bool wide = ra.H > 2048;
-  FK_DISPATCH_BOOL(bfw, BW, FK_DISPATCH_BOOL(bfx, BX, {
-    if (wide) {
-      hipLaunchKernelGGL((moe_router_kernel<BW, BX, 8>), dim3(grid), dim3(256), 0, stream, ra);
-    } else {
-      hipLaunchKernelGGL((moe_router_kernel<BW, BX, 4>), dim3(grid), dim3(256), 0, stream, ra);
-    }
-  }))
+// Co-resident workgroup capacity of a kernel on the current device (cached
+// per device); the grid-barrier kernels never launch more workgroups.
+template <typename K>
+static int resident_capacity(K kernel, int block, size_t shm, int* cache) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] > 0) return cache[dev];
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, shm) != hipSuccess) return 0;
+  cache[dev] = cus * per_cu;
+  return cache[dev];
+}
+
+template <bool BW, bool BX, int NJ, int NJE>
+static int launch_router_t(const RouterArgs& ra, hipStream_t stream) {
+  static int cap_cache[64] = {0};
+  auto kernel = moe_router_kernel<BW, BX, NJ, NJE>;
+  const int cap = resident_capacity(kernel, 256, 0, cap_cache);
+  const int gx = (ra.E + 3) / 4;
+  if (cap < gx) return fail(FK_ERR_UNSUPPORTED, "router grid %d exceeds co-resident capacity %d", gx, cap);
+  int gy = (ra.T + 15) / 16;
+  if (gy > cap / gx) gy = cap / gx;
+  if (gy < 1) gy = 1;
+  hipLaunchKernelGGL(kernel, dim3(gx, gy), dim3(256), 0, stream, ra);
   return check_launch("moe_router_kernel");
+}
+
+static int launch_router(const RouterArgs& ra, int router_dt, int hidden_dt, hipStream_t stream) {
+  const bool bfw = router_dt == FK_DTYPE_BF16, bfx = hidden_dt == FK_DTYPE_BF16;
+  const bool wide = ra.H > 2048, many = ra.E > 256;
+  int st = FK_OK;
+  FK_DISPATCH_BOOL(bfw, BW, FK_DISPATCH_BOOL(bfx, BX, {
+    if (wide) st = many ? launch_router_t<BW, BX, 8, 16>(ra, stream) : launch_router_t<BW, BX, 8, 4>(ra, stream);
+    else st = many ? launch_router_t<BW, BX, 4, 16>(ra, stream) : launch_router_t<BW, BX, 4, 4>(ra, stream);
+  }))
+  return st;
 }
 
 static int launch_experts(const ExpertArgs& ea, int expert_dt, hipStream_t stream) {
@@ -644,19 +715,17 @@ static int launch_experts(const ExpertArgs& ea, int expert_dt, hipStream_t strea
   int st = check_launch("moe_gateup_kernel");
   if (st) return st;
 
-  const int dn_grid = (ea.H + kDownRows - 1) / kDownRows;
+  const int dn_grid = slots * ((ea.H + kDownRows - 1) / kDownRows);
   const bool wide_i = ea.I > 512;
-  const size_t shm = ea.T == 1 ? 0 : (size_t)4 * 2 * ea.T * sizeof(float);
   FK_DISPATCH_BOOL(bfw, BW, {
-    if (ea.T == 1) {
-      if (wide_i) hipLaunchKernelGGL((moe_down_kernel<BW, 2, true>), dim3(dn_grid), dim3(256), 0, stream, ea);
-      else hipLaunchKernelGGL((moe_down_kernel<BW, 1, true>), dim3(dn_grid), dim3(256), 0, stream, ea);
-    } else {
-      if (wide_i) hipLaunchKernelGGL((moe_down_kernel<BW, 2, false>), dim3(dn_grid), dim3(256), shm, stream, ea);
-      else hipLaunchKernelGGL((moe_down_kernel<BW, 1, false>), dim3(dn_grid), dim3(256), shm, stream, ea);
-    }
+    if (wide_i) hipLaunchKernelGGL((moe_down_kernel<BW, 2>), dim3(dn_grid), dim3(256), 0, stream, ea);
+    else hipLaunchKernelGGL((moe_down_kernel<BW, 1>), dim3(dn_grid), dim3(256), 0, stream, ea);
   })
-  return check_launch("moe_down_kernel");
+  st = check_launch("moe_down_kernel");
+  if (st) return st;
+  const size_t total = (size_t)ea.T * ea.H;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, ea);
+  return check_launch("moe_combine_kernel");
 }
 
 static int validate_common(int T, int H, int E, int K) {
@@ -715,10 +784,10 @@ using namespace fk;
 
 extern "C" {
 
-size_t fk_moe_workspace_bytes(int tokens, int top_k, int num_experts, int intermediate) {
-  if (tokens < 1 || top_k < 1 || num_experts < 1 || intermediate < 1) return 0;
+size_t fk_moe_workspace_bytes(int tokens, int top_k, int num_experts, int intermediate, int hidden_size) {
+  if (tokens < 1 || top_k < 1 || num_experts < 1 || intermediate < 1 || hidden_size < 1) return 0;
   MoeWs ws;
-  return moe_ws_layout(tokens, top_k, num_experts, intermediate, nullptr, &ws);
+  return moe_ws_layout(tokens, top_k, num_experts, intermediate, hidden_size, nullptr, &ws);
 }
 
 int fk_moe_router(const void* hidden, int hidden_dtype, const void* norm_weight, int norm_dtype,
@@ -733,10 +802,12 @@ int fk_moe_router(const void* hidden, int hidden_dtype, const void* norm_weight,
     return fail(FK_ERR_DTYPE, "router inputs must be f32 or bf16");
   if (!hidden || !norm_weight || !router_weight || !logits || !topk_ids || !topk_weights)
     return fail(FK_ERR_INVALID, "router pointers must be non-NULL");
-  if (!aligned16(hidden) || !aligned16(router_weight)) return fail(FK_ERR_ALIGNMENT, "hidden and router_weight must be 16-byte aligned");
+  if (!aligned16(hidden) || !aligned16(router_weight) || !aligned16(norm_weight))
+    return fail(FK_ERR_ALIGNMENT, "hidden, norm_weight and router_weight must be 16-byte aligned");
   MoeWs ws;
-  // The router only needs the routing tables; size them for any intermediate.
-  st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, 0, &ws);
+  // The router only needs the routing tables, which precede the
+  // size-dependent activation buffers in every layout.
+  st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, 0, 0, &ws);
   if (st) return st;
   RouterArgs ra;
   ra.x = hidden;
@@ -768,7 +839,7 @@ int fk_moe_align(const void* topk_ids, int ids_dtype, const void* topk_weights, 
   if (topk_weights && !is_float_dtype(weights_dtype)) return fail(FK_ERR_DTYPE, "topk_weights must be f32 or bf16");
   if (!topk_ids) return fail(FK_ERR_INVALID, "topk_ids must be non-NULL");
   MoeWs ws;
-  int st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, 0, &ws);
+  int st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, 0, 0, &ws);
   if (st) return st;
   AlignArgs aa;
   aa.ids = topk_ids;
@@ -797,7 +868,7 @@ int fk_moe_experts(const void* hidden, int hidden_dtype, const void* gate_up, co
   if (st) return st;
   if (!out) return fail(FK_ERR_INVALID, "out must be non-NULL");
   MoeWs ws;
-  st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, intermediate, &ws);
+  st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, intermediate, hidden_size, &ws);
   if (st) return st;
   ExpertArgs ea = make_expert_args(hidden, hidden_dtype, gate_up, down, shared_gate_up, shared_down, shared_gate,
                                    shared_gate_dtype, tokens, hidden_size, intermediate, num_experts, top_k, out,
@@ -817,7 +888,7 @@ int fk_moe_layer(const void* hidden, int hidden_dtype, const void* norm_weight, 
   if (st) return st;
   if (!moe_out) return fail(FK_ERR_INVALID, "moe_out must be non-NULL");
   MoeWs ws;
-  st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, intermediate, &ws);
+  st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, intermediate, hidden_size, &ws);
   if (st) return st;
   st = fk_moe_router(hidden, hidden_dtype, norm_weight, norm_dtype, router_weight, router_dtype, router_bias,
                      bias_dtype, tokens, hidden_size, num_experts, top_k, eps, norm_offset, logits, topk_ids,

@@ -172,7 +172,7 @@ def hip_qwen36_moe_align(topk_ids: Any, num_experts: int, topk_weights: Any | No
     offsets = torch.empty((num_experts + 1,), device=dev, dtype=torch.int32)
     perm = torch.empty((tokens * top_k,), device=dev, dtype=torch.int32)
     inverse = torch.empty((tokens * top_k,), device=dev, dtype=torch.int32)
-    nbytes = _lib.load().fk_moe_workspace_bytes(tokens, top_k, num_experts, 8)
+    nbytes = _lib.load().fk_moe_workspace_bytes(tokens, top_k, num_experts, 8, 8)
     ws = _workspace("moe", dev, nbytes)
     _lib.call(
         "fk_moe_align",
@@ -262,7 +262,7 @@ def hip_qwen36_moe_router_decode(
     _router_bias_checks(router_bias, router_weight.shape[0])
     x = _dense(hidden).reshape(1, -1)
     rw = _dense(router_weight)
-    ws = _workspace("moe", x.device, _lib.load().fk_moe_workspace_bytes(1, top_k, rw.shape[0], 8))
+    ws = _workspace("moe", x.device, _lib.load().fk_moe_workspace_bytes(1, top_k, rw.shape[0], 8, 8))
     logits, ids, weights = _run_router(x, norm_weight, rw, top_k, eps, norm_offset, router_bias, ws)
     return logits.reshape(-1), ids.reshape(-1), weights.reshape(-1)
 
@@ -287,7 +287,7 @@ def hip_qwen36_batched_moe_router_decode(
     _router_bias_checks(router_bias, router_weight.shape[0])
     x = _dense(hidden)
     rw = _dense(router_weight)
-    ws = _workspace("moe", x.device, _lib.load().fk_moe_workspace_bytes(x.shape[0], top_k, rw.shape[0], 8))
+    ws = _workspace("moe", x.device, _lib.load().fk_moe_workspace_bytes(x.shape[0], top_k, rw.shape[0], 8, 8))
     return _run_router(x, norm_weight, rw, top_k, eps, norm_offset, router_bias, ws)
 
 
@@ -344,7 +344,7 @@ def _run_experts(
     dev = hidden2d.device
     lib = _lib.load()
     if ws is None:
-        ws = _workspace("moe", dev, lib.fk_moe_workspace_bytes(tokens, top_k, num_experts, intermediate))
+        ws = _workspace("moe", dev, lib.fk_moe_workspace_bytes(tokens, top_k, num_experts, intermediate, hidden_size))
     stream = _stream(dev)
     if not aligned:
         ids = _dense(ids2d)
@@ -514,7 +514,7 @@ def _moe_full(hidden2d, norm_weight, router_weight, gu_w, dn_w, sgu_w, sdn_w, sg
     num_experts = gu_w.shape[0]
     dev = x.device
     lib = _lib.load()
-    ws = _workspace("moe", dev, lib.fk_moe_workspace_bytes(tokens, top_k, num_experts, intermediate))
+    ws = _workspace("moe", dev, lib.fk_moe_workspace_bytes(tokens, top_k, num_experts, intermediate, hidden_size))
     rw = _dense(router_weight)
     gu, dn, sgu, sdn = _dense(gu_w), _dense(dn_w), _dense(sgu_w), _dense(sdn_w)
     nw = _dense(norm_weight)
@@ -750,6 +750,61 @@ def hip_qwen36_batched_deltanet_recurrent_output(
     return update, next_state
 
 
+def _deltanet_step(hidden, conv_state, recurrent_state, norm_weight, w_qkv, w_z, w_a, w_b, conv1d_weight,
+                   out_proj_weight, linear_norm_weight, a_log, dt_bias, qk_heads, value_heads, head_dim, eps):
+    """Whole DeltaNet step + residual through fk_deltanet_step (projections with
+    the conv fused in, recurrent + gated norm, out-proj)."""
+
+    tensors = (hidden, conv_state, recurrent_state, norm_weight, w_qkv, w_z, w_a, w_b, conv1d_weight,
+               out_proj_weight, linear_norm_weight, a_log, dt_bias)
+    if not all(t.is_cuda for t in tensors):
+        raise ValueError("all DeltaNet inputs must be CUDA tensors")
+    tokens, hidden_size = hidden.shape
+    key_dim, value_dim = qk_heads * head_dim, value_heads * head_dim
+    conv_dim = 2 * key_dim + value_dim
+    if norm_weight.ndim != 1 or norm_weight.shape[0] != hidden_size:
+        raise ValueError("norm_weight must have shape [hidden_size]")
+    expected = {"in_proj_qkv_weight": (w_qkv, (conv_dim, hidden_size)), "in_proj_z_weight": (w_z, (value_dim, hidden_size)),
+                "in_proj_a_weight": (w_a, (value_heads, hidden_size)), "in_proj_b_weight": (w_b, (value_heads, hidden_size)),
+                "out_proj_weight": (out_proj_weight, (out_proj_weight.shape[0], value_dim)),
+                "recurrent_state": (recurrent_state, (value_heads, head_dim, head_dim)),
+                "linear_norm_weight": (linear_norm_weight, (head_dim,)), "a_log": (a_log, (value_heads,)),
+                "dt_bias": (dt_bias, (value_heads,))}
+    for name, (t, shape) in expected.items():
+        if tuple(t.shape) != shape:
+            raise ValueError(f"{name} must have shape {list(shape)}")
+    if conv_state.shape[0] != conv_dim or tuple(conv1d_weight.shape) != (conv_dim, 1, conv_state.shape[1]):
+        raise ValueError("conv_state / conv1d_weight must have shapes [channels, k] / [channels, 1, k]")
+    if value_heads % qk_heads:
+        raise ValueError("value_heads must be divisible by qk_heads")
+    if len({w_qkv.dtype, w_z.dtype, w_a.dtype, w_b.dtype}) != 1:
+        raise ValueError("projection weights must share a dtype")
+    x = _dense(hidden)
+    ts = [_dense(t) for t in (norm_weight, w_qkv, w_z, w_a, w_b, conv_state, conv1d_weight, recurrent_state,
+                              out_proj_weight, linear_norm_weight, a_log, dt_bias)]
+    nw, wq, wz, wa, wb, cs, cw, rs, wo, lnw, al, dtb = ts
+    codes = [_fcode(x, "hidden"), _fcode(nw, "norm_weight"), _fcode(wq, "projection weights"), _fcode(cs, "conv_state"),
+             _fcode(cw, "conv1d_weight"), _fcode(rs, "recurrent_state"), _fcode(wo, "out_proj_weight"),
+             _fcode(lnw, "linear_norm_weight"), _fcode(al, "a_log"), _fcode(dtb, "dt_bias")]
+    dtypes = (ctypes.c_int32 * 10)(*codes)
+    dev = x.device
+    update = torch.empty((tokens, wo.shape[0]), device=dev, dtype=torch.float32)
+    dn_hidden = torch.empty_like(update)
+    next_conv = torch.empty_like(cs)
+    next_rec = torch.empty_like(rs)
+    lib = _lib.load()
+    ws = _workspace("deltanet_step", dev, lib.fk_deltanet_step_workspace_bytes(tokens, qk_heads, value_heads, head_dim))
+    _lib.call(
+        "fk_deltanet_step",
+        x.data_ptr(), nw.data_ptr(), wq.data_ptr(), wz.data_ptr(), wa.data_ptr(), wb.data_ptr(), cs.data_ptr(),
+        cw.data_ptr(), rs.data_ptr(), wo.data_ptr(), lnw.data_ptr(), al.data_ptr(), dtb.data_ptr(),
+        ctypes.cast(dtypes, ctypes.c_void_p), tokens, hidden_size, qk_heads, value_heads, head_dim, cs.shape[1],
+        float(eps), update.data_ptr(), dn_hidden.data_ptr(), next_conv.data_ptr(), next_rec.data_ptr(),
+        ws.data_ptr(), ws.numel(), _stream(dev),
+    )
+    return update, dn_hidden, next_conv, next_rec
+
+
 def hip_qwen36_batched_deltanet_moe_layer_decode(
     hidden, conv_state, recurrent_state, deltanet_norm_weight, in_proj_qkv_weight, in_proj_z_weight,
     in_proj_a_weight, in_proj_b_weight, conv1d_weight, out_proj_weight, linear_norm_weight, a_log, dt_bias,
@@ -761,6 +816,20 @@ def hip_qwen36_batched_deltanet_moe_layer_decode(
     """DeltaNet -> MoE layer, returning the reference's 9-tuple
     `(layer_hidden, deltanet_hidden, deltanet_update, moe_update, conv_state,
     recurrent_state, router_logits, topk_ids, topk_weights)` (reference qwen36_layer.py:204-305)."""
+
+    _require_lib()
+    if hidden.ndim == 2 and 1 <= hidden.shape[0] <= 64 and conv_state.ndim == 2 and conv_state.shape[1] <= 8:
+        dn_update, dn_hidden, next_conv, next_rec = _deltanet_step(
+            hidden, conv_state, recurrent_state, deltanet_norm_weight, in_proj_qkv_weight, in_proj_z_weight,
+            in_proj_a_weight, in_proj_b_weight, conv1d_weight, out_proj_weight, linear_norm_weight, a_log, dt_bias,
+            qk_heads, value_heads, head_dim, eps,
+        )
+        layer_hidden, moe_update, logits, ids, weights = hip_qwen36_batched_moe_layer_decode(
+            dn_hidden, moe_norm_weight, router_weight, expert_gate_up_weight, expert_down_weight,
+            shared_gate_up_weight, shared_down_weight, shared_expert_gate_weight,
+            top_k=top_k, eps=eps, router_bias=router_bias,
+        )
+        return layer_hidden, dn_hidden, dn_update, moe_update, next_conv, next_rec, logits, ids, weights
 
     mixed, z, a_l, b_l = hip_qwen36_batched_deltanet_project(
         hidden, deltanet_norm_weight, in_proj_qkv_weight, in_proj_z_weight, in_proj_a_weight, in_proj_b_weight,

@@ -7,8 +7,9 @@ graph (torch.cuda.CUDAGraph), which is how bench.py times them.
 
   MoeLayerPlan      router + top-k + routing tables + experts + residual
                     (fk_moe_layer), or its two stages separately.
-  DeltaNetStepPlan  projections -> conv -> recurrent/gated-norm/out-proj
-                    (+ residual), writing the next conv / recurrent states.
+  DeltaNetStepPlan  projections + conv -> recurrent/gated-norm -> out-proj
+                    (+ residual) through fk_deltanet_step, writing the next
+                    conv / recurrent states.
 """
 
 from __future__ import annotations
@@ -62,7 +63,7 @@ class MoeLayerPlan:
         self.weights = torch.empty((tokens, top_k), dtype=torch.float32, device=dev)
         self.moe_out = torch.empty((tokens, self.hidden_size), dtype=torch.float32, device=dev)
         self.layer_out = torch.empty_like(self.moe_out)
-        nbytes = self.lib.fk_moe_workspace_bytes(tokens, top_k, self.num_experts, self.intermediate)
+        nbytes = self.lib.fk_moe_workspace_bytes(tokens, top_k, self.num_experts, self.intermediate, self.hidden_size)
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         sg = w.get("shared_expert_gate_weight")
         self._sg = sg
@@ -122,7 +123,8 @@ class MoeLayerPlan:
 
 
 class DeltaNetStepPlan:
-    """One Gated DeltaNet decode step (T rows through one state) + residual."""
+    """One Gated DeltaNet decode step (T rows through one state) + residual,
+    issued as the single fused C-ABI call fk_deltanet_step (three launches)."""
 
     def __init__(
         self,
@@ -145,48 +147,35 @@ class DeltaNetStepPlan:
         self.eps = float(eps)
         H = spec.hidden_size
         self.hidden = hidden if hidden is not None else torch.zeros((tokens, H), dtype=hidden_dtype, device=dev)
-        self.mixed = torch.empty((tokens, w["in_proj_qkv_weight"].shape[0]), dtype=torch.float32, device=dev)
-        self.z = torch.empty((tokens, w["in_proj_z_weight"].shape[0]), dtype=torch.float32, device=dev)
-        self.a = torch.empty((tokens, w["in_proj_a_weight"].shape[0]), dtype=torch.float32, device=dev)
-        self.b = torch.empty_like(self.a)
-        self.conv_out = torch.empty_like(self.mixed)
         self.next_conv_state = torch.empty_like(w["conv_state"])
         self.next_recurrent_state = torch.empty_like(w["recurrent_state"])
         self.update = torch.empty((tokens, H), dtype=torch.float32, device=dev)
         self.hidden_out = torch.empty_like(self.update)
-        nbytes = self.lib.fk_deltanet_workspace_bytes(tokens, spec.deltanet_value_heads, spec.deltanet_head_dim)
+        nbytes = self.lib.fk_deltanet_step_workspace_bytes(
+            tokens, spec.deltanet_qk_heads, spec.deltanet_value_heads, spec.deltanet_head_dim
+        )
         self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
-        names = ("conv_out", "z", "a", "b", "recurrent_state", "out_proj_weight", "linear_norm_weight", "a_log", "dt_bias")
-        tensors = (self.conv_out, self.z, self.a, self.b, w["recurrent_state"], w["out_proj_weight"],
-                   w["linear_norm_weight"], w["a_log"], w["dt_bias"])
-        codes = [_fcode(t, n) for t, n in zip(tensors, names)] + [_fcode(self.hidden, "hidden")]
+        order = ("input_norm_weight", "in_proj_qkv_weight", "conv_state", "conv1d_weight", "recurrent_state",
+                 "out_proj_weight", "linear_norm_weight", "a_log", "dt_bias")
+        codes = [_fcode(self.hidden, "hidden")] + [_fcode(w[k], k) for k in order]
+        for k in ("in_proj_z_weight", "in_proj_a_weight", "in_proj_b_weight"):
+            if w[k].dtype != w["in_proj_qkv_weight"].dtype:
+                raise ValueError("projection weights must share a dtype")
         self._dtypes = (ctypes.c_int32 * 10)(*codes)
 
     def run(self, stream: torch.cuda.Stream | None = None) -> None:
         w, sp = self.w, self.spec
-        s = _stream_handle(stream, self.device)
         _lib.call(
-            "fk_deltanet_project",
-            self.hidden.data_ptr(), _fcode(self.hidden, "hidden"),
-            w["input_norm_weight"].data_ptr(), _fcode(w["input_norm_weight"], "norm"),
+            "fk_deltanet_step",
+            self.hidden.data_ptr(), w["input_norm_weight"].data_ptr(),
             w["in_proj_qkv_weight"].data_ptr(), w["in_proj_z_weight"].data_ptr(),
-            w["in_proj_a_weight"].data_ptr(), w["in_proj_b_weight"].data_ptr(), _fcode(w["in_proj_qkv_weight"], "proj"),
-            self.tokens, sp.hidden_size, self.mixed.shape[1], self.z.shape[1], self.a.shape[1], self.eps, 1.0,
-            self.mixed.data_ptr(), self.z.data_ptr(), self.a.data_ptr(), self.b.data_ptr(), s,
-        )
-        _lib.call(
-            "fk_deltanet_conv",
-            self.mixed.data_ptr(), _lib.FK_DTYPE_F32, w["conv_state"].data_ptr(), _fcode(w["conv_state"], "conv_state"),
-            w["conv1d_weight"].data_ptr(), _fcode(w["conv1d_weight"], "conv1d"), self.tokens, self.mixed.shape[1],
-            w["conv_state"].shape[1], self.conv_out.data_ptr(), self.next_conv_state.data_ptr(), s,
-        )
-        _lib.call(
-            "fk_deltanet_recurrent_output",
-            self.conv_out.data_ptr(), self.z.data_ptr(), self.a.data_ptr(), self.b.data_ptr(),
-            w["recurrent_state"].data_ptr(), w["out_proj_weight"].data_ptr(), w["linear_norm_weight"].data_ptr(),
-            w["a_log"].data_ptr(), w["dt_bias"].data_ptr(), self.hidden.data_ptr(),
-            ctypes.cast(self._dtypes, ctypes.c_void_p),
-            self.tokens, sp.deltanet_qk_heads, sp.deltanet_value_heads, sp.deltanet_head_dim, sp.hidden_size, self.eps,
-            self.update.data_ptr(), self.next_recurrent_state.data_ptr(), self.hidden_out.data_ptr(),
-            self.workspace.data_ptr(), self.workspace.numel(), s,
+            w["in_proj_a_weight"].data_ptr(), w["in_proj_b_weight"].data_ptr(),
+            w["conv_state"].data_ptr(), w["conv1d_weight"].data_ptr(), w["recurrent_state"].data_ptr(),
+            w["out_proj_weight"].data_ptr(), w["linear_norm_weight"].data_ptr(), w["a_log"].data_ptr(),
+            w["dt_bias"].data_ptr(), ctypes.cast(self._dtypes, ctypes.c_void_p),
+            self.tokens, sp.hidden_size, sp.deltanet_qk_heads, sp.deltanet_value_heads, sp.deltanet_head_dim,
+            w["conv_state"].shape[1], self.eps,
+            self.update.data_ptr(), self.hidden_out.data_ptr(), self.next_conv_state.data_ptr(),
+            self.next_recurrent_state.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(),
+            _stream_handle(stream, self.device),
         )

@@ -60,9 +60,10 @@ const char* fk_last_error_detail(void);
 /* ------------------------------------------------------------------------ */
 
 /* Bytes of workspace needed by fk_moe_router / fk_moe_align / fk_moe_experts
- * / fk_moe_layer for this problem size (routing tables, counters, the fp32
- * SwiGLU activations of every routed (token, slot) pair and shared token). */
-size_t fk_moe_workspace_bytes(int tokens, int top_k, int num_experts, int intermediate);
+ * / fk_moe_layer for this problem size (routing tables, counters, and the
+ * fp32 SwiGLU activations and down-projection outputs of every routed
+ * (token, slot) pair and shared-expert token). */
+size_t fk_moe_workspace_bytes(int tokens, int top_k, int num_experts, int intermediate, int hidden_size);
 
 /* Router: n = RMSNorm(x) * (norm_offset + w); logits = n . W^T (+ bias);
  * softmax; top-k ordered by (probability desc, expert id asc); weights
@@ -201,6 +202,31 @@ int fk_deltanet_recurrent_output(const void* mixed_qkv, const void* z,
                                  float* residual_out,
                                  void* workspace, size_t workspace_bytes,
                                  void* stream);
+
+/* Bytes of workspace for fk_deltanet_step. */
+size_t fk_deltanet_step_workspace_bytes(int tokens, int qk_heads, int value_heads, int head_dim);
+
+/* The whole Gated DeltaNet step with the residual, in three launches:
+ * RMSNorm(1+w) + projections with the causal conv fused into the same
+ * kernel, the recurrent rule with the per-head gated RMSNorm, and the
+ * output projection.  update = core W_out^T; hidden_out (nullable) =
+ * hidden + update; next_conv_state / next_recurrent_state keep the dtypes of
+ * their inputs.  `dtypes` holds, in order: hidden, input_norm_weight,
+ * projection weights (qkv/z/a/b share one), conv_state, conv1d_weight,
+ * recurrent_state, out_proj_weight, linear_norm_weight, a_log, dt_bias.
+ * Limits: tokens <= 64, kernel_size <= 8.
+ * Replaces the project -> conv -> recurrent/output -> residual sequence of
+ * triton_qwen36_batched_deltanet_moe_layer_decode (qwen36_layer.py:238-282). */
+int fk_deltanet_step(const void* hidden, const void* input_norm_weight,
+                     const void* w_qkv, const void* w_z, const void* w_a, const void* w_b,
+                     const void* conv_state, const void* conv_weight,
+                     const void* recurrent_state, const void* out_proj_weight,
+                     const void* linear_norm_weight, const void* a_log, const void* dt_bias,
+                     const int32_t* dtypes, int tokens, int hidden_size,
+                     int qk_heads, int value_heads, int head_dim, int kernel_size, float eps,
+                     float* update, float* hidden_out, void* next_conv_state,
+                     void* next_recurrent_state, void* workspace, size_t workspace_bytes,
+                     void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Synthetic (tiny-spec) decode blocks behind the --moe-impl/--deltanet-impl  */

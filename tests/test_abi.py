@@ -39,13 +39,13 @@ def test_status_strings():
 
 def test_workspace_sizes_are_monotone():
     lib = _lib.load()
-    a = lib.fk_moe_workspace_bytes(1, 8, 256, 512)
-    b = lib.fk_moe_workspace_bytes(16, 8, 256, 512)
-    c = lib.fk_moe_workspace_bytes(128, 8, 256, 512)
+    a = lib.fk_moe_workspace_bytes(1, 8, 256, 512, 2048)
+    b = lib.fk_moe_workspace_bytes(16, 8, 256, 512, 2048)
+    c = lib.fk_moe_workspace_bytes(128, 8, 256, 512, 2048)
     assert 0 < a < b < c
-    # activations dominate: (T*K + T) * I * 4 bytes
-    assert c >= (128 * 8 + 128) * 512 * 4
-    assert lib.fk_moe_workspace_bytes(0, 8, 256, 512) == 0
+    # per-pair activations and down outputs dominate: (T*K + T) * (I + H) * 4 bytes
+    assert c >= (128 * 8 + 128) * (512 + 2048) * 4
+    assert lib.fk_moe_workspace_bytes(0, 8, 256, 512, 2048) == 0
     assert lib.fk_deltanet_workspace_bytes(8, 32, 128) >= 2 * 8 * 32 * 128 * 4
 
 

@@ -84,7 +84,7 @@ def _recurrent_inputs(spec, tokens, seed):
     )
 
 
-@pytest.mark.parametrize("spec_name,tokens", [("small", 1), ("small", 4), ("real", 1), ("real", 8)])
+@pytest.mark.parametrize("spec_name,tokens", [("small", 1), ("small", 4), ("small", 17), ("real", 1), ("real", 8), ("real", 20)])
 def test_recurrent_output(device, spec_name, tokens):
     spec = REAL if spec_name == "real" else SMALL
     inp = _recurrent_inputs(spec, tokens, 20 + tokens)
@@ -109,7 +109,7 @@ def test_recurrent_t_rows_equal_t_single_steps(device):
     torch.testing.assert_close(state, final, atol=1e-6, rtol=1e-6)
 
 
-@pytest.mark.parametrize("spec_name,tokens", [("small", 2), ("real", 1), ("real", 8)])
+@pytest.mark.parametrize("spec_name,tokens", [("small", 2), ("small", 17), ("real", 1), ("real", 8)])
 def test_deltanet_moe_layer(device, spec_name, tokens):
     spec = REAL if spec_name == "real" else SMALL
     dn = wl.make_deltanet_weights(spec, seed=40)
