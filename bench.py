@@ -44,8 +44,9 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     p.add_argument("--no-extra", action="store_true", help="skip the batch-1/128 and DeltaNet sub-results")
-    p.add_argument("--only", choices=["moe", "deltanet"], default=None,
-                   help="run a single timing loop (for profilers) and print its line")
+    p.add_argument("--only", choices=["moe", "deltanet", "copy"], default=None,
+                   help="run a single timing loop (for profilers) and print its line; "
+                        "'copy' runs 16 device-to-device copies of 1 GiB (PMC byte-counter calibration)")
     return p.parse_args()
 
 
@@ -74,6 +75,18 @@ def main() -> int:
         return 1
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
+    if args.only == "copy":
+        nbytes = 1 << 30
+        src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(16):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        secs = time.perf_counter() - t0
+        print(json.dumps({"copy_bytes_per_launch": nbytes, "launches": 16, "read_plus_write_tbs": round(2 * nbytes * 16 / secs / 1e12, 3)}))
+        return 0
     spec = qwen36_35b_a3b_spec()
     H, E, I, K = spec.hidden_size, spec.num_experts, spec.expert_intermediate_size, spec.num_routed_experts
     stream = torch.cuda.Stream(dev)
@@ -255,6 +268,15 @@ def main() -> int:
         del w_cpu
 
     expert_frac = main_res["expert_stage_tbs"] * 1e12 / (HBM_PEAK_GBS * 1e9)
+    # HBM bytes per expert stage from the committed rocprofv3 --pmc FETCH_SIZE /
+    # WRITE_SIZE passes (profiles/moe_layer_pmc_traffic.md), when recorded.
+    traffic = None
+    traffic_file = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "pmc_traffic.json")
+    if os.path.exists(traffic_file):
+        with open(traffic_file) as fh:
+            rec = json.load(fh).get(f"moe_layer_t{args.tokens}")
+        if rec:
+            traffic = rec["expert_stage_traffic_bytes"]
     line = {
         "metric": METRIC,
         "value": main_res["us_per_layer_step"],
@@ -286,7 +308,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(expert_frac, 4),
-            "traffic": None,
+            "traffic": traffic,
+            "algorithmic_bytes": main_res["expert_stage_bytes"],
         },
         "layer": main_res,
         "sub_results": sub,
