@@ -237,6 +237,43 @@ __device__ __forceinline__ uint32_t ticket_add(uint32_t* p) {
 __device__ __forceinline__ uint32_t load_coherent(const uint32_t* p) {
   return __hip_atomic_load(const_cast<uint32_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void store_coherent(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Tagged values: an fp32 value and a 32-bit launch tag in one naturally
+// aligned 8-byte word, stored and loaded as single-copy-atomic coherent
+// accesses.  A consumer that reads the tag of the current launch knows the
+// value beside it is this launch's, with no counter or barrier between
+// producer and consumer.
+__device__ __forceinline__ void store_tagged(uint64_t* p, float v, uint32_t tag) {
+  __hip_atomic_store(p, ((uint64_t)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t load_tagged(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t tag_of(uint64_t w) { return (uint32_t)(w >> 32); }
+__device__ __forceinline__ float value_of(uint64_t w) { return __uint_as_float((uint32_t)w); }
+
+// Bounded poll of N tagged words of this lane (src[j] == nullptr: no word):
+// re-reads every word that does not carry `tag` yet, all reads of one round
+// in flight together, until all carry it or kPollLimit rounds have passed.
+// Returns whether all carry the tag.
+constexpr uint32_t kPollLimit = 1u << 16;
+template <int N>
+__device__ __forceinline__ bool poll_tagged(uint64_t (&w)[N], const uint64_t* const (&src)[N], uint32_t tag) {
+  for (uint32_t i = 0; i < kPollLimit; ++i) {
+    bool ready = true;
+#pragma unroll
+    for (int j = 0; j < N; ++j) ready = ready && (src[j] == nullptr || tag_of(w[j]) == tag);
+    if (ready) return true;
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (src[j] != nullptr && tag_of(w[j]) != tag) w[j] = load_tagged(src[j]);
+  }
+  return false;
+}
 
 // Grid-wide barrier for kernels whose grid the host has capped at the number
 // of co-resident workgroups.  Called by one thread per workgroup after the

@@ -37,7 +37,14 @@ constexpr int kDownRowsPerWave = 8; // down rows per wavefront
 constexpr int kDownRows = 4 * kDownRowsPerWave;  // down rows per workgroup
 
 struct MoeWs {
-  uint32_t* tickets;    // [16] self-resetting arrival counters
+  uint32_t* tickets;    // [16] arrival counters; [kTicketEpoch] = fused launch epoch
+  // Single-launch path (T <= 4, E <= 256, I <= 512): tagged hand-off words in
+  // a fixed-size region, so that no offset depends on the problem shape
+  // (fk_moe_router / fk_moe_align lay the workspace out without I and H).
+  uint64_t* f_logits;   // [T, E] router logits (capacity 4 * 256)
+  uint64_t* f_act;      // [(T*K + T), I] SwiGLU activations, permuted rows then shared rows (capacity 36 * 512)
+  uint64_t* f_sgate;    // [T] shared-expert gates
+  uint64_t* f_started;  // [grid] one tagged record per workgroup of the launch (capacity 1024)
   int32_t* counts;      // [E]
   int32_t* offsets;     // [E+1] exclusive prefix of counts
   int32_t* perm;        // [P] permuted position -> pair index t*K+k
@@ -51,6 +58,19 @@ struct MoeWs {
   float* y;             // [(P + T), H] per-pair down-projection outputs
 };
 
+// Counter slots of MoeWs::tickets.
+constexpr int kTicketRouterBarrier = 0;
+constexpr int kTicketRouterTables = 1;
+constexpr int kTicketEpoch = 8;
+constexpr int kTicketError = 15;
+constexpr int kFusedMaxGrid = 1024;
+constexpr size_t kFusedLogitWords = 4 * 256;
+constexpr size_t kFusedActWords = (4 * 8 + 4) * 512;
+constexpr size_t kFusedGateWords = 4;
+
+// Regions sized by I or H come last: fk_moe_router and fk_moe_align lay the
+// workspace out with I = H = 0 and must find the routing tables where
+// fk_moe_experts and fk_moe_layer do.
 static size_t moe_ws_layout(int T, int K, int E, int I, int H, char* base, MoeWs* ws) {
   const size_t P = (size_t)T * K;
   size_t off = 0;
@@ -60,6 +80,10 @@ static size_t moe_ws_layout(int T, int K, int E, int I, int H, char* base, MoeWs
     return base ? base + at : nullptr;
   };
   ws->tickets = reinterpret_cast<uint32_t*>(take(16 * sizeof(uint32_t)));
+  ws->f_logits = reinterpret_cast<uint64_t*>(take(kFusedLogitWords * 8));
+  ws->f_act = reinterpret_cast<uint64_t*>(take(kFusedActWords * 8));
+  ws->f_sgate = reinterpret_cast<uint64_t*>(take(kFusedGateWords * 8));
+  ws->f_started = reinterpret_cast<uint64_t*>(take((size_t)kFusedMaxGrid * 8));
   ws->counts = reinterpret_cast<int32_t*>(take((size_t)E * 4));
   ws->offsets = reinterpret_cast<int32_t*>(take((size_t)(E + 1) * 4));
   ws->perm = reinterpret_cast<int32_t*>(take(P * 4));
@@ -205,78 +229,86 @@ struct RouterArgs {
   MoeWs ws;
 };
 
-// Softmax + top-k of one token by one wavefront.  Lane l owns experts
-// l + 64 j; each lane keeps its best remaining candidate (its "head": highest
-// probability, lowest id on ties) and every round takes the wave maximum of
-// the heads, breaking probability ties toward the lowest expert id.  Weights
-// are renormalised by the sum of the selected probabilities in selection
-// order.
+// Softmax + top-k over logits held in registers (lane l holds experts
+// l + 64 j; -inf where l + 64 j >= E).  Each candidate becomes one 64-bit key
+// (probability bits << 32 | ~expert id): probabilities are non-negative, so
+// key order is probability order with ties going to the lower expert id,
+// and one wave-wide u64 max per round selects the next expert.  Lane k < K
+// ends with the k-th selection; weights are renormalised by the sum of the
+// selected probabilities in selection order.
 template <int NJE>
-__device__ void router_topk_token(const RouterArgs& a, int t, int lane) {
-  float p[NJE];
+__device__ void topk_select_regs(float (&p)[NJE], int E, int K, int lane, int& out_id, float& out_w) {
   float m = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < NJE; ++j) {
-    const int ex = lane + kWave * j;
-    p[j] = ex < a.E ? load_coherent(a.logits + (size_t)t * a.E + ex) : -INFINITY;
-    m = fmaxf(m, p[j]);
-  }
+  for (int j = 0; j < NJE; ++j) m = fmaxf(m, p[j]);
   m = wave_max(m);
   float s = 0.f;
 #pragma unroll
   for (int j = 0; j < NJE; ++j) {
     const int ex = lane + kWave * j;
-    p[j] = ex < a.E ? expf(p[j] - m) : 0.f;
+    p[j] = ex < E ? expf(p[j] - m) : 0.f;
     s += p[j];
   }
   s = wave_sum(s);
+  uint64_t key[NJE];
+  uint64_t head = 0;
 #pragma unroll
-  for (int j = 0; j < NJE; ++j) p[j] = lane + kWave * j < a.E ? p[j] / s : -1.f;  // -1: no expert
-
-  uint32_t taken = 0;
-  float hv = -1.f;
-  int hj = 0;
-  auto refresh_head = [&]() {
-    hv = -1.f;
-    hj = 0;
-#pragma unroll
-    for (int j = 0; j < NJE; ++j)
-      if (!((taken >> j) & 1u) && p[j] > hv) {
-        hv = p[j];
-        hj = j;
-      }
-  };
-  refresh_head();
+  for (int j = 0; j < NJE; ++j) {
+    const int ex = lane + kWave * j;
+    key[j] = ex < E ? ((uint64_t)__float_as_uint(p[j] / s) << 32) | (uint32_t)~ex : 0ull;
+    head = max_u64(head, key[j]);
+  }
   float denom = 0.f;
   int my_id = 0;
   float my_v = 0.f;
-  for (int k = 0; k < a.K; ++k) {
-    const float mv = wave_max(hv);
-    const unsigned long long tied = __ballot(hv == mv);
-    int sel_lane;
-    if (__popcll(tied) == 1) {
-      sel_lane = __ffsll(tied) - 1;
-    } else {
-      const int cand = hv == mv ? lane + kWave * hj : 0x7fffffff;
-      sel_lane = wave_min_i32(cand) & (kWave - 1);
+  for (int k = 0; k < K; ++k) {
+    const uint64_t mk = wave_max_u64(head);
+    if (head == mk) {  // the owning lane retires the key and refreshes its head
+      head = 0;
+#pragma unroll
+      for (int j = 0; j < NJE; ++j) {
+        key[j] = key[j] == mk ? 0ull : key[j];
+        head = max_u64(head, key[j]);
+      }
     }
-    const int sel = __shfl(lane + kWave * hj, sel_lane, kWave);
-    if (lane == sel_lane) {
-      taken |= 1u << hj;
-      refresh_head();
-    }
+    const float mv = __uint_as_float((uint32_t)(mk >> 32));
     denom += mv;
     if (lane == k) {
-      my_id = sel;
+      my_id = (int)~(uint32_t)mk;
       my_v = mv;
     }
   }
+  out_id = my_id;
+  out_w = my_v / denom;
+}
+
+template <int NJE>
+__device__ void topk_select(const float* row, int E, int K, int lane, int& out_id, float& out_w) {
+  float p[NJE];
+#pragma unroll
+  for (int j = 0; j < NJE; ++j) {
+    const int ex = lane + kWave * j;
+    p[j] = ex < E ? load_coherent(row + ex) : -INFINITY;
+  }
+  topk_select_regs<NJE>(p, E, K, lane, out_id, out_w);
+}
+
+// Softmax + top-k of one token by one wavefront: lane k < K ends with the
+// k-th selection.  Lane l owns experts l + 64 j; each lane keeps its best
+// remaining candidate ("head": highest probability, lowest id on ties) and
+// every round takes the wave maximum of the heads, breaking probability ties
+// toward the lowest expert id.  Weights are renormalised by the sum of the
+// selected probabilities in selection order.
+template <int NJE>
+__device__ void router_topk_token(const RouterArgs& a, int t, int lane) {
+  int id;
+  float w;
+  topk_select<NJE>(a.logits + (size_t)t * a.E, a.E, a.K, lane, id, w);
   if (lane < a.K) {
     const size_t o = (size_t)t * a.K + lane;
-    const float w = my_v / denom;
-    a.ids_out[o] = my_id;
+    a.ids_out[o] = id;
     a.w_out[o] = w;
-    store_coherent(a.ws.ids32 + o, my_id);
+    store_coherent(a.ws.ids32 + o, id);
     a.ws.wts[o] = w;
   }
 }
@@ -372,7 +404,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(RouterArgs a) {
   const uint32_t G = gridDim.x * gridDim.y;
   publish_wait();
   __syncthreads();
-  if (threadIdx.x == 0) grid_arrive_and_wait(&a.ws.tickets[0], G, &a.ws.tickets[15]);
+  if (threadIdx.x == 0) grid_arrive_and_wait(&a.ws.tickets[kTicketRouterBarrier], G, &a.ws.tickets[kTicketError]);
   __syncthreads();
 
   const int gw = (blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave;
@@ -380,7 +412,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(RouterArgs a) {
 
   publish_wait();
   __syncthreads();
-  if (threadIdx.x == 0) s_last = ticket_add(&a.ws.tickets[1]) == G - 1;
+  if (threadIdx.x == 0) s_last = ticket_add(&a.ws.tickets[kTicketRouterTables]) == G - 1;
   __syncthreads();
   if (!s_last) return;
   const int P = a.T * a.K;
@@ -389,8 +421,8 @@ __global__ __launch_bounds__(256) void moe_router_kernel(RouterArgs a) {
   build_routing_tables(s_ids, P, a.E, a.ws, s_cnt, s_off, s_rank, s_wcnt);
   if (threadIdx.x == 0) {
     // Every workgroup has passed the barrier (it counted into ticket 1).
-    a.ws.tickets[0] = 0u;
-    a.ws.tickets[1] = 0u;
+    a.ws.tickets[kTicketRouterBarrier] = 0u;
+    a.ws.tickets[kTicketRouterTables] = 0u;
   }
 }
 
@@ -640,6 +672,481 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(ExpertArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Single-launch MoE layer for small batches (T <= 4, H <= 2048, I <= 512,
+// E <= 256, bf16 router and expert weights, shared expert present).
+//
+// 512-thread workgroups, one per CU (grid capped at the co-resident
+// capacity).  Item q of every phase goes to wavefront (q / G) of workgroup
+// (q % G), so consecutive items land on different CUs.
+//   P1  router logits (one expert row per item) and, overlapped, the shared
+//       expert's gate/up + SwiGLU (one intermediate per item) and its gate;
+//       each wavefront then prefetches its shared down row
+//   P2  every workgroup polls the logits of every token, computes the top-k
+//       (one wavefront per token) and the routing tables in LDS
+//   P3  routed gate/up + SwiGLU (one expert intermediate = 2 rows per item);
+//       each wavefront first prefetches its down row of every routed expert
+//       (U <= 16), so down weights stream concurrently with gate/up
+//   P4  every workgroup polls all activations into LDS; down: one output row
+//       per item, per-pair dots, then out[t] = sum_k w[t,k] y[pos(t,k)] +
+//       g_t y[shared t] (slot order, as the multi-launch combine) and
+//       layer_out = x + out.
+// Arithmetic order matches the multi-launch kernels, so both paths give
+// bitwise-identical results.
+//
+// Hand-offs carry a launch tag instead of using barriers: every value that
+// crosses workgroups (logits, activations, shared gates) is written as a
+// tagged word (store_tagged) and polled until it carries this launch's tag,
+// so a consumer waits only for the values it reads.  The tag is
+// epoch + 1, where the epoch is a workspace counter that every wavefront
+// reads at its start; each wavefront posts a started record with its tag,
+// and workgroup 0 advances the epoch once every record of this launch is
+// there (so no wavefront can read the advanced epoch in the same launch).
+// Tags are 32-bit: a word left untouched for exactly 2^32 launches on one
+// workspace would read as current.
+// ---------------------------------------------------------------------------
+constexpr int kFusedMaxTokens = 4;
+constexpr int kFusedMaxPairs = kFusedMaxTokens * 8;
+constexpr int kFusedWaves = 8;
+constexpr int kFusedMaxExperts = 256;
+constexpr int kFusedPrefetch = 16;
+constexpr int kFusedStage = 12;  // tagged loads in flight per thread while staging activations
+constexpr int kFusedChunk = 16;  // routed items per workgroup block: 16 tagged words = one 128-byte line
+static_assert(kFusedLogitWords >= (size_t)kFusedMaxTokens * kFusedMaxExperts, "fused logit region too small");
+static_assert(kFusedActWords >= (size_t)(kFusedMaxPairs + kFusedMaxTokens) * 512, "fused activation region too small");
+static_assert(kFusedGateWords >= (size_t)kFusedMaxTokens, "fused gate region too small");
+
+struct FusedArgs {
+  RouterArgs r;
+  const void* gu;
+  const void* dn;
+  const void* sgu;
+  const void* sdn;
+  const void* sg;
+  int sg_dt;
+  int I;
+  float* out;
+  float* layer_out;
+};
+
+// Gate row i and up row I+i of one expert (bf16, H <= 2048: 4 chunks per
+// lane) against the tokens toks[0..npairs) (token p when toks is NULL);
+// lane 0 writes silu(g)*u of the p-th token to out[p * kFusedChunk].
+template <bool BFX>
+__device__ __forceinline__ void fused_gateup_item(const Raw8<true> (&wg)[4], const Raw8<true> (&wu)[4], const void* x,
+                                                  int H, int lane, int npairs, const int* toks, float* out) {
+  const int nch = H >> 3;
+  for (int pp = 0; pp < npairs; ++pp) {
+    const int t = toks ? toks[pp] : pp;
+    float g = 0.f, u = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = lane + kWave * j;
+      if (c < nch) {
+        float x8[8], a8[8], b8[8];
+        load8_f32<BFX>(x, (size_t)t * H + (size_t)c * 8, x8);
+        raw8_to_f32<true>(wg[j], a8);
+        raw8_to_f32<true>(wu[j], b8);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          g = fmaf(a8[q], x8[q], g);
+          u = fmaf(b8[q], x8[q], u);
+        }
+      }
+    }
+    g = wave_sum(g);
+    u = wave_sum(u);
+    if (lane == 0) out[pp * kFusedChunk] = silu(g) * u;
+  }
+}
+
+// Down-row chunk (8 bf16) of this lane against the activation row staged in LDS.
+__device__ __forceinline__ float dot8_act_lds(const Raw8<true>& w, const float* act_row, int lane, int I) {
+  float d = 0.f;
+  if (lane * 8 < I) {
+    float w8[8], a8[8];
+    raw8_to_f32<true>(w, w8);
+    const float4* p = reinterpret_cast<const float4*>(act_row + lane * 8);
+    const float4 lo = p[0], hi = p[1];
+    a8[0] = lo.x; a8[1] = lo.y; a8[2] = lo.z; a8[3] = lo.w;
+    a8[4] = hi.x; a8[5] = hi.y; a8[6] = hi.z; a8[7] = hi.w;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) d = fmaf(w8[q], a8[q], d);
+  }
+  return d;
+}
+
+template <bool BFX>
+__global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
+  __shared__ __align__(16) int s_ids[kFusedMaxPairs];
+  __shared__ float s_w[kFusedMaxPairs];
+  __shared__ int s_pos[kFusedMaxPairs];         // pair t*K+k -> permuted position
+  __shared__ int s_tok[kFusedMaxPairs];         // permuted position -> token
+  __shared__ int s_active[kFusedMaxPairs];      // routed experts, ascending
+  __shared__ int s_aoff[kFusedMaxPairs + 1];    // first permuted position of each (P at U)
+  __shared__ int s_nact;
+  __shared__ int s_fail;
+  __shared__ uint32_t s_wtag[kFusedWaves];
+  __shared__ float s_chunk[kFusedMaxTokens][kFusedChunk];
+  __shared__ float s_y[kFusedWaves][kFusedMaxPairs + kFusedMaxTokens];
+  extern __shared__ float4 s_act_v[];  // [(P + T) * I] activations, then [T] shared gates
+  float* s_act = reinterpret_cast<float*>(s_act_v);
+  const RouterArgs& a = f.r;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = gridDim.x, b = blockIdx.x;
+  const int NW = G * kFusedWaves;
+  const int q0 = wave * G + b;
+  const int T = a.T, H = a.H, E = a.E, K = a.K, I = f.I, P = T * K;
+  const int nch = H >> 3;
+  uint32_t* err = &a.ws.tickets[kTicketError];
+  const uint32_t tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
+  if (tid == 0) s_fail = 0;
+  __syncthreads();
+
+  // ---------------- P1: router rows, shared gate/up, shared gate -----------
+  // Units of 8 items, one per wavefront: router rows 8u.. (u < nrb), shared
+  // intermediates 8(u - nrb).. (u < nrb + nsb), then the shared gate.  A
+  // unit's results go through LDS and leave as contiguous tagged runs.
+  const int nrb = (E + 7) / 8, nsb = I / 8, nunits = nrb + nsb + 1;
+  for (int unit = b; unit < nunits; unit += G) {
+    if (unit < nrb) {
+      const int e = unit * 8 + wave;
+      float mine = 0.f;
+      if (e < E) {
+        float wn[4][8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = lane + kWave * j;
+          if (c < nch) {
+            float w8[8], n8[8];
+            load8_f32<true>(a.W, (size_t)e * H + (size_t)c * 8, w8);
+            load8_any(a.nw, a.nw_dt, (size_t)c * 8, n8);
+#pragma unroll
+            for (int qq = 0; qq < 8; ++qq) wn[j][qq] = w8[qq] * (a.off + n8[qq]);
+          } else {
+#pragma unroll
+            for (int qq = 0; qq < 8; ++qq) wn[j][qq] = 0.f;
+          }
+        }
+        const float bias = a.bias ? load_scalar(a.bias, a.bias_dt, e) : 0.f;
+        constexpr int TB = 4;
+        for (int t0 = 0; t0 < T; t0 += TB) {
+          float ss[TB], d[TB];
+#pragma unroll
+          for (int tt = 0; tt < TB; ++tt) {
+            ss[tt] = 0.f;
+            d[tt] = 0.f;
+            const int t = t0 + tt;
+            if (t < T) {
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const int c = lane + kWave * j;
+                if (c < nch) {
+                  float x8[8];
+                  load8_f32<BFX>(a.x, (size_t)t * H + (size_t)c * 8, x8);
+#pragma unroll
+                  for (int qq = 0; qq < 8; ++qq) {
+                    ss[tt] = fmaf(x8[qq], x8[qq], ss[tt]);
+                    d[tt] = fmaf(x8[qq], wn[j][qq], d[tt]);
+                  }
+                }
+              }
+            }
+          }
+#pragma unroll
+          for (int tt = 0; tt < TB; ++tt) {
+            ss[tt] = wave_sum(ss[tt]);
+            d[tt] = wave_sum(d[tt]);
+          }
+#pragma unroll
+          for (int tt = 0; tt < TB; ++tt) {
+            const int t = t0 + tt;
+            if (t < T) mine = lane == t ? d[tt] * rsqrtf(ss[tt] / (float)H + a.eps) + bias : mine;
+          }
+        }
+      }
+      if (lane < T) s_chunk[lane][wave] = mine;
+    } else if (unit < nrb + nsb) {
+      const int i = (unit - nrb) * 8 + wave;
+      Raw8<true> wg[4], wu[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = lane + kWave * j;
+        if (c < nch) {
+          wg[j] = load_raw8_stream<true>(f.sgu, (size_t)i * H + (size_t)c * 8);
+          wu[j] = load_raw8_stream<true>(f.sgu, (size_t)(I + i) * H + (size_t)c * 8);
+        }
+      }
+      fused_gateup_item<BFX>(wg, wu, a.x, H, lane, T, nullptr, &s_chunk[0][wave]);
+    } else if (wave == 0) {
+      // Shared-expert gate of every token: one row like the router's.
+      float g8[4][8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = lane + kWave * j;
+        if (f.sg && c < nch) {
+          load8_any(f.sg, f.sg_dt, (size_t)c * 8, g8[j]);
+        } else {
+#pragma unroll
+          for (int qq = 0; qq < 8; ++qq) g8[j][qq] = 0.f;
+        }
+      }
+      for (int t = 0; t < T; ++t) {
+        float d = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = lane + kWave * j;
+          if (c < nch) {
+            float x8[8];
+            load8_f32<BFX>(a.x, (size_t)t * H + (size_t)c * 8, x8);
+#pragma unroll
+            for (int qq = 0; qq < 8; ++qq) d = fmaf(x8[qq], g8[j][qq], d);
+          }
+        }
+        d = wave_sum(d);
+        if (lane == 0) s_chunk[t][0] = f.sg ? sigmoid(d) : 1.f;
+      }
+    }
+    __syncthreads();
+    if (tid < 8 * T) {
+      const int t = tid >> 3, l = tid & 7;
+      const float v = s_chunk[t][l];
+      if (unit < nrb) {
+        const int e = unit * 8 + l;
+        if (e < E) {
+          a.logits[(size_t)t * E + e] = v;
+          store_tagged(a.ws.f_logits + (size_t)t * E + e, v, tag);
+        }
+      } else if (unit < nrb + nsb) {
+        store_tagged(a.ws.f_act + (size_t)(P + t) * I + (unit - nrb) * 8 + l, v, tag);
+      } else if (l == 0) {
+        store_tagged(a.ws.f_sgate + t, v, tag);
+      }
+    }
+    __syncthreads();
+  }
+  // Started record of this workgroup: every wavefront has used the epoch it
+  // read (its LDS write needs the loaded value), so the epoch may advance
+  // once all records of this launch are there.
+  if (lane == 0) s_wtag[wave] = tag;
+  __syncthreads();
+  if (tid == 0) store_tagged(a.ws.f_started + b, __uint_as_float(s_wtag[kFusedWaves - 1]), tag);
+  // This wavefront's first down row (shared expert part) and residual inputs,
+  // fetched early.
+  const int r_first = q0;
+  Raw8<true> sdr;
+  if (r_first < H && lane * 8 < I) sdr = load_raw8_stream<true>(f.sdn, (size_t)r_first * I + (size_t)lane * 8);
+  float x_first = 0.f;
+  if (f.layer_out && r_first < H && lane < T)
+    x_first = load_scalar(a.x, BFX ? FK_DTYPE_BF16 : FK_DTYPE_F32, (size_t)lane * H + r_first);
+
+  // ---------------- P2: top-k of every token, routing tables in LDS --------
+  if (wave < T) {
+    constexpr int NJE = kFusedMaxExperts / kWave;
+    const int t = wave;
+    uint64_t w[NJE];
+    const uint64_t* srcs[NJE];
+#pragma unroll
+    for (int j = 0; j < NJE; ++j) {
+      const int ex = lane + kWave * j;
+      srcs[j] = ex < E ? a.ws.f_logits + (size_t)t * E + ex : nullptr;
+      w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+    }
+    if (!poll_tagged<NJE>(w, srcs, tag)) s_fail = 1;
+    float p[NJE];
+#pragma unroll
+    for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
+    int id;
+    float wt;
+    topk_select_regs<NJE>(p, E, K, lane, id, wt);
+    if (lane < K) {
+      s_ids[t * K + lane] = id;
+      s_w[t * K + lane] = wt;
+    }
+  } else if (b == 0 && wave >= kFusedMaxTokens) {
+    // Workgroup 0 checks that every wavefront of this launch has read the
+    // epoch (its started record carries the tag) before advancing it.
+    constexpr int kChunk = 4;
+    const int nthr = (kFusedWaves - kFusedMaxTokens) * kWave;
+    for (int base = tid - kFusedMaxTokens * kWave; base < G; base += kChunk * nthr) {
+      uint64_t w[kChunk];
+      const uint64_t* srcs[kChunk];
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j) {
+        const int r = base + j * nthr;
+        srcs[j] = r < G ? a.ws.f_started + r : nullptr;
+        w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+      }
+      if (!poll_tagged<kChunk>(w, srcs, tag)) s_fail = 1;
+    }
+  }
+  __syncthreads();
+  if (b == 0 && tid == 0) store_coherent(&a.ws.tickets[kTicketEpoch], tag);
+  if (wave == 0) {
+    // Routing tables from the P <= 32 pair ids, one pair per lane.  Pair l
+    // goes to permuted position rank_l = #{m : id_m < id_l or (id_m == id_l
+    // and m < l)} (stable); it heads its expert's run when no earlier pair
+    // has its id, and the run's index among the routed experts is the number
+    // of distinct smaller ids.
+    const int id = lane < P ? s_ids[lane] : 0x7fffffff;
+    int rank = 0, dups = 0;
+    uint32_t smaller = 0;  // bit m: id_m < id
+    for (int m0 = 0; m0 < P; m0 += 4) {
+      const int4 v4 = *reinterpret_cast<const int4*>(s_ids + m0);  // LDS broadcast
+      const int vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        const int m = m0 + qq;
+        if (m < P) {
+          rank += (vv[qq] < id) | ((vv[qq] == id) & (m < lane));
+          dups += (vv[qq] == id) & (m < lane);
+          smaller |= (uint32_t)(vv[qq] < id) << m;
+        }
+      }
+    }
+    const bool head = lane < P && dups == 0;
+    const uint64_t heads = __ballot(head);
+    const int u = __popc(smaller & (uint32_t)heads);
+    if (lane < P) {
+      s_pos[lane] = rank;
+      s_tok[rank] = lane / K;
+    }
+    if (head) {
+      s_active[u] = id;
+      s_aoff[u] = rank;
+    }
+    if (lane == 0) {
+      const int nu = __popcll(heads);
+      s_nact = nu;
+      s_aoff[nu] = P;
+    }
+  }
+  __syncthreads();
+  const int U = s_nact;
+  if (b == 0) {
+    for (int j = tid; j < P; j += 512) {
+      a.ids_out[j] = s_ids[j];
+      a.w_out[j] = s_w[j];
+    }
+  }
+
+  // ---------------- P3: routed gate/up (+ down-row prefetch) ---------------
+  const bool prefetch = U <= kFusedPrefetch && r_first < H && lane * 8 < I;
+  Raw8<true> dr[kFusedPrefetch];
+  if (prefetch) {
+#pragma unroll
+    for (int u = 0; u < kFusedPrefetch; ++u)
+      if (u < U)
+        dr[u] = load_raw8_stream<true>(f.dn, ((size_t)s_active[u] * H + r_first) * I + (size_t)lane * 8);
+  }
+  // Blocks of kFusedChunk consecutive intermediates of one expert per
+  // workgroup, two per wavefront; each block leaves as one 128-byte line per
+  // routed token.
+  const int bpe = I / kFusedChunk, nblk = U * bpe;
+  for (int blk = b; blk < nblk; blk += G) {
+    const int u = blk / bpe, i0 = (blk - u * bpe) * kFusedChunk;
+    const int e = s_active[u], pa = s_aoff[u], np = s_aoff[u + 1] - pa;
+    const int ia = i0 + 2 * wave;
+    const char* we = reinterpret_cast<const char*>(f.gu) + (size_t)e * 2 * I * H * 2;
+    Raw8<true> ga[4], ua8[4], gb[4], ub8[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = lane + kWave * j;
+      if (c < nch) {
+        ga[j] = load_raw8_stream<true>(we, (size_t)ia * H + (size_t)c * 8);
+        gb[j] = load_raw8_stream<true>(we, (size_t)(ia + 1) * H + (size_t)c * 8);
+        ua8[j] = load_raw8_stream<true>(we, (size_t)(I + ia) * H + (size_t)c * 8);
+        ub8[j] = load_raw8_stream<true>(we, (size_t)(I + ia + 1) * H + (size_t)c * 8);
+      }
+    }
+    fused_gateup_item<BFX>(ga, ua8, a.x, H, lane, np, s_tok + pa, &s_chunk[0][2 * wave]);
+    fused_gateup_item<BFX>(gb, ub8, a.x, H, lane, np, s_tok + pa, &s_chunk[0][2 * wave + 1]);
+    __syncthreads();
+    if (tid < kFusedChunk * np) {
+      const int pp = tid / kFusedChunk, l = tid % kFusedChunk;
+      store_tagged(a.ws.f_act + (size_t)(pa + pp) * I + i0 + l, s_chunk[pp][l], tag);
+    }
+    __syncthreads();
+  }
+
+  // ---------------- P4: stage activations, down rows, combine --------------
+  // Every workgroup polls all activations (and the shared gates) into LDS,
+  // kFusedStage tagged loads in flight per thread.
+  const int n_act = (P + T) * I, n_stage = n_act + T;
+  bool stage_ok = true;
+  for (int base = tid; base < n_stage; base += 512 * kFusedStage) {
+    uint64_t w[kFusedStage];
+    const uint64_t* srcs[kFusedStage];
+#pragma unroll
+    for (int j = 0; j < kFusedStage; ++j) {
+      const int idx = base + j * 512;
+      srcs[j] = idx < n_act ? a.ws.f_act + idx : idx < n_stage ? a.ws.f_sgate + (idx - n_act) : nullptr;
+      w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+    }
+    stage_ok = poll_tagged<kFusedStage>(w, srcs, tag) && stage_ok;
+#pragma unroll
+    for (int j = 0; j < kFusedStage; ++j)
+      if (srcs[j]) s_act[base + j * 512] = value_of(w[j]);
+  }
+  if (!stage_ok) s_fail = 1;
+  __syncthreads();
+  if (tid == 0 && s_fail) __hip_atomic_fetch_or(err, FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  float* y = s_y[wave];
+  const float* s_sg = s_act + n_act;
+  for (int r = q0; r < H; r += NW) {
+    const bool first = r == r_first;
+    // shared expert
+    {
+      Raw8<true> w;
+      if (first) w = sdr;
+      else if (lane * 8 < I) w = load_raw8_stream<true>(f.sdn, (size_t)r * I + (size_t)lane * 8);
+      for (int t = 0; t < T; ++t) {
+        const float d = wave_sum(dot8_act_lds(w, s_act + (size_t)(P + t) * I, lane, I));
+        if (lane == 0) y[P + t] = d;
+      }
+    }
+    if (first && prefetch) {
+#pragma unroll
+      for (int u = 0; u < kFusedPrefetch; ++u) {
+        if (u < U) {
+          for (int pos = s_aoff[u]; pos < s_aoff[u + 1]; ++pos) {
+            const float d = wave_sum(dot8_act_lds(dr[u], s_act + (size_t)pos * I, lane, I));
+            if (lane == 0) y[pos] = d;
+          }
+        }
+      }
+    } else {
+      for (int u0 = 0; u0 < U; u0 += 8) {
+        Raw8<true> wb8[8];
+#pragma unroll
+        for (int v = 0; v < 8; ++v)
+          if (u0 + v < U && lane * 8 < I)
+            wb8[v] = load_raw8_stream<true>(f.dn, ((size_t)s_active[u0 + v] * H + r) * I + (size_t)lane * 8);
+#pragma unroll
+        for (int v = 0; v < 8; ++v) {
+          if (u0 + v < U) {
+            for (int pos = s_aoff[u0 + v]; pos < s_aoff[u0 + v + 1]; ++pos) {
+              const float d = wave_sum(dot8_act_lds(wb8[v], s_act + (size_t)pos * I, lane, I));
+              if (lane == 0) y[pos] = d;
+            }
+          }
+        }
+      }
+    }
+    if (lane < T) {
+      const int t = lane;
+      float acc = 0.f;
+      for (int k = 0; k < K; ++k) acc += s_w[t * K + k] * y[s_pos[t * K + k]];
+      acc += s_sg[t] * y[P + t];
+      const size_t o = (size_t)t * H + r;
+      f.out[o] = acc;
+      if (f.layer_out)
+        f.layer_out[o] = (first ? x_first : load_scalar(a.x, BFX ? FK_DTYPE_BF16 : FK_DTYPE_F32, o)) + acc;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
 static int check_ws(void* ws, size_t bytes, int T, int K, int E, int I, int H, MoeWs* out) {
@@ -672,6 +1179,48 @@ static int resident_capacity(K kernel, int block, size_t shm, int* cache) {
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, shm) != hipSuccess) return 0;
   cache[dev] = cus * per_cu;
   return cache[dev];
+}
+
+static int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
+static bool fused_eligible(int T, int H, int I, int E, int K, int router_dt, int expert_dt, bool has_shared) {
+  return T >= 1 && T <= kFusedMaxTokens && H <= 2048 && I <= 512 && I % kFusedChunk == 0 && E <= kFusedMaxExperts && K <= 8 &&
+         router_dt == FK_DTYPE_BF16 && expert_dt == FK_DTYPE_BF16 && has_shared;
+}
+
+constexpr size_t kFusedMaxDynLds = ((size_t)(kFusedMaxPairs + kFusedMaxTokens) * 512 + kFusedMaxTokens) * sizeof(float);
+
+template <bool BX>
+static int launch_fused_t(const FusedArgs& fa, hipStream_t stream) {
+  static int cap_cache[64] = {0};
+  static bool attr_set[64] = {false};
+  auto kernel = moe_fused_kernel<BX>;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(FK_ERR_LAUNCH, "no current HIP device");
+  if (!attr_set[dev]) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)kFusedMaxDynLds) != hipSuccess)
+      return fail(FK_ERR_LAUNCH, "cannot reserve %zu bytes of LDS for the fused MoE kernel", kFusedMaxDynLds);
+    attr_set[dev] = true;
+  }
+  const size_t shm = ((size_t)(fa.r.T * fa.r.K + fa.r.T) * fa.I + fa.r.T) * sizeof(float);
+  const int cap = resident_capacity(kernel, 512, kFusedMaxDynLds, cap_cache);
+  const int cus = device_cus();
+  const int G = cap < cus ? cap : cus;  // one workgroup per CU
+  if (G < 1) return fail(FK_ERR_UNSUPPORTED, "fused MoE kernel does not fit on this device");
+  if (G > kFusedMaxGrid) return fail(FK_ERR_UNSUPPORTED, "fused MoE grid %d exceeds %d workgroups", G, kFusedMaxGrid);
+  hipLaunchKernelGGL(kernel, dim3(G), dim3(512), shm, stream, fa);
+  return check_launch("moe_fused_kernel");
 }
 
 template <bool BW, bool BX, int NJ, int NJE>
@@ -890,6 +1439,43 @@ int fk_moe_layer(const void* hidden, int hidden_dtype, const void* norm_weight, 
   MoeWs ws;
   st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, intermediate, hidden_size, &ws);
   if (st) return st;
+  if (fused_eligible(tokens, hidden_size, intermediate, num_experts, top_k, router_dtype, expert_dtype,
+                     shared_gate_up != nullptr)) {
+    if (!is_float_dtype(norm_dtype) || (router_bias && !is_float_dtype(bias_dtype)))
+      return fail(FK_ERR_DTYPE, "router inputs must be f32 or bf16");
+    if (!norm_weight || !router_weight || !logits || !topk_ids || !topk_weights)
+      return fail(FK_ERR_INVALID, "router pointers must be non-NULL");
+    if (!aligned16(norm_weight) || !aligned16(router_weight))
+      return fail(FK_ERR_ALIGNMENT, "norm_weight and router_weight must be 16-byte aligned");
+    FusedArgs fa;
+    fa.r.x = hidden;
+    fa.r.nw = norm_weight;
+    fa.r.W = router_weight;
+    fa.r.bias = router_bias;
+    fa.r.nw_dt = norm_dtype;
+    fa.r.bias_dt = bias_dtype;
+    fa.r.T = tokens;
+    fa.r.H = hidden_size;
+    fa.r.E = num_experts;
+    fa.r.K = top_k;
+    fa.r.eps = eps;
+    fa.r.off = norm_offset;
+    fa.r.logits = logits;
+    fa.r.ids_out = topk_ids;
+    fa.r.w_out = topk_weights;
+    fa.r.ws = ws;
+    fa.gu = gate_up;
+    fa.dn = down;
+    fa.sgu = shared_gate_up;
+    fa.sdn = shared_down;
+    fa.sg = shared_gate;
+    fa.sg_dt = shared_gate_dtype;
+    fa.I = intermediate;
+    fa.out = moe_out;
+    fa.layer_out = layer_out;
+    if (hidden_dtype == FK_DTYPE_BF16) return launch_fused_t<true>(fa, as_stream(stream));
+    return launch_fused_t<false>(fa, as_stream(stream));
+  }
   st = fk_moe_router(hidden, hidden_dtype, norm_weight, norm_dtype, router_weight, router_dtype, router_bias,
                      bias_dtype, tokens, hidden_size, num_experts, top_k, eps, norm_offset, logits, topk_ids,
                      topk_weights, workspace, workspace_bytes, stream);

@@ -274,3 +274,41 @@ def test_moe_layer_fp32_hidden(device, real_cpu, real_gpu):
                                      real_cpu["shared_expert_gate_weight"])
     torch.testing.assert_close(moe.cpu(), ref, **tol(torch.bfloat16))
     torch.testing.assert_close(lh.cpu(), x + ref, **tol(torch.bfloat16))
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 3, 4, 16])
+def test_fused_layer_matches_multi_launch(device, real_gpu, tokens):
+    # fk_moe_layer takes the single-launch kernel for T <= 4; router +
+    # experts take the multi-launch path.  Same arithmetic order in both.
+    from fastkernels_amd.plan import MoeLayerPlan
+
+    plan = MoeLayerPlan(real_gpu, tokens)
+    plan.hidden.copy_(wl.make_hidden(tokens, H, seed=70 + tokens).to(device))
+    plan.run()
+    fused = [t.clone() for t in (plan.layer_out, plan.moe_out, plan.logits, plan.ids, plan.weights)]
+    plan.run_router()
+    plan.run_experts()
+    multi = (plan.layer_out, plan.moe_out, plan.logits, plan.ids, plan.weights)
+    torch.cuda.synchronize()
+    assert torch.equal(fused[3], multi[3])
+    for a, b in zip(fused, multi):
+        torch.testing.assert_close(a, b, atol=1e-6, rtol=1e-6)
+
+
+def test_fused_layer_repeated_calls_stay_consistent(device, real_gpu):
+    # tickets reset at the end of every launch: many back-to-back launches
+    # (rotating inputs) must keep giving the first call's answer.
+    from fastkernels_amd.plan import MoeLayerPlan
+
+    plan = MoeLayerPlan(real_gpu, 1)
+    xs = [wl.make_hidden(1, H, seed=80 + i).to(device) for i in range(3)]
+    ref = []
+    for x in xs:
+        plan.hidden.copy_(x)
+        plan.run()
+        ref.append(plan.layer_out.clone())
+    for _ in range(5):
+        for x, r in zip(xs, ref):
+            plan.hidden.copy_(x)
+            plan.run()
+            assert torch.equal(plan.layer_out, r)
