@@ -160,8 +160,11 @@ def main() -> int:
         fns = [p.run for p in plans]
         ms_layer = timed_graph(fns, steps, args.warmup)
         u = distinct(plans)
-        ms_experts = timed_graph([p.run_experts for p in plans], steps, 2)
+        # The router stage writes the routing tables that the expert stage
+        # reads (the single-launch layer keeps its tables in LDS), so it runs
+        # first.
         ms_router = timed_graph([p.run_router for p in plans], steps, 2)
+        ms_experts = timed_graph([p.run_experts for p in plans], steps, 2)
         per_step_u = [u[i % len(u)] for i in range(steps)]
         layer_bytes = sum(wl.moe_layer_bytes(tokens, x, spec) for x in per_step_u) / steps
         expert_bytes = sum(

@@ -140,15 +140,15 @@ __device__ __forceinline__ void load8_act(const float* base, size_t elem_index, 
 }
 
 // ---------------------------------------------------------------------------
-// Wavefront all-reductions (64 lanes) built from DPP lane permutes, one
-// ds_swizzle and v_permlane32_swap instead of six ds_bpermute round trips.
+// Wavefront all-reductions (64 lanes) built from DPP lane permutes and the
+// gfx950 row swaps (v_permlane16_swap, v_permlane32_swap): no LDS round trip.
 // Every lane ends with the full result; the combine order is fixed, so
 // results are bitwise reproducible run to run.
 //   step 1  quad_perm [1,0,3,2]    partner = lane ^ 1
 //   step 2  quad_perm [2,3,0,1]    partner = lane ^ 2
 //   step 3  row_half_mirror        partner = 7 - lane within 8 (other quad)
 //   step 4  row_mirror             partner = 15 - lane within 16 (other 8)
-//   step 5  ds_swizzle xor 16      partner = lane ^ 16
+//   step 5  v_permlane16_swap      partner = lane ^ 16
 //   step 6  v_permlane32_swap      partner = lane ^ 32
 // Steps 3 and 4 are not xor partners, but after steps 1-2 (resp. 1-3) all
 // lanes of the source group hold the same partial, so any lane of the other
@@ -158,15 +158,18 @@ constexpr int kDppQuadXor1 = 0xB1;
 constexpr int kDppQuadXor2 = 0x4E;
 constexpr int kDppRowHalfMirror = 0x141;
 constexpr int kDppRowMirror = 0x140;
-constexpr int kSwizzleXor16 = 0x401F;  // bit mode: and 0x1f, or 0, xor 0x10
 
 template <int CTRL>
 __device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
 }
 
+// Value held by lane ^ 16: v_permlane16_swap exchanges the odd rows of its
+// first operand with the even rows of its second, so with both operands v
+// the first result holds rows (0,0,2,2) and the second rows (1,1,3,3).
 __device__ __forceinline__ uint32_t xor16_u32(uint32_t v) {
-  return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, kSwizzleXor16);
+  auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return ((__lane_id() >> 4) & 1) ? (uint32_t)r[0] : (uint32_t)r[1];
 }
 
 // Value held by lane ^ 32.
@@ -306,6 +309,10 @@ __device__ __forceinline__ int wave_allreduce_i32(int v, Op op) {
 }
 __device__ __forceinline__ int wave_min_i32(int v) {
   return wave_allreduce_i32(v, [](int a, int b) { return a < b ? a : b; });
+}
+// Unsigned max (integer ops fold into the DPP moves; no float canonicalising).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  return (uint32_t)wave_allreduce_i32((int)v, [](int a, int b) { return (uint32_t)a > (uint32_t)b ? a : b; });
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }

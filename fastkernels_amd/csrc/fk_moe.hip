@@ -230,14 +230,73 @@ struct RouterArgs {
 };
 
 // Softmax + top-k over logits held in registers (lane l holds experts
-// l + 64 j; -inf where l + 64 j >= E).  Each candidate becomes one 64-bit key
-// (probability bits << 32 | ~expert id): probabilities are non-negative, so
-// key order is probability order with ties going to the lower expert id,
-// and one wave-wide u64 max per round selects the next expert.  Lane k < K
-// ends with the k-th selection; weights are renormalised by the sum of the
-// selected probabilities in selection order.
+// l + 64 j; -inf where l + 64 j >= E).  Candidate (p, j) of a lane becomes
+// the 32-bit key ((bits(p) + 1) << 2) | (3 - j): probabilities lie in [0, 1],
+// so bits(p) + 1 <= 0x3F800001 and the key fits; 0 marks "no expert" or
+// "taken".  Keys order by probability, then by lower j; two lanes can only
+// hold equal keys for equal p and j, and then the lower lane has the lower
+// expert id.  Each round takes the wave-wide maximum key and the lowest lane
+// holding it, so experts are taken in (probability desc, expert id asc)
+// order.  Each lane keeps its keys sorted, so giving up its head is a shift.
+// Lane k < K ends with the k-th selection; weights are renormalised by the
+// sum of the selected probabilities in selection order.
 template <int NJE>
-__device__ void topk_select_regs(float (&p)[NJE], int E, int K, int lane, int& out_id, float& out_w) {
+__device__ void topk_select_keys32(float (&p)[NJE], int E, int K, int lane, int& out_id, float& out_w) {
+  static_assert(NJE == 4, "keys carry j in two bits");
+  float m = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NJE; ++j) m = fmaxf(m, p[j]);
+  m = wave_max(m);
+  float s = 0.f;
+#pragma unroll
+  for (int j = 0; j < NJE; ++j) {
+    const int ex = lane + kWave * j;
+    p[j] = ex < E ? expf(p[j] - m) : 0.f;
+    s += p[j];
+  }
+  s = wave_sum(s);
+  uint32_t key[NJE];
+#pragma unroll
+  for (int j = 0; j < NJE; ++j)
+    key[j] = lane + kWave * j < E ? ((__float_as_uint(p[j] / s) + 1u) << 2) | (uint32_t)(NJE - 1 - j) : 0u;
+  // Sort the lane's keys descending (keys are distinct within a lane).
+  auto cswap = [](uint32_t& a, uint32_t& b) {
+    const uint32_t hi = a > b ? a : b, lo = a > b ? b : a;
+    a = hi;
+    b = lo;
+  };
+  cswap(key[0], key[1]);
+  cswap(key[2], key[3]);
+  cswap(key[0], key[2]);
+  cswap(key[1], key[3]);
+  cswap(key[1], key[2]);
+  float denom = 0.f;
+  int my_id = 0;
+  float my_v = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const uint32_t mk = wave_max_u32(key[0]);
+    const int sel_lane = __ffsll((unsigned long long)__ballot(key[0] == mk)) - 1;
+    const int sel = sel_lane + kWave * (int)(NJE - 1 - (mk & 3u));
+    const float mv = __uint_as_float((mk >> 2) - 1u);
+    const bool own = lane == sel_lane;
+    key[0] = own ? key[1] : key[0];
+    key[1] = own ? key[2] : key[1];
+    key[2] = own ? key[3] : key[2];
+    key[3] = own ? 0u : key[3];
+    denom += mv;
+    if (lane == k) {
+      my_id = sel;
+      my_v = mv;
+    }
+  }
+  out_id = my_id;
+  out_w = my_v / denom;
+}
+
+// Same selection with 64-bit keys (bits(p) << 32 | ~expert id), for lanes
+// holding more than 4 candidates (E > 256).
+template <int NJE>
+__device__ void topk_select_keys64(float (&p)[NJE], int E, int K, int lane, int& out_id, float& out_w) {
   float m = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NJE; ++j) m = fmaxf(m, p[j]);
@@ -263,7 +322,7 @@ __device__ void topk_select_regs(float (&p)[NJE], int E, int K, int lane, int& o
   float my_v = 0.f;
   for (int k = 0; k < K; ++k) {
     const uint64_t mk = wave_max_u64(head);
-    if (head == mk) {  // the owning lane retires the key and refreshes its head
+    if (head == mk) {
       head = 0;
 #pragma unroll
       for (int j = 0; j < NJE; ++j) {
@@ -280,6 +339,12 @@ __device__ void topk_select_regs(float (&p)[NJE], int E, int K, int lane, int& o
   }
   out_id = my_id;
   out_w = my_v / denom;
+}
+
+template <int NJE>
+__device__ void topk_select_regs(float (&p)[NJE], int E, int K, int lane, int& out_id, float& out_w) {
+  if constexpr (NJE == 4) topk_select_keys32<NJE>(p, E, K, lane, out_id, out_w);
+  else topk_select_keys64<NJE>(p, E, K, lane, out_id, out_w);
 }
 
 template <int NJE>
@@ -775,11 +840,49 @@ __device__ __forceinline__ float dot8_act_lds(const Raw8<true>& w, const float* 
   return d;
 }
 
-template <bool BFX>
+// Routing tables of P <= 32 (token, slot) pairs held one per lane of a
+// wavefront (pair l = t*K + k: expert id, routing weight).  Pair l goes to
+// permuted position rank_l = #{m : id_m < id_l or (id_m == id_l and m < l)}
+// (stable); it heads its expert's run when no earlier pair has its id, and
+// the run's index among the routed experts is the number of distinct
+// smaller ids.
+__device__ __forceinline__ void fused_tables(int id, float wt, int P, int K, int lane, int* s_tok, float* s_wpos,
+                                             int* s_active, int* s_aoff, int* s_nact) {
+  const int myid = lane < P ? id : 0x7fffffff;
+  int rank = 0, dups = 0;
+  uint32_t smaller = 0;  // bit m: id_m < id_l
+  for (int m = 0; m < P; ++m) {
+    const int v = __builtin_amdgcn_readlane(myid, m);
+    rank += (v < myid) | ((v == myid) & (m < lane));
+    dups += (v == myid) & (m < lane);
+    smaller |= (uint32_t)(v < myid) << m;
+  }
+  const bool head = lane < P && dups == 0;
+  const uint64_t heads = __ballot(head);
+  const int u = __popc(smaller & (uint32_t)heads);
+  if (lane < P) {
+    s_tok[rank] = lane / K;
+    s_wpos[rank] = wt;
+  }
+  if (head) {
+    s_active[u] = myid;
+    s_aoff[u] = rank;
+  }
+  if (lane == 0) {
+    const int nu = __popcll(heads);
+    *s_nact = nu;
+    s_aoff[nu] = P;
+  }
+}
+
+// ONE: compiled for a single token (T == 1): 8 prefetched down rows (one per
+// routed expert) and straight-line down code, which keeps the kernel within
+// the register budget of two workgroups' waves per SIMD.
+template <bool BFX, bool ONE>
 __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
+  constexpr int NPF = ONE ? 8 : kFusedPrefetch;
   __shared__ __align__(16) int s_ids[kFusedMaxPairs];
   __shared__ float s_w[kFusedMaxPairs];
-  __shared__ int s_pos[kFusedMaxPairs];         // pair t*K+k -> permuted position
   __shared__ int s_tok[kFusedMaxPairs];         // permuted position -> token
   __shared__ int s_active[kFusedMaxPairs];      // routed experts, ascending
   __shared__ int s_aoff[kFusedMaxPairs + 1];    // first permuted position of each (P at U)
@@ -787,7 +890,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   __shared__ int s_fail;
   __shared__ uint32_t s_wtag[kFusedWaves];
   __shared__ float s_chunk[kFusedMaxTokens][kFusedChunk];
-  __shared__ float s_y[kFusedWaves][kFusedMaxPairs + kFusedMaxTokens];
+  __shared__ float s_wpos[kFusedMaxPairs];      // permuted position -> routing weight
   extern __shared__ float4 s_act_v[];  // [(P + T) * I] activations, then [T] shared gates
   float* s_act = reinterpret_cast<float*>(s_act_v);
   const RouterArgs& a = f.r;
@@ -795,7 +898,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   const int G = gridDim.x, b = blockIdx.x;
   const int NW = G * kFusedWaves;
   const int q0 = wave * G + b;
-  const int T = a.T, H = a.H, E = a.E, K = a.K, I = f.I, P = T * K;
+  const int T = ONE ? 1 : a.T, H = a.H, E = a.E, K = a.K, I = f.I, P = T * K;
   const int nch = H >> 3;
   uint32_t* err = &a.ws.tickets[kTicketError];
   const uint32_t tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
@@ -854,8 +957,10 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
           }
 #pragma unroll
           for (int tt = 0; tt < TB; ++tt) {
-            ss[tt] = wave_sum(ss[tt]);
-            d[tt] = wave_sum(d[tt]);
+            if (t0 + tt < T) {
+              ss[tt] = wave_sum(ss[tt]);
+              d[tt] = wave_sum(d[tt]);
+            }
           }
 #pragma unroll
           for (int tt = 0; tt < TB; ++tt) {
@@ -940,6 +1045,8 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
     x_first = load_scalar(a.x, BFX ? FK_DTYPE_BF16 : FK_DTYPE_F32, (size_t)lane * H + r_first);
 
   // ---------------- P2: top-k of every token, routing tables in LDS --------
+  int tk_id = 0;
+  float tk_w = 0.f;
   if (wave < T) {
     constexpr int NJE = kFusedMaxExperts / kWave;
     const int t = wave;
@@ -955,12 +1062,10 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
     float p[NJE];
 #pragma unroll
     for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
-    int id;
-    float wt;
-    topk_select_regs<NJE>(p, E, K, lane, id, wt);
+    topk_select_regs<NJE>(p, E, K, lane, tk_id, tk_w);
     if (lane < K) {
-      s_ids[t * K + lane] = id;
-      s_w[t * K + lane] = wt;
+      s_ids[t * K + lane] = tk_id;
+      s_w[t * K + lane] = tk_w;
     }
   } else if (b == 0 && wave >= kFusedMaxTokens) {
     // Workgroup 0 checks that every wavefront of this launch has read the
@@ -979,48 +1084,18 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       if (!poll_tagged<kChunk>(w, srcs, tag)) s_fail = 1;
     }
   }
-  __syncthreads();
-  if (b == 0 && tid == 0) store_coherent(&a.ws.tickets[kTicketEpoch], tag);
-  if (wave == 0) {
-    // Routing tables from the P <= 32 pair ids, one pair per lane.  Pair l
-    // goes to permuted position rank_l = #{m : id_m < id_l or (id_m == id_l
-    // and m < l)} (stable); it heads its expert's run when no earlier pair
-    // has its id, and the run's index among the routed experts is the number
-    // of distinct smaller ids.
-    const int id = lane < P ? s_ids[lane] : 0x7fffffff;
-    int rank = 0, dups = 0;
-    uint32_t smaller = 0;  // bit m: id_m < id
-    for (int m0 = 0; m0 < P; m0 += 4) {
-      const int4 v4 = *reinterpret_cast<const int4*>(s_ids + m0);  // LDS broadcast
-      const int vv[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const int m = m0 + qq;
-        if (m < P) {
-          rank += (vv[qq] < id) | ((vv[qq] == id) & (m < lane));
-          dups += (vv[qq] == id) & (m < lane);
-          smaller |= (uint32_t)(vv[qq] < id) << m;
-        }
-      }
-    }
-    const bool head = lane < P && dups == 0;
-    const uint64_t heads = __ballot(head);
-    const int u = __popc(smaller & (uint32_t)heads);
-    if (lane < P) {
-      s_pos[lane] = rank;
-      s_tok[rank] = lane / K;
-    }
-    if (head) {
-      s_active[u] = id;
-      s_aoff[u] = rank;
-    }
-    if (lane == 0) {
-      const int nu = __popcll(heads);
-      s_nact = nu;
-      s_aoff[nu] = P;
-    }
+  if (ONE) {
+    // One token: the top-k wavefront already holds the K pairs in its lanes.
+    if (wave == 0) fused_tables(tk_id, tk_w, P, K, lane, s_tok, s_wpos, s_active, s_aoff, &s_nact);
+    __syncthreads();
+  } else {
+    __syncthreads();
+    if (wave == 0)
+      fused_tables(lane < P ? s_ids[lane] : 0, lane < P ? s_w[lane] : 0.f, P, K, lane, s_tok, s_wpos, s_active,
+                   s_aoff, &s_nact);
+    __syncthreads();
   }
-  __syncthreads();
+  if (b == 0 && tid == 0) store_coherent(&a.ws.tickets[kTicketEpoch], tag);
   const int U = s_nact;
   if (b == 0) {
     for (int j = tid; j < P; j += 512) {
@@ -1030,13 +1105,14 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   }
 
   // ---------------- P3: routed gate/up (+ down-row prefetch) ---------------
-  const bool prefetch = U <= kFusedPrefetch && r_first < H && lane * 8 < I;
-  Raw8<true> dr[kFusedPrefetch];
+  const bool prefetch = U <= NPF && r_first < H && lane * 8 < I;
+  Raw8<true> dr[NPF];
   if (prefetch) {
 #pragma unroll
-    for (int u = 0; u < kFusedPrefetch; ++u)
-      if (u < U)
-        dr[u] = load_raw8_stream<true>(f.dn, ((size_t)s_active[u] * H + r_first) * I + (size_t)lane * 8);
+    for (int u = 0; u < NPF; ++u) {
+      if (u < U) dr[u] = load_raw8_stream<true>(f.dn, ((size_t)s_active[u] * H + r_first) * I + (size_t)lane * 8);
+      else dr[u].a = u32x4{0, 0, 0, 0};
+    }
   }
   // Blocks of kFusedChunk consecutive intermediates of one expert per
   // workgroup, two per wavefront; each block leaves as one 128-byte line per
@@ -1091,30 +1167,51 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   __syncthreads();
   if (tid == 0 && s_fail) __hip_atomic_fetch_or(err, FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-  float* y = s_y[wave];
+  // Down rows: each lane accumulates, per token, the gate- and routing-
+  // weighted partial dots of every expert on its 8 columns; one wave sum per
+  // token gives out[t, r].
   const float* s_sg = s_act + n_act;
   for (int r = q0; r < H; r += NW) {
     const bool first = r == r_first;
-    // shared expert
+    if (ONE && first && prefetch) {
+      // One token, down rows prefetched: expert u sits at permuted position
+      // u; unused slots have zero rows and zero weight, so the code has no
+      // branches and every LDS read can be issued at once.
+      float acc = s_sg[0] * dot8_act_lds(sdr, s_act + (size_t)P * I, lane, I);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float wt = u < U ? s_wpos[u] : 0.f;
+        acc = fmaf(wt, dot8_act_lds(dr[u], s_act + (size_t)(u < U ? u : 0) * I, lane, I), acc);
+      }
+      const float o = wave_sum(acc);
+      if (lane == 0) {
+        f.out[r] = o;
+        if (f.layer_out) f.layer_out[r] = x_first + o;
+      }
+      continue;
+    }
+    float acc[kFusedMaxTokens];
     {
       Raw8<true> w;
       if (first) w = sdr;
       else if (lane * 8 < I) w = load_raw8_stream<true>(f.sdn, (size_t)r * I + (size_t)lane * 8);
-      for (int t = 0; t < T; ++t) {
-        const float d = wave_sum(dot8_act_lds(w, s_act + (size_t)(P + t) * I, lane, I));
-        if (lane == 0) y[P + t] = d;
-      }
-    }
-    if (first && prefetch) {
 #pragma unroll
-      for (int u = 0; u < kFusedPrefetch; ++u) {
-        if (u < U) {
-          for (int pos = s_aoff[u]; pos < s_aoff[u + 1]; ++pos) {
-            const float d = wave_sum(dot8_act_lds(dr[u], s_act + (size_t)pos * I, lane, I));
-            if (lane == 0) y[pos] = d;
-          }
-        }
+      for (int tt = 0; tt < kFusedMaxTokens; ++tt)
+        acc[tt] = tt < T ? s_sg[tt] * dot8_act_lds(w, s_act + (size_t)(P + tt) * I, lane, I) : 0.f;
+    }
+    auto add_expert = [&](const Raw8<true>& w, int u) {
+      for (int pos = s_aoff[u]; pos < s_aoff[u + 1]; ++pos) {
+        const float d = dot8_act_lds(w, s_act + (size_t)pos * I, lane, I);
+        const int t = s_tok[pos];
+        const float wt = s_wpos[pos];
+#pragma unroll
+        for (int tt = 0; tt < kFusedMaxTokens; ++tt) acc[tt] = tt == t ? fmaf(wt, d, acc[tt]) : acc[tt];
       }
+    };
+    if (!ONE && first && prefetch) {
+#pragma unroll
+      for (int u = 0; u < NPF; ++u)
+        if (u < U) add_expert(dr[u], u);
     } else {
       for (int u0 = 0; u0 < U; u0 += 8) {
         Raw8<true> wb8[8];
@@ -1123,25 +1220,21 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
           if (u0 + v < U && lane * 8 < I)
             wb8[v] = load_raw8_stream<true>(f.dn, ((size_t)s_active[u0 + v] * H + r) * I + (size_t)lane * 8);
 #pragma unroll
-        for (int v = 0; v < 8; ++v) {
-          if (u0 + v < U) {
-            for (int pos = s_aoff[u0 + v]; pos < s_aoff[u0 + v + 1]; ++pos) {
-              const float d = wave_sum(dot8_act_lds(wb8[v], s_act + (size_t)pos * I, lane, I));
-              if (lane == 0) y[pos] = d;
-            }
-          }
-        }
+        for (int v = 0; v < 8; ++v)
+          if (u0 + v < U) add_expert(wb8[v], u0 + v);
       }
     }
-    if (lane < T) {
-      const int t = lane;
-      float acc = 0.f;
-      for (int k = 0; k < K; ++k) acc += s_w[t * K + k] * y[s_pos[t * K + k]];
-      acc += s_sg[t] * y[P + t];
-      const size_t o = (size_t)t * H + r;
-      f.out[o] = acc;
-      if (f.layer_out)
-        f.layer_out[o] = (first ? x_first : load_scalar(a.x, BFX ? FK_DTYPE_BF16 : FK_DTYPE_F32, o)) + acc;
+#pragma unroll
+    for (int tt = 0; tt < kFusedMaxTokens; ++tt) {
+      if (tt < T) {
+        const float o = wave_sum(acc[tt]);
+        if (lane == tt) {
+          const size_t off = (size_t)tt * H + r;
+          f.out[off] = o;
+          if (f.layer_out)
+            f.layer_out[off] = (first ? x_first : load_scalar(a.x, BFX ? FK_DTYPE_BF16 : FK_DTYPE_F32, off)) + o;
+        }
+      }
     }
   }
 }
@@ -1200,11 +1293,11 @@ static bool fused_eligible(int T, int H, int I, int E, int K, int router_dt, int
 
 constexpr size_t kFusedMaxDynLds = ((size_t)(kFusedMaxPairs + kFusedMaxTokens) * 512 + kFusedMaxTokens) * sizeof(float);
 
-template <bool BX>
+template <bool BX, bool ONE>
 static int launch_fused_t(const FusedArgs& fa, hipStream_t stream) {
   static int cap_cache[64] = {0};
   static bool attr_set[64] = {false};
-  auto kernel = moe_fused_kernel<BX>;
+  auto kernel = moe_fused_kernel<BX, ONE>;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(FK_ERR_LAUNCH, "no current HIP device");
   if (!attr_set[dev]) {
@@ -1473,8 +1566,10 @@ int fk_moe_layer(const void* hidden, int hidden_dtype, const void* norm_weight, 
     fa.I = intermediate;
     fa.out = moe_out;
     fa.layer_out = layer_out;
-    if (hidden_dtype == FK_DTYPE_BF16) return launch_fused_t<true>(fa, as_stream(stream));
-    return launch_fused_t<false>(fa, as_stream(stream));
+    const bool one = tokens == 1;
+    if (hidden_dtype == FK_DTYPE_BF16)
+      return one ? launch_fused_t<true, true>(fa, as_stream(stream)) : launch_fused_t<true, false>(fa, as_stream(stream));
+    return one ? launch_fused_t<false, true>(fa, as_stream(stream)) : launch_fused_t<false, false>(fa, as_stream(stream));
   }
   st = fk_moe_router(hidden, hidden_dtype, norm_weight, norm_dtype, router_weight, router_dtype, router_bias,
                      bias_dtype, tokens, hidden_size, num_experts, top_k, eps, norm_offset, logits, topk_ids,

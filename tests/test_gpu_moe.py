@@ -279,7 +279,9 @@ def test_moe_layer_fp32_hidden(device, real_cpu, real_gpu):
 @pytest.mark.parametrize("tokens", [1, 2, 3, 4, 16])
 def test_fused_layer_matches_multi_launch(device, real_gpu, tokens):
     # fk_moe_layer takes the single-launch kernel for T <= 4; router +
-    # experts take the multi-launch path.  Same arithmetic order in both.
+    # experts take the multi-launch path.  The router arithmetic is the same
+    # (ids equal, logits and weights to rounding); the expert sums are taken
+    # in a different order (weights folded in before the lane reduction).
     from fastkernels_amd.plan import MoeLayerPlan
 
     plan = MoeLayerPlan(real_gpu, tokens)
@@ -291,12 +293,43 @@ def test_fused_layer_matches_multi_launch(device, real_gpu, tokens):
     multi = (plan.layer_out, plan.moe_out, plan.logits, plan.ids, plan.weights)
     torch.cuda.synchronize()
     assert torch.equal(fused[3], multi[3])
-    for a, b in zip(fused, multi):
+    for a, b in zip(fused[2:], multi[2:]):
         torch.testing.assert_close(a, b, atol=1e-6, rtol=1e-6)
+    for a, b in zip(fused[:2], multi[:2]):
+        torch.testing.assert_close(a, b, atol=1e-5, rtol=1e-5)
+
+
+def test_layer_sizes_interleaved_on_one_workspace(device, real_gpu):
+    # Single-launch (T <= 4) and multi-launch (T > 4) layers, and the
+    # fixed-ids expert path, share the stream's workspace: each call must
+    # match a call on a fresh plan whatever ran before it.
+    from fastkernels_amd.plan import MoeLayerPlan
+
+    w = real_gpu
+    args = (w["norm_weight"], w["router_weight"], w["expert_gate_up_weight"], w["expert_down_weight"],
+            w["shared_gate_up_weight"], w["shared_down_weight"], w["shared_expert_gate_weight"])
+    sizes = [4, 1, 8, 1, 3, 16, 2, 1]
+    xs = {t: wl.make_hidden(t, H, seed=90 + t).to(device) for t in set(sizes)}
+    want = {}
+    for t in set(sizes):
+        plan = MoeLayerPlan(w, t)
+        plan.hidden.copy_(xs[t])
+        plan.run()
+        torch.cuda.synchronize()
+        want[t] = (plan.layer_out.clone(), plan.ids.clone())
+    for t in sizes:
+        lh, moe, logits, ids, wts = hip.hip_qwen36_batched_moe_layer_decode(xs[t], *args, top_k=K)
+        assert torch.equal(ids, want[t][1])
+        torch.testing.assert_close(lh, want[t][0], atol=1e-6, rtol=1e-6)
+        # fixed-ids expert stage on the same workspace after a fused call
+        r = hip.hip_qwen36_batched_routed_shared_experts_decode(
+            xs[t], ids, wts, w["expert_gate_up_weight"], w["expert_down_weight"], w["shared_gate_up_weight"],
+            w["shared_down_weight"], w["shared_expert_gate_weight"])
+        torch.testing.assert_close(r, moe, atol=1e-5, rtol=1e-5)
 
 
 def test_fused_layer_repeated_calls_stay_consistent(device, real_gpu):
-    # tickets reset at the end of every launch: many back-to-back launches
+    # The launch tag advances every launch: many back-to-back launches
     # (rotating inputs) must keep giving the first call's answer.
     from fastkernels_amd.plan import MoeLayerPlan
 
