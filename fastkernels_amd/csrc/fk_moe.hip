@@ -38,11 +38,11 @@ constexpr int kDownRows = 4 * kDownRowsPerWave;  // down rows per workgroup
 
 struct MoeWs {
   uint32_t* tickets;    // [16] arrival counters; [kTicketEpoch] = fused launch epoch
-  // Single-launch path (T <= 4, E <= 256, I <= 512): tagged hand-off words in
+  // Single-launch layer (T <= 2) and small-batch router (T <= 32): tagged hand-off words in
   // a fixed-size region, so that no offset depends on the problem shape
   // (fk_moe_router / fk_moe_align lay the workspace out without I and H).
-  uint64_t* f_logits;   // [T, E] router logits (capacity 4 * 256)
-  uint64_t* f_act;      // [(T*K + T), I] SwiGLU activations, permuted rows then shared rows (capacity 36 * 512)
+  uint64_t* f_logits;   // [T, E] router logits (capacity 32 * 256)
+  uint64_t* f_act;      // [(T*K + T), I] SwiGLU activations, permuted rows then shared rows (capacity 18 * 512)
   uint64_t* f_sgate;    // [T] shared-expert gates
   uint64_t* f_started;  // [grid] one tagged record per workgroup of the launch (capacity 1024)
   int32_t* counts;      // [E]
@@ -64,9 +64,9 @@ constexpr int kTicketRouterTables = 1;
 constexpr int kTicketEpoch = 8;
 constexpr int kTicketError = 15;
 constexpr int kFusedMaxGrid = 1024;
-constexpr size_t kFusedLogitWords = 4 * 256;
-constexpr size_t kFusedActWords = (4 * 8 + 4) * 512;
-constexpr size_t kFusedGateWords = 4;
+constexpr size_t kFusedLogitWords = 32 * 256;  // tagged router: T <= 32
+constexpr size_t kFusedActWords = (2 * 8 + 2) * 512;
+constexpr size_t kFusedGateWords = 2;
 
 // Regions sized by I or H come last: fk_moe_router and fk_moe_align lay the
 // workspace out with I = H = 0 and must find the routing tables where
@@ -100,7 +100,7 @@ static size_t moe_ws_layout(int T, int K, int E, int I, int H, char* base, MoeWs
 
 // ---------------------------------------------------------------------------
 // Routing tables (histogram, offsets, stable permutation, active experts).
-// Runs inside one 256-thread workgroup; `s_ids` holds the P clamped ids.
+// Runs inside one workgroup of NWV wavefronts; `s_ids` holds the P clamped ids.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 #pragma unroll
@@ -118,15 +118,17 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 // running per-expert counts of its segment in s_wcnt[w][e].  A pair's
 // permuted position is offsets[e] + (pairs of e in earlier segments) +
 // (its rank inside its own segment), which preserves (token, slot) order.
-// LDS: s_ids[P] ids, s_rank[P], s_wcnt[4*E], s_cnt[E], s_off[E].
+// LDS: s_ids[P] ids, s_rank[P], s_wcnt[NWV*E], s_cnt[E], s_off[E].
+template <int NWV>
 __device__ void build_routing_tables(const int* s_ids, int P, int E, MoeWs ws, int* s_cnt, int* s_off, int* s_rank,
                                      int* s_wcnt) {
+  constexpr int NTH = NWV * kWave;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  __shared__ int s_wtot[4][2];
-  for (int i = tid; i < 4 * E; i += 256) s_wcnt[i] = 0;
+  __shared__ int s_wtot[NWV][2];
+  for (int i = tid; i < NWV * E; i += NTH) s_wcnt[i] = 0;
   __syncthreads();
 
-  const int seg = (P + 3) / 4;
+  const int seg = (P + NWV - 1) / NWV;
   const int j0 = min(P, wave * seg), j1 = min(P, j0 + seg);
   int* wc = s_wcnt + wave * E;
   for (int c0 = j0; c0 < j1; c0 += kWave) {
@@ -152,9 +154,9 @@ __device__ void build_routing_tables(const int* s_ids, int P, int E, MoeWs ws, i
   __syncthreads();
 
   // Per-expert totals, and per-wave exclusive prefixes in place.
-  for (int e = tid; e < E; e += 256) {
+  for (int e = tid; e < E; e += NTH) {
     int run = 0;
-    for (int w = 0; w < 4; ++w) {
+    for (int w = 0; w < NWV; ++w) {
       const int c = s_wcnt[w * E + e];
       s_wcnt[w * E + e] = run;
       run += c;
@@ -163,7 +165,7 @@ __device__ void build_routing_tables(const int* s_ids, int P, int E, MoeWs ws, i
   }
   __syncthreads();
 
-  const int per = (E + 255) / 256;  // bins per thread (<= 4)
+  const int per = (E + NTH - 1) / NTH;  // bins per thread (<= 4)
   const int base = tid * per;
   int sum = 0, nz = 0;
   for (int q = 0; q < per; ++q) {
@@ -200,10 +202,12 @@ __device__ void build_routing_tables(const int* s_ids, int P, int E, MoeWs ws, i
   }
   if (tid == 0) {
     ws.offsets[E] = P;
-    ws.num_active[0] = s_wtot[0][1] + s_wtot[1][1] + s_wtot[2][1] + s_wtot[3][1];
+    int na = 0;
+    for (int w = 0; w < NWV; ++w) na += s_wtot[w][1];
+    ws.num_active[0] = na;
   }
   __syncthreads();
-  for (int j = tid; j < P; j += 256) {
+  for (int j = tid; j < P; j += NTH) {
     const int w = j / seg;
     const int e = s_ids[j];
     const int r = s_off[e] + s_wcnt[w * E + e] + s_rank[j];
@@ -483,7 +487,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(RouterArgs a) {
   const int P = a.T * a.K;
   for (int j = threadIdx.x; j < P; j += 256) s_ids[j] = load_coherent(a.ws.ids32 + j);
   __syncthreads();
-  build_routing_tables(s_ids, P, a.E, a.ws, s_cnt, s_off, s_rank, s_wcnt);
+  build_routing_tables<4>(s_ids, P, a.E, a.ws, s_cnt, s_off, s_rank, s_wcnt);
   if (threadIdx.x == 0) {
     // Every workgroup has passed the barrier (it counted into ticket 1).
     a.ws.tickets[kTicketRouterBarrier] = 0u;
@@ -521,7 +525,7 @@ __global__ __launch_bounds__(256) void moe_align_kernel(AlignArgs a) {
     a.ws.wts[j] = a.w ? load_scalar(a.w, a.w_dt, j) : 0.f;
   }
   __syncthreads();
-  build_routing_tables(s_ids, P, a.E, a.ws, s_cnt, s_off, s_rank, s_wcnt);
+  build_routing_tables<4>(s_ids, P, a.E, a.ws, s_cnt, s_off, s_rank, s_wcnt);
   __syncthreads();
   // Optional copies of the tables for callers that inspect them.
   for (int e = threadIdx.x; e < a.E; e += 256) {
@@ -737,7 +741,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(ExpertArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Single-launch MoE layer for small batches (T <= 4, H <= 2048, I <= 512,
+// Single-launch MoE layer for small batches (T <= 2, H <= 2048, I <= 512,
 // E <= 256, bf16 router and expert weights, shared expert present).
 //
 // 512-thread workgroups, one per CU (grid capped at the co-resident
@@ -769,7 +773,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(ExpertArgs a) {
 // Tags are 32-bit: a word left untouched for exactly 2^32 launches on one
 // workspace would read as current.
 // ---------------------------------------------------------------------------
-constexpr int kFusedMaxTokens = 4;
+constexpr int kFusedMaxTokens = 2;  // from 3 tokens on, the tagged router + expert kernels are faster
 constexpr int kFusedMaxPairs = kFusedMaxTokens * 8;
 constexpr int kFusedWaves = 8;
 constexpr int kFusedMaxExperts = 256;
@@ -881,6 +885,7 @@ __device__ __forceinline__ void fused_tables(int id, float wt, int P, int K, int
 template <bool BFX, bool ONE>
 __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   constexpr int NPF = ONE ? 8 : kFusedPrefetch;
+  constexpr int NTOK = ONE ? 1 : kFusedMaxTokens;
   __shared__ __align__(16) int s_ids[kFusedMaxPairs];
   __shared__ float s_w[kFusedMaxPairs];
   __shared__ int s_tok[kFusedMaxPairs];         // permuted position -> token
@@ -915,57 +920,53 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       const int e = unit * 8 + wave;
       float mine = 0.f;
       if (e < E) {
+        // All loads of the row (weights, every token, then the norm weight)
+        // are issued before the first use: indices are clamped in range and
+        // out-of-range chunks are zeroed afterwards, so there is no branch
+        // between them.
+        Raw8<true> wr[4];
+        Raw8<BFX> xr[4];  // token 0 (the only one when ONE) rides with the weights
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int cc = min(lane + kWave * j, nch - 1);
+          wr[j] = load_raw8<true>(a.W, (size_t)e * H + (size_t)cc * 8);
+          xr[j] = load_raw8<BFX>(a.x, (size_t)cc * 8);
+        }
         float wn[4][8];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int c = lane + kWave * j;
-          if (c < nch) {
-            float w8[8], n8[8];
-            load8_f32<true>(a.W, (size_t)e * H + (size_t)c * 8, w8);
-            load8_any(a.nw, a.nw_dt, (size_t)c * 8, n8);
+          float w8[8], n8[8];
+          load8_any(a.nw, a.nw_dt, (size_t)min(c, nch - 1) * 8, n8);
+          raw8_to_f32<true>(wr[j], w8);
 #pragma unroll
-            for (int qq = 0; qq < 8; ++qq) wn[j][qq] = w8[qq] * (a.off + n8[qq]);
-          } else {
-#pragma unroll
-            for (int qq = 0; qq < 8; ++qq) wn[j][qq] = 0.f;
-          }
+          for (int qq = 0; qq < 8; ++qq) wn[j][qq] = c < nch ? w8[qq] * (a.off + n8[qq]) : 0.f;
         }
         const float bias = a.bias ? load_scalar(a.bias, a.bias_dt, e) : 0.f;
-        constexpr int TB = 4;
-        for (int t0 = 0; t0 < T; t0 += TB) {
-          float ss[TB], d[TB];
+#pragma unroll 1
+        for (int t = 0; t < NTOK; ++t) {
+          if (t < T) {
+            if (t > 0) {
 #pragma unroll
-          for (int tt = 0; tt < TB; ++tt) {
-            ss[tt] = 0.f;
-            d[tt] = 0.f;
-            const int t = t0 + tt;
-            if (t < T) {
+              for (int j = 0; j < 4; ++j)
+                xr[j] = load_raw8<BFX>(a.x, (size_t)t * H + (size_t)min(lane + kWave * j, nch - 1) * 8);
+            }
+            float ss = 0.f, d = 0.f;
 #pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                const int c = lane + kWave * j;
-                if (c < nch) {
-                  float x8[8];
-                  load8_f32<BFX>(a.x, (size_t)t * H + (size_t)c * 8, x8);
+            for (int j = 0; j < 4; ++j) {
+              const bool in = lane + kWave * j < nch;
+              float x8[8];
+              raw8_to_f32<BFX>(xr[j], x8);
 #pragma unroll
-                  for (int qq = 0; qq < 8; ++qq) {
-                    ss[tt] = fmaf(x8[qq], x8[qq], ss[tt]);
-                    d[tt] = fmaf(x8[qq], wn[j][qq], d[tt]);
-                  }
-                }
+              for (int qq = 0; qq < 8; ++qq) {
+                const float xv = in ? x8[qq] : 0.f;
+                ss = fmaf(xv, xv, ss);
+                d = fmaf(xv, wn[j][qq], d);
               }
             }
-          }
-#pragma unroll
-          for (int tt = 0; tt < TB; ++tt) {
-            if (t0 + tt < T) {
-              ss[tt] = wave_sum(ss[tt]);
-              d[tt] = wave_sum(d[tt]);
-            }
-          }
-#pragma unroll
-          for (int tt = 0; tt < TB; ++tt) {
-            const int t = t0 + tt;
-            if (t < T) mine = lane == t ? d[tt] * rsqrtf(ss[tt] / (float)H + a.eps) + bias : mine;
+            ss = wave_sum(ss);
+            d = wave_sum(d);
+            mine = lane == t ? d * rsqrtf(ss / (float)H + a.eps) + bias : mine;
           }
         }
       }
@@ -983,32 +984,38 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       }
       fused_gateup_item<BFX>(wg, wu, a.x, H, lane, T, nullptr, &s_chunk[0][wave]);
     } else if (wave == 0) {
-      // Shared-expert gate of every token: one row like the router's.
+      // Shared-expert gate of every token: one row like the router's, loads
+      // issued together as there.
+      Raw8<BFX> xr[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xr[j] = load_raw8<BFX>(a.x, (size_t)min(lane + kWave * j, nch - 1) * 8);
       float g8[4][8];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int c = lane + kWave * j;
-        if (f.sg && c < nch) {
-          load8_any(f.sg, f.sg_dt, (size_t)c * 8, g8[j]);
-        } else {
+        if (f.sg) load8_any(f.sg, f.sg_dt, (size_t)min(c, nch - 1) * 8, g8[j]);
 #pragma unroll
-          for (int qq = 0; qq < 8; ++qq) g8[j][qq] = 0.f;
-        }
+        for (int qq = 0; qq < 8; ++qq) g8[j][qq] = (f.sg && c < nch) ? g8[j][qq] : 0.f;
       }
-      for (int t = 0; t < T; ++t) {
-        float d = 0.f;
+#pragma unroll 1
+      for (int t = 0; t < NTOK; ++t) {
+        if (t < T) {
+          if (t > 0) {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int c = lane + kWave * j;
-          if (c < nch) {
+            for (int j = 0; j < 4; ++j)
+              xr[j] = load_raw8<BFX>(a.x, (size_t)t * H + (size_t)min(lane + kWave * j, nch - 1) * 8);
+          }
+          float d = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
             float x8[8];
-            load8_f32<BFX>(a.x, (size_t)t * H + (size_t)c * 8, x8);
+            raw8_to_f32<BFX>(xr[j], x8);
 #pragma unroll
             for (int qq = 0; qq < 8; ++qq) d = fmaf(x8[qq], g8[j][qq], d);
           }
+          d = wave_sum(d);
+          if (lane == 0) s_chunk[t][0] = f.sg ? sigmoid(d) : 1.f;
         }
-        d = wave_sum(d);
-        if (lane == 0) s_chunk[t][0] = f.sg ? sigmoid(d) : 1.f;
       }
     }
     __syncthreads();
@@ -1240,6 +1247,136 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
 }
 
 // ---------------------------------------------------------------------------
+// Router for small batches (T <= 32, E <= 256, H <= 2048): no grid barrier.
+//
+// Workgroup (ub, tb) computes the logits of expert rows 8ub.. (one per
+// wavefront) for tokens 4tb.. (loads of the row and the tokens issued
+// together) and writes them as one tagged 64-byte run per token (the
+// launch-tag protocol of the single-launch layer, same epoch counter).
+// Workgroup 0 then polls every logit, computes the top-k of each token (one
+// wavefront per token), advances the epoch (every workgroup has written
+// logits carrying this launch's tag, so all have read the epoch) and builds
+// the routing tables for the expert stage.  Same arithmetic as
+// moe_router_kernel, so both give identical logits and ids.
+// ---------------------------------------------------------------------------
+constexpr int kTagRouterMaxTokens = 32;
+constexpr int kTagRouterTokensPerUnit = 4;
+
+template <bool BFW, bool BFX>
+__global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
+  constexpr int TU = kTagRouterTokensPerUnit;
+  __shared__ int s_ids[kTagRouterMaxTokens * 8];
+  __shared__ float s_w[kTagRouterMaxTokens * 8];
+  __shared__ int s_rank[kTagRouterMaxTokens * 8];
+  __shared__ int s_wcnt[kFusedWaves * kFusedMaxExperts];
+  __shared__ int s_cnt[kFusedMaxExperts];
+  __shared__ int s_off[kFusedMaxExperts];
+  __shared__ float s_chunk[TU][8];
+  __shared__ int s_fail;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int T = a.T, H = a.H, E = a.E, K = a.K, nch = H >> 3;
+  const int nrb = (E + 7) / 8;
+  const int ub = blockIdx.x % nrb, tb = blockIdx.x / nrb;
+  const int e = ub * 8 + wave, t0 = tb * TU, nt = min(TU, T - t0);
+  const uint32_t tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
+  if (tid == 0) s_fail = 0;
+
+  float mine = 0.f;  // lane t < nt: logit of token t0 + t
+  if (e < E) {
+    Raw8<BFW> wr[4];
+    Raw8<BFX> xr[TU][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int cc = min(lane + kWave * j, nch - 1);
+      wr[j] = load_raw8<BFW>(a.W, (size_t)e * H + (size_t)cc * 8);
+#pragma unroll
+      for (int t = 0; t < TU; ++t) xr[t][j] = load_raw8<BFX>(a.x, (size_t)(t0 + min(t, nt - 1)) * H + (size_t)cc * 8);
+    }
+    float wn[4][8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = lane + kWave * j;
+      float w8[8], n8[8];
+      load8_any(a.nw, a.nw_dt, (size_t)min(c, nch - 1) * 8, n8);
+      raw8_to_f32<BFW>(wr[j], w8);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) wn[j][q] = c < nch ? w8[q] * (a.off + n8[q]) : 0.f;
+    }
+    const float bias = a.bias ? load_scalar(a.bias, a.bias_dt, e) : 0.f;
+#pragma unroll
+    for (int t = 0; t < TU; ++t) {
+      if (t < nt) {
+        float ss = 0.f, d = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bool in = lane + kWave * j < nch;
+          float x8[8];
+          raw8_to_f32<BFX>(xr[t][j], x8);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const float xv = in ? x8[q] : 0.f;
+            ss = fmaf(xv, xv, ss);
+            d = fmaf(xv, wn[j][q], d);
+          }
+        }
+        ss = wave_sum(ss);
+        d = wave_sum(d);
+        mine = lane == t ? d * rsqrtf(ss / (float)H + a.eps) + bias : mine;
+      }
+    }
+  }
+  if (lane < nt) s_chunk[lane][wave] = mine;
+  __syncthreads();
+  if (tid < 8 * nt) {
+    const int t = tid >> 3, l = tid & 7, ee = ub * 8 + l;
+    if (ee < E) {
+      const float v = s_chunk[t][l];
+      a.logits[(size_t)(t0 + t) * E + ee] = v;
+      store_tagged(a.ws.f_logits + (size_t)(t0 + t) * E + ee, v, tag);
+    }
+  }
+  if (blockIdx.x != 0) return;
+
+  // ---- workgroup 0: top-k of every token, epoch, routing tables ----------
+  for (int t = wave; t < T; t += kFusedWaves) {
+    constexpr int NJE = kFusedMaxExperts / kWave;
+    uint64_t w[NJE];
+    const uint64_t* srcs[NJE];
+#pragma unroll
+    for (int j = 0; j < NJE; ++j) {
+      const int ex = lane + kWave * j;
+      srcs[j] = ex < E ? a.ws.f_logits + (size_t)t * E + ex : nullptr;
+      w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+    }
+    if (!poll_tagged<NJE>(w, srcs, tag)) s_fail = 1;
+    float p[NJE];
+#pragma unroll
+    for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
+    int id;
+    float wt;
+    topk_select_regs<NJE>(p, E, K, lane, id, wt);
+    if (lane < K) {
+      s_ids[t * K + lane] = id;
+      s_w[t * K + lane] = wt;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    store_coherent(&a.ws.tickets[kTicketEpoch], tag);
+    if (s_fail) __hip_atomic_fetch_or(&a.ws.tickets[kTicketError], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const int P = T * K;
+  for (int j = tid; j < P; j += kFusedWaves * kWave) {
+    a.ids_out[j] = s_ids[j];
+    a.w_out[j] = s_w[j];
+    a.ws.ids32[j] = s_ids[j];
+    a.ws.wts[j] = s_w[j];
+  }
+  build_routing_tables<kFusedWaves>(s_ids, P, E, a.ws, s_cnt, s_off, s_rank, s_wcnt);
+}
+
+// ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
 static int check_ws(void* ws, size_t bytes, int T, int K, int E, int I, int H, MoeWs* out) {
@@ -1330,8 +1467,29 @@ static int launch_router_t(const RouterArgs& ra, hipStream_t stream) {
   return check_launch("moe_router_kernel");
 }
 
+static bool tagged_router_eligible(const RouterArgs& ra) {
+  return ra.T <= kTagRouterMaxTokens && ra.E <= kFusedMaxExperts && ra.H <= 2048 && ra.K <= 8;
+}
+
+template <bool BW, bool BX>
+static int launch_router_tagged_t(const RouterArgs& ra, hipStream_t stream) {
+  static int cap_cache[64] = {0};
+  auto kernel = moe_router_tagged_kernel<BW, BX>;
+  const int units = ((ra.E + 7) / 8) * ((ra.T + kTagRouterTokensPerUnit - 1) / kTagRouterTokensPerUnit);
+  // Workgroup 0 waits for every other workgroup's logits: all must be resident.
+  const int cap = resident_capacity(kernel, 512, 0, cap_cache);
+  if (units > cap) return fail(FK_ERR_UNSUPPORTED, "router grid %d exceeds co-resident capacity %d", units, cap);
+  hipLaunchKernelGGL(kernel, dim3(units), dim3(512), 0, stream, ra);
+  return check_launch("moe_router_tagged_kernel");
+}
+
 static int launch_router(const RouterArgs& ra, int router_dt, int hidden_dt, hipStream_t stream) {
   const bool bfw = router_dt == FK_DTYPE_BF16, bfx = hidden_dt == FK_DTYPE_BF16;
+  if (tagged_router_eligible(ra)) {
+    int st = FK_OK;
+    FK_DISPATCH_BOOL(bfw, BW, FK_DISPATCH_BOOL(bfx, BX, { st = launch_router_tagged_t<BW, BX>(ra, stream); }))
+    return st;
+  }
   const bool wide = ra.H > 2048, many = ra.E > 256;
   int st = FK_OK;
   FK_DISPATCH_BOOL(bfw, BW, FK_DISPATCH_BOOL(bfx, BX, {
