@@ -103,7 +103,8 @@ __global__ __launch_bounds__(256) void deltanet_project_kernel(ProjArgs a) {
     }
     which[r] = wh;
     lrow[r] = row;
-    wp[r] = reinterpret_cast<const char*>(a.w[wh]) + (size_t)row * a.H * esz;
+    const void* wbase = wh == 0 ? a.w[0] : wh == 1 ? a.w[1] : wh == 2 ? a.w[2] : a.w[3];  // no indexed kernarg load
+    wp[r] = reinterpret_cast<const char*>(wbase) + (size_t)row * a.H * esz;
     op[r] = a.out[wh] ? a.out[wh] + row : nullptr;
     ostride[r] = a.rows[wh];
   }
@@ -512,6 +513,596 @@ __global__ __launch_bounds__(256) void deltanet_out_kernel(OutArgs a) {
 
 
 // ---------------------------------------------------------------------------
+// Single-launch DeltaNet step (fk_deltanet_step for T <= 8, D = 128, bf16
+// weights).  One 512-thread workgroup per CU, grid capped at co-resident
+// capacity, three phases joined by launch-tagged words (the MoE layer's
+// protocol: value + 32-bit launch tag per 8-byte word, polled by consumers;
+// the epoch advances once every workgroup's started record carries the tag):
+//   A  projections: workgroup b owns row tiles b, b+G, .. (16 rows of the
+//      concatenated [qkv | z | a | b] weights); its 8 wavefronts split K and
+//      run v_mfma_f32_16x16x32_bf16 with the normalised tokens as bf16
+//      hi + lo columns (2 per token, so the fp32 activations keep ~16
+//      mantissa bits); partial tiles are summed through LDS.  The owner of
+//      a qkv row applies the causal conv + SiLU over the tokens and rolls
+//      the conv state.  Outputs leave as tagged 128-byte runs.
+//   B  one workgroup per value head: its fp32 state (prefetched into
+//      registers at the start, 32 per thread: thread (column j, quarter g)
+//      holds rows 32g..32g+31 of column j, so the four partial sums of a
+//      column sit in one lane quad and reduce with two DPP steps) runs the
+//      gated delta rule over the tokens; then the gated RMSNorm per token;
+//      normed values leave tagged.
+//   C  workgroup b < H/16 owns output rows 16b..16b+15: W_out tiles are
+//      fetched into registers after phase A, the normed values of every
+//      token are polled into LDS as bf16 hi + lo columns, and MFMA + an LDS
+//      sum over the 8 wavefronts give update (and hidden_out = x + update).
+// ---------------------------------------------------------------------------
+constexpr int kStepMaxTokens = 8;
+constexpr int kStepWaves = 8;
+constexpr int kStepMaxGrid = 1024;
+constexpr int kStepTilesPerWG = 4;  // phase A row tiles per workgroup (host checks)
+constexpr int kStepD = 128;
+constexpr size_t kStepMixWords = (size_t)kStepMaxTokens * 8192;
+constexpr size_t kStepVWords = (size_t)kStepMaxTokens * 4096;
+constexpr size_t kStepHeadWords = (size_t)kStepMaxTokens * 64;
+constexpr int kStepTicketEpoch = 0;
+constexpr int kStepTicketError = 1;
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+struct StepTagWs {
+  uint32_t* tickets;  // [16]: epoch, error flag
+  uint64_t* mix;      // [T, C] conv'd qkv
+  uint64_t* z;        // [T, V]
+  uint64_t* a;        // [T, Hv]
+  uint64_t* b;        // [T, Hv]
+  uint64_t* norm;     // [T, V] gated-RMSNorm output
+  uint64_t* started;  // [grid]
+};
+
+struct StepArgs {
+  const void* x;
+  const void* nw;
+  const void* w[4];  // qkv, z, a, b (bf16, rows of H)
+  const void* conv_state;
+  const void* conv_w;
+  const void* rec_state;
+  const void* w_out;  // bf16 [H, V]
+  const void* lnw;
+  const void* a_log;
+  const void* dt_bias;
+  int T, H, Hk, Hv, C, V, R, KS;
+  float eps;
+  float* update;
+  float* hidden_out;
+  void* next_conv;
+  void* next_rec;
+  StepTagWs tw;
+};
+
+__device__ __forceinline__ uint32_t bf16_pair_hi_lo(float v) {
+  const uint16_t hi = f32_to_bf16_bits(v);
+  const uint16_t lo = f32_to_bf16_bits(v - bf16_bits_to_f32(hi));
+  return (uint32_t)hi | ((uint32_t)lo << 16);
+}
+
+// Raw bits of N elements p[base + i * stride] of a bf16 (BF) or fp32 array;
+// elements from n_valid on repeat element 0, so p[base] must exist and the
+// caller ignores them.  The loads are straight-line, with no per-lane branch,
+// no zeroed destination and no conversion beside them: any of those makes
+// the compiler wait for every load in flight (the weight tiles included)
+// right there.  Bits are turned into values where they are used.
+template <bool BF, int N>
+__device__ __forceinline__ void gather_raw(const void* p, size_t base, size_t stride, int n_valid, uint32_t (&out)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const size_t idx = base + (size_t)(i < n_valid ? i : 0) * stride;
+    out[i] = BF ? (uint32_t)reinterpret_cast<const uint16_t*>(p)[idx] : reinterpret_cast<const uint32_t*>(p)[idx];
+  }
+}
+
+template <bool BF>
+__device__ __forceinline__ float raw_value(uint32_t r) {
+  return __uint_as_float(BF ? r << 16 : r);
+}
+
+// Lane quad sum (lanes 4q..4q+3 hold the four row quarters of a column).
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __uint_as_float(dpp_u32<kDppQuadXor1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppQuadXor2>(__float_as_uint(v)));
+  return v;
+}
+
+// NT: compile-time bound on the tokens (2 or 8), which sizes the token
+// registers.  BFX: hidden states in bf16 (else fp32).  Every other operand
+// has the dtype of the model's own decode: bf16 weights, norm weights, conv
+// state and decay parameters, fp32 recurrent state (the host sends other
+// combinations to the staged kernels).
+template <bool BFX, int NT>
+__global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
+  extern __shared__ float4 s_dyn_v[];
+  char* s_dyn = reinterpret_cast<char*>(s_dyn_v);
+  __shared__ float s_rs[kStepMaxTokens];
+  __shared__ float s_part[kStepMaxTokens][kStepWaves];  // [token][wavefront of that token]
+  __shared__ float s_sc[kStepMaxTokens][4];  // decay, beta (head workgroups)
+  __shared__ uint32_t s_wtag[kStepWaves];
+  __shared__ int s_fail;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = gridDim.x, b = blockIdx.x;
+  const int T = a.T, H = a.H, C = a.C, V = a.V, R = a.R, Hv = a.Hv;
+  const int NC = 2 * T;  // MFMA columns in use: (hi, lo) per token
+  const uint32_t tag = load_coherent(&a.tw.tickets[kStepTicketEpoch]) + 1u;
+  const int n = lane & 15, g4 = lane >> 4;  // MFMA lane -> (column / A row, k group)
+
+  // Roles.  Heads sit on the last Hv workgroups, output tiles on the first
+  // H/16, the epoch keeper just below the heads.
+  const int head = b - (G - Hv);
+  const bool is_head = head >= 0;
+  const bool is_out = b < H / 16;
+  const int keeper = max(0, G - Hv - 1);
+
+  // Loads are issued in the order their data is consumed (the vector memory
+  // counter retires in order): token chunks and norm weight, the phase A
+  // weight tiles, then the operands of the later phases.
+  constexpr int XCH = NT * 2048 / 8 / 512;  // token chunks per thread at H <= 2048
+  // H and V are powers of two (the host checks): indices split by shifts.
+  const int lh = 31 - __builtin_clz((unsigned)H), lv = 31 - __builtin_clz((unsigned)V);
+  const int cpt_sh = lh - 3;  // 8-element chunks per token row: H / 8
+  const int cpt = H >> 3, nchunk = T * cpt;
+  Raw8<BFX> xr[XCH];
+  Raw8<true> nr[XCH];
+#pragma unroll
+  for (int q = 0; q < XCH; ++q) {
+    const int idx8 = tid + q * 512;
+    if (idx8 < nchunk) {
+      xr[q] = load_raw8<BFX>(a.x, (size_t)idx8 * 8);
+      nr[q] = load_raw8<true>(a.nw, (size_t)(idx8 & (cpt - 1)) * 8);
+    }
+  }
+
+  // ---- phase A weight tiles ----------------------------------------------
+  const int ntiles = (R + 15) / 16;
+  const int kw = H >> 3;  // K range of one wavefront (H / 8 waves)
+  const int ks = kw >> 5;  // MFMA steps per tile (H <= 2048: <= 8)
+  // Row-contiguous loads: instruction s of tile i reads rows s*RPI + lane/LPR
+  // of the tile, LPR lanes x 16 B = the wavefront's whole K range of a row,
+  // so every load covers complete cache lines (the MFMA operand layout, 16
+  // rows x 64 B per load, streams at half the rate).  The tile is turned
+  // into the operand layout through the wavefront's LDS area below.
+  const int lpr_sh = lh - 6;  // lanes per row LPR = kw / 8, rows per load RPI = 64 / LPR
+  const int LPR = 1 << lpr_sh, RPI = kWave >> lpr_sh;
+  int ntl = 0;
+  u32x4 av[kStepTilesPerWG][8];
+  {
+#pragma unroll
+    for (int i = 0; i < kStepTilesPerWG; ++i) {
+      const int tile = b + i * G;
+      if (tile < ntiles) ntl = i + 1;
+    }
+    // The matrix boundaries C, C + V, C + V + Hv and R are multiples of 16
+    // (the host checks), so a tile lies in one matrix and the base address
+    // of each load is uniform; the lane adds a fixed byte offset (< RPI rows).
+    // Every slot issues its load: one outside the weights (past the last
+    // tile or past K) reads the first RPI rows of the qkv weight, the same
+    // few lines in every workgroup, and its data is never used.  A load under
+    // a condition would not be counted by the compiler's wait for the token
+    // chunks above, which would then wait for the weight tiles too.
+    const uint32_t lane_off = (uint32_t)((((lane >> lpr_sh) << lh) + (wave << (lh - 3)) + ((lane & (LPR - 1)) << 3)) << 1);
+    const size_t slot_stride = (size_t)RPI << (lh + 1);  // RPI rows of H bf16
+    const char* spare = reinterpret_cast<const char*>(a.w[0]);
+#pragma unroll
+    for (int i = 0; i < kStepTilesPerWG; ++i) {
+      const int tile = b + i * G;
+      const int row0 = tile * 16;
+      const int wh = row0 < C ? 0 : row0 < C + V ? 1 : row0 < C + V + Hv ? 2 : 3;
+      const int r0 = row0 - (wh == 0 ? 0 : wh == 1 ? C : wh == 2 ? C + V : C + V + Hv);
+      const char* tp = reinterpret_cast<const char*>(wh == 0 ? a.w[0] : wh == 1 ? a.w[1] : wh == 2 ? a.w[2] : a.w[3]) +
+                       ((size_t)(tile < ntiles ? r0 : 0) << (lh + 1));
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const char* base = s < ks && tile < ntiles ? tp : spare;
+        av[i][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + lane_off));
+        tp += slot_stride;
+      }
+    }
+  }
+
+  // Small operands of later phases, fetched now so that no phase waits on a
+  // dependent global load: the head's norm weight and decay parameters and
+  // the conv taps of this workgroup's qkv rows (thread i*16 + r: row r of
+  // tile i).
+  uint32_t lnw2[2], alog[1], dtb1[1];
+  gather_raw<true>(a.lnw, lane, 64, 2, lnw2);
+  gather_raw<true>(a.a_log, is_head ? head : 0, 0, 1, alog);
+  gather_raw<true>(a.dt_bias, is_head ? head : 0, 0, 1, dtb1);
+  uint32_t cwin_raw[8], cwk_raw[8];
+  {
+    const int row = (b + (tid >> 4) * G) * 16 + (tid & 15);
+    const bool conv_row = tid < kStepTilesPerWG * 16 && row < C;
+    const int nk = conv_row ? a.KS : 0;
+    gather_raw<true>(a.conv_state, (size_t)(conv_row ? row : 0) * a.KS, 1, nk, cwin_raw);
+    gather_raw<true>(a.conv_w, (size_t)(conv_row ? row : 0) * a.KS, 1, nk, cwk_raw);
+  }
+
+  // ---- stage the normalised tokens as bf16 hi/lo MFMA columns ------------
+  // s_xb: [H/8 chunks][NC][8] bf16.  Chunk q of thread tid is token-major
+  // chunk tid + 512 q; H % 512 == 0, so a wavefront's 64 chunks belong to one
+  // token and the sum of squares reduces in a fixed order.
+  uint16_t* s_xb = reinterpret_cast<uint16_t*>(s_dyn);
+  {
+#pragma unroll
+    for (int q = 0; q < XCH; ++q) {
+      const int idx8 = tid + q * 512;
+      if (idx8 < nchunk) {  // uniform per wavefront
+        float xv[8];
+        raw8_to_f32<BFX>(xr[q], xv);
+        float p = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p = fmaf(xv[e], xv[e], p);
+        p = wave_sum(p);
+        if (lane == 0) s_part[idx8 >> cpt_sh][(idx8 & (cpt - 1)) >> 6] = p;
+      }
+    }
+    if (tid == 0) s_fail = 0;
+    if (lane == 0) s_wtag[wave] = tag;
+    __syncthreads();
+    if (tid < T) {
+      float tot = 0.f;
+      for (int w = 0; w < (cpt >> 6); ++w) tot += s_part[tid][w];
+      s_rs[tid] = rsqrtf(tot / (float)H + a.eps);
+    }
+    if (tid == 0) store_tagged(a.tw.started + b, 0.f, s_wtag[kStepWaves - 1]);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < XCH; ++q) {
+      const int idx8 = tid + q * 512;
+      if (idx8 < nchunk) {
+        const int t = idx8 >> cpt_sh, k0 = (idx8 & (cpt - 1)) << 3;
+        float xv[8], nv[8];
+        raw8_to_f32<BFX>(xr[q], xv);
+        raw8_to_f32<true>(nr[q], nv);
+        uint16_t hi[8], lo[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t hl = bf16_pair_hi_lo(xv[e] * s_rs[t] * (1.0f + nv[e]));
+          hi[e] = (uint16_t)(hl & 0xffffu);
+          lo[e] = (uint16_t)(hl >> 16);
+        }
+        const int c = k0 >> 3;
+        u32x4 vh, vl;
+        vh.x = hi[0] | ((uint32_t)hi[1] << 16); vh.y = hi[2] | ((uint32_t)hi[3] << 16);
+        vh.z = hi[4] | ((uint32_t)hi[5] << 16); vh.w = hi[6] | ((uint32_t)hi[7] << 16);
+        vl.x = lo[0] | ((uint32_t)lo[1] << 16); vl.y = lo[2] | ((uint32_t)lo[3] << 16);
+        vl.z = lo[4] | ((uint32_t)lo[5] << 16); vl.w = lo[6] | ((uint32_t)lo[7] << 16);
+        *reinterpret_cast<u32x4*>(s_xb + ((size_t)c * NC + 2 * t) * 8) = vh;
+        *reinterpret_cast<u32x4*>(s_xb + ((size_t)c * NC + 2 * t + 1) * 8) = vl;
+      }
+    }
+    __syncthreads();
+  }
+
+  // Head workgroups: prefetch the state (thread (j, gq): rows 32gq.., column
+  // j).  Issued only now: the waits above are counted over every path, so
+  // head-only loads in front of them would make the other workgroups wait
+  // for their weight tiles too.
+  const int sj = tid >> 2, sg = tid & 3;
+  uint32_t S_raw[32];
+  if (is_head) gather_raw<false>(a.rec_state, ((size_t)head * kStepD + (size_t)sg * 32) * kStepD + sj, kStepD, 32, S_raw);
+
+  // ---- phase A: projections ---------------------------------------------
+  // LDS: s_xb | per-wavefront transposition areas [8][16 rows][kw*2 + 16 B]
+  // (row pitch padded by 16 B: the 16 rows of an operand read fall in
+  // distinct banks).  Each wavefront's partial sums [tile][16][NC] go to the
+  // start of its own area once its MFMAs are done.
+  const int pitch = kw * 2 + 16;
+  char* s_tw = s_dyn + (size_t)H * NC * 2 + (size_t)wave * 16 * pitch;
+  float* s_red_w = reinterpret_cast<float*>(s_tw);
+  {
+    f32x4_t acc[kStepTilesPerWG];
+#pragma unroll
+    for (int i = 0; i < kStepTilesPerWG; ++i) {
+      acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if (i < ntl) {
+        // tile i: registers -> LDS rows (lanes of one load: RPI rows x kw k)
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+          if (s < ks)
+            *reinterpret_cast<u32x4*>(s_tw + (s * RPI + (lane >> lpr_sh)) * pitch + ((lane & (LPR - 1)) << 4)) = av[i][s];
+        // MFMA steps: operand lane (row n, k group g4) reads 8 k of its row
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          if (s < ks) {
+            const u32x4 wv = *reinterpret_cast<const u32x4*>(s_tw + n * pitch + (s * 32 + g4 * 8) * 2);
+            const int c = ((wave * kw + s * 32) >> 3) + g4;
+            const u32x4 bv = n < NC ? *reinterpret_cast<const u32x4*>(s_xb + ((size_t)c * NC + n) * 8) : u32x4{0, 0, 0, 0};
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wv),
+                                                             __builtin_bit_cast(bf16x8_t, bv), acc[i], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (n < NC) {
+#pragma unroll
+      for (int i = 0; i < kStepTilesPerWG; ++i)
+        if (i < ntl)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) s_red_w[((size_t)i * 16 + g4 * 4 + q) * NC + n] = acc[i][q];
+    }
+    __syncthreads();
+    // One thread per (tile, row): sums the wavefronts' partials (hi + lo)
+    // and finishes the row for every token.
+    if (tid < ntl * 16) {
+      const int i = tid >> 4, r = tid & 15;
+      const int row = (b + i * G) * 16 + r;
+      if (row < R) {
+        float v[kStepMaxTokens];
+#pragma unroll
+        for (int t = 0; t < kStepMaxTokens; ++t) {
+          v[t] = 0.f;
+          if (t < T)
+            for (int w = 0; w < kStepWaves; ++w) {
+              const float* pr = reinterpret_cast<const float*>(s_dyn + (size_t)H * NC * 2 + (size_t)w * 16 * pitch) +
+                                ((size_t)i * 16 + r) * NC;
+              v[t] += pr[2 * t] + pr[2 * t + 1];
+            }
+        }
+        if (row < C) {
+          // causal depthwise conv + SiLU over [state | tokens], state rolled
+          float win[8], wk[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            win[j] = raw_value<true>(cwin_raw[j]);
+            wk[j] = raw_value<true>(cwk_raw[j]);
+          }
+#pragma unroll
+          for (int t = 0; t < kStepMaxTokens; ++t) {
+            if (t < T) {
+#pragma unroll
+              for (int j = 0; j < 7; ++j)
+                if (j + 1 < a.KS) win[j] = win[j + 1];
+#pragma unroll
+              for (int j = 0; j < 8; ++j)
+                if (j == a.KS - 1) win[j] = v[t];
+              float cv = 0.f;
+#pragma unroll
+              for (int j = 0; j < 8; ++j)
+                if (j < a.KS) cv = fmaf(wk[j], win[j], cv);
+              store_tagged(a.tw.mix + (size_t)t * C + row, silu(cv), tag);
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            if (j < a.KS) reinterpret_cast<uint16_t*>(a.next_conv)[(size_t)row * a.KS + j] = f32_to_bf16_bits(win[j]);
+        } else {
+          uint64_t* dst;
+          int stride, off;
+          if (row < C + V) {
+            dst = a.tw.z, stride = V, off = row - C;
+          } else if (row < C + V + Hv) {
+            dst = a.tw.a, stride = Hv, off = row - C - V;
+          } else {
+            dst = a.tw.b, stride = Hv, off = row - C - V - Hv;
+          }
+#pragma unroll
+          for (int t = 0; t < kStepMaxTokens; ++t)
+            if (t < T) store_tagged(dst + (size_t)t * stride + off, v[t], tag);
+        }
+      }
+    }
+    __syncthreads();  // phases B and C reuse the dynamic LDS
+  }
+
+  // ---- W_out tiles for phase C, fetched while the heads run --------------
+  const int kwc = V >> 3, ksc = kwc >> 5;  // V / 8 waves; V <= 4096: <= 16 steps
+  u32x4 ov[16];
+  if (is_out) {
+    const uint16_t* wp = reinterpret_cast<const uint16_t*>(a.w_out) + (size_t)(b * 16 + n) * V;
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+      if (s < ksc) ov[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp + wave * kwc + s * 32 + g4 * 8));
+  }
+  // residual inputs of this workgroup's output rows (thread t*16 + r)
+  uint32_t xres[1];
+  gather_raw<BFX>(a.x, is_out && tid < 16 * T ? (size_t)(tid >> 4) * H + b * 16 + (tid & 15) : 0, 0, 1, xres);
+
+  // ---- epoch keeper ------------------------------------------------------
+  if (b == keeper) {
+    bool ok = true;
+    for (int base = tid; base < G; base += 512 * 2) {
+      uint64_t w[2];
+      const uint64_t* srcs[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = base + j * 512;
+        srcs[j] = r < G ? a.tw.started + r : nullptr;
+        w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+      }
+      ok = poll_tagged<2>(w, srcs, tag) && ok;
+    }
+    if (!ok) s_fail = 1;
+    __syncthreads();
+    if (tid == 0) store_coherent(&a.tw.tickets[kStepTicketEpoch], tag);
+  }
+
+  // ---- phase B: gated delta rule of one value head -----------------------
+  if (is_head) {
+    // s_in: [T][4][128] (q, k, v, z), then [T][2] (a, b)
+    float* s_in = reinterpret_cast<float*>(s_dyn);
+    float* s_ab = s_in + (size_t)T * 4 * kStepD;
+    float* s_o = s_ab + 2 * kStepMaxTokens;  // [T][128]
+    const int hq = head / (Hv / a.Hk);
+    const int per_tok = 4 * kStepD + 2;
+    const int n_in = T * per_tok;
+    bool ok = true;
+    for (int base = tid; base < n_in; base += 512 * 4) {
+      uint64_t w[4];
+      const uint64_t* srcs[4];
+      int dsti[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int idx = base + j * 512;
+        srcs[j] = nullptr;
+        dsti[j] = -1;
+        if (idx < n_in) {
+          const int t = idx / per_tok, r = idx - t * per_tok;
+          if (r < 4 * kStepD) {
+            const int part = r >> 7, e = r & 127;
+            const size_t col = part == 0 ? (size_t)hq * kStepD + e
+                             : part == 1 ? (size_t)a.Hk * kStepD + (size_t)hq * kStepD + e
+                             : part == 2 ? (size_t)2 * a.Hk * kStepD + (size_t)head * kStepD + e
+                                         : (size_t)head * kStepD + e;
+            srcs[j] = part < 3 ? a.tw.mix + (size_t)t * C + col : a.tw.z + (size_t)t * V + col;
+            dsti[j] = (t * 4 + part) * kStepD + e;
+          } else {
+            srcs[j] = (r == 4 * kStepD ? a.tw.a : a.tw.b) + (size_t)t * Hv + head;
+            dsti[j] = T * 4 * kStepD + 2 * t + (r - 4 * kStepD);
+          }
+        }
+        w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+      }
+      ok = poll_tagged<4>(w, srcs, tag) && ok;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (dsti[j] >= 0) s_in[dsti[j]] = value_of(w[j]);
+    }
+    if (!ok) s_fail = 1;
+    __syncthreads();
+    // Per token (wave t): l2-normalise q (times D^-1/2) and k in place; decay and beta.
+    if (wave < T) {
+      const int t = wave;
+      float* q = s_in + (size_t)(t * 4 + 0) * kStepD;
+      float* k = s_in + (size_t)(t * 4 + 1) * kStepD;
+      const float q0 = q[lane], q1 = q[lane + 64], k0 = k[lane], k1 = k[lane + 64];
+      const float sq = wave_sum(q0 * q0 + q1 * q1), sk = wave_sum(k0 * k0 + k1 * k1);
+      const float qs = rsqrtf(sq + a.eps) * rsqrtf((float)kStepD), kss = rsqrtf(sk + a.eps);
+      q[lane] = q0 * qs;
+      q[lane + 64] = q1 * qs;
+      k[lane] = k0 * kss;
+      k[lane + 64] = k1 * kss;
+      if (lane == 0) {
+        const float neg_a = -expf(raw_value<true>(alog[0]));
+        const float gin = s_ab[2 * t] + raw_value<true>(dtb1[0]);
+        s_sc[t][0] = expf(neg_a * (fmaxf(gin, 0.f) + log1pf(expf(-fabsf(gin)))));
+        s_sc[t][1] = 1.f / (1.f + expf(-s_ab[2 * t + 1]));
+      }
+    }
+    __syncthreads();
+    float S[32];
+#pragma unroll
+    for (int m = 0; m < 32; ++m) S[m] = raw_value<false>(S_raw[m]);
+    for (int t = 0; t < T; ++t) {
+      const float decay = s_sc[t][0], beta = s_sc[t][1];
+      float kn[32], qn[32];
+      {
+        const float4* k4 = reinterpret_cast<const float4*>(s_in + (size_t)(t * 4 + 1) * kStepD + sg * 32);
+        const float4* q4 = reinterpret_cast<const float4*>(s_in + (size_t)(t * 4 + 0) * kStepD + sg * 32);
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          const float4 kk = k4[m], qq = q4[m];
+          kn[4 * m] = kk.x; kn[4 * m + 1] = kk.y; kn[4 * m + 2] = kk.z; kn[4 * m + 3] = kk.w;
+          qn[4 * m] = qq.x; qn[4 * m + 1] = qq.y; qn[4 * m + 2] = qq.z; qn[4 * m + 3] = qq.w;
+        }
+      }
+      float part = 0.f;
+#pragma unroll
+      for (int m = 0; m < 32; ++m) {
+        S[m] *= decay;
+        part = fmaf(S[m], kn[m], part);
+      }
+      const float ksum = quad_sum(part);
+      const float delta = (s_in[(size_t)(t * 4 + 2) * kStepD + sj] - ksum) * beta;
+      float op = 0.f;
+#pragma unroll
+      for (int m = 0; m < 32; ++m) {
+        S[m] = fmaf(kn[m], delta, S[m]);
+        op = fmaf(S[m], qn[m], op);
+      }
+      const float o = quad_sum(op);
+      if (sg == 0) s_o[t * kStepD + sj] = o;
+    }
+    __syncthreads();
+    // Gated RMSNorm of each token's head output (wave t), published first;
+    // the state write-back is off the critical path.
+    if (wave < T) {
+      const int t = wave;
+      const float o0 = s_o[t * kStepD + lane], o1 = s_o[t * kStepD + lane + 64];
+      const float rs = rsqrtf(wave_sum(o0 * o0 + o1 * o1) / (float)kStepD + a.eps);
+      const float* z = s_in + (size_t)(t * 4 + 3) * kStepD;
+      uint64_t* dst = a.tw.norm + (size_t)t * V + (size_t)head * kStepD;
+      store_tagged(dst + lane, o0 * rs * raw_value<true>(lnw2[0]) * silu(z[lane]), tag);
+      store_tagged(dst + lane + 64, o1 * rs * raw_value<true>(lnw2[1]) * silu(z[lane + 64]), tag);
+    }
+    {
+      const size_t base = ((size_t)head * kStepD + (size_t)sg * 32) * kStepD + sj;
+#pragma unroll
+      for (int m = 0; m < 32; ++m) reinterpret_cast<float*>(a.next_rec)[base + (size_t)m * kStepD] = S[m];
+    }
+    __syncthreads();  // s_dyn is reused below
+  }
+
+  // ---- phase C: output projection of rows 16b..16b+15 --------------------
+  if (is_out) {
+    uint16_t* s_nb = reinterpret_cast<uint16_t*>(s_dyn);  // [V/8][NC][8] bf16
+    float* s_red2 = reinterpret_cast<float*>(s_dyn + (size_t)V * NC * 2);  // [8][16][NC]
+    const int n_norm = T * V;
+    bool ok = true;
+    for (int base = tid; base < n_norm; base += 512 * 8) {
+      uint64_t w[8];
+      const uint64_t* srcs[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int idx = base + j * 512;
+        srcs[j] = idx < n_norm ? a.tw.norm + idx : nullptr;
+        w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+      }
+      ok = poll_tagged<8>(w, srcs, tag) && ok;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int idx = base + j * 512;
+        if (idx < n_norm) {
+          const int t = idx >> lv, k = idx & (V - 1);
+          const uint32_t hl = bf16_pair_hi_lo(value_of(w[j]));
+          const int c = k >> 3, e = k & 7;
+          s_nb[((size_t)c * NC + 2 * t) * 8 + e] = (uint16_t)(hl & 0xffffu);
+          s_nb[((size_t)c * NC + 2 * t + 1) * 8 + e] = (uint16_t)(hl >> 16);
+        }
+      }
+    }
+    if (!ok) s_fail = 1;
+    __syncthreads();
+    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      if (s < ksc) {
+        const int c = ((wave * kwc + s * 32) >> 3) + g4;
+        const u32x4 bv = n < NC ? *reinterpret_cast<const u32x4*>(s_nb + ((size_t)c * NC + n) * 8) : u32x4{0, 0, 0, 0};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ov[s]),
+                                                      __builtin_bit_cast(bf16x8_t, bv), acc, 0, 0, 0);
+      }
+    }
+    if (n < NC) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) s_red2[((size_t)wave * 16 + g4 * 4 + q) * NC + n] = acc[q];
+    }
+    __syncthreads();
+    if (tid < 16 * T) {
+      const int r = tid & 15, t = tid >> 4;
+      float v = 0.f;
+      for (int w = 0; w < kStepWaves; ++w) {
+        const float* pr = s_red2 + ((size_t)w * 16 + r) * NC;
+        v += pr[2 * t] + pr[2 * t + 1];
+      }
+      const size_t o = (size_t)t * H + b * 16 + r;
+      a.update[o] = v;
+      if (a.hidden_out) a.hidden_out[o] = raw_value<BFX>(xres[0]) + v;
+    }
+  }
+  if (tid == 0 && s_fail)
+    __hip_atomic_fetch_or(&a.tw.tickets[kStepTicketError], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
 static int launch_project(const ProjArgs& pa, int weight_dtype, int hidden_dtype, hipStream_t s) {
@@ -594,6 +1185,7 @@ static int launch_recurrent_output(const RecArgs& ra, const void* out_proj_weigh
 // Step workspace: the recurrent/output workspace followed by the fused
 // projection outputs (conv'd mixed qkv, z, a, b) of every token.
 struct StepWs {
+  StepTagWs tw;  // single-launch step: fixed-size tagged hand-off region first
   DnWs dn;
   float* mixed;
   float* z;
@@ -601,8 +1193,26 @@ struct StepWs {
   float* b;
 };
 
+static size_t step_tag_layout(char* base, StepTagWs* tw) {
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = off;
+    off = align_up(off + bytes, 256);
+    return base ? base + at : nullptr;
+  };
+  tw->tickets = reinterpret_cast<uint32_t*>(take(16 * sizeof(uint32_t)));
+  tw->mix = reinterpret_cast<uint64_t*>(take(kStepMixWords * 8));
+  tw->z = reinterpret_cast<uint64_t*>(take(kStepVWords * 8));
+  tw->a = reinterpret_cast<uint64_t*>(take(kStepHeadWords * 8));
+  tw->b = reinterpret_cast<uint64_t*>(take(kStepHeadWords * 8));
+  tw->norm = reinterpret_cast<uint64_t*>(take(kStepVWords * 8));
+  tw->started = reinterpret_cast<uint64_t*>(take((size_t)kStepMaxGrid * 8));
+  return off;
+}
+
 static size_t step_ws_layout(int T, int Hk, int Hv, int D, char* base, StepWs* ws) {
-  size_t off = align_up(dn_ws_layout(T, Hv, D, base, &ws->dn), 256);
+  size_t off = step_tag_layout(base, &ws->tw);
+  off = align_up(off + dn_ws_layout(T, Hv, D, base ? base + off : nullptr, &ws->dn), 256);
   auto take = [&](size_t bytes) {
     size_t at = off;
     off = align_up(off + bytes, 256);
@@ -613,6 +1223,64 @@ static size_t step_ws_layout(int T, int Hk, int Hv, int D, char* base, StepWs* w
   ws->a = take((size_t)T * Hv * 4);
   ws->b = take((size_t)T * Hv * 4);
   return off;
+}
+
+// Single-launch step: shapes the kernel handles (the real Qwen3.6 layer:
+// H 2048, Hk 16, Hv 32, D 128, C 8192), bf16 projection and output weights.
+// dt: the ten dtype codes of fk_deltanet_step (hidden, norm weight,
+// projections, conv state, conv weight, recurrent state, out projection,
+// gated-norm weight, a_log, dt_bias).
+static bool step_fused_eligible(int T, int H, int Hk, int Hv, int D, const int* dt, int G) {
+  const int C = (2 * Hk + Hv) * D, V = Hv * D, R = C + V + 2 * Hv;
+  bool dtypes_ok = dt[5] == FK_DTYPE_F32;
+  for (int i = 1; i < 10; ++i)
+    if (i != 5 && dt[i] != FK_DTYPE_BF16) dtypes_ok = false;
+  return dtypes_ok && T >= 1 && T <= kStepMaxTokens && D == kStepD && H >= 512 && H <= 2048 && (H & (H - 1)) == 0 &&
+         (V & (V - 1)) == 0 && V >= 256 && V <= 4096 && C <= 8192 && Hv <= 64 && Hv % 16 == 0 && G >= Hv + 1 &&
+         G >= H / 16 &&
+         (R + 15) / 16 <= kStepTilesPerWG * G && G <= kStepMaxGrid;
+}
+
+static size_t step_fused_lds(int T, int H, int V) {
+  const size_t nc = 2 * (size_t)T;
+  const size_t pa = (size_t)H * nc * 2 + (size_t)kStepWaves * 16 * ((size_t)H / kStepWaves * 2 + 16);
+  const size_t pb = ((size_t)T * 4 * kStepD + 2 * kStepMaxTokens + (size_t)T * kStepD) * 4;
+  const size_t pc = (size_t)V * nc * 2 + (size_t)kStepWaves * 16 * nc * 4;
+  return pa > pb ? (pa > pc ? pa : pc) : (pb > pc ? pb : pc);
+}
+
+// Dynamic LDS reserved for the step kernel: its need at T = 8, H = 2048, V = 4096.
+constexpr size_t kStepMaxLds = (size_t)4096 * 16 * 2 + (size_t)kStepWaves * 16 * 16 * 4;
+
+// Grid of the single-launch step (one workgroup per CU, capped at the
+// co-resident capacity), or 0 when the device cannot host it.
+template <bool BX, int NT>
+static int step_grid() {
+  static int cap_cache[64] = {0};
+  static int attr_ok[64] = {0};  // 0 unknown, 1 set, -1 refused
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (attr_ok[dev] == 0)
+    attr_ok[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(deltanet_step_kernel<BX, NT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kStepMaxLds) == hipSuccess
+                       ? 1
+                       : -1;
+  if (attr_ok[dev] < 0) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const int cap = resident_capacity(deltanet_step_kernel<BX, NT>, 512, kStepMaxLds, cap_cache);
+  const int cus = device_cus();
+  const int G = cap < cus ? cap : cus;
+  return G > kStepMaxGrid ? kStepMaxGrid : G;
+}
+
+template <bool BX, int NT>
+static int launch_step_fused(const StepArgs& sa, int G, hipStream_t s) {
+  const size_t shm = step_fused_lds(sa.T, sa.H, sa.V);
+  if (shm > kStepMaxLds) return fail(FK_ERR_UNSUPPORTED, "DeltaNet step needs %zu bytes of LDS", shm);
+  hipLaunchKernelGGL((deltanet_step_kernel<BX, NT>), dim3(G), dim3(512), shm, s, sa);
+  return check_launch("deltanet_step_kernel");
 }
 
 }  // namespace fk
@@ -778,6 +1446,41 @@ int fk_deltanet_step(const void* hidden, const void* input_norm_weight, const vo
   hipStream_t s = as_stream(stream);
 
   const int conv_dim = (2 * qk_heads + value_heads) * head_dim;
+  const bool bx = dtypes[0] == FK_DTYPE_BF16, few = tokens <= 2;
+  const int G = bx ? (few ? step_grid<true, 2>() : step_grid<true, 8>())
+                   : (few ? step_grid<false, 2>() : step_grid<false, 8>());
+  if (G > 0 && step_fused_eligible(tokens, hidden_size, qk_heads, value_heads, head_dim, dtypes, G)) {
+    StepArgs sa;
+    sa.x = hidden;
+    sa.nw = input_norm_weight;
+    sa.w[0] = w_qkv;
+    sa.w[1] = w_z;
+    sa.w[2] = w_a;
+    sa.w[3] = w_b;
+    sa.conv_state = conv_state;
+    sa.conv_w = conv_weight;
+    sa.rec_state = recurrent_state;
+    sa.w_out = out_proj_weight;
+    sa.lnw = linear_norm_weight;
+    sa.a_log = a_log;
+    sa.dt_bias = dt_bias;
+    sa.T = tokens;
+    sa.H = hidden_size;
+    sa.Hk = qk_heads;
+    sa.Hv = value_heads;
+    sa.C = conv_dim;
+    sa.V = value_heads * head_dim;
+    sa.R = conv_dim + sa.V + 2 * value_heads;
+    sa.KS = kernel_size;
+    sa.eps = eps;
+    sa.update = update;
+    sa.hidden_out = hidden_out;
+    sa.next_conv = next_conv_state;
+    sa.next_rec = next_recurrent_state;
+    sa.tw = ws.tw;
+    if (bx) return few ? launch_step_fused<true, 2>(sa, G, s) : launch_step_fused<true, 8>(sa, G, s);
+    return few ? launch_step_fused<false, 2>(sa, G, s) : launch_step_fused<false, 8>(sa, G, s);
+  }
   ProjArgs pa;
   pa.x = hidden;
   pa.nw = input_norm_weight;

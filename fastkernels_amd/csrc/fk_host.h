@@ -28,4 +28,30 @@ inline int check_launch(const char* what) {
   return FK_OK;
 }
 
+// Co-resident workgroup capacity of a kernel on the current device (cached
+// per device); the grid-barrier kernels never launch more workgroups.
+template <typename K>
+inline int resident_capacity(K kernel, int block, size_t shm, int* cache) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] > 0) return cache[dev];
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, shm) != hipSuccess) return 0;
+  cache[dev] = cus * per_cu;
+  return cache[dev];
+}
+
+inline int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cache[dev] = cus;
+  }
+  return cache[dev];
+}
+
 }  // namespace fk

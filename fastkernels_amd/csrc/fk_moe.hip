@@ -1397,32 +1397,6 @@ static int check_ws(void* ws, size_t bytes, int T, int K, int E, int I, int H, M
     __VA_ARGS__                           \
   }
 
-// Co-resident workgroup capacity of a kernel on the current device (cached
-// per device); the grid-barrier kernels never launch more workgroups.
-template <typename K>
-static int resident_capacity(K kernel, int block, size_t shm, int* cache) {
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] > 0) return cache[dev];
-  int cus = 0, per_cu = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, shm) != hipSuccess) return 0;
-  cache[dev] = cus * per_cu;
-  return cache[dev];
-}
-
-static int device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    cache[dev] = cus;
-  }
-  return cache[dev];
-}
-
 static bool fused_eligible(int T, int H, int I, int E, int K, int router_dt, int expert_dt, bool has_shared) {
   return T >= 1 && T <= kFusedMaxTokens && H <= 2048 && I <= 512 && I % kFusedChunk == 0 && E <= kFusedMaxExperts && K <= 8 &&
          router_dt == FK_DTYPE_BF16 && expert_dt == FK_DTYPE_BF16 && has_shared;

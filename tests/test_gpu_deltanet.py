@@ -142,3 +142,65 @@ def test_deltanet_moe_layer(device, spec_name, tokens):
     torch.testing.assert_close(layer_hidden.cpu(), h + r, **tol(torch.bfloat16))
     if near == 0:
         torch.testing.assert_close(layer_hidden.cpu(), ref[0], **tol(torch.bfloat16))
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 8])
+def test_step_single_launch_matches_oracle(device, real_dn, tokens):
+    # fk_deltanet_step at the real shapes takes the single-launch kernel
+    # (MFMA projections with bf16 hi/lo activations, tagged hand-offs).
+    from fastkernels_amd.plan import DeltaNetStepPlan
+
+    x = wl.make_hidden(tokens, REAL.hidden_size, seed=60 + tokens)
+    plan = DeltaNetStepPlan(_to(real_dn, device), tokens, REAL)
+    plan.hidden.copy_(x.to(device))
+    plan.run()
+    torch.cuda.synchronize()
+    update, conv, state = oracle.deltanet_update(
+        x, real_dn["conv_state"], real_dn["recurrent_state"], real_dn, **_dims(REAL))
+    torch.testing.assert_close(plan.update.cpu(), update, **tol(torch.bfloat16))
+    torch.testing.assert_close(plan.hidden_out.cpu(), x.float() + update, **tol(torch.bfloat16))
+    torch.testing.assert_close(plan.next_recurrent_state.cpu(), state, atol=1e-3, rtol=1e-3)
+    torch.testing.assert_close(plan.next_conv_state.cpu().float(), conv.float(), atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("tokens", [1, 8])
+def test_step_single_launch_matches_staged_kernels(device, real_dn, tokens):
+    # Same step through the staged operator kernels (fp32 VALU GEMVs).
+    from fastkernels_amd.plan import DeltaNetStepPlan
+
+    x = wl.make_hidden(tokens, REAL.hidden_size, seed=70 + tokens).to(device)
+    wd = _to(real_dn, device)
+    plan = DeltaNetStepPlan(wd, tokens, REAL)
+    plan.hidden.copy_(x)
+    plan.run()
+    mixed, z, a, b = hip.hip_qwen36_batched_deltanet_project(
+        x, wd["input_norm_weight"], wd["in_proj_qkv_weight"], wd["in_proj_z_weight"],
+        wd["in_proj_a_weight"], wd["in_proj_b_weight"])
+    mixed, conv = hip.hip_qwen36_batched_deltanet_conv(mixed, wd["conv_state"], wd["conv1d_weight"])
+    update, state = hip.hip_qwen36_batched_deltanet_recurrent_output(
+        mixed, z, a, b, wd["recurrent_state"], wd["out_proj_weight"], wd["linear_norm_weight"], wd["a_log"],
+        wd["dt_bias"], **_dims(REAL))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(plan.update, update, atol=1e-4, rtol=1e-3)
+    torch.testing.assert_close(plan.next_recurrent_state, state, atol=1e-5, rtol=1e-4)
+    torch.testing.assert_close(plan.next_conv_state.float(), conv.float(), atol=1e-2, rtol=1e-2)
+
+
+def test_step_single_launch_repeated_calls_stay_consistent(device, real_dn):
+    # The launch tag advances every launch: cycling inputs through one
+    # workspace must keep reproducing each input's first result bit for bit.
+    from fastkernels_amd.plan import DeltaNetStepPlan
+
+    plan = DeltaNetStepPlan(_to(real_dn, device), 2, REAL)
+    xs = [wl.make_hidden(2, REAL.hidden_size, seed=80 + i).to(device) for i in range(3)]
+    first = []
+    for x in xs:
+        plan.hidden.copy_(x)
+        plan.run()
+        first.append((plan.update.clone(), plan.next_recurrent_state.clone()))
+    for _ in range(4):
+        for x, (u, s) in zip(xs, first):
+            plan.hidden.copy_(x)
+            plan.run()
+            assert torch.equal(plan.update, u)
+            assert torch.equal(plan.next_recurrent_state, s)
