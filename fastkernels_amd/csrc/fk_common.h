@@ -91,6 +91,26 @@ __device__ __forceinline__ Raw8<BF16> load_raw8_stream(const void* base, size_t 
   return r;
 }
 
+// Raw bits of N elements p[base + i * stride] of a bf16 (BF) or fp32 array;
+// elements from n_valid on repeat element 0, so p[base] must exist and the
+// caller ignores them.  The loads are straight-line, with no per-lane branch,
+// no zeroed destination and no conversion beside them: any of those makes
+// the compiler wait for every load in flight (the weight tiles included)
+// right there.  Bits are turned into values where they are used.
+template <bool BF, int N>
+__device__ __forceinline__ void gather_raw(const void* p, size_t base, size_t stride, int n_valid, uint32_t (&out)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const size_t idx = base + (size_t)(i < n_valid ? i : 0) * stride;
+    out[i] = BF ? (uint32_t)reinterpret_cast<const uint16_t*>(p)[idx] : reinterpret_cast<const uint32_t*>(p)[idx];
+  }
+}
+
+template <bool BF>
+__device__ __forceinline__ float raw_value(uint32_t r) {
+  return __uint_as_float(BF ? r << 16 : r);
+}
+
 template <bool BF16>
 __device__ __forceinline__ void raw8_to_f32(const Raw8<BF16>& r, float out[8]) {
   if constexpr (BF16) {

@@ -806,13 +806,22 @@ __device__ __forceinline__ void fused_gateup_item(const Raw8<true> (&wg)[4], con
   const int nch = H >> 3;
   for (int pp = 0; pp < npairs; ++pp) {
     const int t = toks ? toks[pp] : pp;
+    // bf16 tokens: the four chunks are loaded together (clamped in range),
+    // so a token costs one round trip, not one per chunk (fp32 chunks are
+    // loaded one at a time, which keeps the registers within budget)
+    Raw8<BFX> xr[BFX ? 4 : 1];
+    if constexpr (BFX) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) xr[j] = load_raw8<BFX>(x, (size_t)t * H + (size_t)min(lane + kWave * j, nch - 1) * 8);
+    }
     float g = 0.f, u = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int c = lane + kWave * j;
       if (c < nch) {
         float x8[8], a8[8], b8[8];
-        load8_f32<BFX>(x, (size_t)t * H + (size_t)c * 8, x8);
+        if constexpr (BFX) raw8_to_f32<BFX>(xr[j], x8);
+        else load8_f32<BFX>(x, (size_t)t * H + (size_t)c * 8, x8);
         raw8_to_f32<true>(wg[j], a8);
         raw8_to_f32<true>(wu[j], b8);
 #pragma unroll
@@ -906,7 +915,11 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   const int T = ONE ? 1 : a.T, H = a.H, E = a.E, K = a.K, I = f.I, P = T * K;
   const int nch = H >> 3;
   uint32_t* err = &a.ws.tickets[kTicketError];
-  const uint32_t tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
+  // The launch tag (epoch + 1) is loaded after the wavefront's P1 weight
+  // loads are issued: computed from a load issued first, it would make every
+  // wavefront wait for that load before issuing anything else.
+  uint32_t tag = 0;
+  bool have_tag = false;
   if (tid == 0) s_fail = 0;
   __syncthreads();
 
@@ -920,24 +933,28 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       const int e = unit * 8 + wave;
       float mine = 0.f;
       if (e < E) {
-        // All loads of the row (weights, every token, then the norm weight)
-        // are issued before the first use: indices are clamped in range and
+        // All loads of the row (weights, token 0, the bf16 norm weight) are
+        // issued before the first use: indices are clamped in range and
         // out-of-range chunks are zeroed afterwards, so there is no branch
-        // between them.
-        Raw8<true> wr[4];
+        // between them (a load whose dtype is tested at run time would wait
+        // for every load before it).
+        Raw8<true> wr[4], nr[4];
         Raw8<BFX> xr[4];  // token 0 (the only one when ONE) rides with the weights
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int cc = min(lane + kWave * j, nch - 1);
           wr[j] = load_raw8<true>(a.W, (size_t)e * H + (size_t)cc * 8);
           xr[j] = load_raw8<BFX>(a.x, (size_t)cc * 8);
+          nr[j] = load_raw8<true>(a.nw, (size_t)cc * 8);
         }
+        tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
+        have_tag = true;
         float wn[4][8];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int c = lane + kWave * j;
           float w8[8], n8[8];
-          load8_any(a.nw, a.nw_dt, (size_t)min(c, nch - 1) * 8, n8);
+          raw8_to_f32<true>(nr[j], n8);
           raw8_to_f32<true>(wr[j], w8);
 #pragma unroll
           for (int qq = 0; qq < 8; ++qq) wn[j][qq] = c < nch ? w8[qq] * (a.off + n8[qq]) : 0.f;
@@ -982,18 +999,30 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
           wu[j] = load_raw8_stream<true>(f.sgu, (size_t)(I + i) * H + (size_t)c * 8);
         }
       }
+      tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
+      have_tag = true;
       fused_gateup_item<BFX>(wg, wu, a.x, H, lane, T, nullptr, &s_chunk[0][wave]);
     } else if (wave == 0) {
       // Shared-expert gate of every token: one row like the router's, loads
       // issued together as there.
+      // (the gate weight is bf16 here; a NULL gate reads the norm weight, a
+      // valid address, and the products are dropped)
       Raw8<BFX> xr[4];
+      Raw8<true> gr[4];
+      const void* gsrc = f.sg ? f.sg : a.nw;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) xr[j] = load_raw8<BFX>(a.x, (size_t)min(lane + kWave * j, nch - 1) * 8);
+      for (int j = 0; j < 4; ++j) {
+        const int cc = min(lane + kWave * j, nch - 1);
+        xr[j] = load_raw8<BFX>(a.x, (size_t)cc * 8);
+        gr[j] = load_raw8<true>(gsrc, (size_t)cc * 8);
+      }
+      tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
+      have_tag = true;
       float g8[4][8];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int c = lane + kWave * j;
-        if (f.sg) load8_any(f.sg, f.sg_dt, (size_t)min(c, nch - 1) * 8, g8[j]);
+        raw8_to_f32<true>(gr[j], g8[j]);
 #pragma unroll
         for (int qq = 0; qq < 8; ++qq) g8[j][qq] = (f.sg && c < nch) ? g8[j][qq] : 0.f;
       }
@@ -1036,6 +1065,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
     }
     __syncthreads();
   }
+  if (!have_tag) tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
   // Started record of this workgroup: every wavefront has used the epoch it
   // read (its LDS write needs the loaded value), so the epoch may advance
   // once all records of this launch are there.
@@ -1047,9 +1077,10 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   const int r_first = q0;
   Raw8<true> sdr;
   if (r_first < H && lane * 8 < I) sdr = load_raw8_stream<true>(f.sdn, (size_t)r_first * I + (size_t)lane * 8);
-  float x_first = 0.f;
-  if (f.layer_out && r_first < H && lane < T)
-    x_first = load_scalar(a.x, BFX ? FK_DTYPE_BF16 : FK_DTYPE_F32, (size_t)lane * H + r_first);
+  // (raw bits, converted where used: a conversion here would wait for the
+  // down-row load above)
+  uint32_t x_first_raw[1];
+  gather_raw<BFX>(a.x, f.layer_out && r_first < H && lane < T ? (size_t)lane * H + r_first : 0, 0, 1, x_first_raw);
 
   // ---------------- P2: top-k of every token, routing tables in LDS --------
   int tk_id = 0;
@@ -1193,7 +1224,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       const float o = wave_sum(acc);
       if (lane == 0) {
         f.out[r] = o;
-        if (f.layer_out) f.layer_out[r] = x_first + o;
+        if (f.layer_out) f.layer_out[r] = raw_value<BFX>(x_first_raw[0]) + o;
       }
       continue;
     }
@@ -1239,7 +1270,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
           const size_t off = (size_t)tt * H + r;
           f.out[off] = o;
           if (f.layer_out)
-            f.layer_out[off] = (first ? x_first : load_scalar(a.x, BFX ? FK_DTYPE_BF16 : FK_DTYPE_F32, off)) + o;
+            f.layer_out[off] = (first ? raw_value<BFX>(x_first_raw[0]) : load_scalar(a.x, BFX ? FK_DTYPE_BF16 : FK_DTYPE_F32, off)) + o;
         }
       }
     }
@@ -1262,7 +1293,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
 constexpr int kTagRouterMaxTokens = 32;
 constexpr int kTagRouterTokensPerUnit = 4;
 
-template <bool BFW, bool BFX>
+template <bool BFW, bool BFX, bool BFN>
 __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   constexpr int TU = kTagRouterTokensPerUnit;
   __shared__ int s_ids[kTagRouterMaxTokens * 8];
@@ -1283,7 +1314,11 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
 
   float mine = 0.f;  // lane t < nt: logit of token t0 + t
   if (e < E) {
+    // Every load of the row is issued before the first use (the norm weight
+    // with a compile-time dtype: a run-time dtype test would wait for every
+    // load before it).
     Raw8<BFW> wr[4];
+    Raw8<BFN> nr[4];
     Raw8<BFX> xr[TU][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -1291,13 +1326,14 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
       wr[j] = load_raw8<BFW>(a.W, (size_t)e * H + (size_t)cc * 8);
 #pragma unroll
       for (int t = 0; t < TU; ++t) xr[t][j] = load_raw8<BFX>(a.x, (size_t)(t0 + min(t, nt - 1)) * H + (size_t)cc * 8);
+      nr[j] = load_raw8<BFN>(a.nw, (size_t)cc * 8);
     }
     float wn[4][8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int c = lane + kWave * j;
       float w8[8], n8[8];
-      load8_any(a.nw, a.nw_dt, (size_t)min(c, nch - 1) * 8, n8);
+      raw8_to_f32<BFN>(nr[j], n8);
       raw8_to_f32<BFW>(wr[j], w8);
 #pragma unroll
       for (int q = 0; q < 8; ++q) wn[j][q] = c < nch ? w8[q] * (a.off + n8[q]) : 0.f;
@@ -1397,9 +1433,14 @@ static int check_ws(void* ws, size_t bytes, int T, int K, int E, int I, int H, M
     __VA_ARGS__                           \
   }
 
-static bool fused_eligible(int T, int H, int I, int E, int K, int router_dt, int expert_dt, bool has_shared) {
+// norm_dt / gate_dt: the router's norm weight and the shared-expert gate
+// weight, which the single-launch kernel reads as bf16 (gate_dt is ignored
+// when there is no gate weight).
+static bool fused_eligible(int T, int H, int I, int E, int K, int router_dt, int expert_dt, bool has_shared, int norm_dt,
+                           bool has_gate, int gate_dt) {
   return T >= 1 && T <= kFusedMaxTokens && H <= 2048 && I <= 512 && I % kFusedChunk == 0 && E <= kFusedMaxExperts && K <= 8 &&
-         router_dt == FK_DTYPE_BF16 && expert_dt == FK_DTYPE_BF16 && has_shared;
+         router_dt == FK_DTYPE_BF16 && expert_dt == FK_DTYPE_BF16 && has_shared && norm_dt == FK_DTYPE_BF16 &&
+         (!has_gate || gate_dt == FK_DTYPE_BF16);
 }
 
 constexpr size_t kFusedMaxDynLds = ((size_t)(kFusedMaxPairs + kFusedMaxTokens) * 512 + kFusedMaxTokens) * sizeof(float);
@@ -1445,10 +1486,10 @@ static bool tagged_router_eligible(const RouterArgs& ra) {
   return ra.T <= kTagRouterMaxTokens && ra.E <= kFusedMaxExperts && ra.H <= 2048 && ra.K <= 8;
 }
 
-template <bool BW, bool BX>
+template <bool BW, bool BX, bool BN>
 static int launch_router_tagged_t(const RouterArgs& ra, hipStream_t stream) {
   static int cap_cache[64] = {0};
-  auto kernel = moe_router_tagged_kernel<BW, BX>;
+  auto kernel = moe_router_tagged_kernel<BW, BX, BN>;
   const int units = ((ra.E + 7) / 8) * ((ra.T + kTagRouterTokensPerUnit - 1) / kTagRouterTokensPerUnit);
   // Workgroup 0 waits for every other workgroup's logits: all must be resident.
   const int cap = resident_capacity(kernel, 512, 0, cap_cache);
@@ -1461,7 +1502,10 @@ static int launch_router(const RouterArgs& ra, int router_dt, int hidden_dt, hip
   const bool bfw = router_dt == FK_DTYPE_BF16, bfx = hidden_dt == FK_DTYPE_BF16;
   if (tagged_router_eligible(ra)) {
     int st = FK_OK;
-    FK_DISPATCH_BOOL(bfw, BW, FK_DISPATCH_BOOL(bfx, BX, { st = launch_router_tagged_t<BW, BX>(ra, stream); }))
+    const bool bfn = ra.nw_dt == FK_DTYPE_BF16;
+    FK_DISPATCH_BOOL(bfw, BW, FK_DISPATCH_BOOL(bfx, BX, FK_DISPATCH_BOOL(bfn, BN, {
+      st = launch_router_tagged_t<BW, BX, BN>(ra, stream);
+    })))
     return st;
   }
   const bool wide = ra.H > 2048, many = ra.E > 256;
@@ -1665,7 +1709,8 @@ int fk_moe_layer(const void* hidden, int hidden_dtype, const void* norm_weight, 
   st = check_ws(workspace, workspace_bytes, tokens, top_k, num_experts, intermediate, hidden_size, &ws);
   if (st) return st;
   if (fused_eligible(tokens, hidden_size, intermediate, num_experts, top_k, router_dtype, expert_dtype,
-                     shared_gate_up != nullptr)) {
+                     shared_gate_up != nullptr, norm_dtype, shared_gate != nullptr, shared_gate_dtype) &&
+      (!shared_gate || aligned16(shared_gate))) {
     if (!is_float_dtype(norm_dtype) || (router_bias && !is_float_dtype(bias_dtype)))
       return fail(FK_ERR_DTYPE, "router inputs must be f32 or bf16");
     if (!norm_weight || !router_weight || !logits || !topk_ids || !topk_weights)
