@@ -632,13 +632,20 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(ExpertArgs a) {
 
   // Shared-expert gate sigmoid(w_g . x_t), once per token.
   if (shared && chunk == 0 && a.sg) {
+    // (a 16-byte aligned gate weight is read 8 elements per load)
+    const bool sg_bf = a.sg_dt == FK_DTYPE_BF16, sg_vec = (reinterpret_cast<uintptr_t>(a.sg) & 15u) == 0;
     for (int t = wave; t < a.T; t += 4) {
       float d = 0.f;
       for (int c = lane; c < nch; c += kWave) {
-        float x8[8];
+        float x8[8], g8[8];
         load8_f32<BFX>(a.x, (size_t)t * a.H + (size_t)c * 8, x8);
+        if (sg_vec && sg_bf) load8_f32<true>(a.sg, (size_t)c * 8, g8);
+        else if (sg_vec) load8_f32<false>(a.sg, (size_t)c * 8, g8);
+        else
 #pragma unroll
-        for (int q = 0; q < 8; ++q) d = fmaf(x8[q], load_scalar(a.sg, a.sg_dt, (size_t)c * 8 + q), d);
+          for (int q = 0; q < 8; ++q) g8[q] = load_scalar(a.sg, a.sg_dt, (size_t)c * 8 + q);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) d = fmaf(x8[q], g8[q], d);
       }
       d = wave_sum(d);
       if (lane == 0) a.ws.sgate[t] = sigmoid(d);
@@ -719,25 +726,41 @@ __global__ __launch_bounds__(256) void moe_down_kernel(ExpertArgs a) {
 
 // out[t, h] = sum_k w[t,k] * y[pos(t,k), h]  (slot order k = 0..K-1)
 //             + g_t * y[P + t, h]            (shared expert, g_t = sigmoid(w_g . x_t) or 1)
-// layer_out = x + out.
+// layer_out = x + out (LO: layer_out is written).  BFX: bf16 hidden
+// states.  Every load is issued
+// before the first use, in two dependent rounds (slot positions, weights,
+// gate and residual input; then the K + 1 rows of y), with indices clamped
+// in range and unused values dropped: a loop over the slots would make
+// each slot wait for its position and then for its y value.
+template <bool BFX, bool LO>
 __global__ __launch_bounds__(256) void moe_combine_kernel(ExpertArgs a) {
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
   const size_t total = (size_t)a.T * a.H;
   if (idx >= total) return;
   const int t = (int)(idx / a.H);
   const int h = (int)(idx - (size_t)t * a.H);
-  const int P = a.T * a.K;
+  const int K = a.K, P = a.T * K;  // K <= 8 (host checks)
+  int inv[8];
+  float wk[8], yv[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int pair = t * K + min(k, K - 1);
+    inv[k] = a.ws.inverse[pair];
+    wk[k] = a.ws.wts[pair];
+  }
+  const float g = a.ws.sgate[t];
+  uint32_t xr[1];
+  if constexpr (LO) gather_raw<BFX>(a.x, idx, 0, 1, xr);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) yv[k] = a.ws.y[(size_t)inv[k] * a.H + h];
+  const float ys = a.ws.y[(size_t)(P + (a.has_shared ? t : 0)) * a.H + h];
   float acc = 0.f;
-  for (int k = 0; k < a.K; ++k) {
-    const int pair = t * a.K + k;
-    acc += a.ws.wts[pair] * a.ws.y[(size_t)a.ws.inverse[pair] * a.H + h];
-  }
-  if (a.has_shared) {
-    const float g = a.sg ? a.ws.sgate[t] : 1.f;
-    acc += g * a.ws.y[(size_t)(P + t) * a.H + h];
-  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k)
+    if (k < K) acc += wk[k] * yv[k];
+  if (a.has_shared) acc += (a.sg ? g : 1.f) * ys;
   a.out[idx] = acc;
-  if (a.layer_out) a.layer_out[idx] = load_scalar(a.x, a.x_dt, idx) + acc;
+  if constexpr (LO) a.layer_out[idx] = raw_value<BFX>(xr[0]) + acc;
 }
 
 // ---------------------------------------------------------------------------
@@ -1542,7 +1565,11 @@ static int launch_experts(const ExpertArgs& ea, int expert_dt, hipStream_t strea
   st = check_launch("moe_down_kernel");
   if (st) return st;
   const size_t total = (size_t)ea.T * ea.H;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, ea);
+  const bool lo = ea.layer_out != nullptr;
+  const dim3 cgrid((unsigned)((total + 255) / 256));
+  FK_DISPATCH_BOOL(bfx, BX, FK_DISPATCH_BOOL(lo, LO, {
+    hipLaunchKernelGGL((moe_combine_kernel<BX, LO>), cgrid, dim3(256), 0, stream, ea);
+  }))
   return check_launch("moe_combine_kernel");
 }
 
