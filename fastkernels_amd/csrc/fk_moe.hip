@@ -45,6 +45,7 @@ struct MoeWs {
   uint64_t* f_act;      // [(T*K + T), I] SwiGLU activations, permuted rows then shared rows (capacity 18 * 512)
   uint64_t* f_sgate;    // [T] shared-expert gates
   uint64_t* f_started;  // [grid] one tagged record per workgroup of the launch (capacity 1024)
+  uint64_t* f_sel;      // [T, K] small-batch router: expert ids chosen per token (capacity 32 * 8)
   int32_t* counts;      // [E]
   int32_t* offsets;     // [E+1] exclusive prefix of counts
   int32_t* perm;        // [P] permuted position -> pair index t*K+k
@@ -67,6 +68,7 @@ constexpr int kFusedMaxGrid = 1024;
 constexpr size_t kFusedLogitWords = 32 * 256;  // tagged router: T <= 32
 constexpr size_t kFusedActWords = (2 * 8 + 2) * 512;
 constexpr size_t kFusedGateWords = 2;
+constexpr size_t kFusedSelWords = 32 * 8;  // small-batch router: T <= 32, K <= 8
 
 // Regions sized by I or H come last: fk_moe_router and fk_moe_align lay the
 // workspace out with I = H = 0 and must find the routing tables where
@@ -84,6 +86,7 @@ static size_t moe_ws_layout(int T, int K, int E, int I, int H, char* base, MoeWs
   ws->f_act = reinterpret_cast<uint64_t*>(take(kFusedActWords * 8));
   ws->f_sgate = reinterpret_cast<uint64_t*>(take(kFusedGateWords * 8));
   ws->f_started = reinterpret_cast<uint64_t*>(take((size_t)kFusedMaxGrid * 8));
+  ws->f_sel = reinterpret_cast<uint64_t*>(take(kFusedSelWords * 8));
   ws->counts = reinterpret_cast<int32_t*>(take((size_t)E * 4));
   ws->offsets = reinterpret_cast<int32_t*>(take((size_t)(E + 1) * 4));
   ws->perm = reinterpret_cast<int32_t*>(take(P * 4));
@@ -226,6 +229,7 @@ struct RouterArgs {
   const void* bias;
   int nw_dt, bias_dt;
   int T, H, E, K;
+  int tu;  // tokens per workgroup of the small-batch router (set by its launcher)
   float eps, off;
   float* logits;
   int64_t* ids_out;
@@ -244,57 +248,90 @@ struct RouterArgs {
 // order.  Each lane keeps its keys sorted, so giving up its head is a shift.
 // Lane k < K ends with the k-th selection; weights are renormalised by the
 // sum of the selected probabilities in selection order.
-template <int NJE>
-__device__ void topk_select_keys32(float (&p)[NJE], int E, int K, int lane, int& out_id, float& out_w) {
-  static_assert(NJE == 4, "keys carry j in two bits");
-  float m = -INFINITY;
+// NT tokens at once (token i in p[i]): the tokens' chains are independent,
+// so their reductions interleave instead of running back to back.
+template <int NT>
+__device__ void topk_select_keys32_multi(float (&p)[NT][4], int E, int K, int lane, int (&out_id)[NT],
+                                         float (&out_w)[NT]) {
+  float m[NT], s[NT];
 #pragma unroll
-  for (int j = 0; j < NJE; ++j) m = fmaxf(m, p[j]);
-  m = wave_max(m);
-  float s = 0.f;
+  for (int i = 0; i < NT; ++i) {
+    m[i] = -INFINITY;
 #pragma unroll
-  for (int j = 0; j < NJE; ++j) {
-    const int ex = lane + kWave * j;
-    p[j] = ex < E ? expf(p[j] - m) : 0.f;
-    s += p[j];
+    for (int j = 0; j < 4; ++j) m[i] = fmaxf(m[i], p[i][j]);
   }
-  s = wave_sum(s);
-  uint32_t key[NJE];
 #pragma unroll
-  for (int j = 0; j < NJE; ++j)
-    key[j] = lane + kWave * j < E ? ((__float_as_uint(p[j] / s) + 1u) << 2) | (uint32_t)(NJE - 1 - j) : 0u;
-  // Sort the lane's keys descending (keys are distinct within a lane).
+  for (int i = 0; i < NT; ++i) m[i] = wave_max(m[i]);
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    s[i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ex = lane + kWave * j;
+      p[i][j] = ex < E ? expf(p[i][j] - m[i]) : 0.f;
+      s[i] += p[i][j];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NT; ++i) s[i] = wave_sum(s[i]);
+  uint32_t key[NT][4];
   auto cswap = [](uint32_t& a, uint32_t& b) {
     const uint32_t hi = a > b ? a : b, lo = a > b ? b : a;
     a = hi;
     b = lo;
   };
-  cswap(key[0], key[1]);
-  cswap(key[2], key[3]);
-  cswap(key[0], key[2]);
-  cswap(key[1], key[3]);
-  cswap(key[1], key[2]);
-  float denom = 0.f;
-  int my_id = 0;
-  float my_v = 0.f;
+  float denom[NT], my_v[NT];
+  int my_id[NT];
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      key[i][j] = lane + kWave * j < E ? ((__float_as_uint(p[i][j] / s[i]) + 1u) << 2) | (uint32_t)(3 - j) : 0u;
+    // Sort the lane's keys descending (keys are distinct within a lane).
+    cswap(key[i][0], key[i][1]);
+    cswap(key[i][2], key[i][3]);
+    cswap(key[i][0], key[i][2]);
+    cswap(key[i][1], key[i][3]);
+    cswap(key[i][1], key[i][2]);
+    denom[i] = 0.f;
+    my_id[i] = 0;
+    my_v[i] = 0.f;
+  }
   for (int k = 0; k < K; ++k) {
-    const uint32_t mk = wave_max_u32(key[0]);
-    const int sel_lane = __ffsll((unsigned long long)__ballot(key[0] == mk)) - 1;
-    const int sel = sel_lane + kWave * (int)(NJE - 1 - (mk & 3u));
-    const float mv = __uint_as_float((mk >> 2) - 1u);
-    const bool own = lane == sel_lane;
-    key[0] = own ? key[1] : key[0];
-    key[1] = own ? key[2] : key[1];
-    key[2] = own ? key[3] : key[2];
-    key[3] = own ? 0u : key[3];
-    denom += mv;
-    if (lane == k) {
-      my_id = sel;
-      my_v = mv;
+#pragma unroll
+    for (int i = 0; i < NT; ++i) {
+      const uint32_t mk = wave_max_u32(key[i][0]);
+      const int sel_lane = __ffsll((unsigned long long)__ballot(key[i][0] == mk)) - 1;
+      const int sel = sel_lane + kWave * (int)(3 - (mk & 3u));
+      const float mv = __uint_as_float((mk >> 2) - 1u);
+      const bool own = lane == sel_lane;
+      key[i][0] = own ? key[i][1] : key[i][0];
+      key[i][1] = own ? key[i][2] : key[i][1];
+      key[i][2] = own ? key[i][3] : key[i][2];
+      key[i][3] = own ? 0u : key[i][3];
+      denom[i] += mv;
+      if (lane == k) {
+        my_id[i] = sel;
+        my_v[i] = mv;
+      }
     }
   }
-  out_id = my_id;
-  out_w = my_v / denom;
+#pragma unroll
+  for (int i = 0; i < NT; ++i) {
+    out_id[i] = my_id[i];
+    out_w[i] = my_v[i] / denom[i];
+  }
+}
+
+template <int NJE>
+__device__ void topk_select_keys32(float (&p)[NJE], int E, int K, int lane, int& out_id, float& out_w) {
+  static_assert(NJE == 4, "keys carry j in two bits");
+  float pm[1][4] = {{p[0], p[1], p[2], p[3]}};
+  int id[1];
+  float w[1];
+  topk_select_keys32_multi<1>(pm, E, K, lane, id, w);
+  out_id = id[0];
+  out_w = w[0];
 }
 
 // Same selection with 64-bit keys (bits(p) << 32 | ~expert id), for lanes
@@ -1304,37 +1341,83 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
 // Router for small batches (T <= 32, E <= 256, H <= 2048): no grid barrier.
 //
 // Workgroup (ub, tb) computes the logits of expert rows 8ub.. (one per
-// wavefront) for tokens 4tb.. (loads of the row and the tokens issued
-// together) and writes them as one tagged 64-byte run per token (the
-// launch-tag protocol of the single-launch layer, same epoch counter).
-// Workgroup 0 then polls every logit, computes the top-k of each token (one
-// wavefront per token), advances the epoch (every workgroup has written
-// logits carrying this launch's tag, so all have read the epoch) and builds
-// the routing tables for the expert stage.  Same arithmetic as
+// wavefront) for tokens tu*tb.. (tu = 2 or 4 tokens per workgroup; loads of
+// the row and the tokens issued together) and writes them as one tagged
+// run per token (the launch-tag protocol of the single-launch layer, same
+// epoch counter).  Workgroup t < T then polls the logits of token t and
+// computes its top-k with one wavefront (a selection is issue-bound, so the
+// tokens go to different CUs), writes the token's ids and weights, and
+// publishes the ids as tagged words.  Workgroup 0 polls the T*K ids,
+// advances the epoch (the ids of every token carry this launch's tag, so
+// every workgroup has written logits with it and has read the epoch) and
+// builds the routing tables for the expert stage.  Same arithmetic as
 // moe_router_kernel, so both give identical logits and ids.
 // ---------------------------------------------------------------------------
 constexpr int kTagRouterMaxTokens = 32;
-constexpr int kTagRouterTokensPerUnit = 4;
+constexpr int kTagRouterTokensPerUnit = 4;  // most tokens per workgroup
+static_assert(kFusedSelWords >= (size_t)kTagRouterMaxTokens * 8, "router selection region too small");
+
+// Routing tables for T <= 32 tokens and E <= 512 experts (one expert per
+// thread of a 512-thread workgroup) from s_mask[e], whose bit t says that
+// token t chose expert e (a token chooses an expert at most once).  Counts
+// are popcounts, offsets their exclusive prefix, and pair j = t*K + k goes
+// to offsets[e] + (earlier tokens that chose e): the stable order by expert
+// of a counting sort, as build_routing_tables gives.
+__device__ void build_routing_tables_masks(const int* s_ids, const uint32_t* s_mask, int T, int K, int E, MoeWs ws,
+                                           int* s_off) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ int s_wtot[kFusedWaves][2];
+  const uint32_t msk = tid < E ? s_mask[tid] : 0u;
+  const int c = __popc(msk), nz = c > 0 ? 1 : 0;
+  const int isum = wave_incl_scan(c, lane), inz = wave_incl_scan(nz, lane);
+  if (lane == kWave - 1) {
+    s_wtot[wave][0] = isum;
+    s_wtot[wave][1] = inz;
+  }
+  __syncthreads();
+  int psum = 0, pnz = 0;
+  for (int w = 0; w < wave; ++w) {
+    psum += s_wtot[w][0];
+    pnz += s_wtot[w][1];
+  }
+  if (tid < E) {
+    const int off = psum + isum - c;
+    s_off[tid] = off;
+    ws.offsets[tid] = off;
+    ws.counts[tid] = c;
+    if (nz) ws.active[pnz + inz - 1] = tid;
+  }
+  const int P = T * K;
+  if (tid == 0) {
+    int na = 0;
+    for (int w = 0; w < kFusedWaves; ++w) na += s_wtot[w][1];
+    ws.offsets[E] = P;
+    ws.num_active[0] = na;
+  }
+  __syncthreads();
+  for (int j = tid; j < P; j += kFusedWaves * kWave) {
+    const int t = j / K, e = s_ids[j];
+    const int pos = s_off[e] + __popc(s_mask[e] & ((1u << t) - 1u));
+    ws.perm[pos] = j;
+    ws.inverse[j] = pos;
+  }
+}
 
 template <bool BFW, bool BFX, bool BFN>
 __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   constexpr int TU = kTagRouterTokensPerUnit;
   __shared__ int s_ids[kTagRouterMaxTokens * 8];
-  __shared__ float s_w[kTagRouterMaxTokens * 8];
-  __shared__ int s_rank[kTagRouterMaxTokens * 8];
-  __shared__ int s_wcnt[kFusedWaves * kFusedMaxExperts];
-  __shared__ int s_cnt[kFusedMaxExperts];
+  __shared__ uint32_t s_mask[kFusedMaxExperts];
   __shared__ int s_off[kFusedMaxExperts];
   __shared__ float s_chunk[TU][8];
   __shared__ int s_fail;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, H = a.H, E = a.E, K = a.K, nch = H >> 3;
-  const int nrb = (E + 7) / 8;
+  const int nrb = (E + 7) / 8, tu = a.tu;
   const int ub = blockIdx.x % nrb, tb = blockIdx.x / nrb;
-  const int e = ub * 8 + wave, t0 = tb * TU, nt = min(TU, T - t0);
+  const int e = ub * 8 + wave, t0 = tb * tu, nt = min(tu, T - t0);
   const uint32_t tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
   if (tid == 0) s_fail = 0;
-
   float mine = 0.f;  // lane t < nt: logit of token t0 + t
   if (e < E) {
     // Every load of the row is issued before the first use (the norm weight
@@ -1394,11 +1477,12 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
       store_tagged(a.ws.f_logits + (size_t)(t0 + t) * E + ee, v, tag);
     }
   }
-  if (blockIdx.x != 0) return;
+  if (blockIdx.x >= T) return;
 
-  // ---- workgroup 0: top-k of every token, epoch, routing tables ----------
-  for (int t = wave; t < T; t += kFusedWaves) {
+  // ---- workgroup t < T: top-k of token t ---------------------------------
+  if (wave == 0) {
     constexpr int NJE = kFusedMaxExperts / kWave;
+    const int t = blockIdx.x;
     uint64_t w[NJE];
     const uint64_t* srcs[NJE];
 #pragma unroll
@@ -1415,9 +1499,34 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
     float wt;
     topk_select_regs<NJE>(p, E, K, lane, id, wt);
     if (lane < K) {
-      s_ids[t * K + lane] = id;
-      s_w[t * K + lane] = wt;
+      const int j = t * K + lane;
+      a.ids_out[j] = id;
+      a.w_out[j] = wt;
+      a.ws.ids32[j] = id;
+      a.ws.wts[j] = wt;
+      store_tagged(a.ws.f_sel + j, __int_as_float(id), tag);
     }
+  }
+  if (blockIdx.x != 0) {
+    if (tid == 0 && s_fail)
+      __hip_atomic_fetch_or(&a.ws.tickets[kTicketError], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
+                            __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
+
+  // ---- workgroup 0: every token's ids, epoch, routing tables --------------
+  for (int i = tid; i < E; i += kFusedWaves * kWave) s_mask[i] = 0u;
+  __syncthreads();
+  const int P = T * K;  // <= 256: one id per thread
+  if (tid < P) {
+    uint64_t w[1];
+    const uint64_t* srcs[1] = {a.ws.f_sel + tid};
+    w[0] = load_tagged(srcs[0]);
+    if (!poll_tagged<1>(w, srcs, tag)) s_fail = 1;
+    // (clamped: after a failed poll the word may come from another launch)
+    const int id = min(max(__float_as_int(value_of(w[0])), 0), E - 1);
+    s_ids[tid] = id;
+    atomicOr(&s_mask[id], 1u << (tid / K));
   }
   __syncthreads();
   if (tid == 0) {
@@ -1425,14 +1534,7 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
     if (s_fail) __hip_atomic_fetch_or(&a.ws.tickets[kTicketError], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT);
   }
-  const int P = T * K;
-  for (int j = tid; j < P; j += kFusedWaves * kWave) {
-    a.ids_out[j] = s_ids[j];
-    a.w_out[j] = s_w[j];
-    a.ws.ids32[j] = s_ids[j];
-    a.ws.wts[j] = s_w[j];
-  }
-  build_routing_tables<kFusedWaves>(s_ids, P, E, a.ws, s_cnt, s_off, s_rank, s_wcnt);
+  build_routing_tables_masks(s_ids, s_mask, T, K, E, a.ws, s_off);
 }
 
 // ---------------------------------------------------------------------------
@@ -1510,12 +1612,16 @@ static bool tagged_router_eligible(const RouterArgs& ra) {
 }
 
 template <bool BW, bool BX, bool BN>
-static int launch_router_tagged_t(const RouterArgs& ra, hipStream_t stream) {
+static int launch_router_tagged_t(const RouterArgs& ra_in, hipStream_t stream) {
   static int cap_cache[64] = {0};
   auto kernel = moe_router_tagged_kernel<BW, BX, BN>;
-  const int units = ((ra.E + 7) / 8) * ((ra.T + kTagRouterTokensPerUnit - 1) / kTagRouterTokensPerUnit);
-  // Workgroup 0 waits for every other workgroup's logits: all must be resident.
+  // Workgroup 0 waits for every other workgroup's logits: all must be
+  // resident.  Two tokens per workgroup where that grid fits, else four.
   const int cap = resident_capacity(kernel, 512, 0, cap_cache);
+  const int nrb = (ra_in.E + 7) / 8;
+  RouterArgs ra = ra_in;
+  ra.tu = nrb * ((ra.T + 1) / 2) <= cap ? 2 : kTagRouterTokensPerUnit;
+  const int units = nrb * ((ra.T + ra.tu - 1) / ra.tu);
   if (units > cap) return fail(FK_ERR_UNSUPPORTED, "router grid %d exceeds co-resident capacity %d", units, cap);
   hipLaunchKernelGGL(kernel, dim3(units), dim3(512), 0, stream, ra);
   return check_launch("moe_router_tagged_kernel");
@@ -1665,6 +1771,7 @@ int fk_moe_router(const void* hidden, int hidden_dtype, const void* norm_weight,
   ra.H = hidden_size;
   ra.E = num_experts;
   ra.K = top_k;
+  ra.tu = kTagRouterTokensPerUnit;
   ra.eps = eps;
   ra.off = norm_offset;
   ra.logits = logits;
@@ -1755,6 +1862,7 @@ int fk_moe_layer(const void* hidden, int hidden_dtype, const void* norm_weight, 
     fa.r.H = hidden_size;
     fa.r.E = num_experts;
     fa.r.K = top_k;
+    fa.r.tu = 1;
     fa.r.eps = eps;
     fa.r.off = norm_offset;
     fa.r.logits = logits;
