@@ -51,6 +51,7 @@ struct MoeWs {
   int32_t* perm;        // [P] permuted position -> pair index t*K+k
   int32_t* inverse;     // [P] pair index -> permuted position
   int32_t* active;      // [E] ids of experts with count > 0, ascending
+  int4* slots;          // [E] per active expert: {id, first permuted position, pair count, token of the first pair}
   int32_t* num_active;  // [1]
   int32_t* ids32;       // [P] clamped expert ids
   float* wts;           // [P] routing weights (fp32)
@@ -92,6 +93,7 @@ static size_t moe_ws_layout(int T, int K, int E, int I, int H, char* base, MoeWs
   ws->perm = reinterpret_cast<int32_t*>(take(P * 4));
   ws->inverse = reinterpret_cast<int32_t*>(take(P * 4));
   ws->active = reinterpret_cast<int32_t*>(take((size_t)E * 4));
+  ws->slots = reinterpret_cast<int4*>(take((size_t)E * 16));
   ws->num_active = reinterpret_cast<int32_t*>(take(4));
   ws->ids32 = reinterpret_cast<int32_t*>(take(P * 4));
   ws->wts = reinterpret_cast<float*>(take(P * 4));
@@ -121,10 +123,12 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 // running per-expert counts of its segment in s_wcnt[w][e].  A pair's
 // permuted position is offsets[e] + (pairs of e in earlier segments) +
 // (its rank inside its own segment), which preserves (token, slot) order.
-// LDS: s_ids[P] ids, s_rank[P], s_wcnt[NWV*E], s_cnt[E], s_off[E].
+// It also writes one record per active expert (ws.slots: id, first position,
+// pair count, token of the first pair) for the expert kernels.
+// LDS: s_ids[P] ids, s_rank[P], s_wcnt[NWV*E], s_cnt[E], s_off[E], s_aidx[E].
 template <int NWV>
-__device__ void build_routing_tables(const int* s_ids, int P, int E, MoeWs ws, int* s_cnt, int* s_off, int* s_rank,
-                                     int* s_wcnt) {
+__device__ void build_routing_tables(const int* s_ids, int P, int E, int K, MoeWs ws, int* s_cnt, int* s_off, int* s_rank,
+                                     int* s_wcnt, int* s_aidx) {
   constexpr int NTH = NWV * kWave;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   __shared__ int s_wtot[NWV][2];
@@ -199,7 +203,11 @@ __device__ void build_routing_tables(const int* s_ids, int P, int E, MoeWs ws, i
       s_off[e] = run;
       ws.offsets[e] = run;
       ws.counts[e] = c;
-      if (c > 0) ws.active[runnz++] = e;
+      if (c > 0) {
+        ws.active[runnz] = e;
+        ws.slots[runnz] = make_int4(e, run, c, 0);
+        s_aidx[e] = runnz++;
+      }
       run += c;
     }
   }
@@ -216,6 +224,7 @@ __device__ void build_routing_tables(const int* s_ids, int P, int E, MoeWs ws, i
     const int r = s_off[e] + s_wcnt[w * E + e] + s_rank[j];
     ws.perm[r] = j;
     ws.inverse[j] = r;
+    if (r == s_off[e]) ws.slots[s_aidx[e]].w = j / K;  // the expert's first pair
   }
 }
 
@@ -433,6 +442,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(RouterArgs a) {
   __shared__ int s_wcnt[4 * kMaxExperts];
   __shared__ int s_cnt[kMaxExperts];
   __shared__ int s_off[kMaxExperts];
+  __shared__ int s_aidx[kMaxExperts];
   __shared__ int s_last;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int e = blockIdx.x * 4 + wave;
@@ -524,7 +534,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(RouterArgs a) {
   const int P = a.T * a.K;
   for (int j = threadIdx.x; j < P; j += 256) s_ids[j] = load_coherent(a.ws.ids32 + j);
   __syncthreads();
-  build_routing_tables<4>(s_ids, P, a.E, a.ws, s_cnt, s_off, s_rank, s_wcnt);
+  build_routing_tables<4>(s_ids, P, a.E, a.K, a.ws, s_cnt, s_off, s_rank, s_wcnt, s_aidx);
   if (threadIdx.x == 0) {
     // Every workgroup has passed the barrier (it counted into ticket 1).
     a.ws.tickets[kTicketRouterBarrier] = 0u;
@@ -552,6 +562,7 @@ __global__ __launch_bounds__(256) void moe_align_kernel(AlignArgs a) {
   __shared__ int s_wcnt[4 * kMaxExperts];
   __shared__ int s_cnt[kMaxExperts];
   __shared__ int s_off[kMaxExperts];
+  __shared__ int s_aidx[kMaxExperts];
   const int P = a.T * a.K;
   for (int j = threadIdx.x; j < P; j += 256) {
     long long v = a.ids_dt == FK_DTYPE_I64 ? reinterpret_cast<const long long*>(a.ids)[j]
@@ -562,7 +573,7 @@ __global__ __launch_bounds__(256) void moe_align_kernel(AlignArgs a) {
     a.ws.wts[j] = a.w ? load_scalar(a.w, a.w_dt, j) : 0.f;
   }
   __syncthreads();
-  build_routing_tables<4>(s_ids, P, a.E, a.ws, s_cnt, s_off, s_rank, s_wcnt);
+  build_routing_tables<4>(s_ids, P, a.E, a.K, a.ws, s_cnt, s_off, s_rank, s_wcnt, s_aidx);
   __syncthreads();
   // Optional copies of the tables for callers that inspect them.
   for (int e = threadIdx.x; e < a.E; e += 256) {
@@ -610,7 +621,7 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(ExpertArgs a) {
 
   const char* W;
   bool shared = false;
-  int pos0, npairs;
+  int pos0, npairs, t = 0;  // t: token of the first pair
   if (a.has_shared && slot == 0) {
     W = reinterpret_cast<const char*>(a.sgu);
     shared = true;
@@ -618,18 +629,29 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(ExpertArgs a) {
     npairs = a.T;
   } else {
     if (a.has_shared) slot -= 1;
-    if (slot >= a.ws.num_active[0]) return;
-    const int e = a.ws.active[slot];
-    W = reinterpret_cast<const char*>(a.gu) + (size_t)e * 2 * a.I * a.H * esz;
-    pos0 = a.ws.offsets[e];
-    npairs = a.ws.counts[e];
+    // The active count and this slot's record (slot < E) are loaded
+    // together: one round trip before the weights can be fetched.
+    const int na = a.ws.num_active[0];
+    const int4 rec = a.ws.slots[slot];
+    if (slot >= na) return;
+    W = reinterpret_cast<const char*>(a.gu) + (size_t)rec.x * 2 * a.I * a.H * esz;
+    pos0 = rec.y;
+    npairs = rec.z;
+    t = rec.w;
   }
 
   const int nch = a.H >> 3;
   const int i0 = chunk * kGateUpRows + wave * 2;  // this wave's two intermediates
   const size_t rows[4] = {(size_t)i0, (size_t)i0 + 1, (size_t)a.I + i0, (size_t)a.I + i0 + 1};
 
-  // Stream the four rows (gate i0, gate i0+1, up i0, up i0+1) once.
+  // The first pair's token chunks are issued first (clamped in range), then
+  // the four rows (gate i0, gate i0+1, up i0, up i0+1), streamed once: the
+  // compiler converts the rows before the pair loop, and chunks issued
+  // after them would wait for that.  Each later pair costs one round trip
+  // (its chunks are loaded together while its token index is fetched).
+  Raw8<BFX> xr[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) xr[j] = load_raw8<BFX>(a.x, (size_t)t * a.H + (size_t)min(lane + kWave * j, nch - 1) * 8);
   Raw8<BFW> wr[4][NJ];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -642,14 +664,15 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(ExpertArgs a) {
 
   for (int pp = 0; pp < npairs; ++pp) {
     const int pos = pos0 + pp;
-    const int t = shared ? pp : a.ws.perm[pos] / a.K;
+    int t_next = 0;
+    if (pp + 1 < npairs) t_next = shared ? pp + 1 : a.ws.perm[pos + 1] / a.K;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int c = lane + kWave * j;
       if (c < nch) {
         float x8[8];
-        load8_f32<BFX>(a.x, (size_t)t * a.H + (size_t)c * 8, x8);
+        raw8_to_f32<BFX>(xr[j], x8);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           float w8[8];
@@ -664,6 +687,11 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(ExpertArgs a) {
     if (lane == 0) {
       float2 v = make_float2(silu(acc[0]) * acc[2], silu(acc[1]) * acc[3]);
       *reinterpret_cast<float2*>(a.ws.act + (size_t)pos * a.I + i0) = v;
+    }
+    if (pp + 1 < npairs) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        xr[j] = load_raw8<BFX>(a.x, (size_t)t_next * a.H + (size_t)min(lane + kWave * j, nch - 1) * 8);
     }
   }
 
@@ -710,16 +738,25 @@ __global__ __launch_bounds__(256) void moe_down_kernel(ExpertArgs a) {
     npairs = a.T;
   } else {
     if (a.has_shared) slot -= 1;
-    if (slot >= a.ws.num_active[0]) return;
-    const int e = a.ws.active[slot];
-    W = reinterpret_cast<const char*>(a.dn) + (size_t)e * a.H * a.I * esz;
-    pos0 = a.ws.offsets[e];
-    npairs = a.ws.counts[e];
+    const int na = a.ws.num_active[0];  // loaded with the record (slot < E)
+    const int4 rec = a.ws.slots[slot];
+    if (slot >= na) return;
+    W = reinterpret_cast<const char*>(a.dn) + (size_t)rec.x * a.H * a.I * esz;
+    pos0 = rec.y;
+    npairs = rec.z;
   }
   const int nci = a.I >> 3;
   const int r0 = chunk * kDownRows + wave * kDownRowsPerWave;
   constexpr int R = kDownRowsPerWave;
 
+  // Activation rows: the first pair's is issued before the weights (the
+  // compiler converts the weights before the pair loop, and loads issued
+  // after them would wait for that), each later pair's is fetched while the
+  // previous pair is computed (chunks clamped in range, out-of-range ones
+  // unused).
+  float av[NJI][8];
+#pragma unroll
+  for (int j = 0; j < NJI; ++j) load8_act(a.ws.act, (size_t)pos0 * a.I + (size_t)min(lane + kWave * j, nci - 1) * 8, av[j]);
   Raw8<BFW> wr[R][NJI];
 #pragma unroll
   for (int r = 0; r < R; ++r)
@@ -731,6 +768,12 @@ __global__ __launch_bounds__(256) void moe_down_kernel(ExpertArgs a) {
 
   for (int pp = 0; pp < npairs; ++pp) {
     const int pos = pos0 + pp;
+    float an[NJI][8];
+    if (pp + 1 < npairs) {
+#pragma unroll
+      for (int j = 0; j < NJI; ++j)
+        load8_act(a.ws.act, (size_t)(pos + 1) * a.I + (size_t)min(lane + kWave * j, nci - 1) * 8, an[j]);
+    }
     float d[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) d[r] = 0.f;
@@ -738,18 +781,22 @@ __global__ __launch_bounds__(256) void moe_down_kernel(ExpertArgs a) {
     for (int j = 0; j < NJI; ++j) {
       const int c = lane + kWave * j;
       if (c < nci) {
-        float av[8];
-        load8_act(a.ws.act, (size_t)pos * a.I + (size_t)c * 8, av);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           if (r0 + r < a.H) {
             float w8[8];
             raw8_to_f32<BFW>(wr[r][j], w8);
 #pragma unroll
-            for (int q = 0; q < 8; ++q) d[r] = fmaf(w8[q], av[q], d[r]);
+            for (int q = 0; q < 8; ++q) d[r] = fmaf(w8[q], av[j][q], d[r]);
           }
         }
       }
+    }
+    if (pp + 1 < npairs) {
+#pragma unroll
+      for (int j = 0; j < NJI; ++j)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) av[j][q] = an[j][q];
     }
     float mine = 0.f;
 #pragma unroll
@@ -1362,7 +1409,8 @@ static_assert(kFusedSelWords >= (size_t)kTagRouterMaxTokens * 8, "router selecti
 // token t chose expert e (a token chooses an expert at most once).  Counts
 // are popcounts, offsets their exclusive prefix, and pair j = t*K + k goes
 // to offsets[e] + (earlier tokens that chose e): the stable order by expert
-// of a counting sort, as build_routing_tables gives.
+// of a counting sort, as build_routing_tables gives (records in ws.slots
+// included).
 __device__ void build_routing_tables_masks(const int* s_ids, const uint32_t* s_mask, int T, int K, int E, MoeWs ws,
                                            int* s_off) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1385,7 +1433,10 @@ __device__ void build_routing_tables_masks(const int* s_ids, const uint32_t* s_m
     s_off[tid] = off;
     ws.offsets[tid] = off;
     ws.counts[tid] = c;
-    if (nz) ws.active[pnz + inz - 1] = tid;
+    if (nz) {
+      ws.active[pnz + inz - 1] = tid;
+      ws.slots[pnz + inz - 1] = make_int4(tid, off, c, __ffs(msk) - 1);  // first pair: lowest token
+    }
   }
   const int P = T * K;
   if (tid == 0) {
