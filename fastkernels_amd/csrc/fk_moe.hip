@@ -666,6 +666,13 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(ExpertArgs a) {
     const int pos = pos0 + pp;
     int t_next = 0;
     if (pp + 1 < npairs) t_next = shared ? pp + 1 : a.ws.perm[pos + 1] / a.K;
+    // The rows are converted to fp32 where they are used, once per pair:
+    // hoisted out of this loop the converted rows would double the
+    // registers the rows take and cost a wavefront per SIMD.
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) asm volatile("" : "+v"(wr[r][j].a));
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
