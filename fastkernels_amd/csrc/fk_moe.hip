@@ -41,11 +41,11 @@ struct MoeWs {
   // Single-launch layer (T <= 2) and small-batch router (T <= 32): tagged hand-off words in
   // a fixed-size region, so that no offset depends on the problem shape
   // (fk_moe_router / fk_moe_align lay the workspace out without I and H).
-  uint64_t* f_logits;   // [T, E] router logits (capacity 32 * 256)
+  uint64_t* f_logits;   // [T, E] router logits (capacity 256 * 256)
   uint64_t* f_act;      // [(T*K + T), I] SwiGLU activations, permuted rows then shared rows (capacity 18 * 512)
   uint64_t* f_sgate;    // [T] shared-expert gates
   uint64_t* f_started;  // [grid] one tagged record per workgroup of the launch (capacity 1024)
-  uint64_t* f_sel;      // [T, K] small-batch router: expert ids chosen per token (capacity 32 * 8)
+  uint64_t* f_sel;      // [T, K] tagged router: expert ids chosen per token (capacity 256 * 8)
   int32_t* counts;      // [E]
   int32_t* offsets;     // [E+1] exclusive prefix of counts
   int32_t* perm;        // [P] permuted position -> pair index t*K+k
@@ -66,10 +66,10 @@ constexpr int kTicketRouterTables = 1;
 constexpr int kTicketEpoch = 8;
 constexpr int kTicketError = 15;
 constexpr int kFusedMaxGrid = 1024;
-constexpr size_t kFusedLogitWords = 32 * 256;  // tagged router: T <= 32
+constexpr size_t kFusedLogitWords = 256 * 256;  // tagged router: T <= 256
 constexpr size_t kFusedActWords = (2 * 8 + 2) * 512;
 constexpr size_t kFusedGateWords = 2;
-constexpr size_t kFusedSelWords = 32 * 8;  // small-batch router: T <= 32, K <= 8
+constexpr size_t kFusedSelWords = 256 * 8;  // tagged router: T <= 256, K <= 8
 
 // Regions sized by I or H come last: fk_moe_router and fk_moe_align lay the
 // workspace out with I = H = 0 and must find the routing tables where
@@ -1392,14 +1392,16 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
 }
 
 // ---------------------------------------------------------------------------
-// Router for small batches (T <= 32, E <= 256, H <= 2048): no grid barrier.
+// Router without grid barrier (T <= 256, E <= 256, H <= 2048).
 //
 // Workgroup (ub, tb) computes the logits of expert rows 8ub.. (one per
-// wavefront) for tokens tu*tb.. (tu = 2 or 4 tokens per workgroup; loads of
-// the row and the tokens issued together) and writes them as one tagged
-// run per token (the launch-tag protocol of the single-launch layer, same
-// epoch counter).  Workgroup t < T then polls the logits of token t and
-// computes its top-k with one wavefront (a selection is issue-bound, so the
+// wavefront) for tokens tu*tb .. tu*tb + tu - 1 (tu from 2 to 32, the
+// smallest whose grid is co-resident), in tiles of 4 tokens: the row and the
+// first tile's tokens are loaded together, each later tile is fetched while
+// the previous one is computed, and every tile leaves as one tagged run per
+// token (the launch-tag protocol of the single-launch layer, same epoch
+// counter).  Workgroup b then polls the logits of tokens b, b + grid, .. and
+// computes each top-k with one wavefront (a selection is issue-bound, so the
 // tokens go to different CUs), writes the token's ids and weights, and
 // publishes the ids as tagged words.  Workgroup 0 polls the T*K ids,
 // advances the epoch (the ids of every token carry this launch's tag, so
@@ -1407,23 +1409,34 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
 // builds the routing tables for the expert stage.  Same arithmetic as
 // moe_router_kernel, so both give identical logits and ids.
 // ---------------------------------------------------------------------------
-constexpr int kTagRouterMaxTokens = 32;
-constexpr int kTagRouterTokensPerUnit = 4;  // most tokens per workgroup
+constexpr int kTagRouterMaxTokens = 256;
+constexpr int kTagRouterTile = 4;       // tokens per tile of the logits loop
+constexpr int kTagRouterMaxPerWg = 32;  // most tokens per workgroup
+constexpr int kMaskWords = kTagRouterMaxTokens / 32;
 static_assert(kFusedSelWords >= (size_t)kTagRouterMaxTokens * 8, "router selection region too small");
+static_assert(kFusedLogitWords >= (size_t)kTagRouterMaxTokens * kFusedMaxExperts, "router logit region too small");
 
-// Routing tables for T <= 32 tokens and E <= 512 experts (one expert per
-// thread of a 512-thread workgroup) from s_mask[e], whose bit t says that
-// token t chose expert e (a token chooses an expert at most once).  Counts
-// are popcounts, offsets their exclusive prefix, and pair j = t*K + k goes
-// to offsets[e] + (earlier tokens that chose e): the stable order by expert
-// of a counting sort, as build_routing_tables gives (records in ws.slots
-// included).
+// Routing tables for T <= 256 tokens and E <= 512 experts (one expert per
+// thread of a 512-thread workgroup) from s_mask[e * ceil(T/32) + t / 32],
+// whose bit t % 32 says that token t chose expert e (a token chooses an
+// expert at most once).  Counts are popcounts, offsets their exclusive
+// prefix, and pair j = t*K + k goes to offsets[e] + (earlier tokens that
+// chose e): the stable order by expert of a counting sort, as
+// build_routing_tables gives (records in ws.slots included).
 __device__ void build_routing_tables_masks(const int* s_ids, const uint32_t* s_mask, int T, int K, int E, MoeWs ws,
                                            int* s_off) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   __shared__ int s_wtot[kFusedWaves][2];
-  const uint32_t msk = tid < E ? s_mask[tid] : 0u;
-  const int c = __popc(msk), nz = c > 0 ? 1 : 0;
+  const int nw = (T + 31) >> 5;
+  int c = 0, first = -1;
+  if (tid < E) {
+    for (int w = nw - 1; w >= 0; --w) {
+      const uint32_t m = s_mask[tid * nw + w];
+      c += __popc(m);
+      if (m) first = w * 32 + __ffs(m) - 1;
+    }
+  }
+  const int nz = c > 0 ? 1 : 0;
   const int isum = wave_incl_scan(c, lane), inz = wave_incl_scan(nz, lane);
   if (lane == kWave - 1) {
     s_wtot[wave][0] = isum;
@@ -1442,7 +1455,7 @@ __device__ void build_routing_tables_masks(const int* s_ids, const uint32_t* s_m
     ws.counts[tid] = c;
     if (nz) {
       ws.active[pnz + inz - 1] = tid;
-      ws.slots[pnz + inz - 1] = make_int4(tid, off, c, __ffs(msk) - 1);  // first pair: lowest token
+      ws.slots[pnz + inz - 1] = make_int4(tid, off, c, first);  // first pair: lowest token
     }
   }
   const int P = T * K;
@@ -1455,44 +1468,67 @@ __device__ void build_routing_tables_masks(const int* s_ids, const uint32_t* s_m
   __syncthreads();
   for (int j = tid; j < P; j += kFusedWaves * kWave) {
     const int t = j / K, e = s_ids[j];
-    const int pos = s_off[e] + __popc(s_mask[e] & ((1u << t) - 1u));
+    const uint32_t* m = s_mask + e * nw;
+    int pos = s_off[e] + __popc(m[t >> 5] & ((1u << (t & 31)) - 1u));
+    for (int w = 0; w < (t >> 5); ++w) pos += __popc(m[w]);
     ws.perm[pos] = j;
     ws.inverse[j] = pos;
   }
 }
 
-template <bool BFW, bool BFX, bool BFN>
+// TILED: a workgroup takes more than one tile of tokens (tu > 4).  The
+// single-tile variant keeps no prefetch registers (two workgroups per CU)
+// and every wavefront sums its tokens' squares beside its dot products; the
+// tiled one, VALU-bound, has wavefront t sum token t's squares once for all
+// rows and the storing threads apply the scale (same expression, so both
+// give the same logits).  Dynamic LDS: workgroup 0's ids [T*K] and token
+// masks [E * ceil(T/32)] (sized by the host for this T).
+template <bool BFW, bool BFX, bool BFN, bool TILED>
 __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
-  constexpr int TU = kTagRouterTokensPerUnit;
-  __shared__ int s_ids[kTagRouterMaxTokens * 8];
-  __shared__ uint32_t s_mask[kFusedMaxExperts];
+  constexpr int TU = kTagRouterTile;
+  extern __shared__ int s_dyn_ids[];
   __shared__ int s_off[kFusedMaxExperts];
   __shared__ float s_chunk[TU][8];
+  __shared__ float s_ss[TU];
   __shared__ int s_fail;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, H = a.H, E = a.E, K = a.K, nch = H >> 3;
   const int nrb = (E + 7) / 8, tu = a.tu;
   const int ub = blockIdx.x % nrb, tb = blockIdx.x / nrb;
-  const int e = ub * 8 + wave, t0 = tb * tu, nt = min(tu, T - t0);
+  const int e = ub * 8 + wave, t0 = tb * tu, ntok = max(0, min(tu, T - t0));
   const uint32_t tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
   if (tid == 0) s_fail = 0;
-  float mine = 0.f;  // lane t < nt: logit of token t0 + t
-  if (e < E) {
-    // Every load of the row is issued before the first use (the norm weight
-    // with a compile-time dtype: a run-time dtype test would wait for every
-    // load before it).
+
+  // ---- logits of rows 8ub.. for tokens t0 .. t0 + ntok - 1 ----------------
+  // Every load of the row is issued with the first tile's tokens, before the
+  // first use (the norm weight with a compile-time dtype: a run-time dtype
+  // test would wait for every load before it); token indices past this
+  // workgroup's last token repeat it (cache hits, not other tokens' lines).
+  const int tlast = t0 + ntok - 1;
+  const bool row = e < E;
+  const int erow = row ? e : 0;
+  Raw8<BFX> xr[TU][4];
+  float wn[4][8];
+  // bias of the row whose logits this thread applies it to: the wavefront's
+  // row, or (tiled) the row this thread stores (thread t*8 + l: row 8ub + l)
+  float bias = 0.f;
+  if (TILED) {
+    if (a.bias && tid < 8 * TU && ub * 8 + (tid & 7) < E) bias = load_scalar(a.bias, a.bias_dt, ub * 8 + (tid & 7));
+  } else if (a.bias && row) {
+    bias = load_scalar(a.bias, a.bias_dt, e);
+  }
+  {
     Raw8<BFW> wr[4];
     Raw8<BFN> nr[4];
-    Raw8<BFX> xr[TU][4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int cc = min(lane + kWave * j, nch - 1);
-      wr[j] = load_raw8<BFW>(a.W, (size_t)e * H + (size_t)cc * 8);
+      wr[j] = load_raw8<BFW>(a.W, (size_t)erow * H + (size_t)cc * 8);
 #pragma unroll
-      for (int t = 0; t < TU; ++t) xr[t][j] = load_raw8<BFX>(a.x, (size_t)(t0 + min(t, nt - 1)) * H + (size_t)cc * 8);
+      for (int t = 0; t < TU; ++t)
+        xr[t][j] = load_raw8<BFX>(a.x, (size_t)min(t0 + t, tlast) * H + (size_t)cc * 8);
       nr[j] = load_raw8<BFN>(a.nw, (size_t)cc * 8);
     }
-    float wn[4][8];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int c = lane + kWave * j;
@@ -1502,67 +1538,128 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
 #pragma unroll
       for (int q = 0; q < 8; ++q) wn[j][q] = c < nch ? w8[q] * (a.off + n8[q]) : 0.f;
     }
-    const float bias = a.bias ? load_scalar(a.bias, a.bias_dt, e) : 0.f;
+  }
+  for (int tt = 0; tt < ntok; tt += TU) {
+    const int nt = min(TU, ntok - tt);
+    // next tile's tokens, fetched while this tile is computed (bf16 tokens;
+    // fp32 ones are fetched after it, which keeps the registers in budget)
+    constexpr bool PF = BFX && TILED;
+    Raw8<BFX> xn[PF ? TU : 1][4];
+    const bool more = TILED && tt + TU < ntok;
+    if (PF && more) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int cc = min(lane + kWave * j, nch - 1);
+#pragma unroll
+        for (int t = 0; t < (PF ? TU : 1); ++t)
+          xn[t][j] = load_raw8<BFX>(a.x, (size_t)min(t0 + tt + TU + t, tlast) * H + (size_t)cc * 8);
+      }
+    }
+    // Wavefront t < TU also sums the squares of token t (the RMSNorm scale
+    // is shared by every row); the storing threads apply it.
+    float mine = 0.f;  // lane t < nt: dot of token t0 + tt + t with the row
 #pragma unroll
     for (int t = 0; t < TU; ++t) {
       if (t < nt) {
-        float ss = 0.f, d = 0.f;
+        if constexpr (!TILED) {
+          float ss = 0.f, d = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bool in = lane + kWave * j < nch;
+            float x8[8];
+            raw8_to_f32<BFX>(xr[t][j], x8);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              const float xv = in ? x8[q] : 0.f;
+              ss = fmaf(xv, xv, ss);
+              d = fmaf(xv, wn[j][q], d);
+            }
+          }
+          ss = wave_sum(ss);
+          d = wave_sum(d);
+          mine = lane == t ? d * rsqrtf(ss / (float)H + a.eps) + bias : mine;
+          continue;
+        }
+        float d = 0.f;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const bool in = lane + kWave * j < nch;
           float x8[8];
           raw8_to_f32<BFX>(xr[t][j], x8);
 #pragma unroll
-          for (int q = 0; q < 8; ++q) {
-            const float xv = in ? x8[q] : 0.f;
-            ss = fmaf(xv, xv, ss);
-            d = fmaf(xv, wn[j][q], d);
-          }
+          for (int q = 0; q < 8; ++q) d = fmaf(in ? x8[q] : 0.f, wn[j][q], d);
         }
-        ss = wave_sum(ss);
         d = wave_sum(d);
-        mine = lane == t ? d * rsqrtf(ss / (float)H + a.eps) + bias : mine;
+        mine = lane == t ? d : mine;
+        if (wave == t) {  // (a branch of its own: a per-element test costs every wavefront)
+          float ss = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bool in = lane + kWave * j < nch;
+            float x8[8];
+            raw8_to_f32<BFX>(xr[t][j], x8);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              const float xv = in ? x8[q] : 0.f;
+              ss = fmaf(xv, xv, ss);
+            }
+          }
+          ss = wave_sum(ss);
+          if (lane == 0) s_ss[t] = ss;
+        }
       }
     }
-  }
-  if (lane < nt) s_chunk[lane][wave] = mine;
-  __syncthreads();
-  if (tid < 8 * nt) {
-    const int t = tid >> 3, l = tid & 7, ee = ub * 8 + l;
-    if (ee < E) {
-      const float v = s_chunk[t][l];
-      a.logits[(size_t)(t0 + t) * E + ee] = v;
-      store_tagged(a.ws.f_logits + (size_t)(t0 + t) * E + ee, v, tag);
+    if (lane < nt) s_chunk[lane][wave] = mine;
+    __syncthreads();
+    if (tid < 8 * nt) {
+      const int t = tid >> 3, l = tid & 7, ee = ub * 8 + l;
+      if (ee < E) {
+        const float v = TILED ? s_chunk[t][l] * rsqrtf(s_ss[t] / (float)H + a.eps) + bias : s_chunk[t][l];
+        const size_t o = (size_t)(t0 + tt + t) * E + ee;
+        a.logits[o] = v;
+        store_tagged(a.ws.f_logits + o, v, tag);
+      }
+    }
+    __syncthreads();  // s_chunk is rewritten by the next tile
+    if (more) {
+#pragma unroll
+      for (int t = 0; t < TU; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if constexpr (PF) xr[t][j] = xn[t][j];
+          else xr[t][j] = load_raw8<BFX>(a.x, (size_t)min(t0 + tt + TU + t, tlast) * H +
+                                                  (size_t)min(lane + kWave * j, nch - 1) * 8);
+        }
     }
   }
-  if (blockIdx.x >= T) return;
 
-  // ---- workgroup t < T: top-k of token t ---------------------------------
+  // ---- top-k of tokens blockIdx.x, blockIdx.x + grid, .. ------------------
   if (wave == 0) {
     constexpr int NJE = kFusedMaxExperts / kWave;
-    const int t = blockIdx.x;
-    uint64_t w[NJE];
-    const uint64_t* srcs[NJE];
+    for (int t = blockIdx.x; t < T; t += gridDim.x) {
+      uint64_t w[NJE];
+      const uint64_t* srcs[NJE];
 #pragma unroll
-    for (int j = 0; j < NJE; ++j) {
-      const int ex = lane + kWave * j;
-      srcs[j] = ex < E ? a.ws.f_logits + (size_t)t * E + ex : nullptr;
-      w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
-    }
-    if (!poll_tagged<NJE>(w, srcs, tag)) s_fail = 1;
-    float p[NJE];
+      for (int j = 0; j < NJE; ++j) {
+        const int ex = lane + kWave * j;
+        srcs[j] = ex < E ? a.ws.f_logits + (size_t)t * E + ex : nullptr;
+        w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+      }
+      if (!poll_tagged<NJE>(w, srcs, tag)) s_fail = 1;
+      float p[NJE];
 #pragma unroll
-    for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
-    int id;
-    float wt;
-    topk_select_regs<NJE>(p, E, K, lane, id, wt);
-    if (lane < K) {
-      const int j = t * K + lane;
-      a.ids_out[j] = id;
-      a.w_out[j] = wt;
-      a.ws.ids32[j] = id;
-      a.ws.wts[j] = wt;
-      store_tagged(a.ws.f_sel + j, __int_as_float(id), tag);
+      for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
+      int id;
+      float wt;
+      topk_select_regs<NJE>(p, E, K, lane, id, wt);
+      if (lane < K) {
+        const int j = t * K + lane;
+        a.ids_out[j] = id;
+        a.w_out[j] = wt;
+        a.ws.ids32[j] = id;
+        a.ws.wts[j] = wt;
+        store_tagged(a.ws.f_sel + j, __int_as_float(id), tag);
+      }
     }
   }
   if (blockIdx.x != 0) {
@@ -1573,18 +1670,34 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   }
 
   // ---- workgroup 0: every token's ids, epoch, routing tables --------------
-  for (int i = tid; i < E; i += kFusedWaves * kWave) s_mask[i] = 0u;
+  const int nmw = (T + 31) >> 5;
+  int* s_ids = s_dyn_ids;
+  uint32_t* s_mask = reinterpret_cast<uint32_t*>(s_dyn_ids + T * K);  // [E][nmw]
+  for (int i = tid; i < E * nmw; i += kFusedWaves * kWave) s_mask[i] = 0u;
   __syncthreads();
-  const int P = T * K;  // <= 256: one id per thread
-  if (tid < P) {
-    uint64_t w[1];
-    const uint64_t* srcs[1] = {a.ws.f_sel + tid};
-    w[0] = load_tagged(srcs[0]);
-    if (!poll_tagged<1>(w, srcs, tag)) s_fail = 1;
-    // (clamped: after a failed poll the word may come from another launch)
-    const int id = min(max(__float_as_int(value_of(w[0])), 0), E - 1);
-    s_ids[tid] = id;
-    atomicOr(&s_mask[id], 1u << (tid / K));
+  const int P = T * K;  // <= 2048: up to 4 ids per thread
+  {
+    constexpr int NP = kTagRouterMaxTokens * 8 / (kFusedWaves * kWave);
+    uint64_t w[NP];
+    const uint64_t* srcs[NP];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int j = tid + i * kFusedWaves * kWave;
+      srcs[i] = j < P ? a.ws.f_sel + j : nullptr;
+      w[i] = srcs[i] ? load_tagged(srcs[i]) : 0ull;
+    }
+    if (!poll_tagged<NP>(w, srcs, tag)) s_fail = 1;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int j = tid + i * kFusedWaves * kWave;
+      if (j < P) {
+        // (clamped: after a failed poll the word may come from another launch)
+        const int id = min(max(__float_as_int(value_of(w[i])), 0), E - 1);
+        const int t = j / K;
+        s_ids[j] = id;
+        atomicOr(&s_mask[id * nmw + (t >> 5)], 1u << (t & 31));
+      }
+    }
   }
   __syncthreads();
   if (tid == 0) {
@@ -1671,17 +1784,33 @@ static bool tagged_router_eligible(const RouterArgs& ra) {
 
 template <bool BW, bool BX, bool BN>
 static int launch_router_tagged_t(const RouterArgs& ra_in, hipStream_t stream) {
-  static int cap_cache[64] = {0};
-  auto kernel = moe_router_tagged_kernel<BW, BX, BN>;
+  static int cap_cache[2][64] = {{0}};
   // Workgroup 0 waits for every other workgroup's logits: all must be
-  // resident.  Two tokens per workgroup where that grid fits, else four.
-  const int cap = resident_capacity(kernel, 512, 0, cap_cache);
+  // resident.  The fewest tokens per workgroup (2, 4, 8, .. 32) whose grid
+  // is co-resident; one tile per workgroup (tu <= 4) takes the single-tile
+  // variant, whose smaller register budget fits more workgroups.
   const int nrb = (ra_in.E + 7) / 8;
   RouterArgs ra = ra_in;
-  ra.tu = nrb * ((ra.T + 1) / 2) <= cap ? 2 : kTagRouterTokensPerUnit;
+  auto pick = [&](int cap) {
+    int tu = 2;
+    while (tu < kTagRouterMaxPerWg && nrb * ((ra.T + tu - 1) / tu) > cap) tu *= 2;
+    return tu;
+  };
+  // (capacities are taken at the largest dynamic LDS, T = 256)
+  constexpr size_t kMaxShm = ((size_t)kTagRouterMaxTokens * 8 + (size_t)kFusedMaxExperts * kMaskWords) * 4;
+  const int cap1 = resident_capacity(moe_router_tagged_kernel<BW, BX, BN, false>, 512, kMaxShm, cap_cache[0]);
+  ra.tu = pick(cap1);
+  int cap = cap1;
+  auto kernel = moe_router_tagged_kernel<BW, BX, BN, false>;
+  if (ra.tu > kTagRouterTile) {
+    kernel = moe_router_tagged_kernel<BW, BX, BN, true>;
+    cap = resident_capacity(kernel, 512, kMaxShm, cap_cache[1]);
+    ra.tu = pick(cap);
+  }
   const int units = nrb * ((ra.T + ra.tu - 1) / ra.tu);
   if (units > cap) return fail(FK_ERR_UNSUPPORTED, "router grid %d exceeds co-resident capacity %d", units, cap);
-  hipLaunchKernelGGL(kernel, dim3(units), dim3(512), 0, stream, ra);
+  const size_t shm = ((size_t)ra.T * ra.K + (size_t)ra.E * ((ra.T + 31) / 32)) * 4;
+  hipLaunchKernelGGL(kernel, dim3(units), dim3(512), shm, stream, ra);
   return check_launch("moe_router_tagged_kernel");
 }
 
@@ -1829,7 +1958,7 @@ int fk_moe_router(const void* hidden, int hidden_dtype, const void* norm_weight,
   ra.H = hidden_size;
   ra.E = num_experts;
   ra.K = top_k;
-  ra.tu = kTagRouterTokensPerUnit;
+  ra.tu = 2;
   ra.eps = eps;
   ra.off = norm_offset;
   ra.logits = logits;

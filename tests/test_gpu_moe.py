@@ -61,7 +61,9 @@ def test_expert_histogram_bit_exact(device, idt):
     assert counts.cpu().numpy().tolist() == oracle.expert_histogram(ids.numpy(), 256).tolist()
 
 
-@pytest.mark.parametrize("tokens,top_k,experts", [(1, 8, 256), (16, 8, 256), (128, 8, 256), (7, 3, 5), (512, 8, 1024)])
+@pytest.mark.parametrize(
+    "tokens,top_k,experts", [(1, 8, 256), (16, 8, 256), (37, 8, 256), (128, 8, 256), (256, 8, 256), (7, 3, 5), (512, 8, 1024)]
+)
 def test_align_tables_bit_exact(device, tokens, top_k, experts):
     rng = np.random.default_rng(tokens * 7 + experts)
     ids = np.stack([rng.choice(experts, size=top_k, replace=False) for _ in range(tokens)])
@@ -90,7 +92,7 @@ def test_router_real_shape(device, dtype):
     torch.testing.assert_close(w.cpu(), o_w[0], atol=1e-4, rtol=1e-4)
 
 
-@pytest.mark.parametrize("tokens", [1, 4, 16, 128])
+@pytest.mark.parametrize("tokens", [1, 4, 16, 37, 128, 256])
 def test_batched_router_and_tables(device, tokens):
     g = torch.Generator().manual_seed(2 + tokens)
     x = (0.02 * torch.randn(tokens, H, generator=g)).bfloat16()
