@@ -44,6 +44,7 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     p.add_argument("--no-extra", action="store_true", help="skip the batch-1/128 and DeltaNet sub-results")
+    p.add_argument("--zipf", action="store_true", help="with --only moe: add the config-2 Zipf router bias")
     p.add_argument("--only", choices=["moe", "deltanet", "copy"], default=None,
                    help="run a single timing loop (for profilers) and print its line; "
                         "'copy' runs 16 device-to-device copies of 1 GiB (PMC byte-counter calibration)")
@@ -204,7 +205,7 @@ def main() -> int:
         }
 
     if args.only == "moe":
-        res = moe_result(args.tokens)
+        res = moe_result(args.tokens, bias=wl.zipf_router_bias(E, seed=0).to(dev) if args.zipf else None)
         res.pop("_plans")
         print(json.dumps(res))
         return 0

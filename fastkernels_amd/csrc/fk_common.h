@@ -61,6 +61,10 @@ struct Raw8 {
   u32x4 b;
 };
 
+// Operand and accumulator types of v_mfma_f32_16x16x32_bf16.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
 template <bool BF16>
 __device__ __forceinline__ Raw8<BF16> load_raw8(const void* base, size_t elem_index) {
   Raw8<BF16> r;

@@ -547,8 +547,6 @@ constexpr size_t kStepHeadWords = (size_t)kStepMaxTokens * 64;
 constexpr int kStepTicketEpoch = 0;
 constexpr int kStepTicketError = 1;
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 struct StepTagWs {
   uint32_t* tickets;  // [16]: epoch, error flag

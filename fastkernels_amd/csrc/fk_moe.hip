@@ -28,6 +28,8 @@
 #include "fk_common.h"
 #include "fk_host.h"
 
+#include <algorithm>
+
 namespace fk {
 
 constexpr int kMaxPairs = 4096;    // T*K handled by the routing-table builder
@@ -852,6 +854,265 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(ExpertArgs a) {
   if (a.has_shared) acc += (a.sg ? g : 1.f) * ys;
   a.out[idx] = acc;
   if constexpr (LO) a.layer_out[idx] = raw_value<BFX>(xr[0]) + acc;
+}
+
+// ---------------------------------------------------------------------------
+// Batched expert stage (T >= 64 tokens, bf16 weights and hidden states):
+// MFMA grouped GEMM over the routing tables.
+//
+// Weight rows are loaded row-contiguously (a wavefront's K range of a row
+// is LPR lanes x 16 B, RPI rows per load: the MFMA operand layout, 16 rows x
+// 64 B per load, streams at half the rate) and each wavefront turns them
+// into v_mfma_f32_16x16x32_bf16 A operands (lane l: row l % 16, k group
+// l / 16 of each 32-wide step) once, through its own LDS area; the tokens of
+// an expert then go through in tiles of 16 columns, each tile one MFMA per
+// 32-wide step and row tile, and the wavefronts' partial tiles are summed
+// in a fixed order through LDS.
+//   gate/up: work item (slot, 16 intermediates) = 16 gate + 16 up rows, 512
+//            threads, K = H split over the 8 wavefronts; the tokens are the
+//            bf16 hidden states themselves (exact products).
+//   down:    work item (slot, 64 output rows), 256 threads, K = I split over
+//            the 4 wavefronts; fp32 activations enter as bf16 hi + lo
+//            columns (8 pairs per tile, ~16 mantissa bits).
+// ---------------------------------------------------------------------------
+constexpr int kMfmaMinTokens = 64;
+constexpr int kGuMfmaRows = 16;   // intermediates per gate/up work item
+constexpr int kDnMfmaRows = 64;   // output rows per down work item
+constexpr int kGuMfmaWaves = 8;
+constexpr int kDnMfmaWaves = 4;
+
+// Shapes the MFMA kernels take (powers of two, so lane splits are shifts).
+static bool mfma_expert_shapes_ok(int H, int I) {
+  return (H == 512 || H == 1024 || H == 2048) && (I == 256 || I == 512);
+}
+
+// Row-contiguous registers v[s] (instruction s: row s*RPI + lane/LPR, 16 B
+// at k = (lane % LPR) * 8 of the wavefront's K range) -> MFMA A operands
+// v[s] (step s: row lane % 16, k = s*32 + (lane / 16) * 8), through the
+// wavefront's LDS area of 16 rows x pitch bytes.  The reads follow the
+// writes in the same wavefront, so LDS order alone makes them see them.
+template <int NS>
+__device__ __forceinline__ void rows_to_mfma_a(u32x4 (&v)[NS], int ks, char* area, int pitch, int lpr_sh, int lane) {
+  const int rpi = kWave >> lpr_sh, lpr = 1 << lpr_sh;
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    if (s < ks) *reinterpret_cast<u32x4*>(area + (s * rpi + (lane >> lpr_sh)) * pitch + ((lane & (lpr - 1)) << 4)) = v[s];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    if (s < ks) v[s] = *reinterpret_cast<const u32x4*>(area + (lane & 15) * pitch + s * 64 + (lane >> 4) * 16);
+}
+
+// Expert record of a slot (the shared expert in slot 0 when present):
+// weights, first permuted position, pair count; false past the active ones.
+__device__ __forceinline__ bool expert_slot(const ExpertArgs& a, int slot, const char* routed, const char* shared_w,
+                                            size_t expert_bytes, const char*& W, int& pos0, int& npairs, bool& shared) {
+  shared = false;
+  if (a.has_shared && slot == 0) {
+    W = shared_w;
+    pos0 = a.T * a.K;
+    npairs = a.T;
+    shared = true;
+    return true;
+  }
+  if (a.has_shared) slot -= 1;
+  const int na = a.ws.num_active[0];  // loaded with the record (slot < E)
+  const int4 rec = a.ws.slots[slot];
+  if (slot >= na) return false;
+  W = routed + (size_t)rec.x * expert_bytes;
+  pos0 = rec.y;
+  npairs = rec.z;
+  return true;
+}
+
+__global__ __launch_bounds__(512) void moe_gateup_mfma_kernel(ExpertArgs a) {
+  extern __shared__ float4 s_gu_v[];
+  char* s_lds = reinterpret_cast<char*>(s_gu_v);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int H = a.H, I = a.I, K = a.K;
+  const int ipb = I / kGuMfmaRows;
+  const int ib = blockIdx.x % ipb, i0 = ib * kGuMfmaRows;
+  const char* W;
+  int pos0, npairs;
+  bool shared;
+  if (!expert_slot(a, blockIdx.x / ipb, reinterpret_cast<const char*>(a.gu), reinterpret_cast<const char*>(a.sgu),
+                   (size_t)2 * I * H * 2, W, pos0, npairs, shared))
+    return;
+  const int lh = 31 - __builtin_clz((unsigned)H);
+  const int kw = H >> 3, ks = kw >> 5;   // K range and 32-wide steps of a wavefront (<= 8)
+  const int lpr_sh = lh - 6;             // LPR = kw / 8 lanes per row
+  const int rpi = kWave >> lpr_sh;
+  const int pitch = kw * 2 + 16;         // (16-byte pad: the 16 rows of an operand read hit distinct banks)
+
+  // gate rows i0.., up rows I + i0.. of this wavefront's K range; slots past
+  // ks read the matrix's first rows (valid, unused)
+  const uint32_t lane_off = (uint32_t)((((lane >> lpr_sh) << lh) + wave * kw + ((lane & ((1 << lpr_sh) - 1)) << 3)) << 1);
+  u32x4 av[2][8];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const char* base = s < ks ? W + ((size_t)(h * I + i0 + s * rpi) << (lh + 1)) : W;
+      av[h][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + lane_off));
+    }
+  char* area = s_lds + (size_t)wave * 16 * pitch;
+  rows_to_mfma_a<8>(av[0], ks, area, pitch, lpr_sh, lane);
+  rows_to_mfma_a<8>(av[1], ks, area, pitch, lpr_sh, lane);
+  __syncthreads();  // the partial tiles below overlap other wavefronts' areas
+
+  float* s_part = reinterpret_cast<float*>(s_lds);  // [wave][gate|up][16 rows][16 columns]
+  const int n = lane & 15, g4 = lane >> 4;
+  for (int tile = 0; tile * 16 < npairs; ++tile) {
+    // column n: pair tile*16 + n (clamped; columns past npairs are dropped)
+    const int p = min(tile * 16 + n, npairs - 1);
+    const int t = shared ? p : a.ws.perm[pos0 + p] / K;
+    u32x4 bv[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+      bv[s] = s < ks ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)t * H +
+                                                       wave * kw + s * 32 + g4 * 8)
+                     : u32x4{0, 0, 0, 0};
+    f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      if (s < ks) {
+        accg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[0][s]),
+                                                       __builtin_bit_cast(bf16x8_t, bv[s]), accg, 0, 0, 0);
+        accu = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[1][s]),
+                                                       __builtin_bit_cast(bf16x8_t, bv[s]), accu, 0, 0, 0);
+      }
+    }
+    if (tile > 0) __syncthreads();  // the previous tile's sums are read
+    float* pw = s_part + (size_t)wave * 512;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      pw[(g4 * 4 + q) * 16 + n] = accg[q];
+      pw[256 + (g4 * 4 + q) * 16 + n] = accu[q];
+    }
+    __syncthreads();
+    if (tid < 256) {
+      const int r = tid >> 4, c = tid & 15;
+      float gs = 0.f, us = 0.f;
+#pragma unroll
+      for (int w = 0; w < kGuMfmaWaves; ++w) {
+        gs += s_part[w * 512 + r * 16 + c];
+        us += s_part[w * 512 + 256 + r * 16 + c];
+      }
+      if (tile * 16 + c < npairs) a.ws.act[(size_t)(pos0 + tile * 16 + c) * I + i0 + r] = silu(gs) * us;
+    }
+  }
+
+  // Shared-expert gate sigmoid(w_g . x_t), once per token (bf16 gate weight
+  // or per element otherwise).
+  if (shared && ib == 0 && a.sg) {
+    const int nch = H >> 3;
+    const bool sg_vec = a.sg_dt == FK_DTYPE_BF16 && (reinterpret_cast<uintptr_t>(a.sg) & 15u) == 0;
+    for (int t = wave; t < a.T; t += kGuMfmaWaves) {
+      float d = 0.f;
+      for (int c = lane; c < nch; c += kWave) {
+        float x8[8], g8[8];
+        load8_f32<true>(a.x, (size_t)t * H + (size_t)c * 8, x8);
+        if (sg_vec) load8_f32<true>(a.sg, (size_t)c * 8, g8);
+        else
+#pragma unroll
+          for (int q = 0; q < 8; ++q) g8[q] = load_scalar(a.sg, a.sg_dt, (size_t)c * 8 + q);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) d = fmaf(x8[q], g8[q], d);
+      }
+      d = wave_sum(d);
+      if (lane == 0) a.ws.sgate[t] = sigmoid(d);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertArgs a) {
+  extern __shared__ float4 s_dn_v[];
+  char* s_lds = reinterpret_cast<char*>(s_dn_v);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int H = a.H, I = a.I;
+  const int rbn = H / kDnMfmaRows;
+  const int rb = blockIdx.x % rbn, r0 = rb * kDnMfmaRows;
+  const char* W;
+  int pos0, npairs;
+  bool shared;
+  if (!expert_slot(a, blockIdx.x / rbn, reinterpret_cast<const char*>(a.dn), reinterpret_cast<const char*>(a.sdn),
+                   (size_t)H * I * 2, W, pos0, npairs, shared))
+    return;
+  const int li = 31 - __builtin_clz((unsigned)I);
+  const int kw = I >> 2, ks = kw >> 5;   // K range and steps of a wavefront (I = 512: 128, 4)
+  const int lpr_sh = li - 5;             // LPR = kw / 8
+  const int rpi = kWave >> lpr_sh;
+  const int pitch = kw * 2 + 16;
+
+  // rows r0 + 16 rt .. of this wavefront's K range (4 row tiles)
+  const uint32_t lane_off = (uint32_t)((((lane >> lpr_sh) << li) + wave * kw + ((lane & ((1 << lpr_sh) - 1)) << 3)) << 1);
+  u32x4 av[4][4];
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const char* base = s < ks ? W + ((size_t)(r0 + rt * 16 + s * rpi) << (li + 1)) : W;
+      av[rt][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + lane_off));
+    }
+  char* area = s_lds + (size_t)wave * 16 * pitch;
+#pragma unroll
+  for (int rt = 0; rt < 4; ++rt) rows_to_mfma_a<4>(av[rt], ks, area, pitch, lpr_sh, lane);
+  __syncthreads();  // the partial tiles below overlap other wavefronts' areas
+
+  float* s_part = reinterpret_cast<float*>(s_lds);  // [wave][row tile][16 rows][16 columns]
+  const int n = lane & 15, g4 = lane >> 4;
+  for (int tile = 0; tile * 8 < npairs; ++tile) {
+    // column n: pair tile*8 + n/2, bf16 hi (n even) or lo (n odd) of its activations
+    const int p = min(tile * 8 + (n >> 1), npairs - 1);
+    const float* ar = a.ws.act + (size_t)(pos0 + p) * I + wave * kw + g4 * 8;
+    u32x4 bv[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      if (s < ks) {
+        const float4 lo4 = *reinterpret_cast<const float4*>(ar + s * 32);
+        const float4 hi4 = *reinterpret_cast<const float4*>(ar + s * 32 + 4);
+        const float v8[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+        uint32_t h[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint16_t hb = f32_to_bf16_bits(v8[e]);
+          h[e] = (n & 1) ? f32_to_bf16_bits(v8[e] - bf16_bits_to_f32(hb)) : hb;
+        }
+        bv[s] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+      } else {
+        bv[s] = u32x4{0, 0, 0, 0};
+      }
+    }
+    f32x4_t acc[4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      acc[rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        if (s < ks)
+          acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[rt][s]),
+                                                            __builtin_bit_cast(bf16x8_t, bv[s]), acc[rt], 0, 0, 0);
+    }
+    if (tile > 0) __syncthreads();  // the previous tile's sums are read
+    float* pw = s_part + (size_t)wave * 1024;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) pw[rt * 256 + (g4 * 4 + q) * 16 + n] = acc[rt][q];
+    __syncthreads();
+    // thread: output row R = tid % 64 (tile R / 16, row R % 16), pairs j and j + 4
+    {
+      const int R = tid & 63, rt = R >> 4, r = R & 15;
+#pragma unroll
+      for (int jj = 0; jj < 2; ++jj) {
+        const int j = (tid >> 6) + jj * 4;
+        float y = 0.f;
+#pragma unroll
+        for (int w = 0; w < kDnMfmaWaves; ++w)
+          y += s_part[w * 1024 + rt * 256 + r * 16 + 2 * j] + s_part[w * 1024 + rt * 256 + r * 16 + 2 * j + 1];
+        if (tile * 8 + j < npairs) a.ws.y[(size_t)(pos0 + tile * 8 + j) * H + r0 + R] = y;
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1833,30 +2094,62 @@ static int launch_router(const RouterArgs& ra, int router_dt, int hidden_dt, hip
   return st;
 }
 
+// Batched expert stage on MFMA: gate/up then down (see moe_gateup_mfma_kernel).
+static int launch_experts_mfma(const ExpertArgs& ea, int slots, hipStream_t stream) {
+  static bool attr_set[64] = {false};
+  const size_t gu_shm = std::max((size_t)16 * kGuMfmaWaves * ((size_t)ea.H / kGuMfmaWaves * 2 + 16),
+                                 (size_t)kGuMfmaWaves * 512 * sizeof(float));
+  const size_t dn_shm = std::max((size_t)16 * kDnMfmaWaves * ((size_t)ea.I / kDnMfmaWaves * 2 + 16),
+                                 (size_t)kDnMfmaWaves * 1024 * sizeof(float));
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(FK_ERR_LAUNCH, "no current HIP device");
+  if (!attr_set[dev]) {
+    // (the largest need, H = 2048: 67,584 bytes)
+    const int max_gu = 16 * kGuMfmaWaves * (2048 / kGuMfmaWaves * 2 + 16);
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_gateup_mfma_kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, max_gu) != hipSuccess)
+      return fail(FK_ERR_LAUNCH, "cannot reserve %d bytes of LDS for the MFMA gate/up kernel", max_gu);
+    attr_set[dev] = true;
+  }
+  hipLaunchKernelGGL(moe_gateup_mfma_kernel, dim3(slots * (ea.I / kGuMfmaRows)), dim3(kGuMfmaWaves * kWave), gu_shm,
+                     stream, ea);
+  int st = check_launch("moe_gateup_mfma_kernel");
+  if (st) return st;
+  hipLaunchKernelGGL(moe_down_mfma_kernel, dim3(slots * (ea.H / kDnMfmaRows)), dim3(kDnMfmaWaves * kWave), dn_shm,
+                     stream, ea);
+  return check_launch("moe_down_mfma_kernel");
+}
+
 static int launch_experts(const ExpertArgs& ea, int expert_dt, hipStream_t stream) {
   const bool bfw = expert_dt == FK_DTYPE_BF16, bfx = ea.x_dt == FK_DTYPE_BF16;
   const bool wide = ea.H > 2048;
   const int max_active = ea.T * ea.K < ea.E ? ea.T * ea.K : ea.E;
   const int slots = max_active + (ea.has_shared ? 1 : 0);
-  const int gu_grid = slots * (ea.I / kGateUpRows);
-  FK_DISPATCH_BOOL(bfw, BW, FK_DISPATCH_BOOL(bfx, BX, {
-    if (wide) {
-      hipLaunchKernelGGL((moe_gateup_kernel<BW, BX, 8>), dim3(gu_grid), dim3(256), 0, stream, ea);
-    } else {
-      hipLaunchKernelGGL((moe_gateup_kernel<BW, BX, 4>), dim3(gu_grid), dim3(256), 0, stream, ea);
-    }
-  }))
-  int st = check_launch("moe_gateup_kernel");
-  if (st) return st;
+  int st = FK_OK;
+  if (ea.T >= kMfmaMinTokens && bfw && bfx && mfma_expert_shapes_ok(ea.H, ea.I)) {
+    st = launch_experts_mfma(ea, slots, stream);
+    if (st) return st;
+  } else {
+    const int gu_grid = slots * (ea.I / kGateUpRows);
+    FK_DISPATCH_BOOL(bfw, BW, FK_DISPATCH_BOOL(bfx, BX, {
+      if (wide) {
+        hipLaunchKernelGGL((moe_gateup_kernel<BW, BX, 8>), dim3(gu_grid), dim3(256), 0, stream, ea);
+      } else {
+        hipLaunchKernelGGL((moe_gateup_kernel<BW, BX, 4>), dim3(gu_grid), dim3(256), 0, stream, ea);
+      }
+    }))
+    st = check_launch("moe_gateup_kernel");
+    if (st) return st;
 
-  const int dn_grid = slots * ((ea.H + kDownRows - 1) / kDownRows);
-  const bool wide_i = ea.I > 512;
-  FK_DISPATCH_BOOL(bfw, BW, {
-    if (wide_i) hipLaunchKernelGGL((moe_down_kernel<BW, 2>), dim3(dn_grid), dim3(256), 0, stream, ea);
-    else hipLaunchKernelGGL((moe_down_kernel<BW, 1>), dim3(dn_grid), dim3(256), 0, stream, ea);
-  })
-  st = check_launch("moe_down_kernel");
-  if (st) return st;
+    const int dn_grid = slots * ((ea.H + kDownRows - 1) / kDownRows);
+    const bool wide_i = ea.I > 512;
+    FK_DISPATCH_BOOL(bfw, BW, {
+      if (wide_i) hipLaunchKernelGGL((moe_down_kernel<BW, 2>), dim3(dn_grid), dim3(256), 0, stream, ea);
+      else hipLaunchKernelGGL((moe_down_kernel<BW, 1>), dim3(dn_grid), dim3(256), 0, stream, ea);
+    })
+    st = check_launch("moe_down_kernel");
+    if (st) return st;
+  }
   const size_t total = (size_t)ea.T * ea.H;
   const bool lo = ea.layer_out != nullptr;
   const dim3 cgrid((unsigned)((total + 255) / 256));
