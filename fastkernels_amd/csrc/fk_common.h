@@ -64,6 +64,14 @@ struct Raw8 {
 // Operand and accumulator types of v_mfma_f32_16x16x32_bf16.
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// Two floats to packed bf16 (a in the low half) by the hardware conversion
+// (v_cvt_pk_bf16_f32, round to nearest even).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
+}
 
 template <bool BF16>
 __device__ __forceinline__ Raw8<BF16> load_raw8(const void* base, size_t elem_index) {

@@ -891,15 +891,15 @@ static bool mfma_expert_shapes_ok(int H, int I) {
 // v[s] (step s: row lane % 16, k = s*32 + (lane / 16) * 8), through the
 // wavefront's LDS area of 16 rows x pitch bytes.  The reads follow the
 // writes in the same wavefront, so LDS order alone makes them see them.
+// NS: MFMA steps of the wavefront's K range (= loads per 16 rows).
 template <int NS>
-__device__ __forceinline__ void rows_to_mfma_a(u32x4 (&v)[NS], int ks, char* area, int pitch, int lpr_sh, int lane) {
+__device__ __forceinline__ void rows_to_mfma_a(u32x4 (&v)[NS], char* area, int pitch, int lpr_sh, int lane) {
   const int rpi = kWave >> lpr_sh, lpr = 1 << lpr_sh;
 #pragma unroll
   for (int s = 0; s < NS; ++s)
-    if (s < ks) *reinterpret_cast<u32x4*>(area + (s * rpi + (lane >> lpr_sh)) * pitch + ((lane & (lpr - 1)) << 4)) = v[s];
+    *reinterpret_cast<u32x4*>(area + (s * rpi + (lane >> lpr_sh)) * pitch + ((lane & (lpr - 1)) << 4)) = v[s];
 #pragma unroll
-  for (int s = 0; s < NS; ++s)
-    if (s < ks) v[s] = *reinterpret_cast<const u32x4*>(area + (lane & 15) * pitch + s * 64 + (lane >> 4) * 16);
+  for (int s = 0; s < NS; ++s) v[s] = *reinterpret_cast<const u32x4*>(area + (lane & 15) * pitch + s * 64 + (lane >> 4) * 16);
 }
 
 // Expert record of a slot (the shared expert in slot 0 when present):
@@ -924,6 +924,8 @@ __device__ __forceinline__ bool expert_slot(const ExpertArgs& a, int slot, const
   return true;
 }
 
+// KS = H / 256: MFMA steps per wavefront (H = 512, 1024, 2048 -> 2, 4, 8).
+template <int KS>
 __global__ __launch_bounds__(512) void moe_gateup_mfma_kernel(ExpertArgs a) {
   extern __shared__ float4 s_gu_v[];
   char* s_lds = reinterpret_cast<char*>(s_gu_v);
@@ -938,25 +940,23 @@ __global__ __launch_bounds__(512) void moe_gateup_mfma_kernel(ExpertArgs a) {
                    (size_t)2 * I * H * 2, W, pos0, npairs, shared))
     return;
   const int lh = 31 - __builtin_clz((unsigned)H);
-  const int kw = H >> 3, ks = kw >> 5;   // K range and 32-wide steps of a wavefront (<= 8)
+  const int kw = H >> 3;                 // K range of a wavefront (KS steps of 32)
   const int lpr_sh = lh - 6;             // LPR = kw / 8 lanes per row
   const int rpi = kWave >> lpr_sh;
   const int pitch = kw * 2 + 16;         // (16-byte pad: the 16 rows of an operand read hit distinct banks)
 
-  // gate rows i0.., up rows I + i0.. of this wavefront's K range; slots past
-  // ks read the matrix's first rows (valid, unused)
+  // gate rows i0.., up rows I + i0.. of this wavefront's K range
   const uint32_t lane_off = (uint32_t)((((lane >> lpr_sh) << lh) + wave * kw + ((lane & ((1 << lpr_sh) - 1)) << 3)) << 1);
-  u32x4 av[2][8];
+  u32x4 av[2][KS];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const char* base = s < ks ? W + ((size_t)(h * I + i0 + s * rpi) << (lh + 1)) : W;
-      av[h][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + lane_off));
-    }
+    for (int s = 0; s < KS; ++s)
+      av[h][s] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(W + ((size_t)(h * I + i0 + s * rpi) << (lh + 1)) + lane_off));
   char* area = s_lds + (size_t)wave * 16 * pitch;
-  rows_to_mfma_a<8>(av[0], ks, area, pitch, lpr_sh, lane);
-  rows_to_mfma_a<8>(av[1], ks, area, pitch, lpr_sh, lane);
+  rows_to_mfma_a<KS>(av[0], area, pitch, lpr_sh, lane);
+  rows_to_mfma_a<KS>(av[1], area, pitch, lpr_sh, lane);
   __syncthreads();  // the partial tiles below overlap other wavefronts' areas
 
   float* s_part = reinterpret_cast<float*>(s_lds);  // [wave][gate|up][16 rows][16 columns]
@@ -965,21 +965,18 @@ __global__ __launch_bounds__(512) void moe_gateup_mfma_kernel(ExpertArgs a) {
     // column n: pair tile*16 + n (clamped; columns past npairs are dropped)
     const int p = min(tile * 16 + n, npairs - 1);
     const int t = shared ? p : a.ws.perm[pos0 + p] / K;
-    u32x4 bv[8];
+    u32x4 bv[KS];
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
-      bv[s] = s < ks ? *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)t * H +
-                                                       wave * kw + s * 32 + g4 * 8)
-                     : u32x4{0, 0, 0, 0};
+    for (int s = 0; s < KS; ++s)
+      bv[s] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.x) + (size_t)t * H + wave * kw + s * 32 +
+                                              g4 * 8);
     f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      if (s < ks) {
-        accg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[0][s]),
-                                                       __builtin_bit_cast(bf16x8_t, bv[s]), accg, 0, 0, 0);
-        accu = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[1][s]),
-                                                       __builtin_bit_cast(bf16x8_t, bv[s]), accu, 0, 0, 0);
-      }
+    for (int s = 0; s < KS; ++s) {
+      accg = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[0][s]),
+                                                     __builtin_bit_cast(bf16x8_t, bv[s]), accg, 0, 0, 0);
+      accu = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[1][s]),
+                                                     __builtin_bit_cast(bf16x8_t, bv[s]), accu, 0, 0, 0);
     }
     if (tile > 0) __syncthreads();  // the previous tile's sums are read
     float* pw = s_part + (size_t)wave * 512;
@@ -1024,6 +1021,8 @@ __global__ __launch_bounds__(512) void moe_gateup_mfma_kernel(ExpertArgs a) {
   }
 }
 
+// KS = I / 128: MFMA steps per wavefront (I = 256, 512 -> 2, 4).
+template <int KS>
 __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertArgs a) {
   extern __shared__ float4 s_dn_v[];
   char* s_lds = reinterpret_cast<char*>(s_dn_v);
@@ -1038,59 +1037,68 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertArgs a) {
                    (size_t)H * I * 2, W, pos0, npairs, shared))
     return;
   const int li = 31 - __builtin_clz((unsigned)I);
-  const int kw = I >> 2, ks = kw >> 5;   // K range and steps of a wavefront (I = 512: 128, 4)
+  const int kw = I >> 2;                 // K range of a wavefront (KS steps of 32)
   const int lpr_sh = li - 5;             // LPR = kw / 8
   const int rpi = kWave >> lpr_sh;
   const int pitch = kw * 2 + 16;
 
+  // The activations of a tile's pairs (column n: pair n/2, bf16 hi for even
+  // n, lo for odd n) do not depend on the weights: the first tile's are
+  // issued before the weight rows, each later tile's while the previous one
+  // is computed.
+  const int n = lane & 15, g4 = lane >> 4;
+  float4 araw[KS][2];
+  auto load_act = [&](int tile) {
+    const int p = min(tile * 8 + (n >> 1), npairs - 1);
+    const float* ar = a.ws.act + (size_t)(pos0 + p) * I + wave * kw + g4 * 8;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      araw[s][0] = *reinterpret_cast<const float4*>(ar + s * 32);
+      araw[s][1] = *reinterpret_cast<const float4*>(ar + s * 32 + 4);
+    }
+  };
+  load_act(0);
+
   // rows r0 + 16 rt .. of this wavefront's K range (4 row tiles)
   const uint32_t lane_off = (uint32_t)((((lane >> lpr_sh) << li) + wave * kw + ((lane & ((1 << lpr_sh) - 1)) << 3)) << 1);
-  u32x4 av[4][4];
+  u32x4 av[4][KS];
 #pragma unroll
   for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const char* base = s < ks ? W + ((size_t)(r0 + rt * 16 + s * rpi) << (li + 1)) : W;
-      av[rt][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + lane_off));
-    }
+    for (int s = 0; s < KS; ++s)
+      av[rt][s] = __builtin_nontemporal_load(
+          reinterpret_cast<const u32x4*>(W + ((size_t)(r0 + rt * 16 + s * rpi) << (li + 1)) + lane_off));
   char* area = s_lds + (size_t)wave * 16 * pitch;
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt) rows_to_mfma_a<4>(av[rt], ks, area, pitch, lpr_sh, lane);
+  for (int rt = 0; rt < 4; ++rt) rows_to_mfma_a<KS>(av[rt], area, pitch, lpr_sh, lane);
   __syncthreads();  // the partial tiles below overlap other wavefronts' areas
 
   float* s_part = reinterpret_cast<float*>(s_lds);  // [wave][row tile][16 rows][16 columns]
-  const int n = lane & 15, g4 = lane >> 4;
   for (int tile = 0; tile * 8 < npairs; ++tile) {
-    // column n: pair tile*8 + n/2, bf16 hi (n even) or lo (n odd) of its activations
-    const int p = min(tile * 8 + (n >> 1), npairs - 1);
-    const float* ar = a.ws.act + (size_t)(pos0 + p) * I + wave * kw + g4 * 8;
-    u32x4 bv[4];
+    u32x4 bv[KS];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (s < ks) {
-        const float4 lo4 = *reinterpret_cast<const float4*>(ar + s * 32);
-        const float4 hi4 = *reinterpret_cast<const float4*>(ar + s * 32 + 4);
-        const float v8[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
-        uint32_t h[8];
+    for (int s = 0; s < KS; ++s) {
+      const float4 lo4 = araw[s][0], hi4 = araw[s][1];
+      const float v8[8] = {lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+      uint32_t h[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint16_t hb = f32_to_bf16_bits(v8[e]);
-          h[e] = (n & 1) ? f32_to_bf16_bits(v8[e] - bf16_bits_to_f32(hb)) : hb;
-        }
-        bv[s] = u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
-      } else {
-        bv[s] = u32x4{0, 0, 0, 0};
+      for (int e = 0; e < 4; ++e) {
+        // hi = bf16(v), lo = bf16(v - hi), both rounded to nearest even
+        const uint32_t hi = pack_bf16x2(v8[2 * e], v8[2 * e + 1]);
+        const uint32_t lo = pack_bf16x2(v8[2 * e] - __uint_as_float(hi << 16), v8[2 * e + 1] - __uint_as_float(hi & 0xffff0000u));
+        h[e] = (n & 1) ? lo : hi;
       }
+      bv[s] = u32x4{h[0], h[1], h[2], h[3]};
     }
+    if ((tile + 1) * 8 < npairs) load_act(tile + 1);
     f32x4_t acc[4];
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       acc[rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        if (s < ks)
-          acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[rt][s]),
-                                                            __builtin_bit_cast(bf16x8_t, bv[s]), acc[rt], 0, 0, 0);
+      for (int s = 0; s < KS; ++s)
+        acc[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, av[rt][s]),
+                                                          __builtin_bit_cast(bf16x8_t, bv[s]), acc[rt], 0, 0, 0);
     }
     if (tile > 0) __syncthreads();  // the previous tile's sums are read
     float* pw = s_part + (size_t)wave * 1024;
@@ -2106,17 +2114,22 @@ static int launch_experts_mfma(const ExpertArgs& ea, int slots, hipStream_t stre
   if (!attr_set[dev]) {
     // (the largest need, H = 2048: 67,584 bytes)
     const int max_gu = 16 * kGuMfmaWaves * (2048 / kGuMfmaWaves * 2 + 16);
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(moe_gateup_mfma_kernel),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, max_gu) != hipSuccess)
-      return fail(FK_ERR_LAUNCH, "cannot reserve %d bytes of LDS for the MFMA gate/up kernel", max_gu);
+    for (const void* k : {reinterpret_cast<const void*>(moe_gateup_mfma_kernel<2>),
+                          reinterpret_cast<const void*>(moe_gateup_mfma_kernel<4>),
+                          reinterpret_cast<const void*>(moe_gateup_mfma_kernel<8>)})
+      if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, max_gu) != hipSuccess)
+        return fail(FK_ERR_LAUNCH, "cannot reserve %d bytes of LDS for the MFMA gate/up kernel", max_gu);
     attr_set[dev] = true;
   }
-  hipLaunchKernelGGL(moe_gateup_mfma_kernel, dim3(slots * (ea.I / kGuMfmaRows)), dim3(kGuMfmaWaves * kWave), gu_shm,
-                     stream, ea);
+  const dim3 gu_grid(slots * (ea.I / kGuMfmaRows)), gu_block(kGuMfmaWaves * kWave);
+  if (ea.H == 2048) hipLaunchKernelGGL(moe_gateup_mfma_kernel<8>, gu_grid, gu_block, gu_shm, stream, ea);
+  else if (ea.H == 1024) hipLaunchKernelGGL(moe_gateup_mfma_kernel<4>, gu_grid, gu_block, gu_shm, stream, ea);
+  else hipLaunchKernelGGL(moe_gateup_mfma_kernel<2>, gu_grid, gu_block, gu_shm, stream, ea);
   int st = check_launch("moe_gateup_mfma_kernel");
   if (st) return st;
-  hipLaunchKernelGGL(moe_down_mfma_kernel, dim3(slots * (ea.H / kDnMfmaRows)), dim3(kDnMfmaWaves * kWave), dn_shm,
-                     stream, ea);
+  const dim3 dn_grid(slots * (ea.H / kDnMfmaRows)), dn_block(kDnMfmaWaves * kWave);
+  if (ea.I == 512) hipLaunchKernelGGL(moe_down_mfma_kernel<4>, dn_grid, dn_block, dn_shm, stream, ea);
+  else hipLaunchKernelGGL(moe_down_mfma_kernel<2>, dn_grid, dn_block, dn_shm, stream, ea);
   return check_launch("moe_down_mfma_kernel");
 }
 
