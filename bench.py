@@ -166,6 +166,8 @@ def main() -> int:
         # first.
         ms_router = timed_graph([p.run_router for p in plans], steps, 2)
         ms_experts = timed_graph([p.run_experts for p in plans], steps, 2)
+        for p in plans:  # no bounded in-kernel wait ran out in any timed step
+            p.check_device(stream)
         per_step_u = [u[i % len(u)] for i in range(steps)]
         layer_bytes = sum(wl.moe_layer_bytes(tokens, x, spec) for x in per_step_u) / steps
         expert_bytes = sum(
@@ -195,6 +197,8 @@ def main() -> int:
             dp.hidden.copy_(wl.make_hidden(tokens, H, seed=50 + r).to(dev))
             dplans.append(dp)
         ms = timed_graph([p.run for p in dplans], args.steps, args.warmup)
+        for p in dplans:
+            p.check_device(stream)
         nbytes = wl.deltanet_step_bytes(tokens, spec)
         return {
             "tokens": tokens,

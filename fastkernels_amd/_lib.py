@@ -26,6 +26,7 @@ FK_ERR_WORKSPACE = 3
 FK_ERR_LAUNCH = 4
 FK_ERR_UNSUPPORTED = 5
 FK_ERR_ALIGNMENT = 6
+FK_ERR_DEVICE = 7
 
 P = c_void_p
 I = c_int
@@ -35,6 +36,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "fk_abi_version": (c_int, []),
     "fk_status_string": (c_char_p, [I]),
     "fk_last_error_detail": (c_char_p, []),
+    "fk_workspace_status": (c_int, [P, c_size_t, I, P]),
     "fk_moe_workspace_bytes": (c_size_t, [I, I, I, I, I]),
     "fk_moe_router": (
         c_int,

@@ -28,10 +28,29 @@ const char* fk_status_string(int status) {
     case FK_ERR_LAUNCH: return "kernel launch failed";
     case FK_ERR_UNSUPPORTED: return "shape outside kernel limits";
     case FK_ERR_ALIGNMENT: return "pointer or row length not 16-byte aligned";
+    case FK_ERR_DEVICE: return "a bounded in-kernel wait ran out; outputs invalid";
     default: return "unknown status";
   }
 }
 
 const char* fk_last_error_detail(void) { return fk::g_last_error; }
+
+int fk_workspace_status(const void* workspace, size_t workspace_bytes, int clear, void* stream) {
+  using namespace fk;
+  if (!workspace || workspace_bytes < (kWorkspaceErrorWord + 1) * sizeof(uint32_t))
+    return fail(FK_ERR_WORKSPACE, "fk_workspace_status: workspace missing or smaller than its header");
+  const hipStream_t s = as_stream(stream);
+  uint32_t* word = reinterpret_cast<uint32_t*>(const_cast<void*>(workspace)) + kWorkspaceErrorWord;
+  uint32_t v = 0;
+  hipError_t err = hipMemcpyAsync(&v, word, sizeof(v), hipMemcpyDeviceToHost, s);
+  if (err == hipSuccess) err = hipStreamSynchronize(s);
+  if (err == hipSuccess && v != 0 && clear) {
+    err = hipMemsetAsync(word, 0, sizeof(uint32_t), s);
+    if (err == hipSuccess) err = hipStreamSynchronize(s);
+  }
+  if (err != hipSuccess) return fail(FK_ERR_LAUNCH, "fk_workspace_status: %s", hipGetErrorString(err));
+  if (v != 0) return fail(FK_ERR_DEVICE, "a kernel's bounded wait ran out (device flags 0x%x)", v);
+  return FK_OK;
+}
 
 }  // extern "C"

@@ -545,11 +545,11 @@ constexpr size_t kStepMixWords = (size_t)kStepMaxTokens * 8192;
 constexpr size_t kStepVWords = (size_t)kStepMaxTokens * 4096;
 constexpr size_t kStepHeadWords = (size_t)kStepMaxTokens * 64;
 constexpr int kStepTicketEpoch = 0;
-constexpr int kStepTicketError = 1;
+constexpr int kStepTicketError = kWorkspaceErrorWord;
 
 
 struct StepTagWs {
-  uint32_t* tickets;  // [16]: epoch, error flag
+  uint32_t* tickets;  // [16]: [0] epoch, [kWorkspaceErrorWord] error flag
   uint64_t* mix;      // [T, C] conv'd qkv
   uint64_t* z;        // [T, V]
   uint64_t* a;        // [T, Hv]

@@ -14,6 +14,10 @@ namespace fk {
 // returns `status`, so call sites read `return fail(FK_ERR_INVALID, "...")`.
 int fail(int status, const char* fmt, ...);
 
+// Word of every polling kernel's workspace (uint32 index) that records a
+// bounded wait that ran out.
+constexpr int kWorkspaceErrorWord = 15;
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline bool is_float_dtype(int dt) { return dt == FK_DTYPE_F32 || dt == FK_DTYPE_BF16; }

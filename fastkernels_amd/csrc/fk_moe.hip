@@ -66,7 +66,7 @@ struct MoeWs {
 constexpr int kTicketRouterBarrier = 0;
 constexpr int kTicketRouterTables = 1;
 constexpr int kTicketEpoch = 8;
-constexpr int kTicketError = 15;
+constexpr int kTicketError = kWorkspaceErrorWord;
 constexpr int kFusedMaxGrid = 1024;
 constexpr size_t kFusedLogitWords = 256 * 256;  // tagged router: T <= 256
 constexpr size_t kFusedActWords = (2 * 8 + 2) * 512;

@@ -29,6 +29,14 @@ def _stream_handle(stream: torch.cuda.Stream | None, device: torch.device) -> in
     return s.cuda_stream
 
 
+def _check_device(workspace: torch.Tensor, device: torch.device, stream: torch.cuda.Stream | None) -> None:
+    """Raise FastKernelsError (FK_ERR_DEVICE) if a bounded in-kernel wait of
+    an earlier step on this workspace ran out; clears the flag.  Synchronises
+    the stream, so call it outside timed or captured regions."""
+
+    _lib.call("fk_workspace_status", workspace.data_ptr(), workspace.numel(), 1, _stream_handle(stream, device))
+
+
 class MoeLayerPlan:
     """One MoE layer (router + experts + residual) at a fixed token count."""
 
@@ -121,6 +129,9 @@ class MoeLayerPlan:
             self.workspace.data_ptr(), self.workspace.numel(), _stream_handle(stream, self.device),
         )
 
+    def check_device(self, stream: torch.cuda.Stream | None = None) -> None:
+        _check_device(self.workspace, self.device, stream)
+
 
 class DeltaNetStepPlan:
     """One Gated DeltaNet decode step (T rows through one state) + residual,
@@ -179,3 +190,6 @@ class DeltaNetStepPlan:
             self.next_recurrent_state.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(),
             _stream_handle(stream, self.device),
         )
+
+    def check_device(self, stream: torch.cuda.Stream | None = None) -> None:
+        _check_device(self.workspace, self.device, stream)

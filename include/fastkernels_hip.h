@@ -48,12 +48,22 @@ enum {
   FK_ERR_WORKSPACE = 3,   /* workspace missing or too small */
   FK_ERR_LAUNCH = 4,      /* hipLaunchKernel / runtime error */
   FK_ERR_UNSUPPORTED = 5, /* shape outside the kernels' limits */
-  FK_ERR_ALIGNMENT = 6    /* pointer or row length breaks 16-byte vector loads */
+  FK_ERR_ALIGNMENT = 6,   /* pointer or row length breaks 16-byte vector loads */
+  FK_ERR_DEVICE = 7       /* a bounded wait inside a kernel ran out (fk_workspace_status) */
 };
 
 int fk_abi_version(void);
 const char* fk_status_string(int status);
 const char* fk_last_error_detail(void);
+
+/* Device error word of a workspace.  The kernels that hand values between
+ * workgroups (fk_moe_router, fk_moe_layer, fk_deltanet_step) poll with a
+ * bounded wait; a wait that runs out sets this word and the kernel ends
+ * normally with invalid outputs.  Synchronises `stream`, then returns FK_OK
+ * or FK_ERR_DEVICE; `clear` != 0 also resets the word (stream-ordered).
+ * No counterpart in the reference: its Triton kernels never wait on another
+ * program.  For callers that want to validate a run (tests, benchmarks). */
+int fk_workspace_status(const void* workspace, size_t workspace_bytes, int clear, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* MoE decode layer                                                          */

@@ -35,6 +35,13 @@ def test_status_strings():
     assert _lib.status_string(_lib.FK_OK) == "ok"
     assert "workspace" in _lib.status_string(_lib.FK_ERR_WORKSPACE)
     assert _lib.status_string(12345) == "unknown status"
+    assert "wait" in _lib.status_string(_lib.FK_ERR_DEVICE)
+
+
+def test_workspace_status_rejects_missing_workspace():
+    # Host-side check: no device access for a NULL or header-less workspace.
+    assert _err("fk_workspace_status", None, 0, 0, None) == _lib.FK_ERR_WORKSPACE
+    assert _err("fk_workspace_status", ctypes.c_void_p(256), 32, 0, None) == _lib.FK_ERR_WORKSPACE
 
 
 def test_workspace_sizes_are_monotone():

@@ -154,7 +154,7 @@ def test_step_single_launch_matches_oracle(device, real_dn, tokens):
     plan = DeltaNetStepPlan(_to(real_dn, device), tokens, REAL)
     plan.hidden.copy_(x.to(device))
     plan.run()
-    torch.cuda.synchronize()
+    plan.check_device()  # no bounded wait ran out (synchronises)
     update, conv, state = oracle.deltanet_update(
         x, real_dn["conv_state"], real_dn["recurrent_state"], real_dn, **_dims(REAL))
     torch.testing.assert_close(plan.update.cpu(), update, **tol(torch.bfloat16))
@@ -204,3 +204,4 @@ def test_step_single_launch_repeated_calls_stay_consistent(device, real_dn):
             plan.run()
             assert torch.equal(plan.update, u)
             assert torch.equal(plan.next_recurrent_state, s)
+    plan.check_device()

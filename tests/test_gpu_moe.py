@@ -293,7 +293,7 @@ def test_fused_layer_matches_multi_launch(device, real_gpu, tokens):
     plan.run_router()
     plan.run_experts()
     multi = (plan.layer_out, plan.moe_out, plan.logits, plan.ids, plan.weights)
-    torch.cuda.synchronize()
+    plan.check_device()  # no bounded wait ran out (synchronises)
     assert torch.equal(fused[3], multi[3])
     for a, b in zip(fused[2:], multi[2:]):
         torch.testing.assert_close(a, b, atol=1e-6, rtol=1e-6)
@@ -347,3 +347,4 @@ def test_fused_layer_repeated_calls_stay_consistent(device, real_gpu):
             plan.hidden.copy_(x)
             plan.run()
             assert torch.equal(plan.layer_out, r)
+    plan.check_device()
