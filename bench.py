@@ -4,8 +4,10 @@
 Headline (the JSON `value`): microseconds per MoE layer decode step at batch
 16, bf16 weights, weights resident in HBM.
 Extra sub-results on the same line: batch 1 (config 0), batch 128 with the
-Zipf router bias (config 2) and the Gated DeltaNet step at batch 1 and 8
-(config 3).
+Zipf router bias (config 2), the Gated DeltaNet step at batch 1 and 8
+(config 3), and a stack of 40 independent resident MoE layers (64.7 GB of
+weights) run 32 times at batch 1 and 8 with the residual carried from layer
+to layer (config 4; cache-cold by construction).
 
 Method: every step is one MoE layer (router + top-k + routing tables +
 experts + residual) issued through the C ABI from a preallocated plan.  K
@@ -45,7 +47,9 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU-baseline sample")
     p.add_argument("--no-extra", action="store_true", help="skip the batch-1/128 and DeltaNet sub-results")
     p.add_argument("--zipf", action="store_true", help="with --only moe: add the config-2 Zipf router bias")
-    p.add_argument("--only", choices=["moe", "deltanet", "copy"], default=None,
+    p.add_argument("--no-stack", action="store_true", help="skip the 40-layer resident stack (config 4)")
+    p.add_argument("--stack-layers", type=int, default=40, help="layers of the config-4 stack")
+    p.add_argument("--only", choices=["moe", "deltanet", "copy", "stack"], default=None,
                    help="run a single timing loop (for profilers) and print its line; "
                         "'copy' runs 16 device-to-device copies of 1 GiB (PMC byte-counter calibration)")
     return p.parse_args()
@@ -117,7 +121,7 @@ def main() -> int:
 
     R = max(1, args.weight_sets)
     log(f"generating {R} MoE weight sets on {torch.cuda.get_device_name(0)}")
-    sets = [] if args.only == "deltanet" else [moe_set(r) for r in range(R)]
+    sets = [] if args.only in ("deltanet", "stack") else [moe_set(r) for r in range(R)]
     torch.cuda.synchronize()
 
     def timed_graph(fns, steps: int, warmup: int) -> float:
@@ -208,6 +212,52 @@ def main() -> int:
             "hbm_frac": round(nbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
         }
 
+    def stack_result(tokens: int, layers: int, steps: int) -> dict:
+        """Config 4: `layers` independent resident MoE layers (weights seeded
+        base + layer), each step running them in order with the residual
+        carried across layers: layer l reads layer l-1's fp32 layer output."""
+
+        lsets = [moe_set(100 + l) for l in range(layers)]
+        lplans = []
+        for l in range(layers):
+            prev = lplans[-1].layer_out if lplans else None
+            lp = MoeLayerPlan(lsets[l], tokens, top_k=K, hidden=prev)
+            if prev is None:
+                lp.hidden.copy_(wl.make_hidden(tokens, H, seed=7).to(dev))
+            lplans.append(lp)
+
+        def step(s):
+            for lp in lplans:
+                lp.run(s)
+
+        ms = timed_graph([step], steps, 2)
+        for lp in lplans:
+            lp.check_device(stream)
+        us_layer = ms * 1e3 / layers
+        u = distinct(lplans)
+        nbytes = sum(
+            wl.moe_layer_bytes(tokens, x, spec, in_bytes=2 if l == 0 else 4) for l, x in enumerate(u)
+        ) / layers
+        res = {
+            "tokens": tokens,
+            "layers": layers,
+            "steps": steps,
+            "us_per_layer_step": round(us_layer, 3),
+            "us_per_stack_step": round(ms * 1e3, 3),
+            "distinct_experts_mean": round(sum(u) / layers, 2),
+            "algorithmic_bytes_per_layer_step": int(nbytes),
+            "resident_weight_bytes": int(sum(sum(t.numel() * t.element_size() for t in s.values()) for s in lsets)),
+            "achieved_tbs": round(nbytes / (us_layer * 1e-6) / 1e12, 3),
+            "hbm_frac": round(nbytes / (us_layer * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
+        }
+        del lplans, lsets
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        return res
+
+    if args.only == "stack":
+        print(json.dumps(stack_result(args.tokens, args.stack_layers, min(args.steps, 32))))
+        return 0
     if args.only == "moe":
         res = moe_result(args.tokens, bias=wl.zipf_router_bias(E, seed=0).to(dev) if args.zipf else None)
         res.pop("_plans")
@@ -243,6 +293,10 @@ def main() -> int:
         log("timing Gated DeltaNet step T=1 and T=8")
         for tokens in (1, 8):
             sub[f"deltanet_t{tokens}"] = deltanet_result(tokens)
+    if not args.no_extra and not args.no_stack:
+        for tokens in (1, 8):
+            log(f"timing the {args.stack_layers}-layer resident stack, T={tokens} (config 4)")
+            sub[f"moe_stack{args.stack_layers}_t{tokens}"] = stack_result(tokens, args.stack_layers, 32)
 
     # -- CPU baseline (oracle on the host cores, bounded sample) ----------------
     cpu = None

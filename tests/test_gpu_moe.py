@@ -267,9 +267,12 @@ def test_moe_layer_deterministic(device, real_gpu):
         assert torch.equal(u, v)
 
 
-def test_moe_layer_fp32_hidden(device, real_cpu, real_gpu):
-    # the real-weight runner feeds fp32 hidden (bench/qwen36_full_decode.py:152)
-    x = wl.make_hidden(2, H, seed=9, dtype=torch.float32)
+@pytest.mark.parametrize("tokens", [1, 2, 8, 64])
+def test_moe_layer_fp32_hidden(device, real_cpu, real_gpu, tokens):
+    # the real-weight runner feeds fp32 hidden (bench/qwen36_full_decode.py:152),
+    # and a layer stack feeds each layer the previous layer's fp32 output:
+    # single-launch (T <= 2), GEMV (T = 8) and T >= 64 expert paths
+    x = wl.make_hidden(tokens, H, seed=9, dtype=torch.float32)
     lh, moe, logits, ids, w = hip.hip_qwen36_batched_moe_layer_decode(x.to(device), *_moe_args(real_gpu), top_k=K)
     ref = oracle.routed_experts(x, ids.cpu(), w.cpu(), real_cpu["expert_gate_up_weight"], real_cpu["expert_down_weight"])
     ref = ref + oracle.shared_expert(x, real_cpu["shared_gate_up_weight"], real_cpu["shared_down_weight"],
