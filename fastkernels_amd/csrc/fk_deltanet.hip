@@ -544,6 +544,7 @@ constexpr int kStepD = 128;
 constexpr size_t kStepMixWords = (size_t)kStepMaxTokens * 8192;
 constexpr size_t kStepVWords = (size_t)kStepMaxTokens * 4096;
 constexpr size_t kStepHeadWords = (size_t)kStepMaxTokens * 64;
+constexpr size_t kStepPartWords = (size_t)8 * kStepMaxTokens * 2048;  // [V/512 <= 8][T][H <= 2048]
 constexpr int kStepTicketEpoch = 0;
 constexpr int kStepTicketError = kWorkspaceErrorWord;
 
@@ -556,6 +557,14 @@ struct StepTagWs {
   uint64_t* b;        // [T, Hv]
   uint64_t* norm;     // [T, V] gated-RMSNorm output
   uint64_t* started;  // [grid]
+  // Polling hints: a tile's (a head's) tag is stored once its outputs are
+  // stored.  A consumer waits on the few hints of its producers before it
+  // reads their outputs, instead of spinning on every output word (which
+  // floods the memory system while the producers still stream).  The
+  // outputs still carry their own tags and are re-read until they do.
+  uint64_t* hint_tile;  // [kStepTilesPerWG * kStepMaxGrid]
+  uint64_t* hint_head;  // [64]
+  uint64_t* part;       // [V / 512][T][H] phase C partial sums
 };
 
 struct StepArgs {
@@ -619,12 +628,12 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   const bool is_out = b < H / 16;
   const int keeper = max(0, G - Hv - 1);
 
-  // Loads are issued in the order their data is consumed (the vector memory
-  // counter retires in order): token chunks and norm weight, the phase A
-  // weight tiles, then the operands of the later phases.
+  // The token chunks and the norm weight are loaded and staged before any
+  // weight load is issued: behind the 50 MB weight stream of every
+  // workgroup, their few lines would come back with the last weight tile.
   constexpr int XCH = NT * 2048 / 8 / 512;  // token chunks per thread at H <= 2048
   // H and V are powers of two (the host checks): indices split by shifts.
-  const int lh = 31 - __builtin_clz((unsigned)H), lv = 31 - __builtin_clz((unsigned)V);
+  const int lh = 31 - __builtin_clz((unsigned)H);
   const int cpt_sh = lh - 3;  // 8-element chunks per token row: H / 8
   const int cpt = H >> 3, nchunk = T * cpt;
   Raw8<BFX> xr[XCH];
@@ -636,70 +645,6 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       xr[q] = load_raw8<BFX>(a.x, (size_t)idx8 * 8);
       nr[q] = load_raw8<true>(a.nw, (size_t)(idx8 & (cpt - 1)) * 8);
     }
-  }
-
-  // ---- phase A weight tiles ----------------------------------------------
-  const int ntiles = (R + 15) / 16;
-  const int kw = H >> 3;  // K range of one wavefront (H / 8 waves)
-  const int ks = kw >> 5;  // MFMA steps per tile (H <= 2048: <= 8)
-  // Row-contiguous loads: instruction s of tile i reads rows s*RPI + lane/LPR
-  // of the tile, LPR lanes x 16 B = the wavefront's whole K range of a row,
-  // so every load covers complete cache lines (the MFMA operand layout, 16
-  // rows x 64 B per load, streams at half the rate).  The tile is turned
-  // into the operand layout through the wavefront's LDS area below.
-  const int lpr_sh = lh - 6;  // lanes per row LPR = kw / 8, rows per load RPI = 64 / LPR
-  const int LPR = 1 << lpr_sh, RPI = kWave >> lpr_sh;
-  int ntl = 0;
-  u32x4 av[kStepTilesPerWG][8];
-  {
-#pragma unroll
-    for (int i = 0; i < kStepTilesPerWG; ++i) {
-      const int tile = b + i * G;
-      if (tile < ntiles) ntl = i + 1;
-    }
-    // The matrix boundaries C, C + V, C + V + Hv and R are multiples of 16
-    // (the host checks), so a tile lies in one matrix and the base address
-    // of each load is uniform; the lane adds a fixed byte offset (< RPI rows).
-    // Every slot issues its load: one outside the weights (past the last
-    // tile or past K) reads the first RPI rows of the qkv weight, the same
-    // few lines in every workgroup, and its data is never used.  A load under
-    // a condition would not be counted by the compiler's wait for the token
-    // chunks above, which would then wait for the weight tiles too.
-    const uint32_t lane_off = (uint32_t)((((lane >> lpr_sh) << lh) + (wave << (lh - 3)) + ((lane & (LPR - 1)) << 3)) << 1);
-    const size_t slot_stride = (size_t)RPI << (lh + 1);  // RPI rows of H bf16
-    const char* spare = reinterpret_cast<const char*>(a.w[0]);
-#pragma unroll
-    for (int i = 0; i < kStepTilesPerWG; ++i) {
-      const int tile = b + i * G;
-      const int row0 = tile * 16;
-      const int wh = row0 < C ? 0 : row0 < C + V ? 1 : row0 < C + V + Hv ? 2 : 3;
-      const int r0 = row0 - (wh == 0 ? 0 : wh == 1 ? C : wh == 2 ? C + V : C + V + Hv);
-      const char* tp = reinterpret_cast<const char*>(wh == 0 ? a.w[0] : wh == 1 ? a.w[1] : wh == 2 ? a.w[2] : a.w[3]) +
-                       ((size_t)(tile < ntiles ? r0 : 0) << (lh + 1));
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const char* base = s < ks && tile < ntiles ? tp : spare;
-        av[i][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + lane_off));
-        tp += slot_stride;
-      }
-    }
-  }
-
-  // Small operands of later phases, fetched now so that no phase waits on a
-  // dependent global load: the head's norm weight and decay parameters and
-  // the conv taps of this workgroup's qkv rows (thread i*16 + r: row r of
-  // tile i).
-  uint32_t lnw2[2], alog[1], dtb1[1];
-  gather_raw<true>(a.lnw, lane, 64, 2, lnw2);
-  gather_raw<true>(a.a_log, is_head ? head : 0, 0, 1, alog);
-  gather_raw<true>(a.dt_bias, is_head ? head : 0, 0, 1, dtb1);
-  uint32_t cwin_raw[8], cwk_raw[8];
-  {
-    const int row = (b + (tid >> 4) * G) * 16 + (tid & 15);
-    const bool conv_row = tid < kStepTilesPerWG * 16 && row < C;
-    const int nk = conv_row ? a.KS : 0;
-    gather_raw<true>(a.conv_state, (size_t)(conv_row ? row : 0) * a.KS, 1, nk, cwin_raw);
-    gather_raw<true>(a.conv_w, (size_t)(conv_row ? row : 0) * a.KS, 1, nk, cwk_raw);
   }
 
   // ---- stage the normalised tokens as bf16 hi/lo MFMA columns ------------
@@ -759,125 +704,195 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     __syncthreads();
   }
 
+  // ---- phase A weight tiles ----------------------------------------------
+  // Loads are issued in the order their data is consumed (the vector memory
+  // counter retires in order): the phase A weight tiles, then the operands
+  // of the later phases.
+  const int ntiles = (R + 15) / 16;
+  const int kw = H >> 3;  // K range of one wavefront's MFMAs (H / 8 waves)
+  const int ks = kw >> 5;  // MFMA steps per tile (H <= 2048: <= 8); also load slots per tile
+  // Whole-row loads: wavefront w reads rows 2w and 2w + 1 of each tile, one
+  // 1 KiB piece of a row per instruction (slot s: row 2w + s / LPR, piece
+  // s % LPR, LPR = H / 512 pieces per row).  Reading the wavefront's MFMA K
+  // range of all 16 rows instead streams at 4.0 TB/s against 5.0 TB/s for
+  // whole rows on this part.  The rows meet in the workgroup's LDS tile.
+  const int lpr_sh = lh - 9;  // log2 of the 1 KiB pieces per row
+  const int LPR = 1 << lpr_sh;
+  int ntl = 0;
+  u32x4 av[kStepTilesPerWG][8];
+  {
+#pragma unroll
+    for (int i = 0; i < kStepTilesPerWG; ++i) {
+      const int tile = b + i * G;
+      if (tile < ntiles) ntl = i + 1;
+    }
+    // The matrix boundaries C, C + V, C + V + Hv and R are multiples of 16
+    // (the host checks), so a tile lies in one matrix and the base address
+    // of each load is uniform; the lane adds a fixed byte offset.  Every
+    // slot issues its load: one outside the weights (past the last tile or
+    // past the row) reads the first KiB of the qkv weight, the same line in
+    // every workgroup, and its data is never used.  A load under a condition
+    // would make the compiler's waits below count it as not issued and wait
+    // for later loads too.
+    const uint32_t lane_off = (uint32_t)((wave << (lh + 2)) + (lane << 4));  // rows 2w.. (2H bytes each) + lane
+    const char* spare = reinterpret_cast<const char*>(a.w[0]);
+#pragma unroll
+    for (int i = 0; i < kStepTilesPerWG; ++i) {
+      const int tile = b + i * G;
+      const int row0 = tile * 16;
+      const int wh = row0 < C ? 0 : row0 < C + V ? 1 : row0 < C + V + Hv ? 2 : 3;
+      const int r0 = row0 - (wh == 0 ? 0 : wh == 1 ? C : wh == 2 ? C + V : C + V + Hv);
+      const char* tp = reinterpret_cast<const char*>(wh == 0 ? a.w[0] : wh == 1 ? a.w[1] : wh == 2 ? a.w[2] : a.w[3]) +
+                       ((size_t)(tile < ntiles ? r0 : 0) << (lh + 1));
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const bool live = s < ks && tile < ntiles;
+        const size_t so = ((size_t)(s >> lpr_sh) << (lh + 1)) + ((size_t)(s & (LPR - 1)) << 10);
+        av[i][s] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(live ? tp + so + lane_off : spare + (lane << 4)));
+      }
+    }
+  }
+
+  // Small operands of later phases, fetched now so that no phase waits on a
+  // dependent global load: the head's norm weight and decay parameters and
+  // the conv taps of this workgroup's qkv rows (thread i*16 + r: row r of
+  // tile i).
+  uint32_t lnw2[2], alog[1], dtb1[1];
+  gather_raw<true>(a.lnw, lane, 64, 2, lnw2);
+  gather_raw<true>(a.a_log, is_head ? head : 0, 0, 1, alog);
+  gather_raw<true>(a.dt_bias, is_head ? head : 0, 0, 1, dtb1);
+  uint32_t cwin_raw[8], cwk_raw[8];
+  {
+    const int row = (b + (tid >> 7) * G) * 16 + ((tid >> 3) & 15);  // thread (tile, row, token) below
+    const bool conv_row = row < C;
+    const int nk = conv_row ? a.KS : 0;
+    gather_raw<true>(a.conv_state, (size_t)(conv_row ? row : 0) * a.KS, 1, nk, cwin_raw);
+    gather_raw<true>(a.conv_w, (size_t)(conv_row ? row : 0) * a.KS, 1, nk, cwk_raw);
+  }
+
   // Head workgroups: prefetch the state (thread (j, gq): rows 32gq.., column
-  // j).  Issued only now: the waits above are counted over every path, so
-  // head-only loads in front of them would make the other workgroups wait
-  // for their weight tiles too.
+  // j).  Issued after the weight tiles: the waits below are counted over
+  // every path, so head-only loads in front of them would make the other
+  // workgroups wait for more of their weight tiles.
   const int sj = tid >> 2, sg = tid & 3;
   uint32_t S_raw[32];
   if (is_head) gather_raw<false>(a.rec_state, ((size_t)head * kStepD + (size_t)sg * 32) * kStepD + sj, kStepD, 32, S_raw);
 
   // ---- phase A: projections ---------------------------------------------
-  // LDS: s_xb | per-wavefront transposition areas [8][16 rows][kw*2 + 16 B]
-  // (row pitch padded by 16 B: the 16 rows of an operand read fall in
-  // distinct banks).  Each wavefront's partial sums [tile][16][NC] go to the
-  // start of its own area once its MFMAs are done.
-  const int pitch = kw * 2 + 16;
-  char* s_tw = s_dyn + (size_t)H * NC * 2 + (size_t)wave * 16 * pitch;
-  float* s_red_w = reinterpret_cast<float*>(s_tw);
+  // LDS: s_xb | the workgroup's tile [16 rows][2H + 16 B] (row pitch padded
+  // by 16 B: the 16 rows of an operand read fall in distinct banks).  Per
+  // tile the wavefronts write their rows, then each runs the MFMAs of its K
+  // range (H / 8) over all 16 rows.  The partial sums [wave][tile][16][NC]
+  // go to the tile area once every tile is done.
+  const int pitch = 2 * H + 16;
+  char* s_tile = s_dyn + (size_t)H * NC * 2;
   {
     f32x4_t acc[kStepTilesPerWG];
 #pragma unroll
     for (int i = 0; i < kStepTilesPerWG; ++i) {
       acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      if (i < ntl) {
-        // tile i: registers -> LDS rows (lanes of one load: RPI rows x kw k)
+      if (i < ntl) {  // uniform per workgroup
 #pragma unroll
         for (int s = 0; s < 8; ++s)
           if (s < ks)
-            *reinterpret_cast<u32x4*>(s_tw + (s * RPI + (lane >> lpr_sh)) * pitch + ((lane & (LPR - 1)) << 4)) = av[i][s];
+            *reinterpret_cast<u32x4*>(s_tile + (2 * wave + (s >> lpr_sh)) * pitch + ((s & (LPR - 1)) << 10) + (lane << 4)) =
+                av[i][s];
+        __syncthreads();
         // MFMA steps: operand lane (row n, k group g4) reads 8 k of its row
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
           if (s < ks) {
-            const u32x4 wv = *reinterpret_cast<const u32x4*>(s_tw + n * pitch + (s * 32 + g4 * 8) * 2);
-            const int c = ((wave * kw + s * 32) >> 3) + g4;
+            const int k = wave * kw + s * 32 + g4 * 8;
+            const u32x4 wv = *reinterpret_cast<const u32x4*>(s_tile + n * pitch + k * 2);
+            const int c = k >> 3;
             const u32x4 bv = n < NC ? *reinterpret_cast<const u32x4*>(s_xb + ((size_t)c * NC + n) * 8) : u32x4{0, 0, 0, 0};
             acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wv),
                                                              __builtin_bit_cast(bf16x8_t, bv), acc[i], 0, 0, 0);
           }
         }
+        __syncthreads();
       }
     }
+    float* s_red = reinterpret_cast<float*>(s_tile);  // [wave][tile][16][NC]
+    const int red_w = kStepTilesPerWG * 16 * NC;
     if (n < NC) {
 #pragma unroll
       for (int i = 0; i < kStepTilesPerWG; ++i)
         if (i < ntl)
 #pragma unroll
-          for (int q = 0; q < 4; ++q) s_red_w[((size_t)i * 16 + g4 * 4 + q) * NC + n] = acc[i][q];
+          for (int q = 0; q < 4; ++q) s_red[(size_t)wave * red_w + ((size_t)i * 16 + g4 * 4 + q) * NC + n] = acc[i][q];
     }
     __syncthreads();
-    // One thread per (tile, row): sums the wavefronts' partials (hi + lo)
-    // and finishes the row for every token.
-    if (tid < ntl * 16) {
-      const int i = tid >> 4, r = tid & 15;
-      const int row = (b + i * G) * 16 + r;
-      if (row < R) {
-        float v[kStepMaxTokens];
+    // One thread per (tile, row, token): sums the wavefronts' partials (hi +
+    // lo) in wavefront order.  A qkv row's sequence [conv state | tokens]
+    // goes through LDS, and each token's thread applies the causal conv to
+    // its window (entries t + 1 .. t + KS) and SiLU.
+    float* s_seq = s_red + (size_t)kStepWaves * red_w;  // [tile][16][16]
+    const int ei = tid >> 7, er = (tid >> 3) & 15, et = tid & 7;
+    const int erow = (b + ei * G) * 16 + er;
+    const bool elive = ei < ntl && erow < R && et < T;
+    float* sq = s_seq + (ei * 16 + er) * 16;
+    float ev = 0.f;
+    if (elive) {
+      const float* pr = s_red + ((size_t)ei * 16 + er) * NC + 2 * et;
+      for (int w = 0; w < kStepWaves; ++w) ev += pr[(size_t)w * red_w] + pr[(size_t)w * red_w + 1];
+      sq[a.KS + et] = ev;
+      if (et == 0 && erow < C) {
 #pragma unroll
-        for (int t = 0; t < kStepMaxTokens; ++t) {
-          v[t] = 0.f;
-          if (t < T)
-            for (int w = 0; w < kStepWaves; ++w) {
-              const float* pr = reinterpret_cast<const float*>(s_dyn + (size_t)H * NC * 2 + (size_t)w * 16 * pitch) +
-                                ((size_t)i * 16 + r) * NC;
-              v[t] += pr[2 * t] + pr[2 * t + 1];
-            }
-        }
-        if (row < C) {
-          // causal depthwise conv + SiLU over [state | tokens], state rolled
-          float win[8], wk[8];
+        for (int q = 0; q < 8; ++q)
+          if (q < a.KS) sq[q] = raw_value<true>(cwin_raw[q]);
+      }
+    }
+    __syncthreads();
+    if (elive) {
+      if (erow < C) {
+        float cv = 0.f;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            win[j] = raw_value<true>(cwin_raw[j]);
-            wk[j] = raw_value<true>(cwk_raw[j]);
-          }
-#pragma unroll
-          for (int t = 0; t < kStepMaxTokens; ++t) {
-            if (t < T) {
-#pragma unroll
-              for (int j = 0; j < 7; ++j)
-                if (j + 1 < a.KS) win[j] = win[j + 1];
-#pragma unroll
-              for (int j = 0; j < 8; ++j)
-                if (j == a.KS - 1) win[j] = v[t];
-              float cv = 0.f;
-#pragma unroll
-              for (int j = 0; j < 8; ++j)
-                if (j < a.KS) cv = fmaf(wk[j], win[j], cv);
-              store_tagged(a.tw.mix + (size_t)t * C + row, silu(cv), tag);
-            }
-          }
+        for (int j = 0; j < 8; ++j)
+          if (j < a.KS) cv = fmaf(raw_value<true>(cwk_raw[j]), sq[et + 1 + j], cv);
+        store_tagged(a.tw.mix + (size_t)et * C + erow, silu(cv), tag);
+        if (et == 0) {
 #pragma unroll
           for (int j = 0; j < 8; ++j)
-            if (j < a.KS) reinterpret_cast<uint16_t*>(a.next_conv)[(size_t)row * a.KS + j] = f32_to_bf16_bits(win[j]);
-        } else {
-          uint64_t* dst;
-          int stride, off;
-          if (row < C + V) {
-            dst = a.tw.z, stride = V, off = row - C;
-          } else if (row < C + V + Hv) {
-            dst = a.tw.a, stride = Hv, off = row - C - V;
-          } else {
-            dst = a.tw.b, stride = Hv, off = row - C - V - Hv;
-          }
-#pragma unroll
-          for (int t = 0; t < kStepMaxTokens; ++t)
-            if (t < T) store_tagged(dst + (size_t)t * stride + off, v[t], tag);
+            if (j < a.KS) reinterpret_cast<uint16_t*>(a.next_conv)[(size_t)erow * a.KS + j] = f32_to_bf16_bits(sq[T + j]);
         }
+      } else {
+        uint64_t* dst;
+        int stride, off;
+        if (erow < C + V) {
+          dst = a.tw.z, stride = V, off = erow - C;
+        } else if (erow < C + V + Hv) {
+          dst = a.tw.a, stride = Hv, off = erow - C - V;
+        } else {
+          dst = a.tw.b, stride = Hv, off = erow - C - V - Hv;
+        }
+        store_tagged(dst + (size_t)et * stride + off, ev, tag);
       }
     }
     __syncthreads();  // phases B and C reuse the dynamic LDS
+    // every thread's stores of the tiles are issued before these hints
+    if (tid < ntl) store_tagged(a.tw.hint_tile + b + tid * G, 0.f, tag);
   }
 
-  // ---- W_out tiles for phase C, fetched while the heads run --------------
-  const int kwc = V >> 3, ksc = kwc >> 5;  // V / 8 waves; V <= 4096: <= 16 steps
+  // ---- W_out for phase C, fetched while the heads run --------------------
+  // Phase C is split over K.  Unit (rb, ks), on workgroup b = rb * nks + ks,
+  // multiplies rows 128 rb .. + 128 of W_out, restricted to the columns
+  // kcu ks .. + kcu of kcu / 128 heads (kcu = min(V, 512)), by those heads'
+  // outputs: wavefront w holds rows 16 w .. + 16 of the block in the MFMA
+  // operand layout.  Each unit reads T * kcu head outputs instead of T * V,
+  // and each output row sums nks partials afterwards.
+  const int kcu = V < 512 ? V : 512, nks = V / kcu, nunits = (H >> 7) * nks;
+  const int ksc = kcu >> 5;  // MFMA steps per unit (<= 16)
+  const bool is_unit = b < nunits;
+  const int urb = is_unit ? b / nks : 0, uks = is_unit ? b - urb * nks : 0;
   u32x4 ov[16];
-  if (is_out) {
-    const uint16_t* wp = reinterpret_cast<const uint16_t*>(a.w_out) + (size_t)(b * 16 + n) * V;
+  if (is_unit) {
+    const uint16_t* wp =
+        reinterpret_cast<const uint16_t*>(a.w_out) + (size_t)(urb * 128 + wave * 16 + n) * V + (size_t)uks * kcu;
 #pragma unroll
     for (int s = 0; s < 16; ++s)
-      if (s < ksc) ov[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp + wave * kwc + s * 32 + g4 * 8));
+      if (s < ksc) ov[s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp + s * 32 + g4 * 8));
   }
   // residual inputs of this workgroup's output rows (thread t*16 + r)
   uint32_t xres[1];
@@ -912,12 +927,38 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     const int per_tok = 4 * kStepD + 2;
     const int n_in = T * per_tok;
     bool ok = true;
-    for (int base = tid; base < n_in; base += 512 * 4) {
-      uint64_t w[4];
-      const uint64_t* srcs[4];
-      int dsti[4];
+    // Hints of the 34 tiles holding this head's q, k, v, z, a and b rows
+    // (one load per lane), then one read of the inputs.
+    if (wave == 0) {
+      constexpr int TPB = kStepD / 16;  // tiles per 128-row block
+      int tl = -1;
+      if (lane < 4 * TPB) {
+        const int part = lane / TPB;
+        const int row0 = part == 0 ? hq * kStepD
+                       : part == 1 ? (a.Hk + hq) * kStepD
+                       : part == 2 ? (2 * a.Hk + head) * kStepD
+                                   : C + head * kStepD;
+        tl = row0 / 16 + lane % TPB;
+      } else if (lane == 4 * TPB) {
+        tl = (C + V + head) / 16;
+      } else if (lane == 4 * TPB + 1) {
+        tl = (C + V + Hv + head) / 16;
+      }
+      uint64_t hw[1];
+      const uint64_t* hs[1] = {tl >= 0 ? a.tw.hint_tile + tl : nullptr};
+      hw[0] = hs[0] ? load_tagged(hs[0]) : 0ull;
+      if (!poll_tagged<1>(hw, hs, tag)) s_fail = 1;
+    }
+    __syncthreads();
+    // one batch of tagged loads in flight covers every input (T <= NT)
+    constexpr int BB = NT <= 2 ? 4 : 12;
+    static_assert(BB * 512 >= NT * (4 * kStepD + 2), "head inputs exceed one poll batch");
+    for (int base = tid; base < n_in; base += 512 * BB) {
+      uint64_t w[BB];
+      const uint64_t* srcs[BB];
+      int dsti[BB];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < BB; ++j) {
         const int idx = base + j * 512;
         srcs[j] = nullptr;
         dsti[j] = -1;
@@ -938,9 +979,9 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         }
         w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
       }
-      ok = poll_tagged<4>(w, srcs, tag) && ok;
+      ok = poll_tagged<BB>(w, srcs, tag) && ok;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < BB; ++j)
         if (dsti[j] >= 0) s_in[dsti[j]] = value_of(w[j]);
     }
     if (!ok) s_fail = 1;
@@ -1010,6 +1051,8 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       store_tagged(dst + lane, o0 * rs * raw_value<true>(lnw2[0]) * silu(z[lane]), tag);
       store_tagged(dst + lane + 64, o1 * rs * raw_value<true>(lnw2[1]) * silu(z[lane + 64]), tag);
     }
+    __syncthreads();
+    if (tid == 0) store_tagged(a.tw.hint_head + head, 0.f, tag);
     {
       const size_t base = ((size_t)head * kStepD + (size_t)sg * 32) * kStepD + sj;
 #pragma unroll
@@ -1018,27 +1061,37 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     __syncthreads();  // s_dyn is reused below
   }
 
-  // ---- phase C: output projection of rows 16b..16b+15 --------------------
-  if (is_out) {
-    uint16_t* s_nb = reinterpret_cast<uint16_t*>(s_dyn);  // [V/8][NC][8] bf16
-    float* s_red2 = reinterpret_cast<float*>(s_dyn + (size_t)V * NC * 2);  // [8][16][NC]
-    const int n_norm = T * V;
+  // ---- phase C1: partial output projection of unit (urb, uks) ------------
+  if (is_unit) {
+    uint16_t* s_nb = reinterpret_cast<uint16_t*>(s_dyn);  // [kcu/8][NC][8] bf16
+    const int h0 = uks * (kcu / kStepD), nh = kcu / kStepD;  // heads of the unit's columns
     bool ok = true;
-    for (int base = tid; base < n_norm; base += 512 * 8) {
-      uint64_t w[8];
-      const uint64_t* srcs[8];
+    if (wave == 0) {
+      uint64_t hw[1];
+      const uint64_t* hs[1] = {lane < nh ? a.tw.hint_head + h0 + lane : nullptr};
+      hw[0] = hs[0] ? load_tagged(hs[0]) : 0ull;
+      if (!poll_tagged<1>(hw, hs, tag)) s_fail = 1;
+    }
+    __syncthreads();
+    // The T * kcu inputs in one batch of tagged loads.
+    constexpr int CB = NT <= 2 ? 2 : 8;
+    static_assert(CB * 512 >= NT * 512, "unit inputs exceed one poll batch");
+    const int lk = 31 - __builtin_clz((unsigned)kcu), n_in = T * kcu;
+    {
+      uint64_t w[CB];
+      const uint64_t* srcs[CB];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int idx = base + j * 512;
-        srcs[j] = idx < n_norm ? a.tw.norm + idx : nullptr;
+      for (int j = 0; j < CB; ++j) {
+        const int idx = tid + j * 512;
+        srcs[j] = idx < n_in ? a.tw.norm + (size_t)(idx >> lk) * V + (size_t)uks * kcu + (idx & (kcu - 1)) : nullptr;
         w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
       }
-      ok = poll_tagged<8>(w, srcs, tag) && ok;
+      ok = poll_tagged<CB>(w, srcs, tag);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int idx = base + j * 512;
-        if (idx < n_norm) {
-          const int t = idx >> lv, k = idx & (V - 1);
+      for (int j = 0; j < CB; ++j) {
+        const int idx = tid + j * 512;
+        if (idx < n_in) {
+          const int t = idx >> lk, k = idx & (kcu - 1);
           const uint32_t hl = bf16_pair_hi_lo(value_of(w[j]));
           const int c = k >> 3, e = k & 7;
           s_nb[((size_t)c * NC + 2 * t) * 8 + e] = (uint16_t)(hl & 0xffffu);
@@ -1052,24 +1105,40 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
       if (s < ksc) {
-        const int c = ((wave * kwc + s * 32) >> 3) + g4;
+        const int c = s * 4 + g4;
         const u32x4 bv = n < NC ? *reinterpret_cast<const u32x4*>(s_nb + ((size_t)c * NC + n) * 8) : u32x4{0, 0, 0, 0};
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ov[s]),
                                                       __builtin_bit_cast(bf16x8_t, bv), acc, 0, 0, 0);
       }
     }
-    if (n < NC) {
+    // hi + lo columns of token t sit in lanes n = 2t and 2t + 1
+    float pq[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) s_red2[((size_t)wave * 16 + g4 * 4 + q) * NC + n] = acc[q];
+    for (int q = 0; q < 4; ++q) pq[q] = acc[q] + __uint_as_float(dpp_u32<kDppQuadXor1>(__float_as_uint(acc[q])));
+    if (n < NC && (n & 1) == 0) {
+      const size_t o = ((size_t)uks * T + (n >> 1)) * H + (size_t)urb * 128 + wave * 16 + g4 * 4;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) store_tagged(a.tw.part + o + q, pq[q], tag);
     }
-    __syncthreads();
+  }
+
+  // ---- phase C2: rows 16b..16b+15 = sum of the nks unit partials ----------
+  if (is_out) {
+    // (nks partials per thread: polled directly, few enough not to need hints)
     if (tid < 16 * T) {
       const int r = tid & 15, t = tid >> 4;
-      float v = 0.f;
-      for (int w = 0; w < kStepWaves; ++w) {
-        const float* pr = s_red2 + ((size_t)w * 16 + r) * NC;
-        v += pr[2 * t] + pr[2 * t + 1];
+      uint64_t w[8];
+      const uint64_t* srcs[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        srcs[j] = j < nks ? a.tw.part + ((size_t)j * T + t) * H + b * 16 + r : nullptr;
+        w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
       }
+      if (!poll_tagged<8>(w, srcs, tag)) s_fail = 1;
+      float v = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (j < nks) v += value_of(w[j]);
       const size_t o = (size_t)t * H + b * 16 + r;
       a.update[o] = v;
       if (a.hidden_out) a.hidden_out[o] = raw_value<BFX>(xres[0]) + v;
@@ -1185,6 +1254,9 @@ static size_t step_tag_layout(char* base, StepTagWs* tw) {
   tw->b = reinterpret_cast<uint64_t*>(take(kStepHeadWords * 8));
   tw->norm = reinterpret_cast<uint64_t*>(take(kStepVWords * 8));
   tw->started = reinterpret_cast<uint64_t*>(take((size_t)kStepMaxGrid * 8));
+  tw->hint_tile = reinterpret_cast<uint64_t*>(take((size_t)kStepTilesPerWG * kStepMaxGrid * 8));
+  tw->hint_head = reinterpret_cast<uint64_t*>(take(64 * 8));
+  tw->part = reinterpret_cast<uint64_t*>(take(kStepPartWords * 8));
   return off;
 }
 
@@ -1215,15 +1287,17 @@ static bool step_fused_eligible(int T, int H, int Hk, int Hv, int D, const int* 
     if (i != 5 && dt[i] != FK_DTYPE_BF16) dtypes_ok = false;
   return dtypes_ok && T >= 1 && T <= kStepMaxTokens && D == kStepD && H >= 512 && H <= 2048 && (H & (H - 1)) == 0 &&
          (V & (V - 1)) == 0 && V >= 256 && V <= 4096 && C <= 8192 && Hv <= 64 && Hv % 16 == 0 && G >= Hv + 1 &&
-         G >= H / 16 &&
+         G >= H / 16 && (H >> 7) * (V / (V < 512 ? V : 512)) <= G - Hv &&
          (R + 15) / 16 <= kStepTilesPerWG * G && G <= kStepMaxGrid;
 }
 
 static size_t step_fused_lds(int T, int H, int V) {
   const size_t nc = 2 * (size_t)T;
-  const size_t pa = (size_t)H * nc * 2 + (size_t)kStepWaves * 16 * ((size_t)H / kStepWaves * 2 + 16);
+  const size_t tile = (size_t)16 * (2 * (size_t)H + 16),
+               red = ((size_t)kStepWaves * kStepTilesPerWG * 16 * nc + kStepTilesPerWG * 16 * 16) * 4;
+  const size_t pa = (size_t)H * nc * 2 + (tile > red ? tile : red);
   const size_t pb = ((size_t)T * 4 * kStepD + 2 * kStepMaxTokens + (size_t)T * kStepD) * 4;
-  const size_t pc = (size_t)V * nc * 2 + (size_t)kStepWaves * 16 * nc * 4;
+  const size_t pc = (size_t)(V < 512 ? V : 512) * nc * 2;
   return pa > pb ? (pa > pc ? pa : pc) : (pb > pc ? pb : pc);
 }
 
