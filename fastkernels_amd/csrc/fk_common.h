@@ -73,6 +73,20 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{a, b}, bf16x2_t));
 }
 
+// Eight floats split as hi = bf16(v) and lo = bf16(v - hi) (both round to
+// nearest even), packed two per dword: MFMA operands whose products keep
+// about 16 bits of each value.
+__device__ __forceinline__ void split_hi_lo8(const float (&v)[8], u32x4& hi, u32x4& lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+    h[p] = pack_bf16x2(v[2 * p], v[2 * p + 1]);
+    l[p] = pack_bf16x2(v[2 * p] - __uint_as_float(h[p] << 16), v[2 * p + 1] - __uint_as_float(h[p] & 0xffff0000u));
+  }
+  hi = u32x4{h[0], h[1], h[2], h[3]};
+  lo = u32x4{l[0], l[1], l[2], l[3]};
+}
+
 template <bool BF16>
 __device__ __forceinline__ Raw8<BF16> load_raw8(const void* base, size_t elem_index) {
   Raw8<BF16> r;

@@ -587,11 +587,14 @@ struct StepArgs {
   StepTagWs tw;
 };
 
-__device__ __forceinline__ uint32_t bf16_pair_hi_lo(float v) {
-  const uint16_t hi = f32_to_bf16_bits(v);
-  const uint16_t lo = f32_to_bf16_bits(v - bf16_bits_to_f32(hi));
-  return (uint32_t)hi | ((uint32_t)lo << 16);
-}
+// Slot of column n of chunk c in an MFMA B-operand staging area
+// [chunks][ncp][8 bf16] (ncp a power of two >= the columns in use).  The
+// column is XOR-swizzled by the chunk: a wavefront writing one column of 64
+// consecutive chunks then spreads over all LDS banks (without it the
+// 16 * ncp-byte chunk stride puts every lane on the same banks), and the 16
+// columns of one chunk that an MFMA operand read takes stay a permutation of
+// the chunk's slots.
+__device__ __forceinline__ int bcol_slot(int c, int n, int ncp) { return c * ncp + (n ^ (c & (ncp - 1))); }
 
 // Lane quad sum (lanes 4q..4q+3 hold the four row quarters of a column).
 __device__ __forceinline__ float quad_sum(float v) {
@@ -618,6 +621,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   const int G = gridDim.x, b = blockIdx.x;
   const int T = a.T, H = a.H, C = a.C, V = a.V, R = a.R, Hv = a.Hv;
   const int NC = 2 * T;  // MFMA columns in use: (hi, lo) per token
+  const int NCP = NC <= 2 ? 2 : NC <= 4 ? 4 : NC <= 8 ? 8 : 16;  // staging columns (power of two)
   const uint32_t tag = load_coherent(&a.tw.tickets[kStepTicketEpoch]) + 1u;
   const int n = lane & 15, g4 = lane >> 4;  // MFMA lane -> (column / A row, k group)
 
@@ -648,7 +652,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   }
 
   // ---- stage the normalised tokens as bf16 hi/lo MFMA columns ------------
-  // s_xb: [H/8 chunks][NC][8] bf16.  Chunk q of thread tid is token-major
+  // s_xb: [H/8 chunks][NCP][8] bf16 (bcol_slot).  Chunk q of thread tid is token-major
   // chunk tid + 512 q; H % 512 == 0, so a wavefront's 64 chunks belong to one
   // token and the sum of squares reduces in a fixed order.
   uint16_t* s_xb = reinterpret_cast<uint16_t*>(s_dyn);
@@ -681,24 +685,16 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       const int idx8 = tid + q * 512;
       if (idx8 < nchunk) {
         const int t = idx8 >> cpt_sh, k0 = (idx8 & (cpt - 1)) << 3;
-        float xv[8], nv[8];
+        float xv[8], nv[8], y[8];
         raw8_to_f32<BFX>(xr[q], xv);
         raw8_to_f32<true>(nr[q], nv);
-        uint16_t hi[8], lo[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t hl = bf16_pair_hi_lo(xv[e] * s_rs[t] * (1.0f + nv[e]));
-          hi[e] = (uint16_t)(hl & 0xffffu);
-          lo[e] = (uint16_t)(hl >> 16);
-        }
-        const int c = k0 >> 3;
+        for (int e = 0; e < 8; ++e) y[e] = xv[e] * s_rs[t] * (1.0f + nv[e]);
         u32x4 vh, vl;
-        vh.x = hi[0] | ((uint32_t)hi[1] << 16); vh.y = hi[2] | ((uint32_t)hi[3] << 16);
-        vh.z = hi[4] | ((uint32_t)hi[5] << 16); vh.w = hi[6] | ((uint32_t)hi[7] << 16);
-        vl.x = lo[0] | ((uint32_t)lo[1] << 16); vl.y = lo[2] | ((uint32_t)lo[3] << 16);
-        vl.z = lo[4] | ((uint32_t)lo[5] << 16); vl.w = lo[6] | ((uint32_t)lo[7] << 16);
-        *reinterpret_cast<u32x4*>(s_xb + ((size_t)c * NC + 2 * t) * 8) = vh;
-        *reinterpret_cast<u32x4*>(s_xb + ((size_t)c * NC + 2 * t + 1) * 8) = vl;
+        split_hi_lo8(y, vh, vl);
+        const int c = k0 >> 3;
+        *reinterpret_cast<u32x4*>(s_xb + (size_t)bcol_slot(c, 2 * t, NCP) * 8) = vh;
+        *reinterpret_cast<u32x4*>(s_xb + (size_t)bcol_slot(c, 2 * t + 1, NCP) * 8) = vl;
       }
     }
     __syncthreads();
@@ -786,7 +782,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   // range (H / 8) over all 16 rows.  The partial sums [wave][tile][16][NC]
   // go to the tile area once every tile is done.
   const int pitch = 2 * H + 16;
-  char* s_tile = s_dyn + (size_t)H * NC * 2;
+  char* s_tile = s_dyn + (size_t)H * NCP * 2;
   {
     f32x4_t acc[kStepTilesPerWG];
 #pragma unroll
@@ -806,7 +802,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
             const int k = wave * kw + s * 32 + g4 * 8;
             const u32x4 wv = *reinterpret_cast<const u32x4*>(s_tile + n * pitch + k * 2);
             const int c = k >> 3;
-            const u32x4 bv = n < NC ? *reinterpret_cast<const u32x4*>(s_xb + ((size_t)c * NC + n) * 8) : u32x4{0, 0, 0, 0};
+            const u32x4 bv = n < NC ? *reinterpret_cast<const u32x4*>(s_xb + (size_t)bcol_slot(c, n, NCP) * 8) : u32x4{0, 0, 0, 0};
             acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wv),
                                                              __builtin_bit_cast(bf16x8_t, bv), acc[i], 0, 0, 0);
           }
@@ -1063,7 +1059,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
 
   // ---- phase C1: partial output projection of unit (urb, uks) ------------
   if (is_unit) {
-    uint16_t* s_nb = reinterpret_cast<uint16_t*>(s_dyn);  // [kcu/8][NC][8] bf16
+    uint16_t* s_nb = reinterpret_cast<uint16_t*>(s_dyn);  // [kcu/8][NCP][8] bf16 (bcol_slot)
     const int h0 = uks * (kcu / kStepD), nh = kcu / kStepD;  // heads of the unit's columns
     bool ok = true;
     if (wave == 0) {
@@ -1073,30 +1069,28 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       if (!poll_tagged<1>(hw, hs, tag)) s_fail = 1;
     }
     __syncthreads();
-    // The T * kcu inputs in one batch of tagged loads.
-    constexpr int CB = NT <= 2 ? 2 : 8;
-    static_assert(CB * 512 >= NT * 512, "unit inputs exceed one poll batch");
-    const int lk = 31 - __builtin_clz((unsigned)kcu), n_in = T * kcu;
+    // The T * kcu inputs: one chunk of 8 consecutive columns per thread.
+    const int lcu = 31 - __builtin_clz((unsigned)kcu) - 3, cpu = 1 << lcu;  // chunks per token
+    static_assert(kStepMaxTokens * 512 / 8 <= 512, "unit inputs exceed one chunk per thread");
     {
-      uint64_t w[CB];
-      const uint64_t* srcs[CB];
+      const int t = tid >> lcu, c = tid & (cpu - 1);
+      const bool live = t < T;
+      uint64_t w[8];
+      const uint64_t* srcs[8];
 #pragma unroll
-      for (int j = 0; j < CB; ++j) {
-        const int idx = tid + j * 512;
-        srcs[j] = idx < n_in ? a.tw.norm + (size_t)(idx >> lk) * V + (size_t)uks * kcu + (idx & (kcu - 1)) : nullptr;
-        w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+      for (int e = 0; e < 8; ++e) {
+        srcs[e] = live ? a.tw.norm + (size_t)t * V + (size_t)uks * kcu + c * 8 + e : nullptr;
+        w[e] = srcs[e] ? load_tagged(srcs[e]) : 0ull;
       }
-      ok = poll_tagged<CB>(w, srcs, tag);
+      ok = poll_tagged<8>(w, srcs, tag);
+      if (live) {
+        float y[8];
 #pragma unroll
-      for (int j = 0; j < CB; ++j) {
-        const int idx = tid + j * 512;
-        if (idx < n_in) {
-          const int t = idx >> lk, k = idx & (kcu - 1);
-          const uint32_t hl = bf16_pair_hi_lo(value_of(w[j]));
-          const int c = k >> 3, e = k & 7;
-          s_nb[((size_t)c * NC + 2 * t) * 8 + e] = (uint16_t)(hl & 0xffffu);
-          s_nb[((size_t)c * NC + 2 * t + 1) * 8 + e] = (uint16_t)(hl >> 16);
-        }
+        for (int e = 0; e < 8; ++e) y[e] = value_of(w[e]);
+        u32x4 vh, vl;
+        split_hi_lo8(y, vh, vl);
+        *reinterpret_cast<u32x4*>(s_nb + (size_t)bcol_slot(c, 2 * t, NCP) * 8) = vh;
+        *reinterpret_cast<u32x4*>(s_nb + (size_t)bcol_slot(c, 2 * t + 1, NCP) * 8) = vl;
       }
     }
     if (!ok) s_fail = 1;
@@ -1106,7 +1100,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     for (int s = 0; s < 16; ++s) {
       if (s < ksc) {
         const int c = s * 4 + g4;
-        const u32x4 bv = n < NC ? *reinterpret_cast<const u32x4*>(s_nb + ((size_t)c * NC + n) * 8) : u32x4{0, 0, 0, 0};
+        const u32x4 bv = n < NC ? *reinterpret_cast<const u32x4*>(s_nb + (size_t)bcol_slot(c, n, NCP) * 8) : u32x4{0, 0, 0, 0};
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, ov[s]),
                                                       __builtin_bit_cast(bf16x8_t, bv), acc, 0, 0, 0);
       }
@@ -1292,12 +1286,12 @@ static bool step_fused_eligible(int T, int H, int Hk, int Hv, int D, const int* 
 }
 
 static size_t step_fused_lds(int T, int H, int V) {
-  const size_t nc = 2 * (size_t)T;
+  const size_t nc = 2 * (size_t)T, ncp = nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 8 ? 8 : 16;
   const size_t tile = (size_t)16 * (2 * (size_t)H + 16),
                red = ((size_t)kStepWaves * kStepTilesPerWG * 16 * nc + kStepTilesPerWG * 16 * 16) * 4;
-  const size_t pa = (size_t)H * nc * 2 + (tile > red ? tile : red);
+  const size_t pa = (size_t)H * ncp * 2 + (tile > red ? tile : red);
   const size_t pb = ((size_t)T * 4 * kStepD + 2 * kStepMaxTokens + (size_t)T * kStepD) * 4;
-  const size_t pc = (size_t)(V < 512 ? V : 512) * nc * 2;
+  const size_t pc = (size_t)(V < 512 ? V : 512) * ncp * 2;
   return pa > pb ? (pa > pc ? pa : pc) : (pb > pc ? pb : pc);
 }
 
