@@ -545,6 +545,10 @@ constexpr size_t kStepMixWords = (size_t)kStepMaxTokens * 8192;
 constexpr size_t kStepVWords = (size_t)kStepMaxTokens * 4096;
 constexpr size_t kStepHeadWords = (size_t)kStepMaxTokens * 64;
 constexpr size_t kStepPartWords = (size_t)8 * kStepMaxTokens * 2048;  // [V/512 <= 8][T][H <= 2048]
+constexpr int kStepHeadWGs = 4;  // workgroups per value head (value columns split four ways)
+constexpr int kStepQCols = kStepD / kStepHeadWGs;  // value columns per head workgroup
+constexpr int kStepInPitch = 2 * kStepD + 2 * kStepQCols + 4;  // head workgroup inputs per token (q, k, v, z, a, b, pad)
+constexpr int kStepValuAhead = 2;  // VALU projections: weight tiles in flight per wavefront
 constexpr int kStepTicketEpoch = 0;
 constexpr int kStepTicketError = kWorkspaceErrorWord;
 
@@ -563,7 +567,8 @@ struct StepTagWs {
   // floods the memory system while the producers still stream).  The
   // outputs still carry their own tags and are re-read until they do.
   uint64_t* hint_tile;  // [kStepTilesPerWG * kStepMaxGrid]
-  uint64_t* hint_head;  // [64]
+  uint64_t* hint_head;  // [64 * kStepHeadWGs] per head workgroup
+  uint64_t* hss;        // [64 * kStepHeadWGs][kStepMaxTokens] head quarters' sums of squares
   uint64_t* part;       // [V / 512][T][H] phase C partial sums
 };
 
@@ -596,20 +601,24 @@ struct StepArgs {
 // the chunk's slots.
 __device__ __forceinline__ int bcol_slot(int c, int n, int ncp) { return c * ncp + (n ^ (c & (ncp - 1))); }
 
-// Lane quad sum (lanes 4q..4q+3 hold the four row quarters of a column).
-__device__ __forceinline__ float quad_sum(float v) {
+// Sum over the 16 lanes of a DPP row (every lane of the row gets it).
+__device__ __forceinline__ float row16_sum(float v) {
   v += __uint_as_float(dpp_u32<kDppQuadXor1>(__float_as_uint(v)));
   v += __uint_as_float(dpp_u32<kDppQuadXor2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppRowHalfMirror>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppRowMirror>(__float_as_uint(v)));
   return v;
 }
 
 // NT: compile-time bound on the tokens (2 or 8), which sizes the token
-// registers.  BFX: hidden states in bf16 (else fp32).  Every other operand
+// registers; NT = 2 also takes the VALU projections (H = 2048 only).  BFX: hidden states in bf16 (else fp32).  Every other operand
 // has the dtype of the model's own decode: bf16 weights, norm weights, conv
 // state and decay parameters, fp32 recurrent state (the host sends other
 // combinations to the staged kernels).
 template <bool BFX, int NT>
 __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
+  // T <= 2 (and H = 2048, which the host checks): phase A on the VALU.
+  constexpr bool VALU_A = NT <= 2;
   extern __shared__ float4 s_dyn_v[];
   char* s_dyn = reinterpret_cast<char*>(s_dyn_v);
   __shared__ float s_rs[kStepMaxTokens];
@@ -617,20 +626,24 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   __shared__ float s_sc[kStepMaxTokens][4];  // decay, beta (head workgroups)
   __shared__ uint32_t s_wtag[kStepWaves];
   __shared__ int s_fail;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ int s_tcnt[kStepTilesPerWG];  // wavefronts done with each phase A tile (VALU path)
+  // (the wavefront index is uniform: kept in a scalar register, so that
+  // addresses derived from it stay scalar too)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, b = blockIdx.x;
-  const int T = a.T, H = a.H, C = a.C, V = a.V, R = a.R, Hv = a.Hv;
+  const int T = a.T, H = VALU_A ? 2048 : a.H, C = a.C, V = a.V, R = a.R, Hv = a.Hv;
   const int NC = 2 * T;  // MFMA columns in use: (hi, lo) per token
   const int NCP = NC <= 2 ? 2 : NC <= 4 ? 4 : NC <= 8 ? 8 : 16;  // staging columns (power of two)
   const uint32_t tag = load_coherent(&a.tw.tickets[kStepTicketEpoch]) + 1u;
   const int n = lane & 15, g4 = lane >> 4;  // MFMA lane -> (column / A row, k group)
 
-  // Roles.  Heads sit on the last Hv workgroups, output tiles on the first
-  // H/16, the epoch keeper just below the heads.
-  const int head = b - (G - Hv);
-  const bool is_head = head >= 0;
+  // Roles.  Each value head runs on kStepHeadWGs workgroups at the end of
+  // the grid (a quarter of the head's value columns each); the phase C
+  // units and the output rows sit on the first workgroups.
+  const int qb = b - (G - kStepHeadWGs * Hv);
+  const bool is_head = qb >= 0;
+  const int head = is_head ? qb / kStepHeadWGs : 0, quarter = is_head ? qb % kStepHeadWGs : 0;
   const bool is_out = b < H / 16;
-  const int keeper = max(0, G - Hv - 1);
 
   // The token chunks and the norm weight are loaded and staged before any
   // weight load is issued: behind the 50 MB weight stream of every
@@ -651,8 +664,9 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     }
   }
 
-  // ---- stage the normalised tokens as bf16 hi/lo MFMA columns ------------
-  // s_xb: [H/8 chunks][NCP][8] bf16 (bcol_slot).  Chunk q of thread tid is token-major
+  // ---- stage the normalised tokens -----------------------------------------
+  // MFMA path: bf16 hi/lo columns in s_xb [H/8 chunks][NCP][8] (bcol_slot);
+  // VALU path: fp32 in s_x [T][H].  Chunk q of thread tid is token-major
   // chunk tid + 512 q; H % 512 == 0, so a wavefront's 64 chunks belong to one
   // token and the sum of squares reduces in a fixed order.
   uint16_t* s_xb = reinterpret_cast<uint16_t*>(s_dyn);
@@ -671,6 +685,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       }
     }
     if (tid == 0) s_fail = 0;
+    if (tid < kStepTilesPerWG) s_tcnt[tid] = 0;
     if (lane == 0) s_wtag[wave] = tag;
     __syncthreads();
     if (tid < T) {
@@ -690,14 +705,34 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         raw8_to_f32<true>(nr[q], nv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) y[e] = xv[e] * s_rs[t] * (1.0f + nv[e]);
-        u32x4 vh, vl;
-        split_hi_lo8(y, vh, vl);
-        const int c = k0 >> 3;
-        *reinterpret_cast<u32x4*>(s_xb + (size_t)bcol_slot(c, 2 * t, NCP) * 8) = vh;
-        *reinterpret_cast<u32x4*>(s_xb + (size_t)bcol_slot(c, 2 * t + 1, NCP) * 8) = vl;
+        if constexpr (VALU_A) {
+          float4* dst = reinterpret_cast<float4*>(reinterpret_cast<float*>(s_dyn) + (size_t)t * H + k0);
+          dst[0] = make_float4(y[0], y[1], y[2], y[3]);
+          dst[1] = make_float4(y[4], y[5], y[6], y[7]);
+        } else {
+          u32x4 vh, vl;
+          split_hi_lo8(y, vh, vl);
+          const int c = k0 >> 3;
+          *reinterpret_cast<u32x4*>(s_xb + (size_t)bcol_slot(c, 2 * t, NCP) * 8) = vh;
+          *reinterpret_cast<u32x4*>(s_xb + (size_t)bcol_slot(c, 2 * t + 1, NCP) * 8) = vl;
+        }
       }
     }
     __syncthreads();
+  }
+
+  // Conv taps (state and weights) of this workgroup's qkv rows, needed by
+  // the first tile's epilogue on the VALU path, so issued before the tiles.
+  uint32_t cwin_raw[8], cwk_raw[8];
+  {
+    // MFMA path: thread (tile, row, token) of the epilogue below; VALU path:
+    // lane 2i + rr < 8 of wavefront w, row 2w + rr of tile i.
+    const int row = VALU_A ? (b + ((lane >> 1) & 3) * G) * 16 + 2 * wave + (lane & 1)
+                           : (b + (tid >> 7) * G) * 16 + ((tid >> 3) & 15);
+    const bool conv_row = row < C;
+    const int nk = conv_row ? a.KS : 0;
+    gather_raw<true>(a.conv_state, (size_t)(conv_row ? row : 0) * a.KS, 1, nk, cwin_raw);
+    gather_raw<true>(a.conv_w, (size_t)(conv_row ? row : 0) * a.KS, 1, nk, cwk_raw);
   }
 
   // ---- phase A weight tiles ----------------------------------------------
@@ -716,65 +751,152 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   const int LPR = 1 << lpr_sh;
   int ntl = 0;
   u32x4 av[kStepTilesPerWG][8];
-  {
 #pragma unroll
-    for (int i = 0; i < kStepTilesPerWG; ++i) {
-      const int tile = b + i * G;
-      if (tile < ntiles) ntl = i + 1;
+  for (int i = 0; i < kStepTilesPerWG; ++i)
+    if (b + i * G < ntiles) ntl = i + 1;
+  // The matrix boundaries C, C + V, C + V + Hv and R are multiples of 16
+  // (the host checks), so a tile lies in one matrix and the base address of
+  // each load is uniform; the lane adds a fixed byte offset.  Every slot
+  // issues its load: one outside the weights (past the last tile or past
+  // the row) reads the first KiB of the qkv weight, the same line in every
+  // workgroup, and its data is never used.  A load under a condition would
+  // make the compiler's waits below count it as not issued and wait for
+  // later loads too.
+  const uint32_t lane_off = (uint32_t)((wave << (lh + 2)) + (lane << 4));  // rows 2w.. (2H bytes each) + lane
+  const char* spare = reinterpret_cast<const char*>(a.w[0]);
+  auto issue_tile = [&](int i) {
+    const int tile = b + i * G;
+    const int row0 = tile * 16;
+    const int wh = row0 < C ? 0 : row0 < C + V ? 1 : row0 < C + V + Hv ? 2 : 3;
+    const int r0 = row0 - (wh == 0 ? 0 : wh == 1 ? C : wh == 2 ? C + V : C + V + Hv);
+    const char* tp = reinterpret_cast<const char*>(wh == 0 ? a.w[0] : wh == 1 ? a.w[1] : wh == 2 ? a.w[2] : a.w[3]) +
+                     ((size_t)(tile < ntiles ? r0 : 0) << (lh + 1));
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const bool live = s < ks && tile < ntiles;
+      const size_t so = ((size_t)(s >> lpr_sh) << (lh + 1)) + ((size_t)(s & (LPR - 1)) << 10);
+      av[i][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(live ? tp + so + lane_off : spare + (lane << 4)));
     }
-    // The matrix boundaries C, C + V, C + V + Hv and R are multiples of 16
-    // (the host checks), so a tile lies in one matrix and the base address
-    // of each load is uniform; the lane adds a fixed byte offset.  Every
-    // slot issues its load: one outside the weights (past the last tile or
-    // past the row) reads the first KiB of the qkv weight, the same line in
-    // every workgroup, and its data is never used.  A load under a condition
-    // would make the compiler's waits below count it as not issued and wait
-    // for later loads too.
-    const uint32_t lane_off = (uint32_t)((wave << (lh + 2)) + (lane << 4));  // rows 2w.. (2H bytes each) + lane
-    const char* spare = reinterpret_cast<const char*>(a.w[0]);
+  };
+  // MFMA path: every tile up front.  VALU path: kStepValuAhead tiles ahead
+  // of the one being reduced, so that tiles complete one after another and
+  // the dot products run under the stream (issued all at once, a
+  // wavefront's first tile completes about as late as its last).
 #pragma unroll
-    for (int i = 0; i < kStepTilesPerWG; ++i) {
-      const int tile = b + i * G;
-      const int row0 = tile * 16;
-      const int wh = row0 < C ? 0 : row0 < C + V ? 1 : row0 < C + V + Hv ? 2 : 3;
-      const int r0 = row0 - (wh == 0 ? 0 : wh == 1 ? C : wh == 2 ? C + V : C + V + Hv);
-      const char* tp = reinterpret_cast<const char*>(wh == 0 ? a.w[0] : wh == 1 ? a.w[1] : wh == 2 ? a.w[2] : a.w[3]) +
-                       ((size_t)(tile < ntiles ? r0 : 0) << (lh + 1));
-#pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const bool live = s < ks && tile < ntiles;
-        const size_t so = ((size_t)(s >> lpr_sh) << (lh + 1)) + ((size_t)(s & (LPR - 1)) << 10);
-        av[i][s] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4*>(live ? tp + so + lane_off : spare + (lane << 4)));
-      }
-    }
-  }
+  for (int i = 0; i < kStepTilesPerWG; ++i)
+    if (!VALU_A || i < kStepValuAhead) issue_tile(i);
 
   // Small operands of later phases, fetched now so that no phase waits on a
-  // dependent global load: the head's norm weight and decay parameters and
-  // the conv taps of this workgroup's qkv rows (thread i*16 + r: row r of
-  // tile i).
-  uint32_t lnw2[2], alog[1], dtb1[1];
-  gather_raw<true>(a.lnw, lane, 64, 2, lnw2);
+  // dependent global load: the head's norm weight and decay parameters.
+  uint32_t lnw1[1], alog[1], dtb1[1];
+  gather_raw<true>(a.lnw, quarter * kStepQCols + (lane & (kStepQCols - 1)), 0, 1, lnw1);
   gather_raw<true>(a.a_log, is_head ? head : 0, 0, 1, alog);
   gather_raw<true>(a.dt_bias, is_head ? head : 0, 0, 1, dtb1);
-  uint32_t cwin_raw[8], cwk_raw[8];
-  {
-    const int row = (b + (tid >> 7) * G) * 16 + ((tid >> 3) & 15);  // thread (tile, row, token) below
-    const bool conv_row = row < C;
-    const int nk = conv_row ? a.KS : 0;
-    gather_raw<true>(a.conv_state, (size_t)(conv_row ? row : 0) * a.KS, 1, nk, cwin_raw);
-    gather_raw<true>(a.conv_w, (size_t)(conv_row ? row : 0) * a.KS, 1, nk, cwk_raw);
-  }
 
-  // Head workgroups: prefetch the state (thread (j, gq): rows 32gq.., column
-  // j).  Issued after the weight tiles: the waits below are counted over
-  // every path, so head-only loads in front of them would make the other
-  // workgroups wait for more of their weight tiles.
-  const int sj = tid >> 2, sg = tid & 3;
-  uint32_t S_raw[32];
-  if (is_head) gather_raw<false>(a.rec_state, ((size_t)head * kStepD + (size_t)sg * 32) * kStepD + sj, kStepD, 32, S_raw);
+  // Head workgroups: prefetch the state.  Thread (jl, g) holds rows
+  // 8g .. 8g + 7 of value column jcol = quarter * 32 + jl.  Issued after the
+  // weight tiles: the waits below are counted over every path, so head-only
+  // loads in front of them would make the other workgroups wait for more of
+  // their weight tiles.
+  const int sjl = tid >> 4, sgr = tid & 15, jcol = quarter * kStepQCols + sjl;
+  uint32_t S_raw[8];
+  if (is_head) gather_raw<false>(a.rec_state, ((size_t)head * kStepD + (size_t)sgr * 8) * kStepD + jcol, kStepD, 8, S_raw);
 
+  if constexpr (VALU_A) {
+    // ---- phase A (T <= 2): whole-row dot products on the VALU --------------
+    // Each wavefront finishes its two rows of a tile as soon as the tile's
+    // loads are in: no LDS round trip and no workgroup barrier, so the work
+    // hides under the weight stream.  Lane l holds elements 512 p + 8 l .. + 7
+    // of a row (p < 4); the tokens' matching elements come from s_x.
+    const float* s_x = reinterpret_cast<const float*>(s_dyn);
+    float xk[NT][4][8];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const float4* src = reinterpret_cast<const float4*>(s_x + (size_t)(t < T ? t : 0) * H + p * 512 + lane * 8);
+        const float4 u0 = src[0], u1 = src[1];
+        xk[t][p][0] = u0.x; xk[t][p][1] = u0.y; xk[t][p][2] = u0.z; xk[t][p][3] = u0.w;
+        xk[t][p][4] = u1.x; xk[t][p][5] = u1.y; xk[t][p][6] = u1.z; xk[t][p][7] = u1.w;
+      }
+#pragma unroll
+    for (int i = 0; i < kStepTilesPerWG; ++i) {
+      if (i < ntl) {  // uniform per workgroup
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          const int row = (b + i * G) * 16 + 2 * wave + rr;
+          float v[NT];
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            v[t] = 0.f;
+            if (t < T) {
+              float d = 0.f;
+#pragma unroll
+              for (int p = 0; p < 4; ++p) {
+                float w8[8];
+                raw8_to_f32<true>(Raw8<true>{av[i][rr * 4 + p]}, w8);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) d = fmaf(w8[e], xk[t][p][e], d);
+              }
+              v[t] = wave_sum(d);
+            }
+          }
+          // the lane holding the row's conv taps finishes the row
+          if (lane == 2 * i + rr) {
+            if (row < C) {
+              // causal conv + SiLU: token t's window is entries t + 1 .. t + KS
+              // of [conv state (KS) | tokens]
+              float st[8], wk[8];
+#pragma unroll
+              for (int j = 0; j < 8; ++j) {
+                st[j] = raw_value<true>(cwin_raw[j]);
+                wk[j] = raw_value<true>(cwk_raw[j]);
+              }
+              auto seq = [&](int q) {
+                float r = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) r = q == j && j < a.KS ? st[j] : r;
+#pragma unroll
+                for (int t = 0; t < NT; ++t) r = q == a.KS + t ? v[t] : r;
+                return r;
+              };
+#pragma unroll
+              for (int t = 0; t < NT; ++t) {
+                if (t < T) {
+                  float cv = 0.f;
+#pragma unroll
+                  for (int j = 0; j < 8; ++j)
+                    if (j < a.KS) cv = fmaf(wk[j], seq(t + 1 + j), cv);
+                  store_tagged(a.tw.mix + (size_t)t * C + row, silu(cv), tag);
+                }
+              }
+#pragma unroll
+              for (int j = 0; j < 8; ++j)
+                if (j < a.KS) reinterpret_cast<uint16_t*>(a.next_conv)[(size_t)row * a.KS + j] = f32_to_bf16_bits(seq(T + j));
+            } else {
+              // (one store site per destination: a destination chosen per
+              // lane would be read from the kernel arguments by a vector load)
+#pragma unroll
+              for (int t = 0; t < NT; ++t) {
+                if (t < T) {
+                  if (row < C + V) store_tagged(a.tw.z + (size_t)t * V + (row - C), v[t], tag);
+                  else if (row < C + V + Hv) store_tagged(a.tw.a + (size_t)t * Hv + (row - C - V), v[t], tag);
+                  else store_tagged(a.tw.b + (size_t)t * Hv + (row - C - V - Hv), v[t], tag);
+                }
+              }
+            }
+          }
+        }
+        // the last wavefront done with tile i stores its hint (every
+        // wavefront's stores of the tile are issued before its count)
+        if (lane == 0 && __hip_atomic_fetch_add(&s_tcnt[i], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+                             kStepWaves - 1)
+          store_tagged(a.tw.hint_tile + b + i * G, 0.f, tag);
+      }
+      if (i + kStepValuAhead < kStepTilesPerWG) issue_tile(i + kStepValuAhead);
+    }
+    __syncthreads();  // phases B and C reuse the dynamic LDS
+  } else {
   // ---- phase A: projections ---------------------------------------------
   // LDS: s_xb | the workgroup's tile [16 rows][2H + 16 B] (row pitch padded
   // by 16 B: the 16 rows of an operand read fall in distinct banks).  Per
@@ -853,22 +975,18 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
           for (int j = 0; j < 8; ++j)
             if (j < a.KS) reinterpret_cast<uint16_t*>(a.next_conv)[(size_t)erow * a.KS + j] = f32_to_bf16_bits(sq[T + j]);
         }
+      } else if (erow < C + V) {  // one store site per destination (see the VALU path)
+        store_tagged(a.tw.z + (size_t)et * V + (erow - C), ev, tag);
+      } else if (erow < C + V + Hv) {
+        store_tagged(a.tw.a + (size_t)et * Hv + (erow - C - V), ev, tag);
       } else {
-        uint64_t* dst;
-        int stride, off;
-        if (erow < C + V) {
-          dst = a.tw.z, stride = V, off = erow - C;
-        } else if (erow < C + V + Hv) {
-          dst = a.tw.a, stride = Hv, off = erow - C - V;
-        } else {
-          dst = a.tw.b, stride = Hv, off = erow - C - V - Hv;
-        }
-        store_tagged(dst + (size_t)et * stride + off, ev, tag);
+        store_tagged(a.tw.b + (size_t)et * Hv + (erow - C - V - Hv), ev, tag);
       }
     }
     __syncthreads();  // phases B and C reuse the dynamic LDS
     // every thread's stores of the tiles are issued before these hints
     if (tid < ntl) store_tagged(a.tw.hint_tile + b + tid * G, 0.f, tag);
+  }
   }
 
   // ---- W_out for phase C, fetched while the heads run --------------------
@@ -881,6 +999,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   const int kcu = V < 512 ? V : 512, nks = V / kcu, nunits = (H >> 7) * nks;
   const int ksc = kcu >> 5;  // MFMA steps per unit (<= 16)
   const bool is_unit = b < nunits;
+  const int keeper = nunits - 1;  // the epoch keeper: the last unit (units wait longest for their inputs)
   const int urb = is_unit ? b / nks : 0, uks = is_unit ? b - urb * nks : 0;
   u32x4 ov[16];
   if (is_unit) {
@@ -913,31 +1032,30 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     if (tid == 0) store_coherent(&a.tw.tickets[kStepTicketEpoch], tag);
   }
 
-  // ---- phase B: gated delta rule of one value head -----------------------
+  // ---- phase B: gated delta rule, a quarter of one value head ------------
   if (is_head) {
-    // s_in: [T][4][128] (q, k, v, z), then [T][2] (a, b)
+    // s_in: [T][kStepInPitch]: q[128], k[128], v[32], z[32] (this quarter's
+    // value columns), a, b; then s_o [T][32].
     float* s_in = reinterpret_cast<float*>(s_dyn);
-    float* s_ab = s_in + (size_t)T * 4 * kStepD;
-    float* s_o = s_ab + 2 * kStepMaxTokens;  // [T][128]
+    float* s_o = s_in + (size_t)T * kStepInPitch;
     const int hq = head / (Hv / a.Hk);
-    const int per_tok = 4 * kStepD + 2;
+    constexpr int per_tok = 2 * kStepD + 2 * kStepQCols + 2;
     const int n_in = T * per_tok;
     bool ok = true;
-    // Hints of the 34 tiles holding this head's q, k, v, z, a and b rows
+    // Hints of the 22 tiles holding this quarter's q, k, v, z, a and b rows
     // (one load per lane), then one read of the inputs.
     if (wave == 0) {
-      constexpr int TPB = kStepD / 16;  // tiles per 128-row block
+      constexpr int TPB = kStepD / 16, TPQ = kStepQCols / 16;  // tiles per 128 rows, per quarter's 32 rows
       int tl = -1;
-      if (lane < 4 * TPB) {
-        const int part = lane / TPB;
-        const int row0 = part == 0 ? hq * kStepD
-                       : part == 1 ? (a.Hk + hq) * kStepD
-                       : part == 2 ? (2 * a.Hk + head) * kStepD
-                                   : C + head * kStepD;
-        tl = row0 / 16 + lane % TPB;
-      } else if (lane == 4 * TPB) {
+      if (lane < 2 * TPB) {
+        tl = ((lane < TPB ? hq : a.Hk + hq) * kStepD) / 16 + lane % TPB;
+      } else if (lane < 2 * TPB + 2 * TPQ) {
+        const int l = lane - 2 * TPB;
+        const int row0 = (l < TPQ ? 2 * a.Hk * kStepD : C) + head * kStepD + quarter * kStepQCols;
+        tl = row0 / 16 + l % TPQ;
+      } else if (lane == 2 * TPB + 2 * TPQ) {
         tl = (C + V + head) / 16;
-      } else if (lane == 4 * TPB + 1) {
+      } else if (lane == 2 * TPB + 2 * TPQ + 1) {
         tl = (C + V + Hv + head) / 16;
       }
       uint64_t hw[1];
@@ -947,35 +1065,33 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     }
     __syncthreads();
     // one batch of tagged loads in flight covers every input (T <= NT)
-    constexpr int BB = NT <= 2 ? 4 : 12;
-    static_assert(BB * 512 >= NT * (4 * kStepD + 2), "head inputs exceed one poll batch");
-    for (int base = tid; base < n_in; base += 512 * BB) {
+    constexpr int BB = NT <= 2 ? 2 : 6;
+    static_assert(BB * 512 >= NT * per_tok, "head inputs exceed one poll batch");
+    {
       uint64_t w[BB];
       const uint64_t* srcs[BB];
       int dsti[BB];
 #pragma unroll
       for (int j = 0; j < BB; ++j) {
-        const int idx = base + j * 512;
+        const int idx = tid + j * 512;
         srcs[j] = nullptr;
         dsti[j] = -1;
         if (idx < n_in) {
           const int t = idx / per_tok, r = idx - t * per_tok;
-          if (r < 4 * kStepD) {
-            const int part = r >> 7, e = r & 127;
-            const size_t col = part == 0 ? (size_t)hq * kStepD + e
-                             : part == 1 ? (size_t)a.Hk * kStepD + (size_t)hq * kStepD + e
-                             : part == 2 ? (size_t)2 * a.Hk * kStepD + (size_t)head * kStepD + e
-                                         : (size_t)head * kStepD + e;
-            srcs[j] = part < 3 ? a.tw.mix + (size_t)t * C + col : a.tw.z + (size_t)t * V + col;
-            dsti[j] = (t * 4 + part) * kStepD + e;
-          } else {
-            srcs[j] = (r == 4 * kStepD ? a.tw.a : a.tw.b) + (size_t)t * Hv + head;
-            dsti[j] = T * 4 * kStepD + 2 * t + (r - 4 * kStepD);
-          }
+          const uint64_t* src;
+          if (r < kStepD) src = a.tw.mix + (size_t)t * C + (size_t)hq * kStepD + r;
+          else if (r < 2 * kStepD) src = a.tw.mix + (size_t)t * C + (size_t)(a.Hk + hq) * kStepD + (r - kStepD);
+          else if (r < 2 * kStepD + kStepQCols)
+            src = a.tw.mix + (size_t)t * C + (size_t)(2 * a.Hk + head) * kStepD + quarter * kStepQCols + (r - 2 * kStepD);
+          else if (r < 2 * kStepD + 2 * kStepQCols)
+            src = a.tw.z + (size_t)t * V + (size_t)head * kStepD + quarter * kStepQCols + (r - 2 * kStepD - kStepQCols);
+          else src = (r == per_tok - 2 ? a.tw.a : a.tw.b) + (size_t)t * Hv + head;
+          srcs[j] = src;
+          dsti[j] = t * kStepInPitch + r;
         }
         w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
       }
-      ok = poll_tagged<BB>(w, srcs, tag) && ok;
+      ok = poll_tagged<BB>(w, srcs, tag);
 #pragma unroll
       for (int j = 0; j < BB; ++j)
         if (dsti[j] >= 0) s_in[dsti[j]] = value_of(w[j]);
@@ -985,8 +1101,8 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     // Per token (wave t): l2-normalise q (times D^-1/2) and k in place; decay and beta.
     if (wave < T) {
       const int t = wave;
-      float* q = s_in + (size_t)(t * 4 + 0) * kStepD;
-      float* k = s_in + (size_t)(t * 4 + 1) * kStepD;
+      float* q = s_in + (size_t)t * kStepInPitch;
+      float* k = q + kStepD;
       const float q0 = q[lane], q1 = q[lane + 64], k0 = k[lane], k1 = k[lane + 64];
       const float sq = wave_sum(q0 * q0 + q1 * q1), sk = wave_sum(k0 * k0 + k1 * k1);
       const float qs = rsqrtf(sq + a.eps) * rsqrtf((float)kStepD), kss = rsqrtf(sk + a.eps);
@@ -995,24 +1111,28 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       k[lane] = k0 * kss;
       k[lane + 64] = k1 * kss;
       if (lane == 0) {
+        const float* ab = s_in + (size_t)t * kStepInPitch + per_tok - 2;
         const float neg_a = -expf(raw_value<true>(alog[0]));
-        const float gin = s_ab[2 * t] + raw_value<true>(dtb1[0]);
+        const float gin = ab[0] + raw_value<true>(dtb1[0]);
         s_sc[t][0] = expf(neg_a * (fmaxf(gin, 0.f) + log1pf(expf(-fabsf(gin)))));
-        s_sc[t][1] = 1.f / (1.f + expf(-s_ab[2 * t + 1]));
+        s_sc[t][1] = 1.f / (1.f + expf(-ab[1]));
       }
     }
     __syncthreads();
-    float S[32];
+    // Recurrence: lanes 16 jl' .. 16 jl' + 15 of a wavefront share a value
+    // column; each holds 8 rows and the column sums reduce over the 16 lanes.
+    float S[8];
 #pragma unroll
-    for (int m = 0; m < 32; ++m) S[m] = raw_value<false>(S_raw[m]);
+    for (int m = 0; m < 8; ++m) S[m] = raw_value<false>(S_raw[m]);
     for (int t = 0; t < T; ++t) {
       const float decay = s_sc[t][0], beta = s_sc[t][1];
-      float kn[32], qn[32];
+      const float* tin = s_in + (size_t)t * kStepInPitch;
+      float kn[8], qn[8];
       {
-        const float4* k4 = reinterpret_cast<const float4*>(s_in + (size_t)(t * 4 + 1) * kStepD + sg * 32);
-        const float4* q4 = reinterpret_cast<const float4*>(s_in + (size_t)(t * 4 + 0) * kStepD + sg * 32);
+        const float4* k4 = reinterpret_cast<const float4*>(tin + kStepD + sgr * 8);
+        const float4* q4 = reinterpret_cast<const float4*>(tin + sgr * 8);
 #pragma unroll
-        for (int m = 0; m < 8; ++m) {
+        for (int m = 0; m < 2; ++m) {
           const float4 kk = k4[m], qq = q4[m];
           kn[4 * m] = kk.x; kn[4 * m + 1] = kk.y; kn[4 * m + 2] = kk.z; kn[4 * m + 3] = kk.w;
           qn[4 * m] = qq.x; qn[4 * m + 1] = qq.y; qn[4 * m + 2] = qq.z; qn[4 * m + 3] = qq.w;
@@ -1020,39 +1140,56 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       }
       float part = 0.f;
 #pragma unroll
-      for (int m = 0; m < 32; ++m) {
+      for (int m = 0; m < 8; ++m) {
         S[m] *= decay;
         part = fmaf(S[m], kn[m], part);
       }
-      const float ksum = quad_sum(part);
-      const float delta = (s_in[(size_t)(t * 4 + 2) * kStepD + sj] - ksum) * beta;
+      const float ksum = row16_sum(part);
+      const float delta = (tin[2 * kStepD + sjl] - ksum) * beta;
       float op = 0.f;
 #pragma unroll
-      for (int m = 0; m < 32; ++m) {
+      for (int m = 0; m < 8; ++m) {
         S[m] = fmaf(kn[m], delta, S[m]);
         op = fmaf(S[m], qn[m], op);
       }
-      const float o = quad_sum(op);
-      if (sg == 0) s_o[t * kStepD + sj] = o;
+      const float o = row16_sum(op);
+      if (sgr == 0) s_o[t * kStepQCols + sjl] = o;
     }
     __syncthreads();
-    // Gated RMSNorm of each token's head output (wave t), published first;
-    // the state write-back is off the critical path.
+    // Gated RMSNorm: the quarters of a head exchange their sums of squares
+    // (tagged) and each normalises its own columns with the four sums added
+    // in quarter order, so all four use the same scale.
     if (wave < T) {
       const int t = wave;
-      const float o0 = s_o[t * kStepD + lane], o1 = s_o[t * kStepD + lane + 64];
-      const float rs = rsqrtf(wave_sum(o0 * o0 + o1 * o1) / (float)kStepD + a.eps);
-      const float* z = s_in + (size_t)(t * 4 + 3) * kStepD;
-      uint64_t* dst = a.tw.norm + (size_t)t * V + (size_t)head * kStepD;
-      store_tagged(dst + lane, o0 * rs * raw_value<true>(lnw2[0]) * silu(z[lane]), tag);
-      store_tagged(dst + lane + 64, o1 * rs * raw_value<true>(lnw2[1]) * silu(z[lane + 64]), tag);
+      const float o = lane < kStepQCols ? s_o[t * kStepQCols + lane] : 0.f;
+      const float ss = wave_sum(o * o);
+      if (lane == 0) {
+        store_tagged(a.tw.hss + ((size_t)head * kStepHeadWGs + quarter) * kStepMaxTokens + t, ss, tag);
+        uint64_t w[kStepHeadWGs];
+        const uint64_t* srcs[kStepHeadWGs];
+#pragma unroll
+        for (int q = 0; q < kStepHeadWGs; ++q) {
+          srcs[q] = a.tw.hss + ((size_t)head * kStepHeadWGs + q) * kStepMaxTokens + t;
+          w[q] = load_tagged(srcs[q]);
+        }
+        if (!poll_tagged<kStepHeadWGs>(w, srcs, tag)) s_fail = 1;
+        float tot = 0.f;
+#pragma unroll
+        for (int q = 0; q < kStepHeadWGs; ++q) tot += value_of(w[q]);
+        s_sc[t][2] = rsqrtf(tot / (float)kStepD + a.eps);
+      }
+      if (lane < kStepQCols) {
+        const float zz = s_in[(size_t)t * kStepInPitch + 2 * kStepD + kStepQCols + lane];
+        store_tagged(a.tw.norm + (size_t)t * V + (size_t)head * kStepD + quarter * kStepQCols + lane,
+                     o * s_sc[t][2] * raw_value<true>(lnw1[0]) * silu(zz), tag);
+      }
     }
     __syncthreads();
-    if (tid == 0) store_tagged(a.tw.hint_head + head, 0.f, tag);
+    if (tid == 0) store_tagged(a.tw.hint_head + qb, 0.f, tag);
     {
-      const size_t base = ((size_t)head * kStepD + (size_t)sg * 32) * kStepD + sj;
+      const size_t base = ((size_t)head * kStepD + (size_t)sgr * 8) * kStepD + jcol;
 #pragma unroll
-      for (int m = 0; m < 32; ++m) reinterpret_cast<float*>(a.next_rec)[base + (size_t)m * kStepD] = S[m];
+      for (int m = 0; m < 8; ++m) reinterpret_cast<float*>(a.next_rec)[base + (size_t)m * kStepD] = S[m];
     }
     __syncthreads();  // s_dyn is reused below
   }
@@ -1062,9 +1199,9 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     uint16_t* s_nb = reinterpret_cast<uint16_t*>(s_dyn);  // [kcu/8][NCP][8] bf16 (bcol_slot)
     const int h0 = uks * (kcu / kStepD), nh = kcu / kStepD;  // heads of the unit's columns
     bool ok = true;
-    if (wave == 0) {
+    if (wave == 0) {  // the head workgroups of those heads
       uint64_t hw[1];
-      const uint64_t* hs[1] = {lane < nh ? a.tw.hint_head + h0 + lane : nullptr};
+      const uint64_t* hs[1] = {lane < nh * kStepHeadWGs ? a.tw.hint_head + h0 * kStepHeadWGs + lane : nullptr};
       hw[0] = hs[0] ? load_tagged(hs[0]) : 0ull;
       if (!poll_tagged<1>(hw, hs, tag)) s_fail = 1;
     }
@@ -1249,7 +1386,8 @@ static size_t step_tag_layout(char* base, StepTagWs* tw) {
   tw->norm = reinterpret_cast<uint64_t*>(take(kStepVWords * 8));
   tw->started = reinterpret_cast<uint64_t*>(take((size_t)kStepMaxGrid * 8));
   tw->hint_tile = reinterpret_cast<uint64_t*>(take((size_t)kStepTilesPerWG * kStepMaxGrid * 8));
-  tw->hint_head = reinterpret_cast<uint64_t*>(take(64 * 8));
+  tw->hint_head = reinterpret_cast<uint64_t*>(take((size_t)64 * kStepHeadWGs * 8));
+  tw->hss = reinterpret_cast<uint64_t*>(take((size_t)64 * kStepHeadWGs * kStepMaxTokens * 8));
   tw->part = reinterpret_cast<uint64_t*>(take(kStepPartWords * 8));
   return off;
 }
@@ -1280,8 +1418,8 @@ static bool step_fused_eligible(int T, int H, int Hk, int Hv, int D, const int* 
   for (int i = 1; i < 10; ++i)
     if (i != 5 && dt[i] != FK_DTYPE_BF16) dtypes_ok = false;
   return dtypes_ok && T >= 1 && T <= kStepMaxTokens && D == kStepD && H >= 512 && H <= 2048 && (H & (H - 1)) == 0 &&
-         (V & (V - 1)) == 0 && V >= 256 && V <= 4096 && C <= 8192 && Hv <= 64 && Hv % 16 == 0 && G >= Hv + 1 &&
-         G >= H / 16 && (H >> 7) * (V / (V < 512 ? V : 512)) <= G - Hv &&
+         (V & (V - 1)) == 0 && V >= 256 && V <= 4096 && C <= 8192 && Hv <= 64 && Hv % 16 == 0 &&
+         G >= H / 16 && (H >> 7) * (V / (V < 512 ? V : 512)) + kStepHeadWGs * Hv <= G &&
          (R + 15) / 16 <= kStepTilesPerWG * G && G <= kStepMaxGrid;
 }
 
@@ -1289,8 +1427,8 @@ static size_t step_fused_lds(int T, int H, int V) {
   const size_t nc = 2 * (size_t)T, ncp = nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 8 ? 8 : 16;
   const size_t tile = (size_t)16 * (2 * (size_t)H + 16),
                red = ((size_t)kStepWaves * kStepTilesPerWG * 16 * nc + kStepTilesPerWG * 16 * 16) * 4;
-  const size_t pa = (size_t)H * ncp * 2 + (tile > red ? tile : red);
-  const size_t pb = ((size_t)T * 4 * kStepD + 2 * kStepMaxTokens + (size_t)T * kStepD) * 4;
+  const size_t pa = T <= 2 ? (size_t)T * H * 4 : (size_t)H * ncp * 2 + (tile > red ? tile : red);
+  const size_t pb = ((size_t)T * kStepInPitch + (size_t)T * kStepQCols) * 4;
   const size_t pc = (size_t)(V < 512 ? V : 512) * ncp * 2;
   return pa > pb ? (pa > pc ? pa : pc) : (pb > pc ? pb : pc);
 }
@@ -1492,7 +1630,8 @@ int fk_deltanet_step(const void* hidden, const void* input_norm_weight, const vo
   hipStream_t s = as_stream(stream);
 
   const int conv_dim = (2 * qk_heads + value_heads) * head_dim;
-  const bool bx = dtypes[0] == FK_DTYPE_BF16, few = tokens <= 2;
+  // T <= 2 takes the VALU projections, written for H = 2048
+  const bool bx = dtypes[0] == FK_DTYPE_BF16, few = tokens <= 2 && hidden_size == 2048;
   const int G = bx ? (few ? step_grid<true, 2>() : step_grid<true, 8>())
                    : (few ? step_grid<false, 2>() : step_grid<false, 8>());
   if (G > 0 && step_fused_eligible(tokens, hidden_size, qk_heads, value_heads, head_dim, dtypes, G)) {
