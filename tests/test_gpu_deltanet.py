@@ -144,10 +144,12 @@ def test_deltanet_moe_layer(device, spec_name, tokens):
         torch.testing.assert_close(layer_hidden.cpu(), ref[0], **tol(torch.bfloat16))
 
 
-@pytest.mark.parametrize("tokens", [1, 2, 8])
+@pytest.mark.parametrize("tokens", [1, 2, 3, 5, 8])
 def test_step_single_launch_matches_oracle(device, real_dn, tokens):
-    # fk_deltanet_step at the real shapes takes the single-launch kernel
-    # (MFMA projections with bf16 hi/lo activations, tagged hand-offs).
+    # fk_deltanet_step at the real shapes takes the single-launch kernel:
+    # VALU projections for T <= 2, MFMA projections with bf16 hi/lo
+    # activations (swizzled staging, T = 3 and 5 use padded columns) above;
+    # heads split over four workgroups; tagged hand-offs.
     from fastkernels_amd.plan import DeltaNetStepPlan
 
     x = wl.make_hidden(tokens, REAL.hidden_size, seed=60 + tokens)
@@ -163,7 +165,7 @@ def test_step_single_launch_matches_oracle(device, real_dn, tokens):
     torch.testing.assert_close(plan.next_conv_state.cpu().float(), conv.float(), atol=1e-2, rtol=1e-2)
 
 
-@pytest.mark.parametrize("tokens", [1, 8])
+@pytest.mark.parametrize("tokens", [1, 2, 5, 8])
 def test_step_single_launch_matches_staged_kernels(device, real_dn, tokens):
     # Same step through the staged operator kernels (fp32 VALU GEMVs).
     from fastkernels_amd.plan import DeltaNetStepPlan
