@@ -944,27 +944,38 @@ __global__ __launch_bounds__(512) void moe_gateup_mfma_kernel(ExpertArgs a) {
                    (size_t)2 * I * H * 2, W, pos0, npairs, shared))
     return;
   const int lh = 31 - __builtin_clz((unsigned)H);
-  const int kw = H >> 3;                 // K range of a wavefront (KS steps of 32)
-  const int lpr_sh = lh - 6;             // LPR = kw / 8 lanes per row
-  const int rpi = kWave >> lpr_sh;
-  const int pitch = kw * 2 + 16;         // (16-byte pad: the 16 rows of an operand read hit distinct banks)
-
-  // gate rows i0.., up rows I + i0.. of this wavefront's K range
-  const uint32_t lane_off = (uint32_t)((((lane >> lpr_sh) << lh) + wave * kw + ((lane & ((1 << lpr_sh) - 1)) << 3)) << 1);
+  const int kw = H >> 3;                 // K range of a wavefront's MFMAs (KS steps of 32)
+  const int pitch = 2 * H + 16;          // LDS tile row (16-byte pad: the 16 rows of an operand read hit distinct banks)
+  // Whole-row loads: wavefront w reads gate rows i0 + 2w, i0 + 2w + 1 and the
+  // same up rows, one 1 KiB piece per load (slot s: row 2w + s / (KS/2),
+  // piece s % (KS/2)); reading its MFMA K range of all 16 rows instead
+  // streams measurably slower on this part.  The gate rows, then the up
+  // rows, meet in the workgroup's LDS tile, from which each wavefront reads
+  // its operands.
+  constexpr int PPR = KS / 2;  // 1 KiB pieces per row
+  const uint32_t lane_off = (uint32_t)((wave << (lh + 2)) + (lane << 4));
   u32x4 av[2][KS];
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int s = 0; s < KS; ++s)
-      av[h][s] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(W + ((size_t)(h * I + i0 + s * rpi) << (lh + 1)) + lane_off));
-  char* area = s_lds + (size_t)wave * 16 * pitch;
-  rows_to_mfma_a<KS>(av[0], area, pitch, lpr_sh, lane);
-  rows_to_mfma_a<KS>(av[1], area, pitch, lpr_sh, lane);
-  __syncthreads();  // the partial tiles below overlap other wavefronts' areas
+      av[h][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          W + ((size_t)(h * I + i0 + s / PPR) << (lh + 1)) + (size_t)(s % PPR) * 1024 + lane_off));
+  const int n = lane & 15, g4 = lane >> 4;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (h > 0) __syncthreads();  // the gate operands are read
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      *reinterpret_cast<u32x4*>(s_lds + (2 * wave + s / PPR) * pitch + (s % PPR) * 1024 + lane * 16) = av[h][s];
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      av[h][s] = *reinterpret_cast<const u32x4*>(s_lds + n * pitch + (wave * kw + s * 32 + g4 * 8) * 2);
+  }
+  __syncthreads();  // the partial tiles below overlap the LDS tile
 
   float* s_part = reinterpret_cast<float*>(s_lds);  // [wave][gate|up][16 rows][16 columns]
-  const int n = lane & 15, g4 = lane >> 4;
   for (int tile = 0; tile * 16 < npairs; ++tile) {
     // column n: pair tile*16 + n (clamped; columns past npairs are dropped)
     const int p = min(tile * 16 + n, npairs - 1);
@@ -2109,15 +2120,14 @@ static int launch_router(const RouterArgs& ra, int router_dt, int hidden_dt, hip
 // Batched expert stage on MFMA: gate/up then down (see moe_gateup_mfma_kernel).
 static int launch_experts_mfma(const ExpertArgs& ea, int slots, hipStream_t stream) {
   static bool attr_set[64] = {false};
-  const size_t gu_shm = std::max((size_t)16 * kGuMfmaWaves * ((size_t)ea.H / kGuMfmaWaves * 2 + 16),
-                                 (size_t)kGuMfmaWaves * 512 * sizeof(float));
+  const size_t gu_shm = std::max((size_t)16 * ((size_t)ea.H * 2 + 16), (size_t)kGuMfmaWaves * 512 * sizeof(float));
   const size_t dn_shm = std::max((size_t)16 * kDnMfmaWaves * ((size_t)ea.I / kDnMfmaWaves * 2 + 16),
                                  (size_t)kDnMfmaWaves * 1024 * sizeof(float));
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(FK_ERR_LAUNCH, "no current HIP device");
   if (!attr_set[dev]) {
-    // (the largest need, H = 2048: 67,584 bytes)
-    const int max_gu = 16 * kGuMfmaWaves * (2048 / kGuMfmaWaves * 2 + 16);
+    // (the largest need, H = 2048: 65,792 bytes)
+    const int max_gu = 16 * (2048 * 2 + 16);
     for (const void* k : {reinterpret_cast<const void*>(moe_gateup_mfma_kernel<2>),
                           reinterpret_cast<const void*>(moe_gateup_mfma_kernel<4>),
                           reinterpret_cast<const void*>(moe_gateup_mfma_kernel<8>)})
