@@ -548,7 +548,7 @@ constexpr size_t kStepPartWords = (size_t)8 * kStepMaxTokens * 2048;  // [V/512 
 constexpr int kStepHeadWGs = 4;  // workgroups per value head (value columns split four ways)
 constexpr int kStepQCols = kStepD / kStepHeadWGs;  // value columns per head workgroup
 constexpr int kStepInPitch = 2 * kStepD + 2 * kStepQCols + 4;  // head workgroup inputs per token (q, k, v, z, a, b, pad)
-constexpr int kStepValuAhead = 2;  // VALU projections: weight tiles in flight per wavefront
+constexpr int kStepTilesAhead = 2;  // phase A weight tiles in flight per wavefront
 constexpr int kStepTicketEpoch = 0;
 constexpr int kStepTicketError = kWorkspaceErrorWord;
 
@@ -778,13 +778,14 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       av[i][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(live ? tp + so + lane_off : spare + (lane << 4)));
     }
   };
-  // MFMA path: every tile up front.  VALU path: kStepValuAhead tiles ahead
-  // of the one being reduced, so that tiles complete one after another and
-  // the dot products run under the stream (issued all at once, a
-  // wavefront's first tile completes about as late as its last).
+  // kStepTilesAhead tiles ahead of the one being reduced, so that tiles
+  // complete one after another and the per-tile work (VALU dot products, or
+  // LDS staging and MFMAs) runs under the stream: issued all at once, a
+  // wavefront's first tile completes about as late as its last, and the
+  // wavefront cannot even issue the rest until the memory pipeline drains.
 #pragma unroll
   for (int i = 0; i < kStepTilesPerWG; ++i)
-    if (!VALU_A || i < kStepValuAhead) issue_tile(i);
+    if (i < kStepTilesAhead) issue_tile(i);
 
   // Small operands of later phases, fetched now so that no phase waits on a
   // dependent global load: the head's norm weight and decay parameters.
@@ -893,7 +894,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
                              kStepWaves - 1)
           store_tagged(a.tw.hint_tile + b + i * G, 0.f, tag);
       }
-      if (i + kStepValuAhead < kStepTilesPerWG) issue_tile(i + kStepValuAhead);
+      if (i + kStepTilesAhead < kStepTilesPerWG) issue_tile(i + kStepTilesAhead);
     }
     __syncthreads();  // phases B and C reuse the dynamic LDS
   } else {
@@ -931,6 +932,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         }
         __syncthreads();
       }
+      if (i + kStepTilesAhead < kStepTilesPerWG) issue_tile(i + kStepTilesAhead);
     }
     float* s_red = reinterpret_cast<float*>(s_tile);  // [wave][tile][16][NC]
     const int red_w = kStepTilesPerWG * 16 * NC;
