@@ -364,7 +364,7 @@ def main() -> int:
             "parallelism": "single-gpu",
         },
         "roofline": {
-            "kernel": "moe_gateup_kernel + moe_down_kernel (expert stage)",
+            "kernel": "moe_gateup_kernel + moe_down_kernel + moe_combine_kernel (expert stage)",
             "bound": "hbm",
             "achieved": round(main_res["expert_stage_tbs"] * 1e3, 1),
             "peak": HBM_PEAK_GBS,
