@@ -243,6 +243,57 @@ __device__ __forceinline__ float wave_max(float v) {
   return wave_allreduce_f32(v, [](float a, float b) { return fmaxf(a, b); });
 }
 
+// Eight wavefront sums at once, transposed: lane l ends with the sum over
+// all 64 lanes of d[l >> 3] (lanes 8r .. 8r + 7 hold row r's total).  Each
+// step halves the values per lane while pairing lanes:
+//   v_permlane32_swap on (d[i], d[i+4]): lanes < 32 keep value i, lanes
+//     >= 32 value i + 4, each summed over {l, l ^ 32};
+//   v_permlane16_swap on (e[i], e[i+2]): value i + 2 (l >> 4), over
+//     {l ^ 0, 16, 32, 48};
+//   row_ror:8 (partner l ^ 8 within the 16-lane row) with each lane keeping
+//     the value of its own bit 3: value l >> 3, over 8 lanes;
+//   quad xor 1, quad xor 2, row half mirror: over the remaining 8 lanes.
+// 22 instructions instead of eight 12-instruction reductions; fixed order.
+constexpr int kDppRowRor8 = 0x128;
+__device__ __forceinline__ float rows8_sum(const float (&d)[8]) {
+  float e[4], f[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(d[i]), __float_as_uint(d[i + 4]), false, false);
+    e[i] = __uint_as_float((uint32_t)r[0]) + __uint_as_float((uint32_t)r[1]);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(e[i]), __float_as_uint(e[i + 2]), false, false);
+    f[i] = __uint_as_float((uint32_t)r[0]) + __uint_as_float((uint32_t)r[1]);
+  }
+  const bool b3 = (__lane_id() >> 3) & 1;
+  const float keep = b3 ? f[1] : f[0], give = b3 ? f[0] : f[1];
+  float g = keep + __uint_as_float(dpp_u32<kDppRowRor8>(__float_as_uint(give)));
+  g += __uint_as_float(dpp_u32<kDppQuadXor1>(__float_as_uint(g)));
+  g += __uint_as_float(dpp_u32<kDppQuadXor2>(__float_as_uint(g)));
+  g += __uint_as_float(dpp_u32<kDppRowHalfMirror>(__float_as_uint(g)));
+  return g;
+}
+
+// Four wavefront sums at once, transposed the same way: lane l ends with
+// the sum over all 64 lanes of d[l >> 4] (14 instructions instead of 48).
+__device__ __forceinline__ float rows4_sum(const float (&d)[4]) {
+  float e[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(d[i]), __float_as_uint(d[i + 2]), false, false);
+    e[i] = __uint_as_float((uint32_t)r[0]) + __uint_as_float((uint32_t)r[1]);
+  }
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(e[0]), __float_as_uint(e[1]), false, false);
+  float g = __uint_as_float((uint32_t)r[0]) + __uint_as_float((uint32_t)r[1]);
+  g += __uint_as_float(dpp_u32<kDppQuadXor1>(__float_as_uint(g)));
+  g += __uint_as_float(dpp_u32<kDppQuadXor2>(__float_as_uint(g)));
+  g += __uint_as_float(dpp_u32<kDppRowHalfMirror>(__float_as_uint(g)));
+  g += __uint_as_float(dpp_u32<kDppRowMirror>(__float_as_uint(g)));
+  return g;
+}
+
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
 
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {

@@ -691,8 +691,10 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(ExpertArgs a) {
         }
       }
     }
+    // the four row sums at once (lanes 16r ..: row r), gathered in lane 0
+    const float rs = rows4_sum(acc);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] = wave_sum(acc[r]);
+    for (int r = 0; r < 4; ++r) acc[r] = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 16 * r));
     if (lane == 0) {
       float2 v = make_float2(silu(acc[0]) * acc[2], silu(acc[1]) * acc[3]);
       *reinterpret_cast<float2*>(a.ws.act + (size_t)pos * a.I + i0) = v;
@@ -811,13 +813,10 @@ __global__ __launch_bounds__(256) void moe_down_kernel(ExpertArgs a) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) av[j][q] = an[j][q];
     }
-    float mine = 0.f;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const float v = wave_sum(d[r]);
-      mine = lane == r ? v : mine;
-    }
-    if (lane < R && r0 + lane < a.H) a.ws.y[(size_t)pos * a.H + r0 + lane] = mine;
+    // the eight row sums at once: lanes 8r .. 8r + 7 hold row r0 + r
+    static_assert(R == 8, "rows8_sum sums eight rows");
+    const float v = rows8_sum(d);
+    if ((lane & 7) == 0 && r0 + (lane >> 3) < a.H) a.ws.y[(size_t)pos * a.H + r0 + (lane >> 3)] = v;
   }
 }
 
