@@ -1540,9 +1540,12 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   }
 
   // ---------------- P3: routed gate/up (+ down-row prefetch) ---------------
-  const bool prefetch = U <= NPF && r_first < H && lane * 8 < I;
+  // (wave-uniform: the down code branches on it and reduces across lanes
+  // with lane swaps, which read inactive lanes' stale registers; lanes past
+  // I load nothing and their dot products are zero)
+  const bool prefetch = U <= NPF && r_first < H;
   Raw8<true> dr[NPF];
-  if (prefetch) {
+  if (prefetch && lane * 8 < I) {
 #pragma unroll
     for (int u = 0; u < NPF; ++u) {
       if (u < U) dr[u] = load_raw8_stream<true>(f.dn, ((size_t)s_active[u] * H + r_first) * I + (size_t)lane * 8);

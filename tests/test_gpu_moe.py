@@ -351,3 +351,27 @@ def test_fused_layer_repeated_calls_stay_consistent(device, real_gpu):
             plan.run()
             assert torch.equal(plan.layer_out, r)
     plan.check_device()
+
+
+@pytest.mark.parametrize("shape", [(32, 512, 128), (256, 2048, 128), (64, 2048, 256), (32, 2048, 512)])
+@pytest.mark.parametrize("tokens", [1, 2, 5])
+def test_moe_layer_reduced_shapes(device, shape, tokens):
+    # Smaller expert counts and intermediate sizes through every small-T
+    # path (single launch at T = 1 and 2, router + GEMV experts at T = 5).
+    # I < 512 leaves lanes of the single-launch kernel's down rows idle,
+    # which must not change its lane reductions.
+    e, h, i = shape
+    g = torch.Generator().manual_seed(5)
+
+    def rnd(*s, sc=0.02):
+        return (torch.randn(*s, generator=g) * sc).to(torch.bfloat16)
+
+    w = [rnd(h, sc=0.1), rnd(e, h), rnd(e, 2 * i, h), rnd(e, h, i), rnd(2 * i, h), rnd(h, i), rnd(1, h)]
+    x = wl.make_hidden(tokens, h, seed=11)
+    lh, moe, logits, ids, wt = hip.hip_qwen36_batched_moe_layer_decode(x.to(device), *[t.to(device) for t in w], top_k=K)
+    ref = oracle.routed_experts(x, ids.cpu(), wt.cpu(), w[2], w[3]) + oracle.shared_expert(x, w[4], w[5], w[6])
+    torch.testing.assert_close(moe.cpu(), ref, **tol(torch.bfloat16))
+    torch.testing.assert_close(lh.cpu(), x.float() + ref, **tol(torch.bfloat16))
+    o_logits = oracle.moe_layer(x, *w, top_k=K)[2]
+    if assert_routing_parity(logits, ids, wt, o_logits, K) == 0:
+        assert torch.equal(ids.cpu(), oracle.moe_layer(x, *w, top_k=K)[3])
