@@ -53,6 +53,8 @@ class MoeLayerPlan:
         hidden_dtype: torch.dtype = torch.bfloat16,
     ) -> None:
         self.lib = _lib.load()
+        if hasattr(weights, "as_dict"):  # packed checkpoint tensors (weights.Qwen36MoEWeights)
+            weights = weights.as_dict()
         w = {k: (None if v is None else _dense(v)) for k, v in weights.items()}
         self.w = w
         gu = w["expert_gate_up_weight"]

@@ -30,6 +30,75 @@ class Qwen36A3BSpec:
     context_length: int
     rope_theta: float = 10000.0
     conv_kernel_size: int = 4
+    layer_types: tuple[str, ...] | None = None
+
+    def layer_kinds(self) -> tuple[str, ...]:
+        """Mixer of each layer: "deltanet_moe" or "attention_moe".  From the
+        config's layer_types when given ("full_attention" -> attention),
+        else three DeltaNet layers then one attention layer, repeated
+        (reference models/qwen36.py:54-62)."""
+
+        if self.layer_types is not None:
+            return tuple("attention_moe" if t == "full_attention" else "deltanet_moe" for t in self.layer_types)
+        cycle = ("deltanet_moe",) * 3 + ("attention_moe",)
+        return tuple(cycle[i % 4] for i in range(self.num_layers))
+
+    def layer_counts(self) -> dict[str, int]:
+        kinds = self.layer_kinds()
+        return {"deltanet_moe": kinds.count("deltanet_moe"), "attention_moe": kinds.count("attention_moe")}
+
+    @classmethod
+    def from_hf_config(cls, config: dict, name: str = "hf-config") -> "Qwen36A3BSpec":
+        """Spec from a Hugging Face config dict (its `text_config` when
+        nested), with the reference's key aliases and defaults (reference
+        models/qwen36.py:116-158)."""
+
+        text = config.get("text_config", config)
+
+        def get(*names: str, default=None):
+            for src in (text, config):
+                for n in names:
+                    if src.get(n) is not None:
+                        return src[n]
+            return default
+
+        rope = get("rope_parameters", default={}) or {}
+        partial = get("partial_rotary_factor", default=rope.get("partial_rotary_factor"))
+        head_dim = int(get("attention_head_dim", "head_dim", default=256))
+        rope_dim = get("rope_dim", "rotary_emb_base_dim")
+        if rope_dim is None and partial is not None:
+            rope_dim = int(head_dim * float(partial))
+        layer_types = get("layer_types")
+        return cls(
+            name=name,
+            hidden_size=int(get("hidden_size")),
+            num_layers=int(get("num_hidden_layers", "num_layers")),
+            num_experts=int(get("num_experts", "n_routed_experts")),
+            num_routed_experts=int(get("num_experts_per_tok", "num_experts_per_token", default=8)),
+            num_shared_experts=int(get("n_shared_experts", "num_shared_experts", default=1)),
+            expert_intermediate_size=int(get("moe_intermediate_size", "expert_intermediate_size", "intermediate_size")),
+            deltanet_value_heads=int(get("num_linear_attention_value_heads", "linear_num_value_heads", default=32)),
+            deltanet_qk_heads=int(get("num_linear_attention_qk_heads", "linear_num_key_heads", default=16)),
+            deltanet_head_dim=int(get("linear_attention_head_dim", "linear_key_head_dim", "linear_value_head_dim",
+                                      default=128)),
+            attention_heads=int(get("num_attention_heads", default=16)),
+            attention_kv_heads=int(get("num_key_value_heads", default=2)),
+            attention_head_dim=head_dim,
+            rope_dim=int(rope_dim or 64),
+            vocab_size=int(get("vocab_size", default=248320)),
+            context_length=int(get("max_position_embeddings", "seq_length", default=262144)),
+            rope_theta=float(get("rope_theta", default=rope.get("rope_theta", 10000.0))),
+            layer_types=tuple(layer_types) if layer_types is not None else None,
+        )
+
+    @classmethod
+    def from_json_file(cls, path, name: str | None = None) -> "Qwen36A3BSpec":
+        import json
+        from pathlib import Path
+
+        p = Path(path)
+        with p.open("r", encoding="utf-8") as fh:
+            return cls.from_hf_config(json.load(fh), name=name or p.stem)
 
     @property
     def gated_up_features(self) -> int:
