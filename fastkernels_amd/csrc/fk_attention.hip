@@ -1,0 +1,396 @@
+// Qwen3.6 gated full-attention decode step for gfx950 (the mixer of one
+// layer in four; the MoE layer follows it).
+//
+// Semantics (reference kernels/triton/qwen36_attention.py:448-577; oracle
+// reference/qwen36_real.py:283-326):
+//   xn = RMSNorm(x) * (1 + w)
+//   per head h: [q_h | gate_h] = rows 2hd*h .. 2hd*h + 2hd - 1 of xn Wq^T
+//   k = xn Wk^T, v = xn Wv^T                      (kv head j serves heads j*G .. j*G + G - 1)
+//   q_h = RMSNorm(q_h) * (1 + w_q), k_j = RMSNorm(k_j) * (1 + w_k)   (over head_dim)
+//   RoPE of the first rope_dim dims at position p = start + t:
+//     interleaved pairs (2i, 2i+1) (the Triton entry point and its test) or
+//     halves (i, i + rope_dim/2) (the torch oracle), angle p * theta^(-2i/rope_dim)
+//   cache[start + t] = (k, v); o_h = softmax(q_h . K_j[0..p] / sqrt(hd)) V_j[0..p]
+//   update = (o * sigmoid(gate)) Wo^T;  hidden_out = x + update
+//
+// Kernels (three launches per step):
+//   projection        the shared normalized projection kernel (fk_deltanet.hip)
+//                     over [Wq | Wk | Wv] (9216 rows at the model shape)
+//   attn_head_kernel  grid (T, heads), 256 threads: head norms and RoPE in
+//                     LDS, the token's new keys recomputed from k (no
+//                     dependence on another workgroup's cache write), online
+//                     softmax over positions split across the 4 wavefronts
+//                     (4 positions in flight per wavefront), gate applied
+//   attn_out_kernel   grid ceil(H/8): 8 rows of Wo per workgroup (2 per
+//                     wavefront, loaded once) against every token; residual
+#include "fk_common.h"
+#include "fk_host.h"
+
+namespace fk {
+
+constexpr int kAttnMaxHeadDim = 256;
+constexpr int kAttnMaxTokens = 32;  // new keys of the step are kept in LDS (T * hd floats)
+constexpr int kAttnOutRows = 8;
+
+struct AttnArgs {
+  const float* qg;      // [T, heads * 2 * hd] projected query/gate pairs
+  const float* k;       // [T, kv_heads * hd]
+  const float* v;       // [T, kv_heads * hd]
+  const void* qn_w;     // [hd]
+  const void* kn_w;     // [hd]
+  int qn_dt, kn_dt;
+  void* kc;             // [max_pos, kv_heads, hd]
+  void* vc;
+  int start, max_pos;
+  int T, heads, kvh, hd, rope_dim;
+  float theta_log2, eps;
+  int interleaved;
+  float* gated;         // [T, heads * hd]  o * sigmoid(gate)
+};
+
+struct AttnWs {
+  float* qg;
+  float* k;
+  float* v;
+  float* gated;
+};
+
+static size_t attn_ws_layout(int T, int heads, int kvh, int hd, char* base, AttnWs* ws) {
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = off;
+    off = align_up(off + bytes, 256);
+    return base ? reinterpret_cast<float*>(base + at) : nullptr;
+  };
+  ws->qg = take((size_t)T * heads * 2 * hd * 4);
+  ws->k = take((size_t)T * kvh * hd * 4);
+  ws->v = take((size_t)T * kvh * hd * 4);
+  ws->gated = take((size_t)T * heads * hd * 4);
+  return off;
+}
+
+template <bool BF>
+__device__ __forceinline__ float4 load4(const void* p, size_t i) {
+  if constexpr (BF) {
+    const uint2 r = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p) + i);
+    return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16),
+                       __uint_as_float(r.y & 0xffff0000u));
+  } else {
+    return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
+  }
+}
+
+template <bool BF>
+__device__ __forceinline__ void store1(void* p, size_t i, float v) {
+  if constexpr (BF) reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v);
+  else reinterpret_cast<float*>(p)[i] = v;
+}
+
+// Sum over the workgroup's 256 threads (one value each); every thread gets it.
+__device__ __forceinline__ float block256_sum(float v, float* s_red) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();  // s_red may still be read from a previous call
+  if (lane == 0) s_red[wave] = v;
+  __syncthreads();
+  return (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+}
+
+// RMSNorm(1 + w) and RoPE at `pos` of one head held one dim per thread
+// (thread d < hd); `s_vec` is the head's LDS row.  Returns dim d's value.
+__device__ __forceinline__ float norm_rope(float x, const void* w, int w_dt, const AttnArgs& a, int pos, float* s_vec,
+                                           float* s_red) {
+  const int d = threadIdx.x;
+  const bool in = d < a.hd;
+  const float ss = block256_sum(in ? x * x : 0.f, s_red);
+  float y = in ? x * rsqrtf(ss / (float)a.hd + a.eps) * (1.f + load_scalar(w, w_dt, d)) : 0.f;
+  const int rd = a.rope_dim;
+  if (in) s_vec[d] = y;
+  __syncthreads();
+  if (d < rd) {
+    int i, partner;
+    float sign;
+    if (a.interleaved) {
+      i = d >> 1;
+      partner = d ^ 1;
+      sign = (d & 1) ? 1.f : -1.f;
+    } else {
+      const int h = rd >> 1;
+      i = d < h ? d : d - h;
+      partner = d < h ? d + h : d - h;
+      sign = d < h ? -1.f : 1.f;
+    }
+    // angle = pos * theta^(-2i / rd), as the reference (fp32)
+    const float inv_freq = exp2f(-(float)(2 * i) / (float)rd * a.theta_log2);
+    float sn, cs;
+    sincosf((float)pos * inv_freq, &sn, &cs);
+    y = y * cs + sign * s_vec[partner] * sn;
+  }
+  __syncthreads();  // s_vec is reused by the caller
+  return y;
+}
+
+template <bool CBF>
+__global__ __launch_bounds__(256) void attn_head_kernel(AttnArgs a) {
+  __shared__ __align__(16) float s_q[kAttnMaxHeadDim];
+  extern __shared__ float4 s_knew_v[];  // [T, hd] new keys
+  float* s_knew = reinterpret_cast<float*>(s_knew_v);
+  __shared__ float s_tmp[kAttnMaxHeadDim];
+  __shared__ float s_red[4];
+  __shared__ float s_m[4], s_l[4];
+  __shared__ __align__(16) float s_acc[4][kAttnMaxHeadDim];
+  const int t = blockIdx.x, h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int hd = a.hd, G = a.heads / a.kvh, j = h / G;
+  const int qw = a.heads * hd, kvw = a.kvh * hd;
+  const int pos = a.start + t;
+  const bool in = tid < hd;
+
+  // query: norm, RoPE, 1/sqrt(hd)
+  const float qraw = in ? a.qg[(size_t)t * 2 * qw + (size_t)h * 2 * hd + tid] : 0.f;
+  const float gate = in ? a.qg[(size_t)t * 2 * qw + (size_t)h * 2 * hd + hd + tid] : 0.f;
+  const float q = norm_rope(qraw, a.qn_w, a.qn_dt, a, pos, s_tmp, s_red);
+  if (in) s_q[tid] = q * rsqrtf((float)hd);
+  // keys of the new positions start .. pos, recomputed here from k
+  for (int u = 0; u <= t; ++u) {
+    const float kraw = in ? a.k[(size_t)u * kvw + (size_t)j * hd + tid] : 0.f;
+    const float kr = norm_rope(kraw, a.kn_w, a.kn_dt, a, a.start + u, s_tmp, s_red);
+    if (in) s_knew[u * hd + tid] = kr;
+  }
+  // the first query head of kv head j writes token t's cache row
+  if (h % G == 0 && in && pos < a.max_pos) {
+    const size_t c = ((size_t)pos * a.kvh + j) * hd + tid;
+    store1<CBF>(a.kc, c, s_knew[t * hd + tid]);
+    store1<CBF>(a.vc, c, a.v[(size_t)t * kvw + (size_t)j * hd + tid]);
+  }
+  __syncthreads();
+
+  // online softmax over positions wave, wave + 4, ..; lane holds dims 4l..4l+3
+  const int d0 = lane * 4;
+  const bool lin = d0 < hd;
+  const float4 q4 = lin ? *reinterpret_cast<const float4*>(s_q + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
+  float m = -INFINITY, l = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  constexpr int NB = 4;  // positions in flight per wavefront
+  for (int p0 = wave; p0 <= pos; p0 += 4 * NB) {
+    float4 kk[NB], vv[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int p = min(p0 + 4 * b, pos);
+      if (!lin) {
+        kk[b] = vv[b] = make_float4(0.f, 0.f, 0.f, 0.f);
+      } else if (p < a.start) {
+        const size_t c = ((size_t)p * a.kvh + j) * hd + d0;
+        kk[b] = load4<CBF>(a.kc, c);
+        vv[b] = load4<CBF>(a.vc, c);
+      } else {
+        kk[b] = *reinterpret_cast<const float4*>(s_knew + (p - a.start) * hd + d0);
+        vv[b] = *reinterpret_cast<const float4*>(a.v + (size_t)(p - a.start) * kvw + (size_t)j * hd + d0);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (p0 + 4 * b > pos) break;
+      const float s = wave_sum(q4.x * kk[b].x + q4.y * kk[b].y + q4.z * kk[b].z + q4.w * kk[b].w);
+      const float mn = fmaxf(m, s);
+      const float f = __expf(m - mn), e = __expf(s - mn);
+      l = l * f + e;
+      acc.x = acc.x * f + e * vv[b].x;
+      acc.y = acc.y * f + e * vv[b].y;
+      acc.z = acc.z * f + e * vv[b].z;
+      acc.w = acc.w * f + e * vv[b].w;
+      m = mn;
+    }
+  }
+  if (lane == 0) {
+    s_m[wave] = m;
+    s_l[wave] = l;
+  }
+  if (lin) *reinterpret_cast<float4*>(&s_acc[wave][d0]) = acc;
+  __syncthreads();
+  if (in) {
+    const float M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+    float L = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float f = s_m[w] == -INFINITY ? 0.f : __expf(s_m[w] - M);  // a wavefront with no position
+      L += s_l[w] * f;
+      o += s_acc[w][tid] * f;
+    }
+    a.gated[(size_t)t * qw + (size_t)h * hd + tid] = (o / L) * sigmoid(gate);
+  }
+}
+
+struct AttnOutArgs {
+  const float* gated;  // [T, K]
+  const void* wo;      // [H, K]
+  const void* x;       // [T, H] residual input (NULL: no residual output)
+  int x_dt;
+  int T, H, K;
+  float* update;
+  float* hidden_out;
+};
+
+// 8 rows of Wo per workgroup (2 per wavefront), K <= 4096, loaded once and
+// applied to every token.
+template <bool BFW>
+__global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
+  constexpr int NJ = 8;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r0 = blockIdx.x * kAttnOutRows + wave * 2;
+  const int nch = a.K >> 3;
+  Raw8<BFW> wr[2][NJ];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int q = 0; q < NJ; ++q) {
+      const int c = lane + kWave * q;
+      if (c < nch && r0 + r < a.H) wr[r][q] = load_raw8_stream<BFW>(a.wo, (size_t)(r0 + r) * a.K + (size_t)c * 8);
+    }
+  for (int t = 0; t < a.T; ++t) {
+    float acc[2] = {0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < NJ; ++q) {
+      const int c = lane + kWave * q;
+      if (c < nch) {
+        float g8[8];
+        load8_act(a.gated, (size_t)t * a.K + (size_t)c * 8, g8);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          float w8[8];
+          raw8_to_f32<BFW>(wr[r][q], w8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[r] = fmaf(w8[e], g8[e], acc[r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) acc[r] = wave_sum(acc[r]);
+    if (lane < 2 && r0 + lane < a.H) {
+      const float u = lane ? acc[1] : acc[0];
+      const size_t o = (size_t)t * a.H + r0 + lane;
+      a.update[o] = u;
+      if (a.hidden_out) a.hidden_out[o] = load_scalar(a.x, a.x_dt, o) + u;
+    }
+  }
+}
+
+static int check_attn_shape(int tokens, int hidden_size, int heads, int kv_heads, int head_dim, int rope_dim) {
+  if (tokens < 1 || tokens > kAttnMaxTokens) return fail(FK_ERR_UNSUPPORTED, "tokens must be in [1, %d]", kAttnMaxTokens);
+  if (hidden_size < 8 || hidden_size % 8 || hidden_size > 4096)
+    return fail(FK_ERR_ALIGNMENT, "hidden_size must be a multiple of 8 in [8, 4096]");
+  if (heads < 1 || kv_heads < 1 || heads % kv_heads) return fail(FK_ERR_INVALID, "heads must be a positive multiple of kv_heads");
+  if (head_dim < 4 || head_dim > kAttnMaxHeadDim || head_dim % 4)
+    return fail(FK_ERR_UNSUPPORTED, "head_dim must be a multiple of 4 in [4, %d]", kAttnMaxHeadDim);
+  if ((long long)heads * head_dim > 4096 || (heads * head_dim) % 8)
+    return fail(FK_ERR_UNSUPPORTED, "heads * head_dim must be a multiple of 8 and <= 4096");
+  if (rope_dim < 0) return fail(FK_ERR_INVALID, "rope_dim must be >= 0");
+  return FK_OK;
+}
+
+}  // namespace fk
+
+using namespace fk;
+
+extern "C" {
+
+size_t fk_attention_workspace_bytes(int tokens, int heads, int kv_heads, int head_dim) {
+  if (tokens < 1 || heads < 1 || kv_heads < 1 || head_dim < 1) return 0;
+  AttnWs ws;
+  return attn_ws_layout(tokens, heads, kv_heads, head_dim, nullptr, &ws);
+}
+
+int fk_attention_project(const void* hidden, int hidden_dtype, const void* norm_weight, int norm_dtype,
+                         const void* q_proj, const void* k_proj, const void* v_proj, int weight_dtype, int tokens,
+                         int hidden_size, int q_rows, int kv_rows, float eps, float norm_offset, float* q_out,
+                         float* k_out, float* v_out, void* stream) {
+  if (tokens < 1) return fail(FK_ERR_INVALID, "tokens must be positive");
+  if (hidden_size < 8 || hidden_size % 8 || hidden_size > 4096)
+    return fail(FK_ERR_ALIGNMENT, "hidden_size must be a multiple of 8 in [8, 4096]");
+  if (q_rows < 1 || kv_rows < 1) return fail(FK_ERR_INVALID, "projection row counts must be positive");
+  if (!is_float_dtype(hidden_dtype) || !is_float_dtype(norm_dtype) || !is_float_dtype(weight_dtype))
+    return fail(FK_ERR_DTYPE, "projection inputs must be f32 or bf16");
+  if (!hidden || !norm_weight || !q_proj || !k_proj || !v_proj || !q_out || !k_out || !v_out)
+    return fail(FK_ERR_INVALID, "projection pointers must be non-NULL");
+  if (!aligned16(hidden) || !aligned16(norm_weight) || !aligned16(q_proj) || !aligned16(k_proj) || !aligned16(v_proj))
+    return fail(FK_ERR_ALIGNMENT, "hidden, norm_weight and projection weights must be 16-byte aligned");
+  const void* const w[4] = {q_proj, k_proj, v_proj, nullptr};
+  const int rows[4] = {q_rows, kv_rows, kv_rows, 0};
+  float* const out[4] = {q_out, k_out, v_out, nullptr};
+  return launch_norm_projection(hidden, hidden_dtype, norm_weight, norm_dtype, w, rows, out, weight_dtype, tokens,
+                                hidden_size, eps, norm_offset, as_stream(stream));
+}
+
+int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_weight, int norm_dtype,
+                        const void* q_proj, const void* k_proj, const void* v_proj, const void* o_proj,
+                        int weight_dtype, const void* q_norm_weight, const void* k_norm_weight, int qk_norm_dtype,
+                        void* key_cache, void* value_cache, int cache_dtype, int max_positions, int start_position,
+                        int tokens, int hidden_size, int heads, int kv_heads, int head_dim, int rope_dim,
+                        float rope_theta, int rope_interleaved, float eps, float qk_eps, float* update,
+                        float* hidden_out, void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_attn_shape(tokens, hidden_size, heads, kv_heads, head_dim, rope_dim);
+  if (st) return st;
+  if (start_position < 0 || start_position + tokens > max_positions)
+    return fail(FK_ERR_INVALID, "decode positions [%d, %d) exceed the cache length %d", start_position,
+                start_position + tokens, max_positions);
+  if (!is_float_dtype(cache_dtype) || !is_float_dtype(qk_norm_dtype)) return fail(FK_ERR_DTYPE, "caches and q/k norms must be f32 or bf16");
+  if (!key_cache || !value_cache || !o_proj || !q_norm_weight || !k_norm_weight || !update)
+    return fail(FK_ERR_INVALID, "attention pointers must be non-NULL");
+  if (!aligned16(o_proj) || !aligned16(key_cache) || !aligned16(value_cache))
+    return fail(FK_ERR_ALIGNMENT, "o_proj and the caches must be 16-byte aligned");
+  if (!rope_interleaved && rope_dim % 2) return fail(FK_ERR_INVALID, "half-split RoPE needs an even rope_dim");
+  AttnWs ws;
+  const size_t need = attn_ws_layout(tokens, heads, kv_heads, head_dim, nullptr, &ws);
+  if (!workspace || workspace_bytes < need)
+    return fail(FK_ERR_WORKSPACE, "attention workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+  attn_ws_layout(tokens, heads, kv_heads, head_dim, reinterpret_cast<char*>(workspace), &ws);
+  const hipStream_t s = as_stream(stream);
+  st = fk_attention_project(hidden, hidden_dtype, norm_weight, norm_dtype, q_proj, k_proj, v_proj, weight_dtype,
+                            tokens, hidden_size, 2 * heads * head_dim, kv_heads * head_dim, eps, 1.0f, ws.qg, ws.k,
+                            ws.v, stream);
+  if (st) return st;
+  AttnArgs a;
+  a.qg = ws.qg;
+  a.k = ws.k;
+  a.v = ws.v;
+  a.qn_w = q_norm_weight;
+  a.kn_w = k_norm_weight;
+  a.qn_dt = a.kn_dt = qk_norm_dtype;
+  a.kc = key_cache;
+  a.vc = value_cache;
+  a.start = start_position;
+  a.max_pos = max_positions;
+  a.T = tokens;
+  a.heads = heads;
+  a.kvh = kv_heads;
+  a.hd = head_dim;
+  const int rd = rope_dim < head_dim ? rope_dim : head_dim;
+  a.rope_dim = rd - rd % 2;
+  a.theta_log2 = log2f(rope_theta);
+  a.eps = qk_eps;
+  a.interleaved = rope_interleaved;
+  a.gated = ws.gated;
+  const size_t shm = (size_t)tokens * head_dim * sizeof(float);
+  if (cache_dtype == FK_DTYPE_BF16)
+    hipLaunchKernelGGL(attn_head_kernel<true>, dim3(tokens, heads), dim3(256), shm, s, a);
+  else
+    hipLaunchKernelGGL(attn_head_kernel<false>, dim3(tokens, heads), dim3(256), shm, s, a);
+  st = check_launch("attn_head_kernel");
+  if (st) return st;
+  AttnOutArgs o;
+  o.gated = ws.gated;
+  o.wo = o_proj;
+  o.x = hidden;
+  o.x_dt = hidden_dtype;
+  o.T = tokens;
+  o.H = hidden_size;
+  o.K = heads * head_dim;
+  o.update = update;
+  o.hidden_out = hidden_out;
+  const dim3 grid((unsigned)((hidden_size + kAttnOutRows - 1) / kAttnOutRows));
+  if (weight_dtype == FK_DTYPE_BF16) hipLaunchKernelGGL(attn_out_kernel<true>, grid, dim3(256), 0, s, o);
+  else hipLaunchKernelGGL(attn_out_kernel<false>, grid, dim3(256), 0, s, o);
+  return check_launch("attn_out_kernel");
+}
+
+}  // extern "C"

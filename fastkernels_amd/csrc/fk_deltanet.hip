@@ -1469,6 +1469,35 @@ static int launch_step_fused(const StepArgs& sa, int G, hipStream_t s) {
   return check_launch("deltanet_step_kernel");
 }
 
+// RMSNorm(x) * (off + w) applied to up to four row-major weight matrices
+// (rows[i] == 0: unused), f32 outputs [T, rows[i]]: the projection kernel
+// without the fused conv, for the other mixers' projections.
+int launch_norm_projection(const void* x, int x_dt, const void* nw, int nw_dt, const void* const (&w)[4],
+                           const int (&rows)[4], float* const (&out)[4], int weight_dt, int T, int H, float eps,
+                           float off, hipStream_t s) {
+  ProjArgs pa;
+  pa.x = x;
+  pa.nw = nw;
+  pa.nw_dt = nw_dt;
+  for (int i = 0; i < 4; ++i) {
+    pa.w[i] = w[i];
+    pa.rows[i] = rows[i];
+    pa.out[i] = out[i];
+  }
+  pa.T = T;
+  pa.H = H;
+  pa.eps = eps;
+  pa.off = off;
+  pa.conv_state = nullptr;
+  pa.cs_dt = FK_DTYPE_F32;
+  pa.conv_w = nullptr;
+  pa.cw_dt = FK_DTYPE_F32;
+  pa.KS = 0;
+  pa.conv_out = nullptr;
+  pa.next_state = nullptr;
+  return launch_project(pa, weight_dt, x_dt, s);
+}
+
 }  // namespace fk
 
 using namespace fk;

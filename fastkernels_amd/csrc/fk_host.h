@@ -18,6 +18,11 @@ int fail(int status, const char* fmt, ...);
 // bounded wait that ran out.
 constexpr int kWorkspaceErrorWord = 15;
 
+// Normalized multi-matrix projection (fk_deltanet.hip), shared by the mixers.
+int launch_norm_projection(const void* x, int x_dt, const void* nw, int nw_dt, const void* const (&w)[4],
+                           const int (&rows)[4], float* const (&out)[4], int weight_dt, int T, int H, float eps,
+                           float off, hipStream_t s);
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline bool is_float_dtype(int dt) { return dt == FK_DTYPE_F32 || dt == FK_DTYPE_BF16; }

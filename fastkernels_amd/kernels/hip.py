@@ -48,6 +48,9 @@ __all__ = [
     "hip_qwen36_batched_deltanet_conv",
     "hip_qwen36_batched_deltanet_recurrent_output",
     "hip_qwen36_batched_deltanet_moe_layer_decode",
+    "hip_qwen36_batched_attention_project",
+    "hip_qwen36_batched_attention_decode",
+    "hip_qwen36_batched_attention_moe_layer_decode",
     "hip_synthetic_qwen36_moe_decode",
     "hip_synthetic_qwen36_deltanet_decode",
     "hip_synthetic_qwen36_deltanet_moe_decode",
@@ -855,6 +858,161 @@ def hip_qwen36_batched_deltanet_moe_layer_decode(
         top_k=top_k, eps=eps, router_bias=router_bias,
     )
     return layer_hidden, dn_hidden, dn_update, moe_update, next_conv, next_rec, logits, ids, weights
+
+
+# ---------------------------------------------------------------------------
+# Gated full attention
+# ---------------------------------------------------------------------------
+def hip_qwen36_batched_attention_project(
+    hidden, norm_weight, q_proj_weight, k_proj_weight, v_proj_weight,
+    *, eps: float = 1e-6, norm_offset: float = 1.0, block_hidden: int = 2048,
+):
+    """RMSNorm(1+w) + the Q (query/gate pairs), K and V projections, f32
+    outputs (reference qwen36_attention.py:168-211)."""
+
+    _require_lib()
+    if hidden.ndim != 2:
+        raise ValueError("hidden must have shape [tokens, hidden_size]")
+    if norm_weight.ndim != 1 or norm_weight.shape[0] != hidden.shape[1]:
+        raise ValueError("norm_weight must have shape [hidden_size]")
+    weights = (q_proj_weight, k_proj_weight, v_proj_weight)
+    for weight in weights:
+        if weight.ndim != 2 or weight.shape[1] != hidden.shape[1]:
+            raise ValueError("weight must have shape [out_width, hidden_size]")
+    if not hidden.is_cuda or not norm_weight.is_cuda or not all(w.is_cuda for w in weights):
+        raise ValueError("hidden, norm_weight, and weight must be CUDA tensors")
+    tokens, hidden_size = hidden.shape
+    if 1 << max(block_hidden - 1, 0).bit_length() < hidden_size:
+        raise ValueError("block_hidden must be at least hidden_size")
+    if k_proj_weight.shape != v_proj_weight.shape:
+        raise ValueError("k_proj_weight and v_proj_weight must have the same shape")
+    if len({w.dtype for w in weights}) != 1:
+        raise ValueError("projection weights must share a dtype")
+    x, nw = _dense(hidden), _dense(norm_weight)
+    wq, wk, wv = (_dense(w) for w in weights)
+    dev = x.device
+    q = torch.empty((tokens, wq.shape[0]), device=dev, dtype=torch.float32)
+    k = torch.empty((tokens, wk.shape[0]), device=dev, dtype=torch.float32)
+    v = torch.empty((tokens, wv.shape[0]), device=dev, dtype=torch.float32)
+    _lib.call(
+        "fk_attention_project",
+        x.data_ptr(), _fcode(x, "hidden"), nw.data_ptr(), _fcode(nw, "norm_weight"),
+        wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), _fcode(wq, "projection weights"),
+        tokens, hidden_size, wq.shape[0], wk.shape[0], float(eps), float(norm_offset),
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), _stream(dev),
+    )
+    return q, k, v
+
+
+def _attention(hidden, key_cache, value_cache, norm_weight, q_proj_weight, k_proj_weight, v_proj_weight,
+               out_proj_weight, q_norm_weight, k_norm_weight, start_position, attention_heads, kv_heads, head_dim,
+               rope_dim, rope_theta, eps, qk_norm_eps, copy_cache, rope_interleaved, residual):
+    if hidden.ndim != 2:
+        raise ValueError("hidden must have shape [tokens, hidden_size]")
+    if key_cache.ndim != 3 or value_cache.ndim != 3:
+        raise ValueError("key/value caches must have shape [positions, kv_heads, head_dim]")
+    if key_cache.shape != value_cache.shape:
+        raise ValueError("key and value caches must have the same shape")
+    if tuple(key_cache.shape[1:]) != (kv_heads, head_dim):
+        raise ValueError("cache shape does not match kv_heads/head_dim")
+    if not all(t.is_cuda for t in (hidden, key_cache, value_cache)):
+        raise ValueError("hidden and caches must be CUDA tensors")
+    if start_position < 0 or start_position + hidden.shape[0] > key_cache.shape[0]:
+        raise ValueError("decode positions exceed cache length")
+    q_width, kv_width = attention_heads * head_dim, kv_heads * head_dim
+    hidden_size = hidden.shape[1]
+    if out_proj_weight.ndim != 2 or out_proj_weight.shape[1] != q_width:
+        raise ValueError("out_proj_weight must have shape [hidden_size, attention_heads * head_dim]")
+    if q_proj_weight.ndim != 2 or q_proj_weight.shape[0] < 2 * q_width or q_proj_weight.shape[1] != hidden_size:
+        raise ValueError("q_proj_weight must have at least 2 * attention_heads * head_dim rows")
+    if tuple(k_proj_weight.shape) != (kv_width, hidden_size) or tuple(v_proj_weight.shape) != (kv_width, hidden_size):
+        raise ValueError("k/v projection weights must have shape [kv_heads * head_dim, hidden_size]")
+    if out_proj_weight.shape[0] != hidden_size:
+        raise ValueError("out_proj_weight must have hidden_size rows")
+    if key_cache.dtype != value_cache.dtype:
+        raise ValueError("key and value caches must share a dtype")
+    if len({w.dtype for w in (q_proj_weight, k_proj_weight, v_proj_weight, out_proj_weight)}) != 1:
+        raise ValueError("projection weights must share a dtype")
+    if q_norm_weight.dtype != k_norm_weight.dtype or q_norm_weight.numel() != head_dim or k_norm_weight.numel() != head_dim:
+        raise ValueError("q_norm_weight and k_norm_weight must have head_dim elements and share a dtype")
+    x = _dense(hidden)
+    tokens = x.shape[0]
+    kc = key_cache.clone() if copy_cache else key_cache
+    vc = value_cache.clone() if copy_cache else value_cache
+    if not kc.is_contiguous() or not vc.is_contiguous():
+        raise ValueError("key/value caches must be contiguous when updated in place")
+    # the query rows past 2 * q_width (if any) are not used
+    wq = _dense(q_proj_weight[: 2 * q_width])
+    wk, wv, wo = _dense(k_proj_weight), _dense(v_proj_weight), _dense(out_proj_weight)
+    nw, qn, kn = _dense(norm_weight), _dense(q_norm_weight), _dense(k_norm_weight)
+    dev = x.device
+    update = torch.empty((tokens, hidden_size), device=dev, dtype=torch.float32)
+    out = torch.empty_like(update) if residual else None
+    nbytes = _lib.load().fk_attention_workspace_bytes(tokens, attention_heads, kv_heads, head_dim)
+    ws = _workspace("attention", dev, nbytes)
+    _lib.call(
+        "fk_attention_decode",
+        x.data_ptr(), _fcode(x, "hidden"), nw.data_ptr(), _fcode(nw, "norm_weight"),
+        wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), wo.data_ptr(), _fcode(wq, "projection weights"),
+        qn.data_ptr(), kn.data_ptr(), _fcode(qn, "q_norm_weight"),
+        kc.data_ptr(), vc.data_ptr(), _fcode(kc, "key_cache"), kc.shape[0], int(start_position),
+        tokens, hidden_size, attention_heads, kv_heads, head_dim, int(rope_dim), float(rope_theta),
+        1 if rope_interleaved else 0, float(eps), float(qk_norm_eps),
+        update.data_ptr(), _ptr(out), ws.data_ptr(), ws.numel(), _stream(dev),
+    )
+    return update, out, kc, vc
+
+
+def hip_qwen36_batched_attention_decode(
+    hidden, key_cache, value_cache, norm_weight, q_proj_weight, k_proj_weight, v_proj_weight, out_proj_weight,
+    q_norm_weight, k_norm_weight,
+    *, start_position: int = 0, attention_heads: int = 16, kv_heads: int = 2, head_dim: int = 256,
+    rope_dim: int = 64, rope_theta: float = 10000.0, eps: float = 1e-6, qk_norm_eps: float = 1e-6,
+    block_hidden: int = 2048, copy_cache: bool = True, rope_interleaved: bool = True,
+):
+    """Gated full-attention decode of `tokens` rows at positions
+    start_position.. through the KV cache: `(update, key_cache, value_cache)`
+    (reference qwen36_attention.py:448-577).  RoPE pairs are interleaved
+    (2i, 2i+1) like the reference entry point; `rope_interleaved=False`
+    rotates halves (i, i + rope_dim/2) like the reference's torch oracle.
+    With copy_cache=False the caches are updated in place."""
+
+    _require_lib()
+    update, _, kc, vc = _attention(
+        hidden, key_cache, value_cache, norm_weight, q_proj_weight, k_proj_weight, v_proj_weight, out_proj_weight,
+        q_norm_weight, k_norm_weight, start_position, attention_heads, kv_heads, head_dim, rope_dim, rope_theta,
+        eps, qk_norm_eps, copy_cache, rope_interleaved, False,
+    )
+    return update, kc, vc
+
+
+def hip_qwen36_batched_attention_moe_layer_decode(
+    hidden, key_cache, value_cache, attention_norm_weight, q_proj_weight, k_proj_weight, v_proj_weight,
+    out_proj_weight, q_norm_weight, k_norm_weight, moe_norm_weight, router_weight, expert_gate_up_weight,
+    expert_down_weight, shared_gate_up_weight, shared_down_weight, shared_expert_gate_weight=None,
+    *, start_position: int = 0, attention_heads: int = 16, kv_heads: int = 2, head_dim: int = 256,
+    rope_dim: int = 64, rope_theta: float = 10000.0, top_k: int = 8, eps: float = 1e-6,
+    qk_norm_eps: float = 1e-6, copy_cache: bool = True, rope_interleaved: bool = True,
+    router_bias: Any | None = None,
+):
+    """Attention -> MoE layer, returning the reference's 9-tuple
+    `(layer_hidden, attention_hidden, attention_update, moe_update, key_cache,
+    value_cache, router_logits, topk_ids, topk_weights)` (reference
+    qwen36_layer.py:109-201); the residual add is fused into the attention
+    output projection."""
+
+    _require_lib()
+    update, attn_hidden, kc, vc = _attention(
+        hidden, key_cache, value_cache, attention_norm_weight, q_proj_weight, k_proj_weight, v_proj_weight,
+        out_proj_weight, q_norm_weight, k_norm_weight, start_position, attention_heads, kv_heads, head_dim,
+        rope_dim, rope_theta, eps, qk_norm_eps, copy_cache, rope_interleaved, True,
+    )
+    layer_hidden, moe_update, logits, ids, weights = hip_qwen36_batched_moe_layer_decode(
+        attn_hidden, moe_norm_weight, router_weight, expert_gate_up_weight, expert_down_weight,
+        shared_gate_up_weight, shared_down_weight, shared_expert_gate_weight,
+        top_k=top_k, eps=eps, router_bias=router_bias,
+    )
+    return layer_hidden, attn_hidden, update, moe_update, kc, vc, logits, ids, weights
 
 
 # ---------------------------------------------------------------------------

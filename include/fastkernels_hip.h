@@ -162,6 +162,47 @@ int fk_residual_add(const void* hidden, int hidden_dtype, const float* update,
                     int64_t n, float* out, void* stream);
 
 /* ------------------------------------------------------------------------ */
+/* Gated full attention (the mixer of every fourth layer)                    */
+/* ------------------------------------------------------------------------ */
+
+/* xn = RMSNorm(x) * (norm_offset + w); q = xn Wq^T (q_rows: query/gate pairs
+ * per head), k = xn Wk^T, v = xn Wv^T (kv_rows each); f32 outputs.
+ * Replaces triton_qwen36_batched_attention_project (qwen36_attention.py:168-211). */
+int fk_attention_project(const void* hidden, int hidden_dtype,
+                         const void* norm_weight, int norm_dtype,
+                         const void* q_proj, const void* k_proj, const void* v_proj,
+                         int weight_dtype, int tokens, int hidden_size, int q_rows,
+                         int kv_rows, float eps, float norm_offset,
+                         float* q_out, float* k_out, float* v_out, void* stream);
+
+/* Bytes of workspace for fk_attention_decode. */
+size_t fk_attention_workspace_bytes(int tokens, int heads, int kv_heads, int head_dim);
+
+/* Gated attention decode of `tokens` (<= 32) rows at positions
+ * start_position ..: projections, per-head RMSNorm(1 + w) of q and k, RoPE
+ * of the first rope_dim dims (rope_interleaved: pairs (2i, 2i+1); else
+ * halves (i, i + rope_dim/2)), the new k/v rows written into the caches
+ * [max_positions, kv_heads, head_dim] (f32 or bf16) in place, causal
+ * softmax attention (GQA: heads / kv_heads query heads per kv head),
+ * o * sigmoid(gate), update = . Wo^T (f32 [T, hidden]) and, when hidden_out
+ * is not NULL, hidden_out = hidden + update.  head_dim <= 256,
+ * heads * head_dim <= 4096.
+ * Replaces triton_qwen36_batched_attention_decode (qwen36_attention.py:448-577)
+ * and the residual add of triton_qwen36_batched_attention_moe_layer_decode
+ * (qwen36_layer.py:109-201). */
+int fk_attention_decode(const void* hidden, int hidden_dtype,
+                        const void* norm_weight, int norm_dtype,
+                        const void* q_proj, const void* k_proj, const void* v_proj,
+                        const void* o_proj, int weight_dtype,
+                        const void* q_norm_weight, const void* k_norm_weight, int qk_norm_dtype,
+                        void* key_cache, void* value_cache, int cache_dtype,
+                        int max_positions, int start_position, int tokens, int hidden_size,
+                        int heads, int kv_heads, int head_dim, int rope_dim, float rope_theta,
+                        int rope_interleaved, float eps, float qk_eps,
+                        float* update, float* hidden_out,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------ */
 /* Gated DeltaNet decode step                                                */
 /* ------------------------------------------------------------------------ */
 

@@ -28,6 +28,13 @@ Pinning (what checks each function against something other than itself):
                       float64 brute force at Hk=2, Hv=4, D=8
   gated RMSNorm       closed form on a constant vector
   synthetic blocks    float64 brute force at the tiny spec
+  rope                position 0 is the identity; pair norms kept; the two
+                      pairings are one dim permutation apart; complex-number
+                      restatement; dot products depend on the offset only
+  attention           torch scaled_dot_product_attention (library routine)
+                      with expanded kv heads and an offset causal mask; one
+                      position gives the value row; cache rows outside the
+                      step untouched
 No function is left "parity unpinned" at the north-star tolerances; the only
 unpinned behaviours are torch.topk's tie order (replaced here by the
 documented lower-id rule) and cross-version bf16 rounding of the synthetic

@@ -34,6 +34,9 @@ __all__ = [
     "deltanet_recurrent_output",
     "deltanet_update",
     "deltanet_moe_layer",
+    "rope",
+    "attention_update",
+    "attention_moe_layer",
     "synthetic_moe_decode",
     "synthetic_deltanet_decode",
 ]
@@ -420,6 +423,136 @@ def deltanet_moe_layer(
         moe_weights.get("shared_expert_gate_weight"), top_k=top_k, eps=eps, router_bias=router_bias,
     )
     return layer_hidden, dn_hidden, update, moe_out, next_conv, next_state, logits, ids, weights
+
+
+# ---------------------------------------------------------------------------
+# Gated full attention
+# ---------------------------------------------------------------------------
+def rope(values: Any, positions: Any, rope_dim: int, theta: float, interleaved: bool = True) -> Any:
+    """RoPE of the first rope_dim (rounded down to even) dims of values
+    [T, heads, hd] at positions [T], angle p * theta^(-2i/rope_dim).
+
+    interleaved: pairs (2i, 2i+1), as the reference Triton entry point
+    (kernels/triton/qwen36_attention.py:270-296) and its test
+    (tests/test_triton_moe.py:1011-1025); otherwise halves (i, i + rd/2),
+    as the reference torch oracle (reference/qwen36_real.py:263-280).
+    """
+
+    x = values.float()
+    rd = min(rope_dim, x.shape[-1])
+    rd -= rd % 2
+    if rd <= 0:
+        return x.clone()
+    inv_freq = 1.0 / (theta ** (torch.arange(0, rd, 2, dtype=torch.float32) / rd))
+    ang = positions.float()[:, None] * inv_freq[None, :]  # [T, rd/2]
+    cos, sin = torch.cos(ang)[:, None, :], torch.sin(ang)[:, None, :]
+    out = x.clone()
+    if interleaved:
+        a, b = x[..., 0:rd:2], x[..., 1:rd:2]
+        out[..., 0:rd:2] = a * cos - b * sin
+        out[..., 1:rd:2] = a * sin + b * cos
+    else:
+        h = rd // 2
+        a, b = x[..., :h], x[..., h:rd]
+        out[..., :h] = a * cos - b * sin
+        out[..., h:rd] = b * cos + a * sin
+    return out
+
+
+def attention_update(
+    hidden: Any,
+    key_cache: Any,
+    value_cache: Any,
+    norm_weight: Any,
+    q_proj_weight: Any,
+    k_proj_weight: Any,
+    v_proj_weight: Any,
+    out_proj_weight: Any,
+    q_norm_weight: Any,
+    k_norm_weight: Any,
+    *,
+    start_position: int,
+    heads: int,
+    kv_heads: int,
+    head_dim: int,
+    rope_dim: int,
+    rope_theta: float,
+    eps: float = 1e-6,
+    qk_eps: float = 1e-6,
+    interleaved: bool = True,
+) -> tuple[Any, Any, Any]:
+    """Gated attention decode (reference/qwen36_real.py:283-326; projection
+    split of kernels/triton/qwen36_attention.py:507-513): `(update, key_cache',
+    value_cache')`, caches [positions, kv_heads, head_dim] updated at
+    start_position .. start_position + T - 1 (returned as copies)."""
+
+    x = hidden.float()
+    T = x.shape[0]
+    qw = heads * head_dim
+    xn = rms_norm(x, norm_weight, eps)
+    qg = (xn @ q_proj_weight.float()[: 2 * qw].t()).reshape(T, heads, 2 * head_dim)
+    q, gate = qg[..., :head_dim], qg[..., head_dim:]
+    k = (xn @ k_proj_weight.float().t()).reshape(T, kv_heads, head_dim)
+    v = (xn @ v_proj_weight.float().t()).reshape(T, kv_heads, head_dim)
+    q = rms_norm(q, q_norm_weight, qk_eps)
+    k = rms_norm(k, k_norm_weight, qk_eps)
+    pos = torch.arange(start_position, start_position + T)
+    q = rope(q, pos, rope_dim, rope_theta, interleaved)
+    k = rope(k, pos, rope_dim, rope_theta, interleaved)
+    kc = key_cache.clone()
+    vc = value_cache.clone()
+    kc[start_position : start_position + T] = k.to(kc.dtype)
+    vc[start_position : start_position + T] = v.to(vc.dtype)
+    keys, vals = kc.float(), vc.float()
+    group = heads // kv_heads
+    attended = torch.empty(T, heads, head_dim)
+    for t in range(T):
+        p = start_position + t
+        for h in range(heads):
+            j = h // group
+            scores = (keys[: p + 1, j] * q[t, h]).sum(-1) * head_dim**-0.5
+            attended[t, h] = (vals[: p + 1, j] * torch.softmax(scores, dim=0)[:, None]).sum(0)
+    update = (attended.reshape(T, qw) * torch.sigmoid(gate.reshape(T, qw))) @ out_proj_weight.float().t()
+    return update, kc, vc
+
+
+def attention_moe_layer(
+    hidden: Any,
+    key_cache: Any,
+    value_cache: Any,
+    attn_weights: dict[str, Any],
+    moe_weights: dict[str, Any],
+    *,
+    start_position: int,
+    heads: int,
+    kv_heads: int,
+    head_dim: int,
+    rope_dim: int,
+    rope_theta: float,
+    top_k: int = 8,
+    eps: float = 1e-6,
+    interleaved: bool = True,
+) -> tuple[Any, ...]:
+    """Attention -> MoE layer in the 9-tuple order of the reference wrapper
+    (kernels/triton/qwen36_layer.py:185-201); maths of
+    reference/qwen36_real.py:378-399.  `attn_weights` keys: input_norm_weight,
+    q_proj_weight, k_proj_weight, v_proj_weight, o_proj_weight, q_norm_weight,
+    k_norm_weight."""
+
+    a = attn_weights
+    update, kc, vc = attention_update(
+        hidden, key_cache, value_cache, a["input_norm_weight"], a["q_proj_weight"], a["k_proj_weight"],
+        a["v_proj_weight"], a["o_proj_weight"], a["q_norm_weight"], a["k_norm_weight"],
+        start_position=start_position, heads=heads, kv_heads=kv_heads, head_dim=head_dim, rope_dim=rope_dim,
+        rope_theta=rope_theta, eps=eps, interleaved=interleaved,
+    )
+    attn_hidden = hidden.float() + update
+    layer_hidden, moe_out, logits, ids, weights = moe_layer(
+        attn_hidden, moe_weights["norm_weight"], moe_weights["router_weight"], moe_weights["expert_gate_up_weight"],
+        moe_weights["expert_down_weight"], moe_weights["shared_gate_up_weight"], moe_weights["shared_down_weight"],
+        moe_weights.get("shared_expert_gate_weight"), top_k=top_k, eps=eps,
+    )
+    return layer_hidden, attn_hidden, update, moe_out, kc, vc, logits, ids, weights
 
 
 # ---------------------------------------------------------------------------

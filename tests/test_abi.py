@@ -148,6 +148,21 @@ def test_deltanet_and_synthetic_validation():
         )
 
 
+def test_attention_validation():
+    x, kc = torch.zeros(2, 16), torch.zeros(4, 2, 4)
+    args = (torch.zeros(16), torch.zeros(32, 16), torch.zeros(8, 16), torch.zeros(8, 16), torch.zeros(16, 16),
+            torch.zeros(4), torch.zeros(4))
+    kw = dict(attention_heads=4, kv_heads=2, head_dim=4, rope_dim=4)
+    with pytest.raises(ValueError, match="key/value caches must have shape"):
+        hip.hip_qwen36_batched_attention_decode(x, torch.zeros(4, 8), kc, *args, **kw)
+    with pytest.raises(ValueError, match="cache shape does not match"):
+        hip.hip_qwen36_batched_attention_decode(x, torch.zeros(4, 2, 8), torch.zeros(4, 2, 8), *args, **kw)
+    with pytest.raises(ValueError, match="CUDA tensors"):
+        hip.hip_qwen36_batched_attention_decode(x, kc, kc.clone(), *args, **kw)
+    with pytest.raises(ValueError, match="weight must have shape"):
+        hip.hip_qwen36_batched_attention_project(x, torch.zeros(16), torch.zeros(32, 8), args[2], args[3])
+
+
 def test_triton_aliases_cover_reference_hot_path_names():
     expected = {
         "triton_expert_histogram", "triton_fused_swiglu", "triton_qwen36_batched_moe_decode",
@@ -158,7 +173,8 @@ def test_triton_aliases_cover_reference_hot_path_names():
         "triton_qwen36_moe_decode", "triton_qwen36_moe_router_decode", "triton_qwen36_routed_experts_decode",
         "triton_qwen36_routed_shared_experts_decode", "triton_qwen36_single_expert_mlp_decode",
         "triton_synthetic_qwen36_deltanet_decode", "triton_synthetic_qwen36_deltanet_moe_decode",
-        "triton_synthetic_qwen36_moe_decode",
+        "triton_synthetic_qwen36_moe_decode", "triton_qwen36_batched_attention_project",
+        "triton_qwen36_batched_attention_decode", "triton_qwen36_batched_attention_moe_layer_decode",
     }
     assert expected == set(hip.TRITON_ALIASES)
     for name in expected:
