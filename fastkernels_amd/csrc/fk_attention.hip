@@ -41,6 +41,7 @@ struct AttnArgs {
   int qn_dt, kn_dt;
   void* kc;             // [max_pos, kv_heads, hd]
   void* vc;
+  const int* start_dev; // when set: the start position, read at run time (graph replays)
   int start, max_pos;
   int T, heads, kvh, hd, rope_dim;
   float theta_log2, eps;
@@ -143,8 +144,14 @@ __global__ __launch_bounds__(256) void attn_head_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hd = a.hd, G = a.heads / a.kvh, j = h / G;
   const int qw = a.heads * hd, kvw = a.kvh * hd;
-  const int pos = a.start + t;
   const bool in = tid < hd;
+  const int start = a.start_dev ? *a.start_dev : a.start;
+  if (start < 0 || start + a.T > a.max_pos) {
+    // a run-time position past the cache: no cache access, NaN outputs
+    if (in) a.gated[(size_t)t * qw + (size_t)h * hd + tid] = __builtin_nanf("");
+    return;
+  }
+  const int pos = start + t;
 
   // query: norm, RoPE, 1/sqrt(hd)
   const float qraw = in ? a.qg[(size_t)t * 2 * qw + (size_t)h * 2 * hd + tid] : 0.f;
@@ -154,11 +161,11 @@ __global__ __launch_bounds__(256) void attn_head_kernel(AttnArgs a) {
   // keys of the new positions start .. pos, recomputed here from k
   for (int u = 0; u <= t; ++u) {
     const float kraw = in ? a.k[(size_t)u * kvw + (size_t)j * hd + tid] : 0.f;
-    const float kr = norm_rope(kraw, a.kn_w, a.kn_dt, a, a.start + u, s_tmp, s_red);
+    const float kr = norm_rope(kraw, a.kn_w, a.kn_dt, a, start + u, s_tmp, s_red);
     if (in) s_knew[u * hd + tid] = kr;
   }
   // the first query head of kv head j writes token t's cache row
-  if (h % G == 0 && in && pos < a.max_pos) {
+  if (h % G == 0 && in) {
     const size_t c = ((size_t)pos * a.kvh + j) * hd + tid;
     store1<CBF>(a.kc, c, s_knew[t * hd + tid]);
     store1<CBF>(a.vc, c, a.v[(size_t)t * kvw + (size_t)j * hd + tid]);
@@ -179,13 +186,13 @@ __global__ __launch_bounds__(256) void attn_head_kernel(AttnArgs a) {
       const int p = min(p0 + 4 * b, pos);
       if (!lin) {
         kk[b] = vv[b] = make_float4(0.f, 0.f, 0.f, 0.f);
-      } else if (p < a.start) {
+      } else if (p < start) {
         const size_t c = ((size_t)p * a.kvh + j) * hd + d0;
         kk[b] = load4<CBF>(a.kc, c);
         vv[b] = load4<CBF>(a.vc, c);
       } else {
-        kk[b] = *reinterpret_cast<const float4*>(s_knew + (p - a.start) * hd + d0);
-        vv[b] = *reinterpret_cast<const float4*>(a.v + (size_t)(p - a.start) * kvw + (size_t)j * hd + d0);
+        kk[b] = *reinterpret_cast<const float4*>(s_knew + (p - start) * hd + d0);
+        vv[b] = *reinterpret_cast<const float4*>(a.v + (size_t)(p - start) * kvw + (size_t)j * hd + d0);
       }
     }
 #pragma unroll
@@ -275,6 +282,10 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
   }
 }
 
+// Advances a device-held decode position (one thread), so a captured step
+// can move its own position forward between graph replays.
+__global__ void position_advance_kernel(int32_t* position, int delta) { *position += delta; }
+
 static int check_attn_shape(int tokens, int hidden_size, int heads, int kv_heads, int head_dim, int rope_dim) {
   if (tokens < 1 || tokens > kAttnMaxTokens) return fail(FK_ERR_UNSUPPORTED, "tokens must be in [1, %d]", kAttnMaxTokens);
   if (hidden_size < 8 || hidden_size % 8 || hidden_size > 4096)
@@ -325,12 +336,12 @@ int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_w
                         const void* q_proj, const void* k_proj, const void* v_proj, const void* o_proj,
                         int weight_dtype, const void* q_norm_weight, const void* k_norm_weight, int qk_norm_dtype,
                         void* key_cache, void* value_cache, int cache_dtype, int max_positions, int start_position,
-                        int tokens, int hidden_size, int heads, int kv_heads, int head_dim, int rope_dim,
+                        const int32_t* start_position_device, int tokens, int hidden_size, int heads, int kv_heads, int head_dim, int rope_dim,
                         float rope_theta, int rope_interleaved, float eps, float qk_eps, float* update,
                         float* hidden_out, void* workspace, size_t workspace_bytes, void* stream) {
   int st = check_attn_shape(tokens, hidden_size, heads, kv_heads, head_dim, rope_dim);
   if (st) return st;
-  if (start_position < 0 || start_position + tokens > max_positions)
+  if (!start_position_device && (start_position < 0 || start_position + tokens > max_positions))
     return fail(FK_ERR_INVALID, "decode positions [%d, %d) exceed the cache length %d", start_position,
                 start_position + tokens, max_positions);
   if (!is_float_dtype(cache_dtype) || !is_float_dtype(qk_norm_dtype)) return fail(FK_ERR_DTYPE, "caches and q/k norms must be f32 or bf16");
@@ -359,6 +370,7 @@ int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_w
   a.kc = key_cache;
   a.vc = value_cache;
   a.start = start_position;
+  a.start_dev = start_position_device;
   a.max_pos = max_positions;
   a.T = tokens;
   a.heads = heads;
@@ -391,6 +403,12 @@ int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_w
   if (weight_dtype == FK_DTYPE_BF16) hipLaunchKernelGGL(attn_out_kernel<true>, grid, dim3(256), 0, s, o);
   else hipLaunchKernelGGL(attn_out_kernel<false>, grid, dim3(256), 0, s, o);
   return check_launch("attn_out_kernel");
+}
+
+int fk_position_advance(int32_t* position, int delta, void* stream) {
+  if (!position) return fail(FK_ERR_INVALID, "position must be non-NULL");
+  hipLaunchKernelGGL(position_advance_kernel, dim3(1), dim3(1), 0, as_stream(stream), position, delta);
+  return check_launch("position_advance_kernel");
 }
 
 }  // extern "C"

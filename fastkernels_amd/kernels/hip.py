@@ -955,7 +955,7 @@ def _attention(hidden, key_cache, value_cache, norm_weight, q_proj_weight, k_pro
         x.data_ptr(), _fcode(x, "hidden"), nw.data_ptr(), _fcode(nw, "norm_weight"),
         wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), wo.data_ptr(), _fcode(wq, "projection weights"),
         qn.data_ptr(), kn.data_ptr(), _fcode(qn, "q_norm_weight"),
-        kc.data_ptr(), vc.data_ptr(), _fcode(kc, "key_cache"), kc.shape[0], int(start_position),
+        kc.data_ptr(), vc.data_ptr(), _fcode(kc, "key_cache"), kc.shape[0], int(start_position), None,
         tokens, hidden_size, attention_heads, kv_heads, head_dim, int(rope_dim), float(rope_theta),
         1 if rope_interleaved else 0, float(eps), float(qk_norm_eps),
         update.data_ptr(), _ptr(out), ws.data_ptr(), ws.numel(), _stream(dev),

@@ -10,6 +10,10 @@ graph (torch.cuda.CUDAGraph), which is how bench.py times them.
   DeltaNetStepPlan  projections + conv -> recurrent/gated-norm -> out-proj
                     (+ residual) through fk_deltanet_step, writing the next
                     conv / recurrent states.
+  AttentionStepPlan gated full attention (+ residual) through
+                    fk_attention_decode at a device-held position that the
+                    step advances itself (fk_position_advance), with the KV
+                    caches it owns updated in place.
 """
 
 from __future__ import annotations
@@ -195,3 +199,76 @@ class DeltaNetStepPlan:
 
     def check_device(self, stream: torch.cuda.Stream | None = None) -> None:
         _check_device(self.workspace, self.device, stream)
+
+
+class AttentionStepPlan:
+    """One gated full-attention decode step of `tokens` rows + residual.
+
+    The plan owns the KV caches ([max_positions, kv_heads, head_dim]) and a
+    device int32 `position`; every run decodes at that position and then
+    advances it by `tokens`, so a step captured once in a HIP graph decodes
+    successive positions on replay.  `set_position()` rewinds it.
+    """
+
+    def __init__(
+        self,
+        weights: Any,
+        tokens: int,
+        spec: Qwen36A3BSpec | None = None,
+        *,
+        max_positions: int,
+        cache_dtype: torch.dtype = torch.float32,
+        start_position: int = 0,
+        eps: float = 1e-6,
+        rope_interleaved: bool = True,
+        hidden: torch.Tensor | None = None,
+        hidden_dtype: torch.dtype = torch.bfloat16,
+    ) -> None:
+        self.lib = _lib.load()
+        if hasattr(weights, "as_dict"):
+            weights = weights.as_dict()
+        spec = spec or qwen36_35b_a3b_spec()
+        self.spec = spec
+        w = {k: _dense(v) for k, v in weights.items() if v is not None}
+        self.w = w
+        dev = w["q_proj_weight"].device
+        self.device = dev
+        self.tokens = tokens
+        self.eps = float(eps)
+        self.interleaved = 1 if rope_interleaved else 0
+        H, heads, kvh, hd = spec.hidden_size, spec.attention_heads, spec.attention_kv_heads, spec.attention_head_dim
+        qw = heads * hd
+        if w["q_proj_weight"].shape[0] < 2 * qw:
+            raise ValueError("q_proj_weight must have at least 2 * attention_heads * head_dim rows")
+        self._wq = w["q_proj_weight"][: 2 * qw]
+        self.max_positions = max_positions
+        self.hidden = hidden if hidden is not None else torch.zeros((tokens, H), dtype=hidden_dtype, device=dev)
+        self.key_cache = torch.zeros((max_positions, kvh, hd), dtype=cache_dtype, device=dev)
+        self.value_cache = torch.zeros_like(self.key_cache)
+        self.position = torch.tensor([start_position], dtype=torch.int32, device=dev)
+        self.update = torch.empty((tokens, H), dtype=torch.float32, device=dev)
+        self.hidden_out = torch.empty_like(self.update)
+        nbytes = self.lib.fk_attention_workspace_bytes(tokens, heads, kvh, hd)
+        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        self._codes = (_fcode(self.hidden, "hidden"), _fcode(w["input_norm_weight"], "input_norm_weight"),
+                       _fcode(self._wq, "q_proj_weight"), _fcode(w["q_norm_weight"], "q_norm_weight"),
+                       _fcode(self.key_cache, "key_cache"))
+
+    def set_position(self, position: int) -> None:
+        self.position.fill_(int(position))
+
+    def run(self, stream: torch.cuda.Stream | None = None) -> None:
+        w, sp = self.w, self.spec
+        s = _stream_handle(stream, self.device)
+        hc, nc, wc, qc, cc = self._codes
+        _lib.call(
+            "fk_attention_decode",
+            self.hidden.data_ptr(), hc, w["input_norm_weight"].data_ptr(), nc,
+            self._wq.data_ptr(), w["k_proj_weight"].data_ptr(), w["v_proj_weight"].data_ptr(),
+            w["o_proj_weight"].data_ptr(), wc, w["q_norm_weight"].data_ptr(), w["k_norm_weight"].data_ptr(), qc,
+            self.key_cache.data_ptr(), self.value_cache.data_ptr(), cc, self.max_positions, 0,
+            self.position.data_ptr(), self.tokens, sp.hidden_size, sp.attention_heads, sp.attention_kv_heads,
+            sp.attention_head_dim, sp.rope_dim, float(sp.rope_theta), self.interleaved, self.eps, self.eps,
+            self.update.data_ptr(), self.hidden_out.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(), s,
+        )
+        _lib.call("fk_position_advance", self.position.data_ptr(), self.tokens, s)

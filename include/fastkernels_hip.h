@@ -186,7 +186,10 @@ size_t fk_attention_workspace_bytes(int tokens, int heads, int kv_heads, int hea
  * softmax attention (GQA: heads / kv_heads query heads per kv head),
  * o * sigmoid(gate), update = . Wo^T (f32 [T, hidden]) and, when hidden_out
  * is not NULL, hidden_out = hidden + update.  head_dim <= 256,
- * heads * head_dim <= 4096.
+ * heads * head_dim <= 4096.  start_position_device (nullable): a device
+ * int32 read at run time in place of start_position, so one captured HIP
+ * graph can decode successive positions; a value with start + tokens past
+ * max_positions gives NaN updates and leaves the caches untouched.
  * Replaces triton_qwen36_batched_attention_decode (qwen36_attention.py:448-577)
  * and the residual add of triton_qwen36_batched_attention_moe_layer_decode
  * (qwen36_layer.py:109-201). */
@@ -196,11 +199,17 @@ int fk_attention_decode(const void* hidden, int hidden_dtype,
                         const void* o_proj, int weight_dtype,
                         const void* q_norm_weight, const void* k_norm_weight, int qk_norm_dtype,
                         void* key_cache, void* value_cache, int cache_dtype,
-                        int max_positions, int start_position, int tokens, int hidden_size,
+                        int max_positions, int start_position,
+                        const int32_t* start_position_device, int tokens, int hidden_size,
                         int heads, int kv_heads, int head_dim, int rope_dim, float rope_theta,
                         int rope_interleaved, float eps, float qk_eps,
                         float* update, float* hidden_out,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* *position += delta on the device (one thread): advances the decode
+ * position of a captured step.  No counterpart in the reference, whose
+ * decode loop passes positions from the host. */
+int fk_position_advance(int32_t* position, int delta, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Gated DeltaNet decode step                                                */
