@@ -49,7 +49,8 @@ def parse_args() -> argparse.Namespace:
     p.add_argument("--zipf", action="store_true", help="with --only moe: add the config-2 Zipf router bias")
     p.add_argument("--no-stack", action="store_true", help="skip the 40-layer resident stack (config 4)")
     p.add_argument("--stack-layers", type=int, default=40, help="layers of the config-4 stack")
-    p.add_argument("--only", choices=["moe", "deltanet", "copy", "stack"], default=None,
+    p.add_argument("--context", type=int, default=1024, help="with --only attention: cached positions before the step")
+    p.add_argument("--only", choices=["moe", "deltanet", "copy", "stack", "attention", "model"], default=None,
                    help="run a single timing loop (for profilers) and print its line; "
                         "'copy' runs 16 device-to-device copies of 1 GiB (PMC byte-counter calibration)")
     return p.parse_args()
@@ -72,7 +73,7 @@ def main() -> int:
     import torch
 
     from fastkernels_amd import workloads as wl
-    from fastkernels_amd.plan import DeltaNetStepPlan, MoeLayerPlan
+    from fastkernels_amd.plan import AttentionStepPlan, DeltaNetStepPlan, MoeLayerPlan
     from fastkernels_amd.spec import qwen36_35b_a3b_spec
 
     if not torch.cuda.is_available():
@@ -121,7 +122,7 @@ def main() -> int:
 
     R = max(1, args.weight_sets)
     log(f"generating {R} MoE weight sets on {torch.cuda.get_device_name(0)}")
-    sets = [] if args.only in ("deltanet", "stack") else [moe_set(r) for r in range(R)]
+    sets = [] if args.only in ("deltanet", "stack", "attention", "model") else [moe_set(r) for r in range(R)]
     torch.cuda.synchronize()
 
     def timed_graph(fns, steps: int, warmup: int) -> float:
@@ -212,12 +213,87 @@ def main() -> int:
             "hbm_frac": round(nbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
         }
 
-    def stack_result(tokens: int, layers: int, steps: int) -> dict:
+    def attention_result(tokens: int, context: int, nsets: int = R) -> dict:
+        """Gated attention step of `tokens` rows after `context` cached
+        positions (f32 caches), weights rotated over `nsets` sets."""
+
+        aplans = []
+        steps = args.steps
+        for r in range(nsets):
+            w = wl.make_attention_weights(spec, seed=3000 + r, device=dev)
+            # every run advances the position: room for warmup + capture-time + timed steps
+            ap = AttentionStepPlan(w, tokens, spec, max_positions=context + (args.warmup + 2 * steps + 8) * tokens,
+                                   start_position=context)
+            ap.hidden.copy_(wl.make_hidden(tokens, H, seed=70 + r).to(dev))
+            aplans.append(ap)
+        ms = timed_graph([p.run for p in aplans], steps, args.warmup)
+        nbytes = wl.attention_step_bytes(tokens, context, spec)
+        return {
+            "tokens": tokens,
+            "context": context,
+            "us_per_step": round(ms * 1e3, 3),
+            "algorithmic_bytes_per_step": nbytes,
+            "achieved_tbs": round(nbytes / (ms * 1e-3) / 1e12, 3),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+        }
+
+    def model_result(tokens: int, lsets: list, steps: int = 16) -> dict:
+        """Full resident decode step: the spec's 40 layers (DeltaNet or gated
+        attention mixer, then the MoE block), captured once per parity and
+        replayed (fastkernels_amd.runner)."""
+
+        from fastkernels_amd.runner import ResidentDecodeRunner
+
+        layers = []
+        for l, kind in enumerate(spec.layer_kinds()):
+            if kind == "deltanet_moe":
+                mixer = wl.make_deltanet_weights(spec, seed=4000 + l, device=dev)
+            else:
+                mixer = wl.make_attention_weights(spec, seed=4000 + l, device=dev)
+            layers.append((kind, mixer, lsets[l % len(lsets)]))
+        runner = ResidentDecodeRunner(layers, tokens, spec, max_positions=(steps + 8) * tokens)
+        runner.hidden.copy_(wl.make_hidden(tokens, H, seed=8).to(dev))
+        runner.capture(stream)
+        with torch.cuda.stream(stream):
+            runner.replay()
+            runner.replay()
+            stream.synchronize()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record(stream)
+            for _ in range(steps):
+                runner.replay()
+            end.record(stream)
+        end.synchronize()
+        ms = start.elapsed_time(end) / steps
+        runner.check_device(stream)
+        u = distinct(runner.moes)
+        counts = spec.layer_counts()
+        nbytes = (sum(wl.moe_layer_bytes(tokens, x, spec, in_bytes=4) for x in u)
+                  + counts["deltanet_moe"] * wl.deltanet_step_bytes(tokens, spec)
+                  + counts["attention_moe"] * wl.attention_step_bytes(tokens, 4 * tokens, spec))
+        res = {
+            "tokens": tokens,
+            "layers": len(layers),
+            "layer_counts": counts,
+            "us_per_decode_step": round(ms * 1e3, 3),
+            "tokens_per_s": round(tokens / (ms * 1e-3), 1),
+            "algorithmic_bytes_per_step": int(nbytes),
+            "achieved_tbs": round(nbytes / (ms * 1e-3) / 1e12, 3),
+            "hbm_frac": round(nbytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+            "note": "graph replays of one decode step; attention context grows from 0 (bytes counted at 4 tokens)",
+        }
+        del runner, layers
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+        return res
+
+    def stack_result(tokens: int, layers: int, steps: int, lsets: list | None = None) -> dict:
         """Config 4: `layers` independent resident MoE layers (weights seeded
         base + layer), each step running them in order with the residual
         carried across layers: layer l reads layer l-1's fp32 layer output."""
 
-        lsets = [moe_set(100 + l) for l in range(layers)]
+        lsets = lsets if lsets is not None else [moe_set(100 + l) for l in range(layers)]
         lplans = []
         for l in range(layers):
             prev = lplans[-1].layer_out if lplans else None
@@ -250,13 +326,19 @@ def main() -> int:
             "achieved_tbs": round(nbytes / (us_layer * 1e-6) / 1e12, 3),
             "hbm_frac": round(nbytes / (us_layer * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
         }
-        del lplans, lsets
+        del lplans
         torch.cuda.synchronize()
-        torch.cuda.empty_cache()
         return res
 
     if args.only == "stack":
         print(json.dumps(stack_result(args.tokens, args.stack_layers, min(args.steps, 32))))
+        return 0
+    if args.only == "attention":
+        print(json.dumps(attention_result(args.tokens, args.context)))
+        return 0
+    if args.only == "model":
+        msets = [moe_set(100 + l) for l in range(spec.num_layers)]
+        print(json.dumps(model_result(args.tokens, msets)))
         return 0
     if args.only == "moe":
         res = moe_result(args.tokens, bias=wl.zipf_router_bias(E, seed=0).to(dev) if args.zipf else None)
@@ -293,10 +375,18 @@ def main() -> int:
         log("timing Gated DeltaNet step T=1 and T=8")
         for tokens in (1, 8):
             sub[f"deltanet_t{tokens}"] = deltanet_result(tokens)
+        log("timing the gated attention step T=1 after 1024 cached positions")
+        sub["attention_t1_ctx1024"] = attention_result(1, 1024)
     if not args.no_extra and not args.no_stack:
+        lsets = [moe_set(100 + l) for l in range(max(args.stack_layers, spec.num_layers))]
         for tokens in (1, 8):
             log(f"timing the {args.stack_layers}-layer resident stack, T={tokens} (config 4)")
-            sub[f"moe_stack{args.stack_layers}_t{tokens}"] = stack_result(tokens, args.stack_layers, 32)
+            sub[f"moe_stack{args.stack_layers}_t{tokens}"] = stack_result(tokens, args.stack_layers, 32, lsets)
+        log(f"timing the full {spec.num_layers}-layer decode step (DeltaNet/attention + MoE), T=1")
+        sub["model_decode_t1"] = model_result(1, lsets)
+        del lsets
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
 
     # -- CPU baseline (oracle on the host cores, bounded sample) ----------------
     cpu = None

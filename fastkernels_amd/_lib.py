@@ -61,7 +61,6 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [P, I, P, I, P, P, P, P, I, P, P, I, P, P, I, I, I, P, I, I, I, I, I, I, c_float, I, c_float, c_float,
          P, P, P, c_size_t, P],
     ),
-    "fk_position_advance": (c_int, [P, I, P]),
     "fk_deltanet_project": (
         c_int,
         [P, I, P, I, P, P, P, P, I, I, I, I, I, I, c_float, c_float, P, P, P, P, P],

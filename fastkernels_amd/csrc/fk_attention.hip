@@ -16,13 +16,16 @@
 // Kernels (three launches per step):
 //   projection        the shared normalized projection kernel (fk_deltanet.hip)
 //                     over [Wq | Wk | Wv] (9216 rows at the model shape)
-//   attn_head_kernel  grid (T, heads), 256 threads: head norms and RoPE in
-//                     LDS, the token's new keys recomputed from k (no
-//                     dependence on another workgroup's cache write), online
-//                     softmax over positions split across the 4 wavefronts
-//                     (4 positions in flight per wavefront), gate applied
+//   attn_split_kernel grid (position chunks, kv heads, T), 256 threads: the
+//                     G query heads of one kv head over one chunk of
+//                     positions (each cached row read once per chunk), head
+//                     norms and RoPE in LDS, the step's new keys recomputed
+//                     from k (no dependence on another workgroup's cache
+//                     write), online softmax; the last chunk to finish merges
+//                     the chunks and applies the gate
 //   attn_out_kernel   grid ceil(H/8): 8 rows of Wo per workgroup (2 per
-//                     wavefront, loaded once) against every token; residual
+//                     wavefront, loaded once) against every token; residual;
+//                     advances a device-held position
 #include "fk_common.h"
 #include "fk_host.h"
 
@@ -47,13 +50,20 @@ struct AttnArgs {
   float theta_log2, eps;
   int interleaved;
   float* gated;         // [T, heads * hd]  o * sigmoid(gate)
+  float* part;          // [T, heads, max_chunks, hd + 2] per-chunk (max, sum, weighted values)
+  uint32_t* tickets;    // [T, kv_heads] chunk arrivals (self-resetting)
+  int chunk, max_chunks;
 };
 
+constexpr int kAttnMaxChunks = 64;  // position chunks per (token, kv head): the merge reads at most this many
+
 struct AttnWs {
+  uint32_t* tickets;
   float* qg;
   float* k;
   float* v;
   float* gated;
+  float* part;
 };
 
 static size_t attn_ws_layout(int T, int heads, int kvh, int hd, char* base, AttnWs* ws) {
@@ -63,10 +73,12 @@ static size_t attn_ws_layout(int T, int heads, int kvh, int hd, char* base, Attn
     off = align_up(off + bytes, 256);
     return base ? reinterpret_cast<float*>(base + at) : nullptr;
   };
+  ws->tickets = reinterpret_cast<uint32_t*>(take((size_t)T * kvh * 4));
   ws->qg = take((size_t)T * heads * 2 * hd * 4);
   ws->k = take((size_t)T * kvh * hd * 4);
   ws->v = take((size_t)T * kvh * hd * 4);
   ws->gated = take((size_t)T * heads * hd * 4);
+  ws->part = take((size_t)T * heads * kAttnMaxChunks * (hd + 2) * 4);
   return off;
 }
 
@@ -131,65 +143,129 @@ __device__ __forceinline__ float norm_rope(float x, const void* w, int w_dt, con
   return y;
 }
 
+// Workgroup (chunk c, kv head j, token t): positions c*C .. c*C + C - 1 (of
+// 0 .. p, p = start + t) for the G <= 8 query heads of kv head j, so each
+// cached row is read once per chunk.  Wavefront w takes positions c*C + w,
+// + 4, .., eight in flight; per position the G dot products are summed over
+// the lanes at once (rows8_sum) and each head keeps an online softmax (max,
+// sum, 4 dims of the weighted value sum per lane).  The chunk's per-head
+// partials go to the workspace; the workgroup that arrives last for (t, j)
+// (device-scope ticket, release/acquire) merges the chunks, applies the gate
+// and resets the ticket.
 template <bool CBF>
-__global__ __launch_bounds__(256) void attn_head_kernel(AttnArgs a) {
-  __shared__ __align__(16) float s_q[kAttnMaxHeadDim];
-  extern __shared__ float4 s_knew_v[];  // [T, hd] new keys
-  float* s_knew = reinterpret_cast<float*>(s_knew_v);
+__global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
+  constexpr int MAXG = 8, NB = 8;
+  extern __shared__ float4 s_dyn[];  // [G][hd] scaled queries, then [T][hd] new keys
   __shared__ float s_tmp[kAttnMaxHeadDim];
   __shared__ float s_red[4];
-  __shared__ float s_m[4], s_l[4];
+  __shared__ float s_m[4][MAXG], s_l[4][MAXG];
   __shared__ __align__(16) float s_acc[4][kAttnMaxHeadDim];
-  const int t = blockIdx.x, h = blockIdx.y;
+  __shared__ int s_last;
+  __shared__ float s_ss[4][MAXG];
+  __shared__ float s_cm2[MAXG][kAttnMaxChunks], s_cl2[MAXG][kAttnMaxChunks], s_L[MAXG];
+  const int c = blockIdx.x, j = blockIdx.y, t = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hd = a.hd, G = a.heads / a.kvh, j = h / G;
+  const int hd = a.hd, G = a.heads / a.kvh;
   const int qw = a.heads * hd, kvw = a.kvh * hd;
   const bool in = tid < hd;
+  float* s_q = reinterpret_cast<float*>(s_dyn);
+  float* s_knew = s_q + MAXG * hd;
   const int start = a.start_dev ? *a.start_dev : a.start;
   if (start < 0 || start + a.T > a.max_pos) {
     // a run-time position past the cache: no cache access, NaN outputs
-    if (in) a.gated[(size_t)t * qw + (size_t)h * hd + tid] = __builtin_nanf("");
+    if (c == 0 && in)
+      for (int g = 0; g < G; ++g) a.gated[(size_t)t * qw + (size_t)(j * G + g) * hd + tid] = __builtin_nanf("");
     return;
   }
-  const int pos = start + t;
+  const int pos = start + t, C = a.chunk;
+  const int nc = (pos + C) / C;  // chunks covering 0 .. pos
+  if (c >= nc) return;
+  const int p_lo = c * C, p_hi = min(p_lo + C, pos + 1);
 
-  // query: norm, RoPE, 1/sqrt(hd)
-  const float qraw = in ? a.qg[(size_t)t * 2 * qw + (size_t)h * 2 * hd + tid] : 0.f;
-  const float gate = in ? a.qg[(size_t)t * 2 * qw + (size_t)h * 2 * hd + hd + tid] : 0.f;
-  const float q = norm_rope(qraw, a.qn_w, a.qn_dt, a, pos, s_tmp, s_red);
-  if (in) s_q[tid] = q * rsqrtf((float)hd);
-  // keys of the new positions start .. pos, recomputed here from k
-  for (int u = 0; u <= t; ++u) {
-    const float kraw = in ? a.k[(size_t)u * kvw + (size_t)j * hd + tid] : 0.f;
-    const float kr = norm_rope(kraw, a.kn_w, a.kn_dt, a, start + u, s_tmp, s_red);
+  // queries of the G heads at once (thread d: dim d of every head): norms
+  // from one transposed lane reduction, RoPE at pos, 1/sqrt(hd)
+  {
+    float xq[MAXG], sq[MAXG];
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g) {
+      xq[g] = in && g < G ? a.qg[(size_t)t * 2 * qw + (size_t)(j * G + g) * 2 * hd + tid] : 0.f;
+      sq[g] = xq[g] * xq[g];
+    }
+    const float r = rows8_sum(sq);
+    if ((lane & 7) == 0) s_ss[wave][lane >> 3] = r;
+    __syncthreads();
+    const float wq = in ? 1.f + load_scalar(a.qn_w, a.qn_dt, tid) : 0.f;
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g) {
+      const float tot = (s_ss[0][g] + s_ss[1][g]) + (s_ss[2][g] + s_ss[3][g]);
+      xq[g] = xq[g] * rsqrtf(tot / (float)hd + a.eps) * wq;
+      if (in && g < G) s_q[g * hd + tid] = xq[g];
+    }
+    __syncthreads();
+    const int rd = a.rope_dim;
+    if (tid < rd) {
+      int i, partner;
+      float sign;
+      if (a.interleaved) {
+        i = tid >> 1;
+        partner = tid ^ 1;
+        sign = (tid & 1) ? 1.f : -1.f;
+      } else {
+        const int hh = rd >> 1;
+        i = tid < hh ? tid : tid - hh;
+        partner = tid < hh ? tid + hh : tid - hh;
+        sign = tid < hh ? -1.f : 1.f;
+      }
+      const float inv_freq = exp2f(-(float)(2 * i) / (float)rd * a.theta_log2);
+      float sn, cs;
+      sincosf((float)pos * inv_freq, &sn, &cs);
+#pragma unroll
+      for (int g = 0; g < MAXG; ++g)
+        if (g < G) xq[g] = xq[g] * cs + sign * s_q[g * hd + partner] * sn;
+    }
+    __syncthreads();
+    const float scale = rsqrtf((float)hd);
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g)
+      if (in && g < G) s_q[g * hd + tid] = xq[g] * scale;
+  }
+  // new keys of this chunk's positions (start .. pos), from k
+  const int u_lo = max(p_lo, start) - start, u_hi = p_hi - 1 - start;
+  for (int u = u_lo; u <= u_hi; ++u) {
+    const float kr = norm_rope(in ? a.k[(size_t)u * kvw + (size_t)j * hd + tid] : 0.f, a.kn_w, a.kn_dt, a,
+                               start + u, s_tmp, s_red);
     if (in) s_knew[u * hd + tid] = kr;
   }
-  // the first query head of kv head j writes token t's cache row
-  if (h % G == 0 && in) {
-    const size_t c = ((size_t)pos * a.kvh + j) * hd + tid;
-    store1<CBF>(a.kc, c, s_knew[t * hd + tid]);
-    store1<CBF>(a.vc, c, a.v[(size_t)t * kvw + (size_t)j * hd + tid]);
+  // the chunk holding position pos writes token t's cache row of kv head j
+  if (c == nc - 1 && in) {
+    const size_t cr = ((size_t)pos * a.kvh + j) * hd + tid;
+    store1<CBF>(a.kc, cr, s_knew[t * hd + tid]);
+    store1<CBF>(a.vc, cr, a.v[(size_t)t * kvw + (size_t)j * hd + tid]);
   }
   __syncthreads();
 
-  // online softmax over positions wave, wave + 4, ..; lane holds dims 4l..4l+3
   const int d0 = lane * 4;
   const bool lin = d0 < hd;
-  const float4 q4 = lin ? *reinterpret_cast<const float4*>(s_q + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
-  float m = -INFINITY, l = 0.f;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  constexpr int NB = 4;  // positions in flight per wavefront
-  for (int p0 = wave; p0 <= pos; p0 += 4 * NB) {
+  float4 q4[MAXG], acc[MAXG];
+  float m[MAXG], l[MAXG];
+#pragma unroll
+  for (int g = 0; g < MAXG; ++g) {
+    q4[g] = lin && g < G ? *reinterpret_cast<const float4*>(s_q + g * hd + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+  }
+  for (int p0 = p_lo + wave; p0 < p_hi; p0 += 4 * NB) {
     float4 kk[NB], vv[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const int p = min(p0 + 4 * b, pos);
+      const int p = min(p0 + 4 * b, p_hi - 1);
       if (!lin) {
         kk[b] = vv[b] = make_float4(0.f, 0.f, 0.f, 0.f);
       } else if (p < start) {
-        const size_t c = ((size_t)p * a.kvh + j) * hd + d0;
-        kk[b] = load4<CBF>(a.kc, c);
-        vv[b] = load4<CBF>(a.vc, c);
+        const size_t cr = ((size_t)p * a.kvh + j) * hd + d0;
+        kk[b] = load4<CBF>(a.kc, cr);
+        vv[b] = load4<CBF>(a.vc, cr);
       } else {
         kk[b] = *reinterpret_cast<const float4*>(s_knew + (p - start) * hd + d0);
         vv[b] = *reinterpret_cast<const float4*>(a.v + (size_t)(p - start) * kvw + (size_t)j * hd + d0);
@@ -197,34 +273,122 @@ __global__ __launch_bounds__(256) void attn_head_kernel(AttnArgs a) {
     }
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      if (p0 + 4 * b > pos) break;
-      const float s = wave_sum(q4.x * kk[b].x + q4.y * kk[b].y + q4.z * kk[b].z + q4.w * kk[b].w);
-      const float mn = fmaxf(m, s);
-      const float f = __expf(m - mn), e = __expf(s - mn);
-      l = l * f + e;
-      acc.x = acc.x * f + e * vv[b].x;
-      acc.y = acc.y * f + e * vv[b].y;
-      acc.z = acc.z * f + e * vv[b].z;
-      acc.w = acc.w * f + e * vv[b].w;
-      m = mn;
+      if (p0 + 4 * b >= p_hi) break;
+      float d[MAXG];
+#pragma unroll
+      for (int g = 0; g < MAXG; ++g)
+        d[g] = q4[g].x * kk[b].x + q4[g].y * kk[b].y + q4[g].z * kk[b].z + q4[g].w * kk[b].w;
+      const float sr = rows8_sum(d);  // lanes 8g ..: head g's score
+#pragma unroll
+      for (int g = 0; g < MAXG; ++g) {
+        if (g >= G) break;
+        const float sg = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(sr), 8 * g));
+        const float mn = fmaxf(m[g], sg);
+        const float f = __expf(m[g] - mn), e = __expf(sg - mn);
+        l[g] = l[g] * f + e;
+        acc[g].x = acc[g].x * f + e * vv[b].x;
+        acc[g].y = acc[g].y * f + e * vv[b].y;
+        acc[g].z = acc[g].z * f + e * vv[b].z;
+        acc[g].w = acc[g].w * f + e * vv[b].w;
+        m[g] = mn;
+      }
     }
   }
-  if (lane == 0) {
-    s_m[wave] = m;
-    s_l[wave] = l;
-  }
-  if (lin) *reinterpret_cast<float4*>(&s_acc[wave][d0]) = acc;
-  __syncthreads();
-  if (in) {
-    const float M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+  // merge the 4 wavefronts per head: one chunk (short contexts) writes the
+  // gated output directly; otherwise the chunk partial (m, l, acc[hd]) goes
+  // to the workspace
+  const int maxc = a.max_chunks;
+  for (int g = 0; g < G; ++g) {
+    if (lane == 0) {
+      s_m[wave][g] = m[g];
+      s_l[wave][g] = l[g];
+    }
+    if (lin) *reinterpret_cast<float4*>(&s_acc[wave][d0]) = acc[g];
+    __syncthreads();
+    const float M = fmaxf(fmaxf(s_m[0][g], s_m[1][g]), fmaxf(s_m[2][g], s_m[3][g]));
     float L = 0.f, o = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const float f = s_m[w] == -INFINITY ? 0.f : __expf(s_m[w] - M);  // a wavefront with no position
-      L += s_l[w] * f;
-      o += s_acc[w][tid] * f;
+      const float f = s_m[w][g] == -INFINITY ? 0.f : __expf(s_m[w][g] - M);
+      L += s_l[w][g] * f;
+      o += in ? s_acc[w][tid] * f : 0.f;
     }
-    a.gated[(size_t)t * qw + (size_t)h * hd + tid] = (o / L) * sigmoid(gate);
+    if (nc == 1) {
+      if (in) {
+        const size_t qb = (size_t)t * 2 * qw + (size_t)(j * G + g) * 2 * hd;
+        a.gated[(size_t)t * qw + (size_t)(j * G + g) * hd + tid] = (o / L) * sigmoid(a.qg[qb + hd + tid]);
+      }
+    } else {
+      float* part = a.part + ((size_t)(t * a.heads + j * G + g) * maxc + c) * (hd + 2);
+      if (in) part[2 + tid] = o;
+      if (tid == 0) {
+        part[0] = M;
+        part[1] = L;
+      }
+    }
+    __syncthreads();  // s_m / s_acc are rewritten for the next head
+  }
+  if (nc == 1) return;
+  if (tid == 0) {
+    uint32_t* ticket = a.tickets + t * a.kvh + j;
+    const uint32_t arrived = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) + 1u;
+    s_last = arrived == (uint32_t)nc;
+    if (s_last) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // last arrival: merge the nc chunks.  Chunk statistics of every head go
+  // through LDS in one pass; then wavefront w merges heads w, w + 4 with 16-byte
+  // loads of 4 dims per lane, 8 chunks in flight.
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  for (int e = tid; e < G * nc; e += 256) {
+    const int g = e / nc, cc = e - g * nc;
+    const float* pc = a.part + ((size_t)(t * a.heads + j * G + g) * maxc + cc) * (hd + 2);
+    s_cm2[g][cc] = pc[0];
+    s_cl2[g][cc] = pc[1];
+  }
+  __syncthreads();
+  if (tid < G) {
+    float M = -INFINITY;
+    for (int cc = 0; cc < nc; ++cc) M = fmaxf(M, s_cm2[tid][cc]);
+    float L = 0.f;
+    for (int cc = 0; cc < nc; ++cc) {
+      const float f = s_cm2[tid][cc] == -INFINITY ? 0.f : __expf(s_cm2[tid][cc] - M);
+      s_cm2[tid][cc] = f;
+      L += s_cl2[tid][cc] * f;
+    }
+    s_L[tid] = L;
+  }
+  __syncthreads();
+  for (int g = wave; g < G; g += 4) {
+    if (!lin) continue;
+    const size_t qb = (size_t)t * 2 * qw + (size_t)(j * G + g) * 2 * hd + hd + d0;
+    const float4 gate = make_float4(a.qg[qb + 0], a.qg[qb + 1], a.qg[qb + 2], a.qg[qb + 3]);  // issued first
+    const float* base = a.part + (size_t)(t * a.heads + j * G + g) * maxc * (hd + 2) + 2 + d0;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c0 = 0; c0 < nc; c0 += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const int cc = min(c0 + b, nc - 1);
+        const float* src = base + (size_t)cc * (hd + 2);
+        v[b] = make_float4(src[0], src[1], src[2], src[3]);
+      }
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const float f = c0 + b < nc ? s_cm2[g][c0 + b] : 0.f;
+        o.x += v[b].x * f;
+        o.y += v[b].y * f;
+        o.z += v[b].z * f;
+        o.w += v[b].w * f;
+      }
+    }
+    const float inv = 1.f / s_L[g];
+    const size_t ob = (size_t)t * qw + (size_t)(j * G + g) * hd + d0;
+    a.gated[ob + 0] = o.x * inv * sigmoid(gate.x);
+    a.gated[ob + 1] = o.y * inv * sigmoid(gate.y);
+    a.gated[ob + 2] = o.z * inv * sigmoid(gate.z);
+    a.gated[ob + 3] = o.w * inv * sigmoid(gate.w);
   }
 }
 
@@ -236,6 +400,7 @@ struct AttnOutArgs {
   int T, H, K;
   float* update;
   float* hidden_out;
+  int* advance;  // nullable: *advance += T at the end of the step (device-held position)
 };
 
 // 8 rows of Wo per workgroup (2 per wavefront), K <= 4096, loaded once and
@@ -280,17 +445,16 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
       if (a.hidden_out) a.hidden_out[o] = load_scalar(a.x, a.x_dt, o) + u;
     }
   }
+  // the attention launch before this one has read the position
+  if (a.advance && blockIdx.x == 0 && threadIdx.x == 0) *a.advance += a.T;
 }
-
-// Advances a device-held decode position (one thread), so a captured step
-// can move its own position forward between graph replays.
-__global__ void position_advance_kernel(int32_t* position, int delta) { *position += delta; }
 
 static int check_attn_shape(int tokens, int hidden_size, int heads, int kv_heads, int head_dim, int rope_dim) {
   if (tokens < 1 || tokens > kAttnMaxTokens) return fail(FK_ERR_UNSUPPORTED, "tokens must be in [1, %d]", kAttnMaxTokens);
   if (hidden_size < 8 || hidden_size % 8 || hidden_size > 4096)
     return fail(FK_ERR_ALIGNMENT, "hidden_size must be a multiple of 8 in [8, 4096]");
   if (heads < 1 || kv_heads < 1 || heads % kv_heads) return fail(FK_ERR_INVALID, "heads must be a positive multiple of kv_heads");
+  if (heads / kv_heads > 8) return fail(FK_ERR_UNSUPPORTED, "at most 8 query heads per kv head");
   if (head_dim < 4 || head_dim > kAttnMaxHeadDim || head_dim % 4)
     return fail(FK_ERR_UNSUPPORTED, "head_dim must be a multiple of 4 in [4, %d]", kAttnMaxHeadDim);
   if ((long long)heads * head_dim > 4096 || (heads * head_dim) % 8)
@@ -382,12 +546,20 @@ int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_w
   a.eps = qk_eps;
   a.interleaved = rope_interleaved;
   a.gated = ws.gated;
-  const size_t shm = (size_t)tokens * head_dim * sizeof(float);
-  if (cache_dtype == FK_DTYPE_BF16)
-    hipLaunchKernelGGL(attn_head_kernel<true>, dim3(tokens, heads), dim3(256), shm, s, a);
-  else
-    hipLaunchKernelGGL(attn_head_kernel<false>, dim3(tokens, heads), dim3(256), shm, s, a);
-  st = check_launch("attn_head_kernel");
+  a.part = ws.part;
+  a.tickets = ws.tickets;
+  // chunks of >= 32 positions, at most kAttnMaxChunks of them over the
+  // positions the step can reach (the cache length when the position is
+  // only known on the device)
+  const int reach = start_position_device ? max_positions : start_position + tokens;
+  a.chunk = (reach + kAttnMaxChunks - 1) / kAttnMaxChunks;
+  if (a.chunk < 32) a.chunk = 32;  // contexts below 32 positions: one chunk, no merge
+  a.max_chunks = kAttnMaxChunks;
+  const dim3 grid((unsigned)((reach + a.chunk - 1) / a.chunk), (unsigned)kv_heads, (unsigned)tokens);
+  const size_t shm = (size_t)(8 + tokens) * head_dim * sizeof(float);
+  if (cache_dtype == FK_DTYPE_BF16) hipLaunchKernelGGL(attn_split_kernel<true>, grid, dim3(256), shm, s, a);
+  else hipLaunchKernelGGL(attn_split_kernel<false>, grid, dim3(256), shm, s, a);
+  st = check_launch("attn_split_kernel");
   if (st) return st;
   AttnOutArgs o;
   o.gated = ws.gated;
@@ -399,16 +571,11 @@ int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_w
   o.K = heads * head_dim;
   o.update = update;
   o.hidden_out = hidden_out;
-  const dim3 grid((unsigned)((hidden_size + kAttnOutRows - 1) / kAttnOutRows));
-  if (weight_dtype == FK_DTYPE_BF16) hipLaunchKernelGGL(attn_out_kernel<true>, grid, dim3(256), 0, s, o);
-  else hipLaunchKernelGGL(attn_out_kernel<false>, grid, dim3(256), 0, s, o);
+  o.advance = const_cast<int*>(start_position_device);
+  const dim3 ogrid((unsigned)((hidden_size + kAttnOutRows - 1) / kAttnOutRows));
+  if (weight_dtype == FK_DTYPE_BF16) hipLaunchKernelGGL(attn_out_kernel<true>, ogrid, dim3(256), 0, s, o);
+  else hipLaunchKernelGGL(attn_out_kernel<false>, ogrid, dim3(256), 0, s, o);
   return check_launch("attn_out_kernel");
-}
-
-int fk_position_advance(int32_t* position, int delta, void* stream) {
-  if (!position) return fail(FK_ERR_INVALID, "position must be non-NULL");
-  hipLaunchKernelGGL(position_advance_kernel, dim3(1), dim3(1), 0, as_stream(stream), position, delta);
-  return check_launch("position_advance_kernel");
 }
 
 }  // extern "C"

@@ -12,7 +12,7 @@ graph (torch.cuda.CUDAGraph), which is how bench.py times them.
                     conv / recurrent states.
   AttentionStepPlan gated full attention (+ residual) through
                     fk_attention_decode at a device-held position that the
-                    step advances itself (fk_position_advance), with the KV
+                    step advances itself, with the KV
                     caches it owns updated in place.
 """
 
@@ -205,8 +205,8 @@ class AttentionStepPlan:
     """One gated full-attention decode step of `tokens` rows + residual.
 
     The plan owns the KV caches ([max_positions, kv_heads, head_dim]) and a
-    device int32 `position`; every run decodes at that position and then
-    advances it by `tokens`, so a step captured once in a HIP graph decodes
+    device int32 `position`; every run decodes at that position and its last
+    kernel advances it by `tokens`, so a step captured once in a HIP graph decodes
     successive positions on replay.  `set_position()` rewinds it.
     """
 
@@ -271,4 +271,3 @@ class AttentionStepPlan:
             sp.attention_head_dim, sp.rope_dim, float(sp.rope_theta), self.interleaved, self.eps, self.eps,
             self.update.data_ptr(), self.hidden_out.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(), s,
         )
-        _lib.call("fk_position_advance", self.position.data_ptr(), self.tokens, s)

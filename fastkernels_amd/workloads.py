@@ -177,6 +177,40 @@ def deltanet_step_bytes(tokens: int, spec: Qwen36A3BSpec | None = None, *, weigh
     return weights + state + conv_state + io
 
 
+def attention_step_bytes(tokens: int, context: int, spec: Qwen36A3BSpec | None = None, *, weight_bytes: int = 2,
+                         cache_bytes: int = 4) -> int:
+    """Gated attention step: Wq (query + gate rows), Wk, Wv, Wo and the norm
+    weights, the cached keys and values of the `context` earlier positions
+    (read once) and the new rows written, plus per-token inputs/outputs."""
+
+    spec = spec or qwen36_35b_a3b_spec()
+    H, heads, kvh, hd = spec.hidden_size, spec.attention_heads, spec.attention_kv_heads, spec.attention_head_dim
+    weights = (2 * heads * hd * H + 2 * kvh * hd * H + H * heads * hd + H + 2 * hd) * weight_bytes
+    cache = 2 * (context + tokens) * kvh * hd * cache_bytes
+    io = tokens * H * weight_bytes + 2 * tokens * H * 4
+    return weights + cache + io
+
+
+def make_attention_weights(
+    spec: Qwen36A3BSpec | None = None, *, seed: int, dtype=torch.bfloat16, device: Any = "cpu"
+) -> dict[str, torch.Tensor]:
+    """Gated-attention weights (keys of `Qwen36AttentionWeights` without the
+    post-attention norm, which belongs to the MoE block)."""
+
+    spec = spec or qwen36_35b_a3b_spec()
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    H, heads, kvh, hd = spec.hidden_size, spec.attention_heads, spec.attention_kv_heads, spec.attention_head_dim
+    return {
+        "input_norm_weight": _randn(gen, (H,), WEIGHT_SCALE, dtype, device),
+        "q_proj_weight": _randn(gen, (2 * heads * hd, H), WEIGHT_SCALE, dtype, device),
+        "k_proj_weight": _randn(gen, (kvh * hd, H), WEIGHT_SCALE, dtype, device),
+        "v_proj_weight": _randn(gen, (kvh * hd, H), WEIGHT_SCALE, dtype, device),
+        "o_proj_weight": _randn(gen, (H, heads * hd), WEIGHT_SCALE, dtype, device),
+        "q_norm_weight": _randn(gen, (hd,), WEIGHT_SCALE, dtype, device),
+        "k_norm_weight": _randn(gen, (hd,), WEIGHT_SCALE, dtype, device),
+    }
+
+
 def expected_distinct_experts(tokens: int, spec: Qwen36A3BSpec | None = None) -> float:
     spec = spec or qwen36_35b_a3b_spec()
     E, K = spec.num_experts, spec.num_routed_experts

@@ -186,10 +186,12 @@ size_t fk_attention_workspace_bytes(int tokens, int heads, int kv_heads, int hea
  * softmax attention (GQA: heads / kv_heads query heads per kv head),
  * o * sigmoid(gate), update = . Wo^T (f32 [T, hidden]) and, when hidden_out
  * is not NULL, hidden_out = hidden + update.  head_dim <= 256,
- * heads * head_dim <= 4096.  start_position_device (nullable): a device
- * int32 read at run time in place of start_position, so one captured HIP
- * graph can decode successive positions; a value with start + tokens past
- * max_positions gives NaN updates and leaves the caches untouched.
+ * heads * head_dim <= 4096, heads / kv_heads <= 8.  start_position_device
+ * (nullable, no reference counterpart): a device int32 read at run time in
+ * place of start_position and advanced by `tokens` at the end of the step,
+ * so one captured HIP graph decodes successive positions; a value with
+ * start + tokens past max_positions gives NaN updates and leaves the caches
+ * untouched.
  * Replaces triton_qwen36_batched_attention_decode (qwen36_attention.py:448-577)
  * and the residual add of triton_qwen36_batched_attention_moe_layer_decode
  * (qwen36_layer.py:109-201). */
@@ -205,11 +207,6 @@ int fk_attention_decode(const void* hidden, int hidden_dtype,
                         int rope_interleaved, float eps, float qk_eps,
                         float* update, float* hidden_out,
                         void* workspace, size_t workspace_bytes, void* stream);
-
-/* *position += delta on the device (one thread): advances the decode
- * position of a captured step.  No counterpart in the reference, whose
- * decode loop passes positions from the host. */
-int fk_position_advance(int32_t* position, int delta, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* Gated DeltaNet decode step                                                */
