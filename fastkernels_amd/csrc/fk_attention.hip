@@ -14,8 +14,9 @@
 //   update = (o * sigmoid(gate)) Wo^T;  hidden_out = x + update
 //
 // Kernels (three launches per step):
-//   projection        the shared normalized projection kernel (fk_deltanet.hip)
-//                     over [Wq | Wk | Wv] (9216 rows at the model shape)
+//   attn_proj_kernel  RMSNorm folded into a GEMV over [Wq | Wk | Wv] (9216
+//                     rows at the model shape); H > 2048 takes the shared
+//                     normalized projection kernel of fk_deltanet.hip
 //   attn_split_kernel grid (position chunks, kv heads, T), 256 threads: the
 //                     G query heads of one kv head over one chunk of
 //                     positions (each cached row read once per chunk), head
@@ -53,8 +54,10 @@ struct AttnArgs {
   float* part;          // [T, heads, max_chunks, hd + 2] per-chunk (max, sum, weighted values)
   uint32_t* tickets;    // [T, kv_heads] chunk arrivals (self-resetting)
   int chunk, max_chunks;
+  int hsplit;           // workgroups per kv head: each takes G / hsplit of its query heads
 };
 
+constexpr int kAttnMaxKvHeads = 64;
 constexpr int kAttnMaxChunks = 64;  // position chunks per (token, kv head): the merge reads at most this many
 
 struct AttnWs {
@@ -73,7 +76,10 @@ static size_t attn_ws_layout(int T, int heads, int kvh, int hd, char* base, Attn
     off = align_up(off + bytes, 256);
     return base ? reinterpret_cast<float*>(base + at) : nullptr;
   };
-  ws->tickets = reinterpret_cast<uint32_t*>(take((size_t)T * kvh * 4));
+  // (t, kv head, head split) tickets in a region of fixed size at the start
+  // of every layout, so calls of different shapes sharing a workspace find
+  // them at zero
+  ws->tickets = reinterpret_cast<uint32_t*>(take((size_t)kAttnMaxTokens * kAttnMaxKvHeads * 8 * 4));
   ws->qg = take((size_t)T * heads * 2 * hd * 4);
   ws->k = take((size_t)T * kvh * hd * 4);
   ws->v = take((size_t)T * kvh * hd * 4);
@@ -163,9 +169,10 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   __shared__ int s_last;
   __shared__ float s_ss[4][MAXG];
   __shared__ float s_cm2[MAXG][kAttnMaxChunks], s_cl2[MAXG][kAttnMaxChunks], s_L[MAXG];
-  const int c = blockIdx.x, j = blockIdx.y, t = blockIdx.z;
+  const int c = blockIdx.x, j = blockIdx.y / a.hsplit, hs = blockIdx.y - j * a.hsplit, t = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int hd = a.hd, G = a.heads / a.kvh;
+  const int hd = a.hd, G = a.heads / a.kvh / a.hsplit;  // query heads of this workgroup
+  const int hb = j * (a.heads / a.kvh) + hs * G;          // the first of them
   const int qw = a.heads * hd, kvw = a.kvh * hd;
   const bool in = tid < hd;
   float* s_q = reinterpret_cast<float*>(s_dyn);
@@ -174,7 +181,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   if (start < 0 || start + a.T > a.max_pos) {
     // a run-time position past the cache: no cache access, NaN outputs
     if (c == 0 && in)
-      for (int g = 0; g < G; ++g) a.gated[(size_t)t * qw + (size_t)(j * G + g) * hd + tid] = __builtin_nanf("");
+      for (int g = 0; g < G; ++g) a.gated[(size_t)t * qw + (size_t)(hb + g) * hd + tid] = __builtin_nanf("");
     return;
   }
   const int pos = start + t, C = a.chunk;
@@ -184,11 +191,14 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 
   // queries of the G heads at once (thread d: dim d of every head): norms
   // from one transposed lane reduction, RoPE at pos, 1/sqrt(hd)
+  float gate[MAXG];  // this thread's gate values, loaded with the queries (used at the end)
   {
     float xq[MAXG], sq[MAXG];
 #pragma unroll
     for (int g = 0; g < MAXG; ++g) {
-      xq[g] = in && g < G ? a.qg[(size_t)t * 2 * qw + (size_t)(j * G + g) * 2 * hd + tid] : 0.f;
+      const size_t qb = (size_t)t * 2 * qw + (size_t)(hb + g) * 2 * hd + tid;
+      xq[g] = in && g < G ? a.qg[qb] : 0.f;
+      gate[g] = in && g < G ? a.qg[qb + hd] : 0.f;
       sq[g] = xq[g] * xq[g];
     }
     const float r = rows8_sum(sq);
@@ -314,12 +324,12 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
       o += in ? s_acc[w][tid] * f : 0.f;
     }
     if (nc == 1) {
-      if (in) {
-        const size_t qb = (size_t)t * 2 * qw + (size_t)(j * G + g) * 2 * hd;
-        a.gated[(size_t)t * qw + (size_t)(j * G + g) * hd + tid] = (o / L) * sigmoid(a.qg[qb + hd + tid]);
-      }
+      float gg = gate[0];
+#pragma unroll
+      for (int k = 1; k < MAXG; ++k) gg = g == k ? gate[k] : gg;
+      if (in) a.gated[(size_t)t * qw + (size_t)(hb + g) * hd + tid] = (o / L) * sigmoid(gg);
     } else {
-      float* part = a.part + ((size_t)(t * a.heads + j * G + g) * maxc + c) * (hd + 2);
+      float* part = a.part + ((size_t)(t * a.heads + hb + g) * maxc + c) * (hd + 2);
       if (in) part[2 + tid] = o;
       if (tid == 0) {
         part[0] = M;
@@ -330,7 +340,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   }
   if (nc == 1) return;
   if (tid == 0) {
-    uint32_t* ticket = a.tickets + t * a.kvh + j;
+    uint32_t* ticket = a.tickets + (t * a.kvh + j) * a.hsplit + hs;
     const uint32_t arrived = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) + 1u;
     s_last = arrived == (uint32_t)nc;
     if (s_last) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -343,7 +353,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   for (int e = tid; e < G * nc; e += 256) {
     const int g = e / nc, cc = e - g * nc;
-    const float* pc = a.part + ((size_t)(t * a.heads + j * G + g) * maxc + cc) * (hd + 2);
+    const float* pc = a.part + ((size_t)(t * a.heads + hb + g) * maxc + cc) * (hd + 2);
     s_cm2[g][cc] = pc[0];
     s_cl2[g][cc] = pc[1];
   }
@@ -362,9 +372,9 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   __syncthreads();
   for (int g = wave; g < G; g += 4) {
     if (!lin) continue;
-    const size_t qb = (size_t)t * 2 * qw + (size_t)(j * G + g) * 2 * hd + hd + d0;
+    const size_t qb = (size_t)t * 2 * qw + (size_t)(hb + g) * 2 * hd + hd + d0;
     const float4 gate = make_float4(a.qg[qb + 0], a.qg[qb + 1], a.qg[qb + 2], a.qg[qb + 3]);  // issued first
-    const float* base = a.part + (size_t)(t * a.heads + j * G + g) * maxc * (hd + 2) + 2 + d0;
+    const float* base = a.part + (size_t)(t * a.heads + hb + g) * maxc * (hd + 2) + 2 + d0;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int c0 = 0; c0 < nc; c0 += 8) {
       float4 v[8];
@@ -384,11 +394,106 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
       }
     }
     const float inv = 1.f / s_L[g];
-    const size_t ob = (size_t)t * qw + (size_t)(j * G + g) * hd + d0;
+    const size_t ob = (size_t)t * qw + (size_t)(hb + g) * hd + d0;
     a.gated[ob + 0] = o.x * inv * sigmoid(gate.x);
     a.gated[ob + 1] = o.y * inv * sigmoid(gate.y);
     a.gated[ob + 2] = o.z * inv * sigmoid(gate.z);
     a.gated[ob + 3] = o.w * inv * sigmoid(gate.w);
+  }
+}
+
+// Normalised projection of the attention inputs: rows of [Wq | Wk | Wv]
+// (16 per workgroup, 4 whole rows per wavefront in registers), every token.
+// RMSNorm(x) * (1 + w) is folded in: acc = sum W[r,c] * x[c] * (1 + w[c]),
+// out = acc * rsqrt(mean(x^2) + eps).  Token 0's x and the norm weight are
+// loaded before the rows (the load queue retires in order); the four row
+// sums leave through one transposed lane reduction.
+struct AttnProjArgs {
+  const void* x;
+  const void* nw;
+  int nw_dt;
+  const void* w[3];
+  float* out[3];
+  int rows[3];
+  int T, H;
+  float eps, off;
+};
+constexpr int kAttnProjRows = 16;
+
+template <bool BFW, bool BFX>
+__global__ __launch_bounds__(256) void attn_proj_kernel(AttnProjArgs a) {
+  constexpr int NJ = 4;  // H <= 2048: 4 chunks of 8 per lane
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int nch = a.H >> 3;
+  int row = blockIdx.x * kAttnProjRows + wave * 4;  // first of this wavefront's 4 rows (one matrix)
+  const int R = a.rows[0] + a.rows[1] + a.rows[2];
+  if (row >= R) return;
+  int m = 0;
+  if (row >= a.rows[0]) {
+    row -= a.rows[0];
+    m = 1;
+    if (row >= a.rows[1]) {
+      row -= a.rows[1];
+      m = 2;
+    }
+  }
+  const char* W = reinterpret_cast<const char*>(m == 0 ? a.w[0] : m == 1 ? a.w[1] : a.w[2]);
+  float* out = m == 0 ? a.out[0] : m == 1 ? a.out[1] : a.out[2];
+  const int ostride = m == 0 ? a.rows[0] : m == 1 ? a.rows[1] : a.rows[2];
+  const size_t esz = BFW ? 2 : 4;
+  Raw8<BFX> xr[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int cc = min(lane + kWave * j, nch - 1);
+    xr[j] = load_raw8<BFX>(a.x, (size_t)cc * 8);
+  }
+  float nw8[NJ][8];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) load8_any(a.nw, a.nw_dt, (size_t)min(lane + kWave * j, nch - 1) * 8, nw8[j]);
+  Raw8<BFW> wr[4][NJ];
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int c = min(lane + kWave * j, nch - 1);
+      wr[r][j] = load_raw8_stream<BFW>(W + (size_t)(row + r) * a.H * esz, (size_t)c * 8);
+    }
+  for (int t = 0; t < a.T; ++t) {
+    if (t > 0) {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        xr[j] = load_raw8<BFX>(a.x, (size_t)t * a.H + (size_t)min(lane + kWave * j, nch - 1) * 8);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        asm volatile("" : "+v"(wr[r][j].a));  // rows converted where used, once per token
+        if constexpr (!BFW) asm volatile("" : "+v"(wr[r][j].b));
+      }
+    float acc[4] = {0.f, 0.f, 0.f, 0.f}, ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (lane + kWave * j < nch) {
+        float x8[8];
+        raw8_to_f32<BFX>(xr[j], x8);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          ss = fmaf(x8[q], x8[q], ss);
+          x8[q] *= a.off + nw8[j][q];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float w8[8];
+          raw8_to_f32<BFW>(wr[r][j], w8);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[r] = fmaf(w8[q], x8[q], acc[r]);
+        }
+      }
+    }
+    ss = wave_sum(ss);
+    const float v = rows4_sum(acc) * rsqrtf(ss / (float)a.H + a.eps);  // lanes 16r ..: row r
+    if ((lane & 15) == 0) out[(size_t)t * ostride + row + (lane >> 4)] = v;
   }
 }
 
@@ -455,6 +560,7 @@ static int check_attn_shape(int tokens, int hidden_size, int heads, int kv_heads
     return fail(FK_ERR_ALIGNMENT, "hidden_size must be a multiple of 8 in [8, 4096]");
   if (heads < 1 || kv_heads < 1 || heads % kv_heads) return fail(FK_ERR_INVALID, "heads must be a positive multiple of kv_heads");
   if (heads / kv_heads > 8) return fail(FK_ERR_UNSUPPORTED, "at most 8 query heads per kv head");
+  if (kv_heads > kAttnMaxKvHeads) return fail(FK_ERR_UNSUPPORTED, "kv_heads must be <= %d", kAttnMaxKvHeads);
   if (head_dim < 4 || head_dim > kAttnMaxHeadDim || head_dim % 4)
     return fail(FK_ERR_UNSUPPORTED, "head_dim must be a multiple of 4 in [4, %d]", kAttnMaxHeadDim);
   if ((long long)heads * head_dim > 4096 || (heads * head_dim) % 8)
@@ -489,6 +595,33 @@ int fk_attention_project(const void* hidden, int hidden_dtype, const void* norm_
     return fail(FK_ERR_INVALID, "projection pointers must be non-NULL");
   if (!aligned16(hidden) || !aligned16(norm_weight) || !aligned16(q_proj) || !aligned16(k_proj) || !aligned16(v_proj))
     return fail(FK_ERR_ALIGNMENT, "hidden, norm_weight and projection weights must be 16-byte aligned");
+  if (hidden_size <= 2048 && q_rows % 4 == 0 && kv_rows % 4 == 0) {
+    AttnProjArgs pa;
+    pa.x = hidden;
+    pa.nw = norm_weight;
+    pa.nw_dt = norm_dtype;
+    pa.w[0] = q_proj;
+    pa.w[1] = k_proj;
+    pa.w[2] = v_proj;
+    pa.out[0] = q_out;
+    pa.out[1] = k_out;
+    pa.out[2] = v_out;
+    pa.rows[0] = q_rows;
+    pa.rows[1] = kv_rows;
+    pa.rows[2] = kv_rows;
+    pa.T = tokens;
+    pa.H = hidden_size;
+    pa.eps = eps;
+    pa.off = norm_offset;
+    const dim3 grid((unsigned)((q_rows + 2 * kv_rows + kAttnProjRows - 1) / kAttnProjRows));
+    const bool bw = weight_dtype == FK_DTYPE_BF16, bx = hidden_dtype == FK_DTYPE_BF16;
+    const hipStream_t s = as_stream(stream);
+    if (bw && bx) hipLaunchKernelGGL((attn_proj_kernel<true, true>), grid, dim3(256), 0, s, pa);
+    else if (bw) hipLaunchKernelGGL((attn_proj_kernel<true, false>), grid, dim3(256), 0, s, pa);
+    else if (bx) hipLaunchKernelGGL((attn_proj_kernel<false, true>), grid, dim3(256), 0, s, pa);
+    else hipLaunchKernelGGL((attn_proj_kernel<false, false>), grid, dim3(256), 0, s, pa);
+    return check_launch("attn_proj_kernel");
+  }
   const void* const w[4] = {q_proj, k_proj, v_proj, nullptr};
   const int rows[4] = {q_rows, kv_rows, kv_rows, 0};
   float* const out[4] = {q_out, k_out, v_out, nullptr};
@@ -555,7 +688,13 @@ int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_w
   a.chunk = (reach + kAttnMaxChunks - 1) / kAttnMaxChunks;
   if (a.chunk < 32) a.chunk = 32;  // contexts below 32 positions: one chunk, no merge
   a.max_chunks = kAttnMaxChunks;
-  const dim3 grid((unsigned)((reach + a.chunk - 1) / a.chunk), (unsigned)kv_heads, (unsigned)tokens);
+  const int nchunks = (reach + a.chunk - 1) / a.chunk;
+  // split a kv head's query heads over workgroups while the grid is small
+  // (short contexts); long contexts keep them together (rows read once)
+  const int G = heads / kv_heads;
+  a.hsplit = 1;
+  while (a.hsplit * 2 <= G && G % (a.hsplit * 2) == 0 && nchunks * kv_heads * tokens * a.hsplit < 128) a.hsplit *= 2;
+  const dim3 grid((unsigned)nchunks, (unsigned)(kv_heads * a.hsplit), (unsigned)tokens);
   const size_t shm = (size_t)(8 + tokens) * head_dim * sizeof(float);
   if (cache_dtype == FK_DTYPE_BF16) hipLaunchKernelGGL(attn_split_kernel<true>, grid, dim3(256), shm, s, a);
   else hipLaunchKernelGGL(attn_split_kernel<false>, grid, dim3(256), shm, s, a);
