@@ -1520,8 +1520,21 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
     }
   }
   if (ONE) {
-    // One token: the top-k wavefront already holds the K pairs in its lanes.
-    if (wave == 0) fused_tables(tk_id, tk_w, P, K, lane, s_tok, s_wpos, s_active, s_aoff, &s_nact);
+    // One token: the top-k wavefront holds the K pairs in its lanes, each a
+    // distinct expert, so the tables are the selection itself (expert u at
+    // permuted position u, selection order) with no sort.
+    if (wave == 0) {
+      if (lane < K) {
+        s_active[lane] = tk_id;
+        s_aoff[lane] = lane;
+        s_wpos[lane] = tk_w;
+        s_tok[lane] = 0;
+      }
+      if (lane == 0) {
+        s_aoff[K] = K;
+        s_nact = K;
+      }
+    }
     __syncthreads();
   } else {
     __syncthreads();
