@@ -24,7 +24,7 @@
 //                     from k (no dependence on another workgroup's cache
 //                     write), online softmax; the last chunk to finish merges
 //                     the chunks and applies the gate
-//   attn_out_kernel   grid ceil(H/8): 8 rows of Wo per workgroup (2 per
+//   attn_out_kernel   grid ceil(H/4): 4 rows of Wo per workgroup (1 per
 //                     wavefront, loaded once) against every token; residual;
 //                     advances a device-held position
 #include "fk_common.h"
@@ -34,7 +34,7 @@ namespace fk {
 
 constexpr int kAttnMaxHeadDim = 256;
 constexpr int kAttnMaxTokens = 32;  // new keys of the step are kept in LDS (T * hd floats)
-constexpr int kAttnOutRows = 8;
+constexpr int kAttnOutRows = 4;  // Wo rows per out-projection workgroup (1 per wavefront)
 
 struct AttnArgs {
   const float* qg;      // [T, heads * 2 * hd] projected query/gate pairs
@@ -508,24 +508,26 @@ struct AttnOutArgs {
   int* advance;  // nullable: *advance += T at the end of the step (device-held position)
 };
 
-// 8 rows of Wo per workgroup (2 per wavefront), K <= 4096, loaded once and
+// 4 rows of Wo per workgroup (1 per wavefront), K <= 4096, loaded once and
 // applied to every token.
 template <bool BFW>
 __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
-  constexpr int NJ = 8;
+  constexpr int NJ = 8, RPW = kAttnOutRows / 4;  // rows per wavefront
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r0 = blockIdx.x * kAttnOutRows + wave * 2;
+  const int r0 = blockIdx.x * kAttnOutRows + wave * RPW;
   const int nch = a.K >> 3;
-  Raw8<BFW> wr[2][NJ];
+  Raw8<BFW> wr[RPW][NJ];
 #pragma unroll
-  for (int r = 0; r < 2; ++r)
+  for (int r = 0; r < RPW; ++r)
 #pragma unroll
     for (int q = 0; q < NJ; ++q) {
       const int c = lane + kWave * q;
       if (c < nch && r0 + r < a.H) wr[r][q] = load_raw8_stream<BFW>(a.wo, (size_t)(r0 + r) * a.K + (size_t)c * 8);
     }
   for (int t = 0; t < a.T; ++t) {
-    float acc[2] = {0.f, 0.f};
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) acc[r] = 0.f;
 #pragma unroll
     for (int q = 0; q < NJ; ++q) {
       const int c = lane + kWave * q;
@@ -533,7 +535,7 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
         float g8[8];
         load8_act(a.gated, (size_t)t * a.K + (size_t)c * 8, g8);
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
+        for (int r = 0; r < RPW; ++r) {
           float w8[8];
           raw8_to_f32<BFW>(wr[r][q], w8);
 #pragma unroll
@@ -542,9 +544,11 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
       }
     }
 #pragma unroll
-    for (int r = 0; r < 2; ++r) acc[r] = wave_sum(acc[r]);
-    if (lane < 2 && r0 + lane < a.H) {
-      const float u = lane ? acc[1] : acc[0];
+    for (int r = 0; r < RPW; ++r) acc[r] = wave_sum(acc[r]);
+    if (lane < RPW && r0 + lane < a.H) {
+      float u = acc[0];
+#pragma unroll
+      for (int r = 1; r < RPW; ++r) u = lane == r ? acc[r] : u;
       const size_t o = (size_t)t * a.H + r0 + lane;
       a.update[o] = u;
       if (a.hidden_out) a.hidden_out[o] = load_scalar(a.x, a.x_dt, o) + u;
