@@ -20,12 +20,51 @@ device so a captured step stays valid:
 
 from __future__ import annotations
 
+from dataclasses import dataclass
 from typing import Any, Sequence
 
 import torch
 
 from .plan import AttentionStepPlan, DeltaNetStepPlan, MoeLayerPlan
 from .spec import Qwen36A3BSpec, qwen36_35b_a3b_spec
+
+
+@dataclass(frozen=True)
+class Qwen36RealDecodeState:
+    """Per-sequence decode state (reference reference/qwen36_real.py:12-20):
+    DeltaNet conv and recurrent states, attention KV caches, in layer order
+    within each kind, and the next position."""
+
+    deltanet_conv_states: tuple[Any, ...]
+    deltanet_recurrent_states: tuple[Any, ...]
+    attention_key_cache: tuple[Any, ...]
+    attention_value_cache: tuple[Any, ...]
+    position: int = 0
+
+
+def initial_qwen36_real_decode_state(
+    spec: Qwen36A3BSpec,
+    *,
+    max_positions: int | None = None,
+    conv_kernel_size: int = 4,
+    device: Any = "cpu",
+    dtype: Any = None,
+) -> Qwen36RealDecodeState:
+    """Zero states and caches for one sequence (reference reference/qwen36_real.py:40-80)."""
+
+    dtype = dtype or torch.float32
+    counts = spec.layer_counts()
+    conv_dim = spec.deltanet_conv_dim
+    rec = spec.deltanet_recurrent_state_shape()
+    cache = spec.attention_cache_shape(max_positions)
+    z = lambda shape: torch.zeros(shape, device=device, dtype=dtype)  # noqa: E731
+    return Qwen36RealDecodeState(
+        deltanet_conv_states=tuple(z((conv_dim, conv_kernel_size)) for _ in range(counts["deltanet_moe"])),
+        deltanet_recurrent_states=tuple(z(rec) for _ in range(counts["deltanet_moe"])),
+        attention_key_cache=tuple(z(cache) for _ in range(counts["attention_moe"])),
+        attention_value_cache=tuple(z(cache) for _ in range(counts["attention_moe"])),
+        position=0,
+    )
 
 
 def _tensors(w: Any) -> dict[str, Any]:
@@ -138,6 +177,40 @@ class ResidentDecodeRunner:
     def kv_cache(self, i: int) -> tuple[torch.Tensor, torch.Tensor]:
         p = self.mixers[i][0]
         return p.key_cache, p.value_cache
+
+    def state(self) -> Qwen36RealDecodeState:
+        """The state the next step reads (device tensors, not copies; the
+        position is read back from the device)."""
+
+        dn = [i for i, k in enumerate(self.kinds) if k == "deltanet_moe"]
+        at = [i for i, k in enumerate(self.kinds) if k == "attention_moe"]
+        pos = int(self.mixers[at[0]][0].position.item()) if at else 0
+        return Qwen36RealDecodeState(
+            deltanet_conv_states=tuple(self.deltanet_state(i)[0] for i in dn),
+            deltanet_recurrent_states=tuple(self.deltanet_state(i)[1] for i in dn),
+            attention_key_cache=tuple(self.kv_cache(i)[0] for i in at),
+            attention_value_cache=tuple(self.kv_cache(i)[1] for i in at),
+            position=pos,
+        )
+
+    def load_state(self, state: Qwen36RealDecodeState) -> None:
+        """Copy a sequence's state into the buffers the next step reads
+        (caches up to the shorter of the two lengths)."""
+
+        dn = [i for i, k in enumerate(self.kinds) if k == "deltanet_moe"]
+        at = [i for i, k in enumerate(self.kinds) if k == "attention_moe"]
+        if len(state.deltanet_conv_states) != len(dn) or len(state.attention_key_cache) != len(at):
+            raise ValueError("state does not match the runner's layer kinds")
+        for i, conv, rec in zip(dn, state.deltanet_conv_states, state.deltanet_recurrent_states):
+            c, r = self.deltanet_state(i)
+            c.copy_(conv)
+            r.copy_(rec)
+        for i, kc, vc in zip(at, state.attention_key_cache, state.attention_value_cache):
+            k, v = self.kv_cache(i)
+            n = min(k.shape[0], kc.shape[0])
+            k[:n].copy_(kc[:n])
+            v[:n].copy_(vc[:n])
+        self.set_position(state.position)
 
     def set_position(self, position: int) -> None:
         for pair, kind in zip(self.mixers, self.kinds):

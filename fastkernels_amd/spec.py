@@ -43,6 +43,11 @@ class Qwen36A3BSpec:
         cycle = ("deltanet_moe",) * 3 + ("attention_moe",)
         return tuple(cycle[i % 4] for i in range(self.num_layers))
 
+    def attention_cache_shape(self, max_positions: int | None = None) -> tuple[int, int, int]:
+        """KV cache of one attention layer: [positions, kv_heads, head_dim]."""
+
+        return (max_positions or self.context_length, self.attention_kv_heads, self.attention_head_dim)
+
     def layer_counts(self) -> dict[str, int]:
         kinds = self.layer_kinds()
         return {"deltanet_moe": kinds.count("deltanet_moe"), "attention_moe": kinds.count("attention_moe")}

@@ -110,3 +110,22 @@ def test_runner_graph_replay_equals_eager(device, model):
     assert torch.equal(eager.deltanet_state(1)[1], graphed.deltanet_state(1)[1])
     eager.check_device()
     graphed.check_device()
+
+
+def test_runner_state_transfers_between_runners(device, model):
+    # two steps on runner A, its state loaded into a fresh runner B: the
+    # third step must agree bit for bit
+    tokens = 1
+    a = ResidentDecodeRunner(_on(device, model), tokens, SPEC, max_positions=8)
+    b = ResidentDecodeRunner(_on(device, model), tokens, SPEC, max_positions=8)
+    for s in range(2):
+        a.hidden.copy_(wl.make_hidden(tokens, H, seed=120 + s).to(device))
+        a.step()
+    st = a.state()
+    assert st.position == 2 and len(st.deltanet_recurrent_states) == 3 and len(st.attention_key_cache) == 1
+    b.load_state(st)
+    x = wl.make_hidden(tokens, H, seed=130).to(device)
+    a.hidden.copy_(x)
+    b.hidden.copy_(x)
+    ya, yb = a.step().clone(), b.step().clone()
+    assert torch.equal(ya, yb)

@@ -276,3 +276,15 @@ def test_safetensors_single_file_and_mixer_loaders(tmp_path):
     assert at.o_proj_weight.shape == (H, SPEC.attention_heads * SPEC.attention_head_dim)
     with pytest.raises(FileNotFoundError):
         SafetensorsCheckpoint(tmp_path / "empty_dir_does_not_exist")
+
+
+def test_initial_decode_state_shapes():
+    from fastkernels_amd.runner import initial_qwen36_real_decode_state
+
+    spec = qwen36_35b_a3b_spec()
+    st = initial_qwen36_real_decode_state(spec, max_positions=64)
+    assert len(st.deltanet_conv_states) == 30 and len(st.attention_key_cache) == 10
+    assert st.deltanet_conv_states[0].shape == (8192, 4)
+    assert st.deltanet_recurrent_states[0].shape == (32, 128, 128)
+    assert st.attention_key_cache[0].shape == (64, 2, 256) and st.position == 0
+    assert all(float(t.abs().sum()) == 0.0 for t in st.deltanet_conv_states + st.attention_value_cache)
