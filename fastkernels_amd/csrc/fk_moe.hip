@@ -20,8 +20,8 @@
 //   2. moe_gateup_kernel   grid slots x (I/8); a slot is one active expert or
 //      the shared expert; each workgroup streams 8 gate + 8 up rows of its
 //      expert once and applies them to every pair routed there.
-//   3. moe_down_kernel     grid slots x (H/32); each workgroup streams 32
-//      contiguous down rows (32 KB at I=512) of one expert and writes
+//   3. moe_down_kernel     grid slots x (H/16); each workgroup streams 16
+//      contiguous down rows (16 KB at I=512) of one expert and writes
 //      y[pair, rows] for every pair routed there.
 //   4. moe_combine_kernel  out[t] = sum_k w[t,k] y[pos(t,k)] + g_t y[shared t]
 //      in slot order, and layer_out = x + out (deterministic, no atomics).
@@ -35,7 +35,7 @@ namespace fk {
 constexpr int kMaxPairs = 4096;    // T*K handled by the routing-table builder
 constexpr int kMaxExperts = 1024;  // matches the reference router limit
 constexpr int kGateUpRows = 8;     // intermediates per gate/up workgroup (2 per wave)
-constexpr int kDownRowsPerWave = 8; // down rows per wavefront
+constexpr int kDownRowsPerWave = 4; // down rows per wavefront
 constexpr int kDownRows = 4 * kDownRowsPerWave;  // down rows per workgroup
 
 struct MoeWs {
@@ -777,8 +777,10 @@ __global__ __launch_bounds__(256) void moe_down_kernel(ExpertArgs a) {
 
   for (int pp = 0; pp < npairs; ++pp) {
     const int pos = pos0 + pp;
-    // rows converted where used (as in the gate/up kernel): 78 registers
-    // instead of 112, six wavefronts per SIMD instead of four
+    // rows converted where used (as in the gate/up kernel).  Four rows per
+    // wavefront keep it at 49 registers and eight wavefronts per SIMD: at
+    // eight or sixteen rows per wavefront (fewer, longer streams, 4-6
+    // wavefronts per SIMD) the T = 16 expert stage measured 2-12 us slower.
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -813,10 +815,10 @@ __global__ __launch_bounds__(256) void moe_down_kernel(ExpertArgs a) {
 #pragma unroll
         for (int q = 0; q < 8; ++q) av[j][q] = an[j][q];
     }
-    // the eight row sums at once: lanes 8r .. 8r + 7 hold row r0 + r
-    static_assert(R == 8, "rows8_sum sums eight rows");
-    const float v = rows8_sum(d);
-    if ((lane & 7) == 0 && r0 + (lane >> 3) < a.H) a.ws.y[(size_t)pos * a.H + r0 + (lane >> 3)] = v;
+    // the four row sums at once: lanes 16r .. 16r + 15 hold row r0 + r
+    static_assert(R == 4, "rows4_sum sums four rows");
+    const float v = rows4_sum(d);
+    if ((lane & 15) == 0 && r0 + (lane >> 4) < a.H) a.ws.y[(size_t)pos * a.H + r0 + (lane >> 4)] = v;
   }
 }
 
