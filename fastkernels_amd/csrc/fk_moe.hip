@@ -729,8 +729,8 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(ExpertArgs a) {
   }
 }
 
-// Down projection, expert-major.  Workgroup (slot, row chunk) streams 32
-// contiguous rows of the slot's down matrix (8 per wavefront, one 16-byte
+// Down projection, expert-major.  Workgroup (slot, row chunk) streams 16
+// contiguous rows of the slot's down matrix (4 per wavefront, one 16-byte
 // load per lane per row at I=512, all issued before use) and, for every pair
 // routed to the slot, writes y[pos, row] = W_d[e][row] . act[pos].
 template <bool BFW, int NJI>
