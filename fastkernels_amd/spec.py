@@ -28,9 +28,25 @@ class Qwen36A3BSpec:
     rope_dim: int
     vocab_size: int
     context_length: int
-    rope_theta: float = 10000.0
-    conv_kernel_size: int = 4
     layer_types: tuple[str, ...] | None = None
+    rope_theta: float = 10000.0
+    # (not in the reference spec: the conv window, which the reference fixes
+    # by its state shape; last so positional construction matches the reference)
+    conv_kernel_size: int = 4
+
+    @property
+    def active_experts_per_token(self) -> int:
+        """Routed plus shared experts each token runs (reference models/qwen36.py:34-36)."""
+
+        return self.num_routed_experts + self.num_shared_experts
+
+    @property
+    def attention_heads_per_kv_head(self) -> int:
+        """Query heads per kv head (reference models/qwen36.py:48-52)."""
+
+        if self.attention_heads % self.attention_kv_heads:
+            raise ValueError("attention_heads must be divisible by attention_kv_heads")
+        return self.attention_heads // self.attention_kv_heads
 
     def layer_kinds(self) -> tuple[str, ...]:
         """Mixer of each layer: "deltanet_moe" or "attention_moe".  From the
@@ -52,17 +68,37 @@ class Qwen36A3BSpec:
         kinds = self.layer_kinds()
         return {"deltanet_moe": kinds.count("deltanet_moe"), "attention_moe": kinds.count("attention_moe")}
 
+    def decode_shapes(self, max_positions: int | None = None) -> dict[str, tuple[int, ...]]:
+        """Per-step decode tensors by name (reference models/qwen36.py:85-95):
+        the stacked synthetic-layout DeltaNet states and KV caches over the
+        layers of each kind, the router logits and the packed expert weights."""
+
+        counts = self.layer_counts()
+        cache = self.attention_cache_shape(max_positions)
+        return {
+            "hidden_state": (self.hidden_size,),
+            "deltanet_states": (counts["deltanet_moe"], *self.deltanet_state_shape()),
+            "attention_key_cache": (counts["attention_moe"], *cache),
+            "attention_value_cache": (counts["attention_moe"], *cache),
+            "router_logits": (self.num_experts,),
+            "expert_gate_up_weight": (self.num_experts, self.gated_up_features, self.hidden_size),
+            "expert_down_weight": (self.num_experts, self.hidden_size, self.expert_intermediate_size),
+        }
+
     @classmethod
     def from_hf_config(cls, config: dict, name: str = "hf-config") -> "Qwen36A3BSpec":
         """Spec from a Hugging Face config dict (its `text_config` when
-        nested), with the reference's key aliases and defaults (reference
-        models/qwen36.py:116-158)."""
+        nested), with the reference's key aliases, their precedence and
+        defaults (reference models/qwen36.py:117-161)."""
 
         text = config.get("text_config", config)
 
+        # aliases in order; for each alias the text config first, then the
+        # top level (an earlier alias at the top level wins over a later one
+        # in text_config)
         def get(*names: str, default=None):
-            for src in (text, config):
-                for n in names:
+            for n in names:
+                for src in (text, config):
                     if src.get(n) is not None:
                         return src[n]
             return default
@@ -92,8 +128,8 @@ class Qwen36A3BSpec:
             rope_dim=int(rope_dim or 64),
             vocab_size=int(get("vocab_size", default=248320)),
             context_length=int(get("max_position_embeddings", "seq_length", default=262144)),
-            rope_theta=float(get("rope_theta", default=rope.get("rope_theta", 10000.0))),
             layer_types=tuple(layer_types) if layer_types is not None else None,
+            rope_theta=float(get("rope_theta", default=rope.get("rope_theta", 10000.0))),
         )
 
     @classmethod

@@ -263,10 +263,13 @@ int fk_deltanet_recurrent_output(const void* mixed_qkv, const void* z,
 /* Bytes of workspace for fk_deltanet_step. */
 size_t fk_deltanet_step_workspace_bytes(int tokens, int qk_heads, int value_heads, int head_dim);
 
-/* The whole Gated DeltaNet step with the residual, in three launches:
- * RMSNorm(1+w) + projections with the causal conv fused into the same
- * kernel, the recurrent rule with the per-head gated RMSNorm, and the
- * output projection.  update = core W_out^T; hidden_out (nullable) =
+/* The whole Gated DeltaNet step with the residual: RMSNorm(1+w) +
+ * projections with the causal conv, the recurrent rule with the per-head
+ * gated RMSNorm, and the output projection.  At the model's shapes and
+ * dtypes (tokens <= 8, head_dim 128, bf16 weights, fp32 recurrent state)
+ * this is one launch (deltanet_step_kernel); other shapes run three staged
+ * launches (projection + conv, recurrent + gated norm, output projection).
+ * update = core W_out^T; hidden_out (nullable) =
  * hidden + update; next_conv_state / next_recurrent_state keep the dtypes of
  * their inputs.  `dtypes` holds, in order: hidden, input_norm_weight,
  * projection weights (qkv/z/a/b share one), conv_state, conv1d_weight,

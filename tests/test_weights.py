@@ -233,6 +233,40 @@ def test_spec_layer_kinds_and_hf_config():
     assert spec.rope_dim == 8 and spec.rope_theta == 1e7 and spec.deltanet_value_heads == 32
 
 
+def test_spec_alias_precedence_is_per_alias_then_source():
+    # reference models/qwen36.py:120-127: each alias is tried in text_config
+    # and then at the top level before the next alias is looked at
+    cfg = {"moe_intermediate_size": 512, "num_experts": 64,
+           "text_config": {"intermediate_size": 6144, "n_routed_experts": 32, "hidden_size": 2048,
+                           "num_hidden_layers": 4, "num_layers": 9}}
+    spec = Qwen36A3BSpec.from_hf_config(cfg)
+    assert spec.expert_intermediate_size == 512
+    assert spec.num_experts == 64
+    assert spec.num_layers == 4  # the first alias in text_config wins over the second
+    # a None value falls through to the next source / alias
+    cfg = {"text_config": {"moe_intermediate_size": None, "hidden_size": 8, "num_hidden_layers": 1,
+                           "num_experts": 2, "expert_intermediate_size": 24}, "moe_intermediate_size": 40}
+    assert Qwen36A3BSpec.from_hf_config(cfg).expert_intermediate_size == 40
+
+
+def test_spec_positional_order_and_derived_members():
+    # field order of reference models/qwen36.py:15-32: layer_types, then rope_theta
+    spec = Qwen36A3BSpec("s", 64, 4, 8, 2, 1, 16, 4, 2, 8, 4, 2, 8, 4, 128, 32,
+                         ("linear_attention",) * 3 + ("full_attention",), 5e5)
+    assert spec.layer_types[-1] == "full_attention" and spec.rope_theta == 5e5
+    assert spec.active_experts_per_token == 3
+    assert spec.attention_heads_per_kv_head == 2
+    shapes = spec.decode_shapes(max_positions=10)
+    assert shapes["deltanet_states"] == (3, 2, 8, 16)
+    assert shapes["attention_key_cache"] == (1, 10, 2, 8) == shapes["attention_value_cache"]
+    assert shapes["router_logits"] == (8,) and shapes["hidden_state"] == (64,)
+    assert shapes["expert_gate_up_weight"] == (8, 32, 64) and shapes["expert_down_weight"] == (8, 64, 16)
+    real = qwen36_35b_a3b_spec()
+    assert real.active_experts_per_token == 9 and real.attention_heads_per_kv_head == 8
+    with pytest.raises(ValueError, match="divisible"):
+        dataclasses.replace(real, attention_kv_heads=3).attention_heads_per_kv_head
+
+
 def _save_two_shards(tmp_path, with_index: bool):
     safetensors = pytest.importorskip("safetensors.torch")
     t = split_moe("model.layers.0")
