@@ -37,6 +37,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "fk_status_string": (c_char_p, [I]),
     "fk_last_error_detail": (c_char_p, []),
     "fk_workspace_status": (c_int, [P, c_size_t, I, P]),
+    "fk_workspace_set_poll_limit": (c_int, [P, c_size_t, ctypes.c_longlong, P]),
     "fk_moe_workspace_bytes": (c_size_t, [I, I, I, I, I]),
     "fk_moe_router": (
         c_int,

@@ -13,6 +13,19 @@ int fail(int status, const char* fmt, ...) {
   return status;
 }
 
+// Stream-ordered header updates (kernels rather than memsets, so that a
+// caller may also record them into a HIP graph).
+__global__ void ws_clear_error_kernel(uint32_t* header) {
+  if (header[kWorkspaceErrorWord] != 0u) {
+    header[kWorkspaceErrorWord] = 0u;
+    // every word written so far carries a tag <= epoch + 1: the next launch
+    // (tag epoch + 2) takes none of them for its own
+    header[kWorkspaceEpochWord] += 1u;
+  }
+}
+
+__global__ void ws_set_word_kernel(uint32_t* header, int word, uint32_t value) { header[word] = value; }
+
 }  // namespace fk
 
 extern "C" {
@@ -45,12 +58,25 @@ int fk_workspace_status(const void* workspace, size_t workspace_bytes, int clear
   hipError_t err = hipMemcpyAsync(&v, word, sizeof(v), hipMemcpyDeviceToHost, s);
   if (err == hipSuccess) err = hipStreamSynchronize(s);
   if (err == hipSuccess && v != 0 && clear) {
-    err = hipMemsetAsync(word, 0, sizeof(uint32_t), s);
+    hipLaunchKernelGGL(ws_clear_error_kernel, dim3(1), dim3(1), 0, s,
+                       reinterpret_cast<uint32_t*>(const_cast<void*>(workspace)));
+    err = hipGetLastError();
     if (err == hipSuccess) err = hipStreamSynchronize(s);
   }
   if (err != hipSuccess) return fail(FK_ERR_LAUNCH, "fk_workspace_status: %s", hipGetErrorString(err));
   if (v != 0) return fail(FK_ERR_DEVICE, "a kernel's bounded wait ran out (device flags 0x%x)", v);
   return FK_OK;
+}
+
+int fk_workspace_set_poll_limit(void* workspace, size_t workspace_bytes, long long limit, void* stream) {
+  using namespace fk;
+  if (!workspace || workspace_bytes < (kWorkspaceErrorWord + 1) * sizeof(uint32_t))
+    return fail(FK_ERR_WORKSPACE, "fk_workspace_set_poll_limit: workspace missing or smaller than its header");
+  if (limit > (long long)0x7fffffff) return fail(FK_ERR_INVALID, "poll limit must be < 2^31 (got %lld)", limit);
+  const uint32_t value = limit < 0 ? 0u : (uint32_t)limit + 1u;
+  hipLaunchKernelGGL(ws_set_word_kernel, dim3(1), dim3(1), 0, as_stream(stream), reinterpret_cast<uint32_t*>(workspace),
+                     kWorkspacePollWord, value);
+  return check_launch("ws_set_word_kernel");
 }
 
 }  // extern "C"

@@ -357,12 +357,13 @@ __device__ __forceinline__ float value_of(uint64_t w) { return __uint_as_float((
 
 // Bounded poll of N tagged words of this lane (src[j] == nullptr: no word):
 // re-reads every word that does not carry `tag` yet, all reads of one round
-// in flight together, until all carry it or kPollLimit rounds have passed.
-// Returns whether all carry the tag.
+// in flight together, until all carry it or `limit` rounds have passed
+// (limit 0: gives up at once).  Returns whether all carry the tag.
 constexpr uint32_t kPollLimit = 1u << 16;
 template <int N>
-__device__ __forceinline__ bool poll_tagged(uint64_t (&w)[N], const uint64_t* const (&src)[N], uint32_t tag) {
-  for (uint32_t i = 0; i < kPollLimit; ++i) {
+__device__ __forceinline__ bool poll_tagged(uint64_t (&w)[N], const uint64_t* const (&src)[N], uint32_t tag,
+                                            uint32_t limit) {
+  for (uint32_t i = 0; i < limit; ++i) {
     bool ready = true;
 #pragma unroll
     for (int j = 0; j < N; ++j) ready = ready && (src[j] == nullptr || tag_of(w[j]) == tag);
@@ -377,21 +378,47 @@ __device__ __forceinline__ bool poll_tagged(uint64_t (&w)[N], const uint64_t* co
 
 // Grid-wide barrier for kernels whose grid the host has capped at the number
 // of co-resident workgroups.  Called by one thread per workgroup after the
-// workgroup's publishing stores have been waited for.  The wait is bounded:
-// after `kSpinLimit` polls the workgroup records FK_DEVICE_ERR_BARRIER in
-// `*error` and continues, so a broken launch configuration can produce wrong
-// results but never a hang.
+// workgroup's publishing stores have been waited for.  The wait is bounded
+// (`limit` polls, see wait_limits): a wait that runs out records
+// FK_DEVICE_ERR_BARRIER in `*error` and returns false, so a broken launch
+// configuration gives flagged, poisoned results but never a hang.
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr uint32_t FK_DEVICE_ERR_BARRIER = 1u;
 
-__device__ __forceinline__ void grid_arrive_and_wait(uint32_t* counter, uint32_t target, uint32_t* error) {
+__device__ __forceinline__ bool grid_arrive_and_wait(uint32_t* counter, uint32_t target, uint32_t* error,
+                                                     uint32_t limit) {
   ticket_add(counter);
-  for (uint32_t i = 0; i < kSpinLimit; ++i) {
-    if (load_coherent(counter) >= target) return;
+  for (uint32_t i = 0; i < limit; ++i) {
+    if (load_coherent(counter) >= target) return true;
     __builtin_amdgcn_s_sleep(2);
   }
   __hip_atomic_fetch_or(error, FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return false;
 }
+
+// Wait bounds of a launch from its workspace header (16 words: epoch at
+// `epoch_word`, host-set poll bound + 1 at word 14, error flag at word 15):
+// 0 while the error flag is set (every wait gives up, outputs are NaN),
+// else the host's bound, else the built-in one.  `spin` is the grid
+// barrier's bound.  Also returns the launch tag, epoch + 1.
+struct WaitLimits {
+  uint32_t tag;
+  uint32_t poll;
+  uint32_t spin;
+};
+__device__ __forceinline__ WaitLimits wait_limits(const uint32_t* header, int epoch_word) {
+  const uint32_t epoch = load_coherent(&header[epoch_word]);
+  const uint32_t set = load_coherent(&header[14]);
+  const uint32_t err = load_coherent(&header[15]);
+  WaitLimits w;
+  w.tag = epoch + 1u;
+  w.poll = err ? 0u : set ? set - 1u : kPollLimit;
+  w.spin = err ? 0u : set ? set - 1u : kSpinLimit;
+  return w;
+}
+
+// Poisoned value of an output whose inputs a failed wait left invalid.
+__device__ __forceinline__ float poison_if(bool bad, float v) { return bad ? __builtin_nanf("") : v; }
 
 // Integer wave all-reductions (same lane schedule as wave_allreduce_f32).
 template <typename Op>

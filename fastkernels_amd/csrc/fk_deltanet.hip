@@ -549,12 +549,12 @@ constexpr int kStepHeadWGs = 4;  // workgroups per value head (value columns spl
 constexpr int kStepQCols = kStepD / kStepHeadWGs;  // value columns per head workgroup
 constexpr int kStepInPitch = 2 * kStepD + 2 * kStepQCols + 4;  // head workgroup inputs per token (q, k, v, z, a, b, pad)
 constexpr int kStepTilesAhead = 2;  // phase A weight tiles in flight per wavefront
-constexpr int kStepTicketEpoch = 0;
+constexpr int kStepTicketEpoch = kWorkspaceEpochWord;
 constexpr int kStepTicketError = kWorkspaceErrorWord;
 
 
 struct StepTagWs {
-  uint32_t* tickets;  // [16]: [0] epoch, [kWorkspaceErrorWord] error flag
+  uint32_t* tickets;  // [16] workspace header: epoch, poll bound, error flag (fk_host.h)
   uint64_t* mix;      // [T, C] conv'd qkv
   uint64_t* z;        // [T, V]
   uint64_t* a;        // [T, Hv]
@@ -634,7 +634,8 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   const int T = a.T, H = VALU_A ? 2048 : a.H, C = a.C, V = a.V, R = a.R, Hv = a.Hv;
   const int NC = 2 * T;  // MFMA columns in use: (hi, lo) per token
   const int NCP = NC <= 2 ? 2 : NC <= 4 ? 4 : NC <= 8 ? 8 : 16;  // staging columns (power of two)
-  const uint32_t tag = load_coherent(&a.tw.tickets[kStepTicketEpoch]) + 1u;
+  const WaitLimits wl = wait_limits(a.tw.tickets, kStepTicketEpoch);
+  const uint32_t tag = wl.tag, plim = wl.poll;
   const int n = lane & 15, g4 = lane >> 4;  // MFMA lane -> (column / A row, k group)
 
   // Roles.  Each value head runs on kStepHeadWGs workgroups at the end of
@@ -1027,11 +1028,13 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         srcs[j] = r < G ? a.tw.started + r : nullptr;
         w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
       }
-      ok = poll_tagged<2>(w, srcs, tag) && ok;
+      ok = poll_tagged<2>(w, srcs, tag, plim) && ok;
     }
     if (!ok) s_fail = 1;
     __syncthreads();
-    if (tid == 0) store_coherent(&a.tw.tickets[kStepTicketEpoch], tag);
+    // (not after a failed wait: a workgroup that has not read the epoch yet
+    // would take the next launch's tag; the error word poisons later launches)
+    if (tid == 0 && !s_fail) store_coherent(&a.tw.tickets[kStepTicketEpoch], tag);
   }
 
   // ---- phase B: gated delta rule, a quarter of one value head ------------
@@ -1063,7 +1066,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       uint64_t hw[1];
       const uint64_t* hs[1] = {tl >= 0 ? a.tw.hint_tile + tl : nullptr};
       hw[0] = hs[0] ? load_tagged(hs[0]) : 0ull;
-      if (!poll_tagged<1>(hw, hs, tag)) s_fail = 1;
+      if (!poll_tagged<1>(hw, hs, tag, plim)) s_fail = 1;
     }
     __syncthreads();
     // one batch of tagged loads in flight covers every input (T <= NT)
@@ -1093,13 +1096,15 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         }
         w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
       }
-      ok = poll_tagged<BB>(w, srcs, tag);
+      ok = poll_tagged<BB>(w, srcs, tag, plim);
 #pragma unroll
       for (int j = 0; j < BB; ++j)
         if (dsti[j] >= 0) s_in[dsti[j]] = value_of(w[j]);
     }
     if (!ok) s_fail = 1;
     __syncthreads();
+    // inputs incomplete (a failed wait): the head's outputs and state are NaN
+    const bool bad_in = s_fail;
     // Per token (wave t): l2-normalise q (times D^-1/2) and k in place; decay and beta.
     if (wave < T) {
       const int t = wave;
@@ -1174,11 +1179,12 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
           srcs[q] = a.tw.hss + ((size_t)head * kStepHeadWGs + q) * kStepMaxTokens + t;
           w[q] = load_tagged(srcs[q]);
         }
-        if (!poll_tagged<kStepHeadWGs>(w, srcs, tag)) s_fail = 1;
+        const bool hok = poll_tagged<kStepHeadWGs>(w, srcs, tag, plim);
+        if (!hok) s_fail = 1;
         float tot = 0.f;
 #pragma unroll
         for (int q = 0; q < kStepHeadWGs; ++q) tot += value_of(w[q]);
-        s_sc[t][2] = rsqrtf(tot / (float)kStepD + a.eps);
+        s_sc[t][2] = poison_if(!hok || bad_in, rsqrtf(tot / (float)kStepD + a.eps));
       }
       if (lane < kStepQCols) {
         const float zz = s_in[(size_t)t * kStepInPitch + 2 * kStepD + kStepQCols + lane];
@@ -1191,7 +1197,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     {
       const size_t base = ((size_t)head * kStepD + (size_t)sgr * 8) * kStepD + jcol;
 #pragma unroll
-      for (int m = 0; m < 8; ++m) reinterpret_cast<float*>(a.next_rec)[base + (size_t)m * kStepD] = S[m];
+      for (int m = 0; m < 8; ++m) reinterpret_cast<float*>(a.next_rec)[base + (size_t)m * kStepD] = poison_if(bad_in, S[m]);
     }
     __syncthreads();  // s_dyn is reused below
   }
@@ -1205,7 +1211,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       uint64_t hw[1];
       const uint64_t* hs[1] = {lane < nh * kStepHeadWGs ? a.tw.hint_head + h0 * kStepHeadWGs + lane : nullptr};
       hw[0] = hs[0] ? load_tagged(hs[0]) : 0ull;
-      if (!poll_tagged<1>(hw, hs, tag)) s_fail = 1;
+      if (!poll_tagged<1>(hw, hs, tag, plim)) s_fail = 1;
     }
     __syncthreads();
     // The T * kcu inputs: one chunk of 8 consecutive columns per thread.
@@ -1221,7 +1227,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         srcs[e] = live ? a.tw.norm + (size_t)t * V + (size_t)uks * kcu + c * 8 + e : nullptr;
         w[e] = srcs[e] ? load_tagged(srcs[e]) : 0ull;
       }
-      ok = poll_tagged<8>(w, srcs, tag);
+      ok = poll_tagged<8>(w, srcs, tag, plim);
       if (live) {
         float y[8];
 #pragma unroll
@@ -1234,6 +1240,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     }
     if (!ok) s_fail = 1;
     __syncthreads();
+    const bool bad_unit = s_fail;
     f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
@@ -1251,7 +1258,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     if (n < NC && (n & 1) == 0) {
       const size_t o = ((size_t)uks * T + (n >> 1)) * H + (size_t)urb * 128 + wave * 16 + g4 * 4;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) store_tagged(a.tw.part + o + q, pq[q], tag);
+      for (int q = 0; q < 4; ++q) store_tagged(a.tw.part + o + q, poison_if(bad_unit, pq[q]), tag);
     }
   }
 
@@ -1267,11 +1274,13 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         srcs[j] = j < nks ? a.tw.part + ((size_t)j * T + t) * H + b * 16 + r : nullptr;
         w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
       }
-      if (!poll_tagged<8>(w, srcs, tag)) s_fail = 1;
+      const bool pok = poll_tagged<8>(w, srcs, tag, plim);
+      if (!pok) s_fail = 1;
       float v = 0.f;
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         if (j < nks) v += value_of(w[j]);
+      v = poison_if(!pok, v);
       const size_t o = (size_t)t * H + b * 16 + r;
       a.update[o] = v;
       if (a.hidden_out) a.hidden_out[o] = raw_value<BFX>(xres[0]) + v;

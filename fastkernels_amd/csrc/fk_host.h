@@ -14,8 +14,16 @@ namespace fk {
 // returns `status`, so call sites read `return fail(FK_ERR_INVALID, "...")`.
 int fail(int status, const char* fmt, ...);
 
-// Word of every polling kernel's workspace (uint32 index) that records a
-// bounded wait that ran out.
+// Header of every polling kernel's workspace: 16 uint32 words at its start.
+// Word kWorkspaceEpochWord is the launch epoch of the tagged hand-offs (a
+// launch tags its words epoch + 1); kWorkspacePollWord is the host-set
+// bound on every in-kernel wait plus one (0: the built-in bound);
+// kWorkspaceErrorWord records a bounded wait that ran out.  While the error
+// word is set, every wait of a kernel on the workspace gives up at once and
+// its outputs are NaN, until fk_workspace_status(clear) resets the word and
+// advances the epoch past every word written so far.
+constexpr int kWorkspaceEpochWord = 8;
+constexpr int kWorkspacePollWord = 14;
 constexpr int kWorkspaceErrorWord = 15;
 
 // Normalized multi-matrix projection (fk_deltanet.hip), shared by the mixers.

@@ -415,12 +415,17 @@ __device__ void topk_select(const float* row, int E, int K, int lane, int& out_i
 // remaining candidate ("head": highest probability, lowest id on ties) and
 // every round takes the wave maximum of the heads, breaking probability ties
 // toward the lowest expert id.  Weights are renormalised by the sum of the
-// selected probabilities in selection order.
+// selected probabilities in selection order.  `bad`: the logits may be
+// incomplete (a failed wait): ids are clamped in range, weights are NaN.
 template <int NJE>
-__device__ void router_topk_token(const RouterArgs& a, int t, int lane) {
+__device__ void router_topk_token(const RouterArgs& a, int t, int lane, bool bad) {
   int id;
   float w;
   topk_select<NJE>(a.logits + (size_t)t * a.E, a.E, a.K, lane, id, w);
+  if (bad) {
+    id = min(max(id, 0), a.E - 1);
+    w = poison_if(true, w);
+  }
   if (lane < a.K) {
     const size_t o = (size_t)t * a.K + lane;
     a.ids_out[o] = id;
@@ -446,8 +451,10 @@ __global__ __launch_bounds__(256) void moe_router_kernel(RouterArgs a) {
   __shared__ int s_off[kMaxExperts];
   __shared__ int s_aidx[kMaxExperts];
   __shared__ int s_last;
+  __shared__ int s_bad;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int e = blockIdx.x * 4 + wave;
+  const uint32_t spin = wait_limits(a.ws.tickets, kTicketEpoch).spin;
   const int nch = a.H >> 3;
   const int tile = (a.T + gridDim.y - 1) / gridDim.y;
   const int tb = blockIdx.y * tile;
@@ -522,11 +529,13 @@ __global__ __launch_bounds__(256) void moe_router_kernel(RouterArgs a) {
   const uint32_t G = gridDim.x * gridDim.y;
   publish_wait();
   __syncthreads();
-  if (threadIdx.x == 0) grid_arrive_and_wait(&a.ws.tickets[kTicketRouterBarrier], G, &a.ws.tickets[kTicketError]);
+  if (threadIdx.x == 0)
+    s_bad = !grid_arrive_and_wait(&a.ws.tickets[kTicketRouterBarrier], G, &a.ws.tickets[kTicketError], spin);
   __syncthreads();
+  const bool bad = s_bad;
 
   const int gw = (blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave;
-  for (int t = gw; t < a.T; t += (int)G * 4) router_topk_token<NJE>(a, t, lane);
+  for (int t = gw; t < a.T; t += (int)G * 4) router_topk_token<NJE>(a, t, lane, bad);
 
   publish_wait();
   __syncthreads();
@@ -829,11 +838,14 @@ __global__ __launch_bounds__(256) void moe_down_kernel(ExpertArgs a) {
 // before the first use, in two dependent rounds (slot positions, weights,
 // gate and residual input; then the K + 1 rows of y), with indices clamped
 // in range and unused values dropped: a loop over the slots would make
-// each slot wait for its position and then for its y value.
+// each slot wait for its position and then for its y value.  While the
+// workspace's error word is set (a wait of the router that built the
+// tables ran out, now or in an earlier uncleared call) the outputs are NaN.
 template <bool BFX, bool LO>
 __global__ __launch_bounds__(256) void moe_combine_kernel(ExpertArgs a) {
   const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
   const size_t total = (size_t)a.T * a.H;
+  const bool bad = load_coherent(&a.ws.tickets[kTicketError]) != 0u;
   if (idx >= total) return;
   const int t = (int)(idx / a.H);
   const int h = (int)(idx - (size_t)t * a.H);
@@ -857,6 +869,7 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(ExpertArgs a) {
   for (int k = 0; k < 8; ++k)
     if (k < K) acc += wk[k] * yv[k];
   if (a.has_shared) acc += (a.sg ? g : 1.f) * ys;
+  acc = poison_if(bad, acc);
   a.out[idx] = acc;
   if constexpr (LO) a.layer_out[idx] = raw_value<BFX>(xr[0]) + acc;
 }
@@ -1317,7 +1330,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   // The launch tag (epoch + 1) is loaded after the wavefront's P1 weight
   // loads are issued: computed from a load issued first, it would make every
   // wavefront wait for that load before issuing anything else.
-  uint32_t tag = 0;
+  uint32_t tag = 0, plim = 0;
   bool have_tag = false;
   if (tid == 0) s_fail = 0;
   __syncthreads();
@@ -1346,7 +1359,11 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
           xr[j] = load_raw8<BFX>(a.x, (size_t)cc * 8);
           nr[j] = load_raw8<true>(a.nw, (size_t)cc * 8);
         }
-        tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
+        {
+          const WaitLimits wl = wait_limits(a.ws.tickets, kTicketEpoch);
+          tag = wl.tag;
+          plim = wl.poll;
+        }
         have_tag = true;
         float wn[4][8];
 #pragma unroll
@@ -1398,7 +1415,11 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
           wu[j] = load_raw8_stream<true>(f.sgu, (size_t)(I + i) * H + (size_t)c * 8);
         }
       }
-      tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
+      {
+        const WaitLimits wl = wait_limits(a.ws.tickets, kTicketEpoch);
+        tag = wl.tag;
+        plim = wl.poll;
+      }
       have_tag = true;
       fused_gateup_item<BFX>(wg, wu, a.x, H, lane, T, nullptr, &s_chunk[0][wave]);
     } else if (wave == 0) {
@@ -1415,7 +1436,11 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
         xr[j] = load_raw8<BFX>(a.x, (size_t)cc * 8);
         gr[j] = load_raw8<true>(gsrc, (size_t)cc * 8);
       }
-      tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
+      {
+        const WaitLimits wl = wait_limits(a.ws.tickets, kTicketEpoch);
+        tag = wl.tag;
+        plim = wl.poll;
+      }
       have_tag = true;
       float g8[4][8];
 #pragma unroll
@@ -1464,7 +1489,11 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
     }
     __syncthreads();
   }
-  if (!have_tag) tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
+  if (!have_tag) {
+    const WaitLimits wl = wait_limits(a.ws.tickets, kTicketEpoch);
+    tag = wl.tag;
+    plim = wl.poll;
+  }
   // Started record of this workgroup: every wavefront has used the epoch it
   // read (its LDS write needs the loaded value), so the epoch may advance
   // once all records of this launch are there.
@@ -1495,11 +1524,15 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       srcs[j] = ex < E ? a.ws.f_logits + (size_t)t * E + ex : nullptr;
       w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
     }
-    if (!poll_tagged<NJE>(w, srcs, tag)) s_fail = 1;
+    const bool ok = poll_tagged<NJE>(w, srcs, tag, plim);
+    if (!ok) s_fail = 1;
     float p[NJE];
 #pragma unroll
     for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
     topk_select_regs<NJE>(p, E, K, lane, tk_id, tk_w);
+    // (after a failed wait the logits may be stale: ids stay in range and
+    // every output of this workgroup is poisoned below)
+    if (!ok) tk_id = min(max(tk_id, 0), E - 1);
     if (lane < K) {
       s_ids[t * K + lane] = tk_id;
       s_w[t * K + lane] = tk_w;
@@ -1518,7 +1551,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
         srcs[j] = r < G ? a.ws.f_started + r : nullptr;
         w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
       }
-      if (!poll_tagged<kChunk>(w, srcs, tag)) s_fail = 1;
+      if (!poll_tagged<kChunk>(w, srcs, tag, plim)) s_fail = 1;
     }
   }
   if (ONE) {
@@ -1545,12 +1578,17 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
                    s_aoff, &s_nact);
     __syncthreads();
   }
-  if (b == 0 && tid == 0) store_coherent(&a.ws.tickets[kTicketEpoch], tag);
+  // A failed wait poisons every later output of the workgroup.  Workgroup 0
+  // advances the epoch only when every workgroup has read it (all started
+  // records carry this launch's tag): otherwise a late workgroup would take
+  // the next launch's tag and publish words that launch reads as its own.
+  const bool bad = s_fail;
+  if (b == 0 && tid == 0 && !bad) store_coherent(&a.ws.tickets[kTicketEpoch], tag);
   const int U = s_nact;
   if (b == 0) {
     for (int j = tid; j < P; j += 512) {
       a.ids_out[j] = s_ids[j];
-      a.w_out[j] = s_w[j];
+      a.w_out[j] = poison_if(bad, s_w[j]);
     }
   }
 
@@ -1592,7 +1630,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
     __syncthreads();
     if (tid < kFusedChunk * np) {
       const int pp = tid / kFusedChunk, l = tid % kFusedChunk;
-      store_tagged(a.ws.f_act + (size_t)(pa + pp) * I + i0 + l, s_chunk[pp][l], tag);
+      store_tagged(a.ws.f_act + (size_t)(pa + pp) * I + i0 + l, poison_if(bad, s_chunk[pp][l]), tag);
     }
     __syncthreads();
   }
@@ -1611,14 +1649,15 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       srcs[j] = idx < n_act ? a.ws.f_act + idx : idx < n_stage ? a.ws.f_sgate + (idx - n_act) : nullptr;
       w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
     }
-    stage_ok = poll_tagged<kFusedStage>(w, srcs, tag) && stage_ok;
+    stage_ok = poll_tagged<kFusedStage>(w, srcs, tag, plim) && stage_ok;
 #pragma unroll
     for (int j = 0; j < kFusedStage; ++j)
       if (srcs[j]) s_act[base + j * 512] = value_of(w[j]);
   }
   if (!stage_ok) s_fail = 1;
   __syncthreads();
-  if (tid == 0 && s_fail) __hip_atomic_fetch_or(err, FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const bool bad_out = s_fail;
+  if (tid == 0 && bad_out) __hip_atomic_fetch_or(err, FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
   // Down rows: each lane accumulates, per token, the gate- and routing-
   // weighted partial dots of every expert on its 8 columns; one wave sum per
@@ -1636,7 +1675,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
         const float wt = u < U ? s_wpos[u] : 0.f;
         acc = fmaf(wt, dot8_act_lds(dr[u], s_act + (size_t)(u < U ? u : 0) * I, lane, I), acc);
       }
-      const float o = wave_sum(acc);
+      const float o = poison_if(bad_out, wave_sum(acc));
       if (lane == 0) {
         f.out[r] = o;
         if (f.layer_out) f.layer_out[r] = raw_value<BFX>(x_first_raw[0]) + o;
@@ -1680,7 +1719,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
 #pragma unroll
     for (int tt = 0; tt < kFusedMaxTokens; ++tt) {
       if (tt < T) {
-        const float o = wave_sum(acc[tt]);
+        const float o = poison_if(bad_out, wave_sum(acc[tt]));
         if (lane == tt) {
           const size_t off = (size_t)tt * H + r;
           f.out[off] = o;
@@ -1797,7 +1836,8 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   const int nrb = (E + 7) / 8, tu = a.tu;
   const int ub = blockIdx.x % nrb, tb = blockIdx.x / nrb;
   const int e = ub * 8 + wave, t0 = tb * tu, ntok = max(0, min(tu, T - t0));
-  const uint32_t tag = load_coherent(&a.ws.tickets[kTicketEpoch]) + 1u;
+  const WaitLimits wl = wait_limits(a.ws.tickets, kTicketEpoch);
+  const uint32_t tag = wl.tag;
   if (tid == 0) s_fail = 0;
 
   // ---- logits of rows 8ub.. for tokens t0 .. t0 + ntok - 1 ----------------
@@ -1946,13 +1986,18 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
         srcs[j] = ex < E ? a.ws.f_logits + (size_t)t * E + ex : nullptr;
         w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
       }
-      if (!poll_tagged<NJE>(w, srcs, tag)) s_fail = 1;
+      const bool ok = poll_tagged<NJE>(w, srcs, tag, wl.poll);
+      if (!ok) s_fail = 1;
       float p[NJE];
 #pragma unroll
       for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
       int id;
       float wt;
       topk_select_regs<NJE>(p, E, K, lane, id, wt);
+      if (!ok) {  // stale logits: ids kept in range, weights poisoned
+        id = min(max(id, 0), E - 1);
+        wt = poison_if(true, wt);
+      }
       if (lane < K) {
         const int j = t * K + lane;
         a.ids_out[j] = id;
@@ -1987,7 +2032,7 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
       srcs[i] = j < P ? a.ws.f_sel + j : nullptr;
       w[i] = srcs[i] ? load_tagged(srcs[i]) : 0ull;
     }
-    if (!poll_tagged<NP>(w, srcs, tag)) s_fail = 1;
+    if (!poll_tagged<NP>(w, srcs, tag, wl.poll)) s_fail = 1;
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
       const int j = tid + i * kFusedWaves * kWave;
@@ -2002,9 +2047,12 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   }
   __syncthreads();
   if (tid == 0) {
-    store_coherent(&a.ws.tickets[kTicketEpoch], tag);
-    if (s_fail) __hip_atomic_fetch_or(&a.ws.tickets[kTicketError], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
+    // (not after a failed wait: a workgroup that has not read the epoch yet
+    // would take the next launch's tag; the error word, which the expert
+    // stage and every later launch on this workspace read, poisons them)
+    if (!s_fail) store_coherent(&a.ws.tickets[kTicketEpoch], tag);
+    else __hip_atomic_fetch_or(&a.ws.tickets[kTicketError], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
   }
   build_routing_tables_masks(s_ids, s_mask, T, K, E, a.ws, s_off);
 }

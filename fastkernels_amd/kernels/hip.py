@@ -54,6 +54,7 @@ __all__ = [
     "hip_synthetic_qwen36_moe_decode",
     "hip_synthetic_qwen36_deltanet_decode",
     "hip_synthetic_qwen36_deltanet_moe_decode",
+    "workspace_status",
     "TRITON_ALIASES",
 ]
 
@@ -113,6 +114,39 @@ def _workspace(kind: str, device: torch.device, nbytes: int) -> torch.Tensor:
             ws = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
             _workspaces[key] = ws
         return ws
+
+
+# Workspaces whose kernels wait on other workgroups (bounded waits, error word).
+_POLLING_KINDS = ("moe", "deltanet_step")
+
+
+def workspace_status(device: Any = None, *, clear: bool = True) -> None:
+    """Raise FastKernelsError (FK_ERR_DEVICE) if a bounded in-kernel wait of
+    an operator call on `device` (any stream) ran out since the last check.
+
+    The MoE and DeltaNet-step kernels hand values between workgroups and
+    assume all workgroups of a launch are resident at once; a wait that runs
+    out leaves NaN in the outputs built from incomplete inputs, and every
+    later call on the same cached workspace gives NaN until this check
+    clears the flag (`clear=True`).  Synchronises the workspaces' streams.
+    No counterpart in the reference (its kernels never wait on each other).
+    """
+
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    index = dev.index if dev.index is not None else torch.cuda.current_device()
+    lib = _lib.load()
+    failed: list[tuple[str, int, str]] = []
+    with _ws_lock:
+        items = [(k, ws) for k, ws in _workspaces.items() if k[0] in _POLLING_KINDS and k[1] == index]
+    for (kind, _, stream), ws in items:
+        status = lib.fk_workspace_status(ws.data_ptr(), ws.numel(), 1 if clear else 0, stream)
+        if status == _lib.FK_ERR_DEVICE:
+            failed.append((kind, status, lib.fk_last_error_detail().decode()))
+        elif status != _lib.FK_OK:
+            raise _lib.FastKernelsError("fk_workspace_status", status, lib.fk_last_error_detail().decode())
+    if failed:
+        kind, status, detail = failed[0]
+        raise _lib.FastKernelsError(f"fk_workspace_status ({kind} workspace)", status, detail)
 
 
 def _require_lib() -> None:

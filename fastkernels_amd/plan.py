@@ -41,6 +41,16 @@ def _check_device(workspace: torch.Tensor, device: torch.device, stream: torch.c
     _lib.call("fk_workspace_status", workspace.data_ptr(), workspace.numel(), 1, _stream_handle(stream, device))
 
 
+def _set_poll_limit(workspace: torch.Tensor, device: torch.device, limit: int | None,
+                    stream: torch.cuda.Stream | None) -> None:
+    """Bound every in-kernel wait of later steps to `limit` poll rounds
+    (stream-ordered; None restores the built-in bound, 0 makes every wait
+    give up at once: flagged NaN outputs, every kernel still ends)."""
+
+    _lib.call("fk_workspace_set_poll_limit", workspace.data_ptr(), workspace.numel(),
+              -1 if limit is None else int(limit), _stream_handle(stream, device))
+
+
 class MoeLayerPlan:
     """One MoE layer (router + experts + residual) at a fixed token count."""
 
@@ -138,10 +148,14 @@ class MoeLayerPlan:
     def check_device(self, stream: torch.cuda.Stream | None = None) -> None:
         _check_device(self.workspace, self.device, stream)
 
+    def set_poll_limit(self, limit: int | None, stream: torch.cuda.Stream | None = None) -> None:
+        _set_poll_limit(self.workspace, self.device, limit, stream)
+
 
 class DeltaNetStepPlan:
     """One Gated DeltaNet decode step (T rows through one state) + residual,
-    issued as the single fused C-ABI call fk_deltanet_step (three launches)."""
+    issued as one C-ABI call, fk_deltanet_step (one launch at the model's
+    shapes and dtypes)."""
 
     def __init__(
         self,
@@ -199,6 +213,9 @@ class DeltaNetStepPlan:
 
     def check_device(self, stream: torch.cuda.Stream | None = None) -> None:
         _check_device(self.workspace, self.device, stream)
+
+    def set_poll_limit(self, limit: int | None, stream: torch.cuda.Stream | None = None) -> None:
+        _set_poll_limit(self.workspace, self.device, limit, stream)
 
 
 class AttentionStepPlan:

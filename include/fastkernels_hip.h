@@ -56,14 +56,30 @@ int fk_abi_version(void);
 const char* fk_status_string(int status);
 const char* fk_last_error_detail(void);
 
-/* Device error word of a workspace.  The kernels that hand values between
- * workgroups (fk_moe_router, fk_moe_layer, fk_deltanet_step) poll with a
- * bounded wait; a wait that runs out sets this word and the kernel ends
- * normally with invalid outputs.  Synchronises `stream`, then returns FK_OK
- * or FK_ERR_DEVICE; `clear` != 0 also resets the word (stream-ordered).
+/* Device error word of a workspace of fk_moe_router / fk_moe_align /
+ * fk_moe_experts / fk_moe_layer or fk_deltanet_step.  Those kernels hand
+ * values between workgroups and assume that every workgroup of a launch is
+ * resident at once (the host caps their grids at the device's co-resident
+ * capacity); each wait is bounded.  A wait that runs out (another process
+ * or stream holding CUs for long) sets the error word, the kernel ends
+ * normally and the outputs its workgroups produced from incomplete inputs
+ * are NaN (routing weights, MoE outputs, DeltaNet update and recurrent
+ * state).  While the word stays set, every later call on the workspace
+ * gives NaN outputs.  This call synchronises `stream`, then returns FK_OK
+ * or FK_ERR_DEVICE; `clear` != 0 also resets the word (stream-ordered),
+ * after which calls give valid outputs again.
  * No counterpart in the reference: its Triton kernels never wait on another
- * program.  For callers that want to validate a run (tests, benchmarks). */
+ * program.  For callers that validate a run (tests, benchmarks). */
 int fk_workspace_status(const void* workspace, size_t workspace_bytes, int clear, void* stream);
+
+/* Bound on every in-kernel wait of the calls on `workspace` (same
+ * workspaces as fk_workspace_status), stream-ordered: `limit` poll rounds
+ * (0: each wait gives up at once, so every such call flags FK_ERR_DEVICE
+ * and gives NaN outputs, and every kernel still ends); a negative `limit`
+ * restores the built-in bound.  No counterpart in the reference: a test
+ * hook for the failure path, and a knob for callers that prefer an early
+ * flagged failure to a long wait. */
+int fk_workspace_set_poll_limit(void* workspace, size_t workspace_bytes, long long limit, void* stream);
 
 /* ------------------------------------------------------------------------ */
 /* MoE decode layer                                                          */

@@ -42,6 +42,9 @@ def test_workspace_status_rejects_missing_workspace():
     # Host-side check: no device access for a NULL or header-less workspace.
     assert _err("fk_workspace_status", None, 0, 0, None) == _lib.FK_ERR_WORKSPACE
     assert _err("fk_workspace_status", ctypes.c_void_p(256), 32, 0, None) == _lib.FK_ERR_WORKSPACE
+    assert _err("fk_workspace_set_poll_limit", None, 0, 0, None) == _lib.FK_ERR_WORKSPACE
+    assert _err("fk_workspace_set_poll_limit", ctypes.c_void_p(256), 32, 0, None) == _lib.FK_ERR_WORKSPACE
+    assert _err("fk_workspace_set_poll_limit", ctypes.c_void_p(256), 4096, 1 << 31, None) == _lib.FK_ERR_INVALID
 
 
 def test_workspace_sizes_are_monotone():

@@ -1,0 +1,169 @@
+"""Config 4: a stack of independent resident MoE layers run in order.
+
+Each layer reads the previous layer's fp32 layer output as its hidden
+state, as the reference's layer wrapper hands it on
+(kernels/triton/qwen36_layer.py:94-106) and as bench.py's stack leg runs
+it.  Two checks:
+  * reduced shapes, 4 layers, 3 decode steps at T = 1 and T = 8: every
+    layer's outputs against `oracle.moe_layer` applied to that layer's
+    input (bf16 input at layer 0, fp32 from layer 1 on);
+  * the full configuration, 40 layers of the real shape (64.7 GB
+    resident), T = 1 and T = 8: outputs finite, layer_out = layer_in + moe
+    bit for bit, each layer's routing equal to a standalone plan's on the
+    same input, and a captured HIP graph of the whole stack replayed three
+    times equal to the eager run bit for bit.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import pytest
+import torch
+
+import oracle
+from fastkernels_amd import workloads as wl
+from fastkernels_amd.plan import MoeLayerPlan
+from fastkernels_amd.spec import qwen36_35b_a3b_spec
+from tests.parity import assert_routing_parity, tol
+
+pytestmark = pytest.mark.gpu
+
+SPEC = qwen36_35b_a3b_spec()
+SMALL = dataclasses.replace(SPEC, num_experts=64, expert_intermediate_size=256, hidden_size=1024)
+K = 8
+
+
+def _chain(weight_sets, tokens, first_hidden):
+    plans = []
+    for w in weight_sets:
+        prev = plans[-1].layer_out if plans else None
+        plans.append(MoeLayerPlan(w, tokens, top_k=K, hidden=prev))
+    plans[0].hidden.copy_(first_hidden)
+    return plans
+
+
+def _moe_args(w):
+    return (w["norm_weight"], w["router_weight"], w["expert_gate_up_weight"], w["expert_down_weight"],
+            w["shared_gate_up_weight"], w["shared_down_weight"], w["shared_expert_gate_weight"])
+
+
+@pytest.mark.parametrize("tokens", [1, 8])
+def test_stack_layers_match_oracle_layer_by_layer(device, tokens):
+    layers, steps = 4, 3
+    cpu_sets = [wl.make_moe_weights(SMALL, seed=400 + l) for l in range(layers)]
+    gpu_sets = [{k: (None if v is None else v.to(device)) for k, v in s.items()} for s in cpu_sets]
+    plans = _chain(gpu_sets, tokens, torch.zeros(tokens, SMALL.hidden_size, dtype=torch.bfloat16, device=device))
+    for step in range(steps):
+        print(f"stack reduced T={tokens} step={step}", flush=True)
+        x0 = wl.make_hidden(tokens, SMALL.hidden_size, seed=410 + step)
+        plans[0].hidden.copy_(x0.to(device))
+        for p in plans:
+            p.run()
+        torch.cuda.synchronize()
+        for l, (p, w) in enumerate(zip(plans, cpu_sets)):
+            x = p.hidden.cpu()
+            assert x.dtype == (torch.bfloat16 if l == 0 else torch.float32)
+            o_lh, o_moe, o_logits, o_ids, _ = oracle.moe_layer(x, *_moe_args(w), top_k=K)
+            torch.testing.assert_close(p.logits.cpu(), o_logits, atol=1e-4, rtol=1e-4)
+            near = assert_routing_parity(p.logits, p.ids, p.weights, o_logits, K)
+            # under the kernel's own routing (always comparable)
+            ref = oracle.routed_experts(x, p.ids.cpu(), p.weights.cpu(), w["expert_gate_up_weight"],
+                                        w["expert_down_weight"])
+            ref = ref + oracle.shared_expert(x, w["shared_gate_up_weight"], w["shared_down_weight"],
+                                             w["shared_expert_gate_weight"])
+            torch.testing.assert_close(p.moe_out.cpu(), ref, **tol(torch.bfloat16))
+            torch.testing.assert_close(p.layer_out.cpu(), x.float() + ref, **tol(torch.bfloat16))
+            if near == 0:
+                assert torch.equal(p.ids.cpu(), o_ids)
+                torch.testing.assert_close(p.layer_out.cpu(), o_lh, **tol(torch.bfloat16))
+        for p in plans:
+            p.check_device()
+
+
+def _device_set(layer: int, device):
+    """Config-4 layer `layer` at the real shape, drawn on the device (seeded)."""
+
+    H, E, I = SPEC.hidden_size, SPEC.num_experts, SPEC.expert_intermediate_size
+    g = torch.Generator(device=device).manual_seed(5000 + layer)
+
+    def rnd(*shape):
+        out = torch.empty(shape, device=device, dtype=torch.bfloat16)
+        rows = shape[0]
+        step = 32 if len(shape) == 3 else rows
+        for s in range(0, rows, step):
+            out[s : s + step] = (torch.randn(min(step, rows - s), *shape[1:], generator=g, device=device)
+                                 * wl.WEIGHT_SCALE).to(torch.bfloat16)
+        return out
+
+    return {
+        "norm_weight": torch.zeros(H, device=device, dtype=torch.bfloat16),
+        "router_weight": rnd(E, H),
+        "expert_gate_up_weight": rnd(E, 2 * I, H),
+        "expert_down_weight": rnd(E, H, I),
+        "shared_gate_up_weight": rnd(2 * I, H),
+        "shared_down_weight": rnd(H, I),
+        "shared_expert_gate_weight": rnd(H),
+    }
+
+
+@pytest.fixture(scope="module")
+def stack40(device):
+    sets = []
+    for l in range(40):
+        sets.append(_device_set(l, device))
+        if l % 10 == 9:
+            print(f"generated {l + 1}/40 resident layers", flush=True)
+    torch.cuda.synchronize()
+    yield sets
+    sets.clear()
+    torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("tokens", [1, 8])
+def test_stack40_full_shape_properties_and_graph_replay(device, stack40, tokens):
+    H = SPEC.hidden_size
+    plans = _chain(stack40, tokens, wl.make_hidden(tokens, H, seed=7).to(device))
+    print(f"stack40 T={tokens}: eager", flush=True)
+    for p in plans:
+        p.run()
+    torch.cuda.synchronize()
+    for p in plans:
+        p.check_device()
+    eager = [(p.moe_out.clone(), p.layer_out.clone(), p.ids.clone(), p.logits.clone()) for p in plans]
+    for l, (p, (moe, lo, ids, _)) in enumerate(zip(plans, eager)):
+        assert bool(torch.isfinite(lo).all()), f"layer {l}"
+        assert torch.equal(lo, p.hidden.float() + moe), f"layer {l}: layer_out != layer_in + moe"
+        # ids: distinct per token, in range
+        assert int(ids.min()) >= 0 and int(ids.max()) < SPEC.num_experts
+        assert all(len(set(r)) == K for r in ids.cpu().tolist())
+    # every layer's routing equals a standalone plan's on the same input
+    for l in (0, 1, 19, 39):
+        solo = MoeLayerPlan(stack40[l], tokens, top_k=K, hidden_dtype=plans[l].hidden.dtype)
+        solo.hidden.copy_(plans[l].hidden)
+        solo.run()
+        torch.cuda.synchronize()
+        assert torch.equal(solo.ids, eager[l][2]), f"layer {l}"
+        assert torch.equal(solo.logits, eager[l][3]), f"layer {l}"
+        assert torch.equal(solo.layer_out, eager[l][1]), f"layer {l}"
+        solo.check_device()
+    # the whole stack captured as one graph, replayed three times
+    print(f"stack40 T={tokens}: graph", flush=True)
+    stream = torch.cuda.Stream(device)
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph, stream=stream):
+        for p in plans:
+            p.run(stream)
+    for replay in range(3):
+        for p in plans:  # clobber the outputs so stale values cannot pass
+            p.moe_out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for l, (p, (moe, lo, ids, logits)) in enumerate(zip(plans, eager)):
+            assert torch.equal(p.moe_out, moe), f"replay {replay} layer {l}"
+            assert torch.equal(p.layer_out, lo) and torch.equal(p.ids, ids) and torch.equal(p.logits, logits)
+    for p in plans:
+        p.check_device()
+    del graph
