@@ -52,6 +52,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [P, I, P, I, P, I, P, I, P, P, I, P, P, P, I, I, I, I, I, I, c_float, c_float, P, P, P, P, P, P, c_size_t, P],
     ),
+    "fk_moe_layer_noalloc": (
+        c_int,
+        [P, I, P, I, P, I, P, I, P, P, I, P, P, P, I, I, I, I, I, I, c_float, c_float, P, P, P, P, P, P],
+    ),
     "fk_expert_histogram": (c_int, [P, I, c_int64, I, P, P]),
     "fk_fused_swiglu": (c_int, [P, I, c_int64, I, P, P]),
     "fk_residual_add": (c_int, [P, I, P, c_int64, P, P]),

@@ -29,6 +29,7 @@
 #include "fk_host.h"
 
 #include <algorithm>
+#include <mutex>
 
 namespace fk {
 
@@ -2301,6 +2302,52 @@ static ExpertArgs make_expert_args(const void* hidden, int hidden_dt, const void
   return ea;
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free MoE layer: the workspace of fk_moe_layer lives in a
+// file-scope device array instead of caller memory.  Each GPU the library
+// runs on holds its own copy (kNoAllocScratchBytes) until the process ends;
+// every call on that GPU shares it.
+// ---------------------------------------------------------------------------
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[64] = {nullptr};
+
+__global__ __launch_bounds__(256) void zero_fill_kernel(u32x4* p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+    p[i] = u32x4{0u, 0u, 0u, 0u};
+}
+
+// Device address of this GPU's scratch array.  On the first call on a
+// device (with that device current) the address is taken with
+// hipGetSymbolAddress -- the array's name is only a host-side stand-in --
+// and the array is zero-filled on `stream` (the workspace contract: zero
+// once, then self-resetting).  That first call must not be under graph
+// capture: a captured fill would re-zero the launch epoch on every replay.
+static int noalloc_scratch(hipStream_t stream, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(FK_ERR_LAUNCH, "no current HIP device");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &cs) != hipSuccess) return fail(FK_ERR_LAUNCH, "hipStreamIsCapturing failed");
+    if (cs != hipStreamCaptureStatusNone)
+      return fail(FK_ERR_UNSUPPORTED,
+                  "the first fk_moe_layer_noalloc call on a device clears its scratch and must not be captured");
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail(FK_ERR_LAUNCH, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    hipLaunchKernelGGL(zero_fill_kernel, dim3(1024), dim3(256), 0, stream, reinterpret_cast<u32x4*>(p),
+                       kNoAllocScratchBytes / 16);
+    const int st = check_launch("zero_fill_kernel");
+    if (st) return st;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FK_OK;
+}
+
 }  // namespace fk
 
 using namespace fk;
@@ -2463,6 +2510,32 @@ int fk_moe_layer(const void* hidden, int hidden_dtype, const void* norm_weight, 
                                    shared_gate_dtype, tokens, hidden_size, intermediate, num_experts, top_k,
                                    moe_out, layer_out, ws);
   return launch_experts(ea, expert_dtype, as_stream(stream));
+}
+
+int fk_moe_layer_noalloc(const void* hidden, int hidden_dtype, const void* norm_weight, int norm_dtype,
+                         const void* router_weight, int router_dtype, const void* router_bias, int bias_dtype,
+                         const void* gate_up, const void* down, int expert_dtype, const void* shared_gate_up,
+                         const void* shared_down, const void* shared_gate, int shared_gate_dtype, int tokens,
+                         int hidden_size, int intermediate, int num_experts, int top_k, float eps,
+                         float norm_offset, float* logits, int64_t* topk_ids, float* topk_weights, float* moe_out,
+                         float* layer_out, void* stream) {
+  int st = validate_experts(hidden, hidden_dtype, gate_up, down, expert_dtype, shared_gate_up, shared_down,
+                            shared_gate, shared_gate_dtype, tokens, hidden_size, intermediate, num_experts, top_k);
+  if (st) return st;
+  MoeWs ws;
+  const size_t need = moe_ws_layout(tokens, top_k, num_experts, intermediate, hidden_size, nullptr, &ws);
+  if (need > kNoAllocScratchBytes)
+    return fail(FK_ERR_UNSUPPORTED,
+                "fk_moe_layer_noalloc: this problem needs %zu bytes of scratch, more than the %zu bytes each GPU "
+                "holds (use fk_moe_layer with a workspace of fk_moe_workspace_bytes)",
+                need, kNoAllocScratchBytes);
+  void* ptr = nullptr;
+  st = noalloc_scratch(as_stream(stream), &ptr);
+  if (st) return st;
+  return fk_moe_layer(hidden, hidden_dtype, norm_weight, norm_dtype, router_weight, router_dtype, router_bias,
+                      bias_dtype, gate_up, down, expert_dtype, shared_gate_up, shared_down, shared_gate,
+                      shared_gate_dtype, tokens, hidden_size, intermediate, num_experts, top_k, eps, norm_offset,
+                      logits, topk_ids, topk_weights, moe_out, layer_out, ptr, kNoAllocScratchBytes, stream);
 }
 
 }  // extern "C"

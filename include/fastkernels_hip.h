@@ -161,6 +161,34 @@ int fk_moe_layer(const void* hidden, int hidden_dtype,
                  float* moe_out, float* layer_out,
                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* fk_moe_layer without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * The workspace is a file-scope device array of FK_MOE_NOALLOC_SCRATCH_BYTES
+ * (16 MiB) that each GPU the library runs on holds until the process ends;
+ * a problem whose fk_moe_workspace_bytes exceeds it returns
+ * FK_ERR_UNSUPPORTED (at the model's shape: up to 174 tokens).  The call
+ * allocates nothing.  The first call on a device zero-fills the array on
+ * `stream` and must not be under graph capture; later calls may be.  Every
+ * call on a GPU shares that GPU's array, so calls that overlap on one GPU
+ * (on different streams, or from several threads) race and give wrong
+ * results; serialise them.  A bounded in-kernel wait that runs out gives
+ * NaN outputs for this call and every later one on the GPU (the array keeps
+ * the flag; callers that need to recover use fk_moe_layer with their own
+ * workspace and fk_workspace_status). */
+#define FK_MOE_NOALLOC_SCRATCH_BYTES (16u << 20)
+int fk_moe_layer_noalloc(const void* hidden, int hidden_dtype,
+                         const void* norm_weight, int norm_dtype,
+                         const void* router_weight, int router_dtype,
+                         const void* router_bias, int bias_dtype,
+                         const void* gate_up, const void* down, int expert_dtype,
+                         const void* shared_gate_up, const void* shared_down,
+                         const void* shared_gate, int shared_gate_dtype,
+                         int tokens, int hidden_size, int intermediate,
+                         int num_experts, int top_k, float eps, float norm_offset,
+                         float* logits, int64_t* topk_ids, float* topk_weights,
+                         float* moe_out, float* layer_out, void* stream);
+
 /* counts[e] = #{i : ids[i] == e} over n ids (int32 or int64); ids outside
  * [0, num_experts) are ignored.  counts is overwritten.
  * Replaces triton_expert_histogram (moe.py:87-102) as a standalone op. */
