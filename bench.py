@@ -60,6 +60,117 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def cpu_model_name() -> str:
+    """The host CPU's model string (/proc/cpuinfo), for the CPU baseline."""
+
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def copy_bandwidth_tbs(torch, dev) -> float:
+    """Read + write TB/s of 16 device-to-device copies of 1 GiB."""
+
+    nbytes = 1 << 30
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(16):
+        dst.copy_(src)
+    end.record()
+    end.synchronize()
+    secs = start.elapsed_time(end) * 1e-3
+    del src, dst
+    torch.cuda.empty_cache()
+    return round(2 * nbytes * 16 / secs / 1e12, 3)
+
+
+def read_bandwidth_tbs(torch, dev) -> float:
+    """TB/s of fk_stream_read over 4 GiB (16-byte non-temporal loads, as the
+    weight streams use), 8 timed passes after one warm pass."""
+
+    from fastkernels_amd import _lib
+
+    nbytes = 4 << 30
+    src = torch.ones(nbytes // 2, dtype=torch.bfloat16, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    _lib.call("fk_stream_read", src.data_ptr(), nbytes, sink.data_ptr(), stream.cuda_stream)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(8):
+        _lib.call("fk_stream_read", src.data_ptr(), nbytes, sink.data_ptr(), stream.cuda_stream)
+    end.record(stream)
+    end.synchronize()
+    secs = start.elapsed_time(end) * 1e-3
+    del src, sink
+    torch.cuda.empty_cache()
+    return round(nbytes * 8 / secs / 1e12, 3)
+
+
+def cpu_time(fn, seconds: float, min_iters: int = 2) -> tuple[float, int]:
+    """Microseconds per call of fn() after one warmup call, over >= min_iters
+    calls and about `seconds` of wall time."""
+
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        if n >= min_iters and time.perf_counter() - t0 > seconds:
+            break
+    return (time.perf_counter() - t0) / n * 1e6, n
+
+
+def cpu_other_configs(oracle, torch, wl, spec, w_cpu, args_cpu, cpu_layers, K, E, H) -> dict:
+    """The oracle on the other BASELINE configs (same inputs as the GPU
+    runs' weight set 0), a few seconds each."""
+
+    out = {}
+    x1 = wl.make_hidden(1, H, seed=1)
+    us, n = cpu_time(lambda: oracle.moe_layer(x1, *args_cpu, top_k=K), 3.0)
+    out["moe_t1"] = {"us_per_layer_step": round(us, 1), "iterations": n}
+    x128 = wl.make_hidden(128, H, seed=1)
+    bias = wl.zipf_router_bias(E, seed=0)
+    us, n = cpu_time(lambda: oracle.moe_layer(x128, *args_cpu, top_k=K, router_bias=bias), 4.0)
+    out["moe_t128_zipf"] = {"us_per_layer_step": round(us, 1), "iterations": n}
+    d = wl.make_deltanet_weights(spec, seed=2000)
+    kw = dict(qk_heads=spec.deltanet_qk_heads, value_heads=spec.deltanet_value_heads, head_dim=spec.deltanet_head_dim)
+    for tokens in (1, 8):
+        x = wl.make_hidden(tokens, H, seed=50)
+        us, n = cpu_time(lambda: oracle.deltanet_update(x, d["conv_state"], d["recurrent_state"], d, **kw), 3.0)
+        out[f"deltanet_t{tokens}"] = {"us_per_step": round(us, 1), "iterations": n}
+    if cpu_layers:
+        args_l = [(w["norm_weight"], w["router_weight"], w["expert_gate_up_weight"], w["expert_down_weight"],
+                   w["shared_gate_up_weight"], w["shared_down_weight"], w["shared_expert_gate_weight"])
+                  for w in cpu_layers]
+        for tokens in (1, 8):
+            x0 = wl.make_hidden(tokens, H, seed=7)
+
+            def two_layers():
+                h = oracle.moe_layer(x0, *args_l[0], top_k=K)[0]
+                oracle.moe_layer(h, *args_l[1], top_k=K)
+
+            us, n = cpu_time(two_layers, 3.0)
+            out[f"moe_stack40_t{tokens}"] = {
+                "us_per_layer_step": round(us / 2, 1),
+                "us_per_stack_step_extrapolated": round(us / 2 * 40, 1),
+                "iterations": n,
+                "sample": "layers 0 and 1 of the stack chained (fp32 hidden into layer 1); the 40-layer step "
+                          "extrapolated as 40 x the per-layer time (the full stack needs 64.7 GB of host RAM)",
+            }
+    return out
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -110,9 +221,11 @@ def main() -> int:
                 out[s : s + 32] = rnd(min(32, shape[0] - s), *shape[1:])
             return out
 
+        # (the router weight comes from the CPU generator, as the tests draw
+        # it, so the config-2 Zipf calibration holds for these very sets)
         return {
             "norm_weight": torch.zeros(H, device=dev, dtype=torch.bfloat16),
-            "router_weight": rnd(E, H),
+            "router_weight": wl.make_router_weight(spec, seed=r).to(dev),
             "expert_gate_up_weight": rnd_big(E, 2 * I, H),
             "expert_down_weight": rnd_big(E, H, I),
             "shared_gate_up_weight": rnd(2 * I, H),
@@ -367,9 +480,22 @@ def main() -> int:
         r128 = moe_result(128, bias=bias, nsets=min(R, 4), steps=min(args.steps, 32))
         p128 = r128.pop("_plans")
         torch.cuda.synchronize()
-        counts = torch.bincount(p128[0].ids.reshape(-1), minlength=E)
-        r128["hottest_expert_tokens"] = int(counts.max())
+        r128["hottest_expert_tokens"] = [int(torch.bincount(p.ids.reshape(-1), minlength=E).max()) for p in p128]
         r128["zipf_alpha"] = wl.ZIPF_ALPHA
+        # MFMA utilisation of the expert stage (dense bf16 peak 2.5 PFLOP/s):
+        # useful flops are 2 per multiply-add of the (token, slot) pairs'
+        # gate/up (2I x H) and down (H x I) products plus the shared expert's;
+        # the kernels execute more (tokens padded to 16-column tiles, and the
+        # down kernel's fp32 activations as two bf16 columns each, hi + lo).
+        n_rows = 128 * K + 128
+        useful = n_rows * 6 * H * I
+        cnt = torch.bincount(p128[0].ids.reshape(-1), minlength=E).tolist() + [128]  # + the shared expert
+        gu_cols = sum(-(-c // 16) * 16 for c in cnt)  # gate/up: 16 tokens per tile
+        dn_cols = sum(-(-c // 8) * 16 for c in cnt)  # down: 8 tokens (hi + lo columns) per tile
+        executed = gu_cols * 4 * H * I + dn_cols * 2 * H * I
+        r128["mfma_flops_useful"] = int(useful)
+        r128["mfma_flops_executed_set0"] = int(executed)
+        r128["mfma_util"] = round(useful / (r128["expert_stage_us"] * 1e-6) / 2.5e15, 5)
         sub["moe_t128_zipf"] = r128
         del p128
         log("timing Gated DeltaNet step T=1 and T=8")
@@ -377,8 +503,11 @@ def main() -> int:
             sub[f"deltanet_t{tokens}"] = deltanet_result(tokens)
         log("timing the gated attention step T=1 after 1024 cached positions")
         sub["attention_t1_ctx1024"] = attention_result(1, 1024)
+    cpu_layers = None
     if not args.no_extra and not args.no_stack:
         lsets = [moe_set(100 + l) for l in range(max(args.stack_layers, spec.num_layers))]
+        if not args.no_cpu_baseline:  # two config-4 layers for the CPU baseline's stack sample
+            cpu_layers = [{k: v.cpu() for k, v in lsets[l].items()} for l in range(2)]
         for tokens in (1, 8):
             log(f"timing the {args.stack_layers}-layer resident stack, T={tokens} (config 4)")
             sub[f"moe_stack{args.stack_layers}_t{tokens}"] = stack_result(tokens, args.stack_layers, 32, lsets)
@@ -387,6 +516,12 @@ def main() -> int:
         del lsets
         torch.cuda.synchronize()
         torch.cuda.empty_cache()
+
+    # -- measured device-copy bandwidth (read + write), for the fraction of a
+    # bandwidth this GPU actually reaches ---------------------------------------
+    log("device copy bandwidth (1 GiB, 16 copies) and read-stream bandwidth (4 GiB, 8 passes)")
+    copy_tbs = copy_bandwidth_tbs(torch, dev)
+    read_tbs = read_bandwidth_tbs(torch, dev)
 
     # -- CPU baseline (oracle on the host cores, bounded sample) ----------------
     cpu = None
@@ -414,9 +549,11 @@ def main() -> int:
             "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"MoE layer T={args.tokens} (weight set 0, same bytes as the GPU run), {n} iterations after 1 warmup",
-            "cpu_model": platform.processor() or platform.machine(),
+            "cpu_model": cpu_model_name(),
             "os_cpu_count": os.cpu_count(),
         }
+        if not args.no_extra:
+            cpu["other_configs"] = cpu_other_configs(oracle, torch, wl, spec, w_cpu, args_cpu, cpu_layers, K, E, H)
         del w_cpu
 
     expert_frac = main_res["expert_stage_tbs"] * 1e12 / (HBM_PEAK_GBS * 1e9)
@@ -429,6 +566,10 @@ def main() -> int:
             rec = json.load(fh).get(f"moe_layer_t{args.tokens}")
         if rec:
             traffic = rec["expert_stage_traffic_bytes"]
+    for r in [main_res, *sub.values()]:
+        if isinstance(r, dict) and "achieved_tbs" in r:
+            r["frac_of_measured_copy"] = round(r["achieved_tbs"] / copy_tbs, 4) if copy_tbs else None
+            r["frac_of_measured_read"] = round(r["achieved_tbs"] / read_tbs, 4) if read_tbs else None
     line = {
         "metric": METRIC,
         "value": main_res["us_per_layer_step"],
@@ -461,8 +602,18 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(expert_frac, 4),
             "traffic": traffic,
+            "traffic_source": "profiles/pmc_traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes of this "
+                              "workload's expert stage, scaled by a 1 GiB copy calibration (not measured in this run)"
+                              if traffic is not None else None,
             "algorithmic_bytes": main_res["expert_stage_bytes"],
+            "scope": "expert stage only (3 launches); the whole layer step, router included, is layer.hbm_frac",
+            "frac_of_measured_copy": round(main_res["expert_stage_tbs"] / copy_tbs, 4) if copy_tbs else None,
+            "frac_of_measured_read": round(main_res["expert_stage_tbs"] / read_tbs, 4) if read_tbs else None,
         },
+        "copy_bandwidth_tbs": copy_tbs,
+        "read_bandwidth_tbs": read_tbs,
+        "measured_bandwidth_note": "copy: torch device-to-device copy of 1 GiB, read + write bytes; read: "
+                                   "fk_stream_read over 4 GiB, 16-byte non-temporal loads like the weight streams",
         "layer": main_res,
         "sub_results": sub,
         "cpu_baseline": cpu,

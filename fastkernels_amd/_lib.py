@@ -59,6 +59,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "fk_expert_histogram": (c_int, [P, I, c_int64, I, P, P]),
     "fk_fused_swiglu": (c_int, [P, I, c_int64, I, P, P]),
     "fk_residual_add": (c_int, [P, I, P, c_int64, P, P]),
+    "fk_stream_read": (c_int, [P, c_size_t, P, P]),
     "fk_attention_workspace_bytes": (c_size_t, [I, I, I, I]),
     "fk_attention_project": (c_int, [P, I, P, I, P, P, P, I, I, I, I, I, c_float, c_float, P, P, P, P]),
     "fk_attention_decode": (

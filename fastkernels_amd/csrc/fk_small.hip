@@ -242,7 +242,41 @@ __global__ __launch_bounds__(256) void synthetic_deltanet_kernel(SynDnArgs a) {
 
 using namespace fk;
 
+// Read-only stream (bandwidth probe): every 16-byte vector of [src, src +
+// n16) is loaded once, non-temporal, four loads in flight per thread per
+// iteration; the values feed an XOR whose result is stored only if it hits
+// a value the host never passes, so the loads stay and nothing is written.
+__global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* src, size_t n16, uint32_t never,
+                                                          uint32_t* sink) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  uint32_t acc = 0u;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const u32x4 a = __builtin_nontemporal_load(src + i);
+    const u32x4 b = __builtin_nontemporal_load(src + i + stride);
+    const u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
+    const u32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
+    acc ^= a.x ^ a.y ^ a.z ^ a.w ^ b.x ^ b.y ^ b.z ^ b.w ^ c.x ^ c.y ^ c.z ^ c.w ^ d.x ^ d.y ^ d.z ^ d.w;
+  }
+  for (; i < n16; i += stride) {
+    const u32x4 a = __builtin_nontemporal_load(src + i);
+    acc ^= a.x ^ a.y ^ a.z ^ a.w;
+  }
+  if (acc == never) sink[0] = acc;
+}
+
 extern "C" {
+
+int fk_stream_read(const void* src, size_t bytes, uint32_t* sink, void* stream) {
+  if (!src || !sink) return fail(FK_ERR_INVALID, "src and sink must be non-NULL");
+  if (!aligned16(src) || bytes % 16) return fail(FK_ERR_ALIGNMENT, "src must be 16-byte aligned and bytes a multiple of 16");
+  const int cus = device_cus();
+  if (cus < 1) return fail(FK_ERR_LAUNCH, "no current HIP device");
+  // 32 workgroups of 256 threads per CU (8 per SIMD)
+  hipLaunchKernelGGL(stream_read_kernel, dim3(cus * 32), dim3(256), 0, as_stream(stream),
+                     reinterpret_cast<const u32x4*>(src), bytes / 16, 0x9e3779b9u, sink);
+  return check_launch("stream_read_kernel");
+}
 
 int fk_expert_histogram(const void* ids, int ids_dtype, int64_t n, int num_experts, int32_t* counts, void* stream) {
   if (!is_index_dtype(ids_dtype)) return fail(FK_ERR_DTYPE, "ids must be int32 or int64");

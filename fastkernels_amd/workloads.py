@@ -31,9 +31,11 @@ from .spec import Qwen36A3BSpec, qwen36_35b_a3b_spec
 WEIGHT_SCALE = 0.02
 STATE_SCALE = 0.1
 ZIPF_S = 1.1
-# Chosen so that at T=128 (seed 0) the hottest experts receive 20-60 tokens;
-# see tests/test_workloads.py for the check.
-ZIPF_ALPHA = 0.35
+# Chosen so that at T=128 the hottest expert receives 20-60 tokens (40-54)
+# for each of the router weights make_router_weight(seed=r), r = 0..7, with
+# hidden states make_hidden(128, seed=r + 1): the weight sets bench.py
+# times; tests/test_workloads.py checks it.
+ZIPF_ALPHA = 0.28
 
 
 def _randn(gen: torch.Generator, shape: tuple[int, ...], scale: float, dtype: torch.dtype, device: Any) -> torch.Tensor:
@@ -57,6 +59,15 @@ def _randn_chunked(gen, shape, scale, dtype, device, chunk: int = 16) -> torch.T
 def make_hidden(tokens: int, hidden_size: int, *, seed: int, dtype=torch.bfloat16, device: Any = "cpu") -> torch.Tensor:
     gen = torch.Generator(device="cpu").manual_seed(seed)
     return _randn(gen, (tokens, hidden_size), 1.0, dtype, device)
+
+
+def make_router_weight(spec: Qwen36A3BSpec | None = None, *, seed: int, dtype=torch.bfloat16, device: Any = "cpu") -> torch.Tensor:
+    """The router weight [E, H] of `make_moe_weights(seed=seed)` (its first
+    draw), without drawing the experts."""
+
+    spec = spec or qwen36_35b_a3b_spec()
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    return _randn(gen, (spec.num_experts, spec.hidden_size), WEIGHT_SCALE, dtype, device)
 
 
 def make_moe_weights(
