@@ -13,7 +13,7 @@
 //   cache[start + t] = (k, v); o_h = softmax(q_h . K_j[0..p] / sqrt(hd)) V_j[0..p]
 //   update = (o * sigmoid(gate)) Wo^T;  hidden_out = x + update
 //
-// Kernels (three launches per step):
+// Kernels (four launches per step):
 //   attn_proj_kernel  RMSNorm folded into a GEMV over [Wq | Wk | Wv] (9216
 //                     rows at the model shape); H > 2048 takes the shared
 //                     normalized projection kernel of fk_deltanet.hip
@@ -22,13 +22,18 @@
 //                     positions (each cached row read once per chunk), head
 //                     norms and RoPE in LDS, the step's new keys recomputed
 //                     from k (no dependence on another workgroup's cache
-//                     write), online softmax; the last chunk to finish merges
-//                     the chunks and applies the gate
+//                     write), online softmax; a single chunk writes the
+//                     gated output, more chunks leave per-chunk partials
+//   attn_merge_kernel grid (heads, T), one thread per dim: merges the chunk
+//                     partials and applies the gate (returns at once when
+//                     one chunk covered the positions)
 //   attn_out_kernel   grid ceil(H/4): 4 rows of Wo per workgroup (1 per
 //                     wavefront, loaded once) against every token; residual;
 //                     advances a device-held position
 #include "fk_common.h"
 #include "fk_host.h"
+
+#include <type_traits>
 
 namespace fk {
 
@@ -52,7 +57,6 @@ struct AttnArgs {
   int interleaved;
   float* gated;         // [T, heads * hd]  o * sigmoid(gate)
   float* part;          // [T, heads, max_chunks, hd + 2] per-chunk (max, sum, weighted values)
-  uint32_t* tickets;    // [T, kv_heads] chunk arrivals (self-resetting)
   int chunk, max_chunks;
   int hsplit;           // workgroups per kv head: each takes G / hsplit of its query heads
 };
@@ -61,7 +65,6 @@ constexpr int kAttnMaxKvHeads = 64;
 constexpr int kAttnMaxChunks = 64;  // position chunks per (token, kv head): the merge reads at most this many
 
 struct AttnWs {
-  uint32_t* tickets;
   float* qg;
   float* k;
   float* v;
@@ -76,10 +79,6 @@ static size_t attn_ws_layout(int T, int heads, int kvh, int hd, char* base, Attn
     off = align_up(off + bytes, 256);
     return base ? reinterpret_cast<float*>(base + at) : nullptr;
   };
-  // (t, kv head, head split) tickets in a region of fixed size at the start
-  // of every layout, so calls of different shapes sharing a workspace find
-  // them at zero
-  ws->tickets = reinterpret_cast<uint32_t*>(take((size_t)kAttnMaxTokens * kAttnMaxKvHeads * 8 * 4));
   ws->qg = take((size_t)T * heads * 2 * hd * 4);
   ws->k = take((size_t)T * kvh * hd * 4);
   ws->v = take((size_t)T * kvh * hd * 4);
@@ -99,6 +98,27 @@ __device__ __forceinline__ float4 load4(const void* p, size_t i) {
   }
 }
 
+// Four consecutive elements of a cache row, raw (bf16: 8 bytes, converted
+// where used, so a pass of rows in flight takes half the registers).
+template <bool BF>
+struct Row4 {
+  typename std::conditional<BF, uint2, float4>::type r;
+  __device__ __forceinline__ float4 f4() const {
+    if constexpr (BF)
+      return make_float4(__uint_as_float(r.x << 16), __uint_as_float(r.x & 0xffff0000u), __uint_as_float(r.y << 16),
+                         __uint_as_float(r.y & 0xffff0000u));
+    else
+      return r;
+  }
+};
+template <bool BF>
+__device__ __forceinline__ Row4<BF> load_row4(const void* p, size_t i) {
+  Row4<BF> v;
+  if constexpr (BF) v.r = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p) + i);
+  else v.r = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
+  return v;
+}
+
 template <bool BF>
 __device__ __forceinline__ void store1(void* p, size_t i, float v) {
   if constexpr (BF) reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16_bits(v);
@@ -116,13 +136,13 @@ __device__ __forceinline__ float block256_sum(float v, float* s_red) {
 }
 
 // RMSNorm(1 + w) and RoPE at `pos` of one head held one dim per thread
-// (thread d < hd); `s_vec` is the head's LDS row.  Returns dim d's value.
-__device__ __forceinline__ float norm_rope(float x, const void* w, int w_dt, const AttnArgs& a, int pos, float* s_vec,
-                                           float* s_red) {
+// (thread d < hd; wd: the norm weight of dim d); `s_vec` is the head's LDS
+// row.  Returns dim d's value.
+__device__ __forceinline__ float norm_rope(float x, float wd, const AttnArgs& a, int pos, float* s_vec, float* s_red) {
   const int d = threadIdx.x;
   const bool in = d < a.hd;
   const float ss = block256_sum(in ? x * x : 0.f, s_red);
-  float y = in ? x * rsqrtf(ss / (float)a.hd + a.eps) * (1.f + load_scalar(w, w_dt, d)) : 0.f;
+  float y = in ? x * rsqrtf(ss / (float)a.hd + a.eps) * (1.f + wd) : 0.f;
   const int rd = a.rope_dim;
   if (in) s_vec[d] = y;
   __syncthreads();
@@ -154,21 +174,21 @@ __device__ __forceinline__ float norm_rope(float x, const void* w, int w_dt, con
 // cached row is read once per chunk.  Wavefront w takes positions c*C + w,
 // + 4, .., eight in flight; per position the G dot products are summed over
 // the lanes at once (rows8_sum) and each head keeps an online softmax (max,
-// sum, 4 dims of the weighted value sum per lane).  The chunk's per-head
-// partials go to the workspace; the workgroup that arrives last for (t, j)
-// (device-scope ticket, release/acquire) merges the chunks, applies the gate
-// and resets the ticket.
+// sum, 4 dims of the weighted value sum per lane).  The wavefronts' states
+// are combined through LDS; with one chunk the gated output is written
+// here, otherwise the chunk's per-head partials go to the workspace and
+// attn_merge_kernel combines the chunks (a separate launch: merging in the
+// last workgroup to arrive costs a device-scope release/acquire per
+// workgroup and a serial chain of partial loads in that workgroup).
 template <bool CBF>
 __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
-  constexpr int MAXG = 8, NB = 8;
+  constexpr int MAXG = 8, NB = CBF ? 4 : 8;  // (a bf16 cache also holds its step's own values: fewer rows in flight)
   extern __shared__ float4 s_dyn[];  // [G][hd] scaled queries, then [T][hd] new keys
   __shared__ float s_tmp[kAttnMaxHeadDim];
   __shared__ float s_red[4];
   __shared__ float s_m[4][MAXG], s_l[4][MAXG];
-  __shared__ __align__(16) float s_acc[4][kAttnMaxHeadDim];
-  __shared__ int s_last;
+  __shared__ __align__(16) float s_acc[4][MAXG][kAttnMaxHeadDim];
   __shared__ float s_ss[4][MAXG];
-  __shared__ float s_cm2[MAXG][kAttnMaxChunks], s_cl2[MAXG][kAttnMaxChunks], s_L[MAXG];
   const int c = blockIdx.x, j = blockIdx.y / a.hsplit, hs = blockIdx.y - j * a.hsplit, t = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hd = a.hd, G = a.heads / a.kvh / a.hsplit;  // query heads of this workgroup
@@ -189,22 +209,71 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   if (c >= nc) return;
   const int p_lo = c * C, p_hi = min(p_lo + C, pos + 1);
 
-  // queries of the G heads at once (thread d: dim d of every head): norms
-  // from one transposed lane reduction, RoPE at pos, 1/sqrt(hd)
+  // Loads first, in the order their data is used: the queries (and gates),
+  // then this wavefront's first pass of cached rows, which arrive while the
+  // queries are normalised and rotated.  Every load is unconditional
+  // (clamped in range, unused values dropped after): a load under a
+  // condition makes the compiler wait for the loads before it.
+  const int d0 = lane * 4;
+  const bool lin = d0 < hd;
+  const int dl = lin ? d0 : 0;  // (idle lanes read dim 0)
   float gate[MAXG];  // this thread's gate values, loaded with the queries (used at the end)
-  {
+  float4 q4[MAXG], acc[MAXG];
+  float m[MAXG], l[MAXG];
+  // OWN: the chunk holds some of the step's own positions (start ..), whose
+  // keys are recomputed here and whose values come from v; their cache rows
+  // are stale and are read only to keep the loads unconditional.
+  auto body = [&](auto own_tag) {
+    constexpr bool OWN = decltype(own_tag)::value;
     float xq[MAXG], sq[MAXG];
+    const int dq = in ? tid : 0;
 #pragma unroll
     for (int g = 0; g < MAXG; ++g) {
-      const size_t qb = (size_t)t * 2 * qw + (size_t)(hb + g) * 2 * hd + tid;
-      xq[g] = in && g < G ? a.qg[qb] : 0.f;
-      gate[g] = in && g < G ? a.qg[qb + hd] : 0.f;
+      const size_t qb = (size_t)t * 2 * qw + (size_t)(hb + min(g, G - 1)) * 2 * hd + dq;
+      xq[g] = a.qg[qb];
+      gate[g] = a.qg[qb + hd];
+    }
+    const uint32_t qnw = elem_word(a.qn_w, a.qn_dt, dq);
+    // the key norm weight and the first own position's k (OWN chunks)
+    const uint32_t knw = elem_word(a.kn_w, a.kn_dt, dq);
+    const int u_lo = max(p_lo, start) - start, u_hi = p_hi - 1 - start;
+    const float k_first = a.k[(size_t)(OWN ? u_lo : 0) * kvw + (size_t)j * hd + dq];
+    // (an fp32 cache takes the step's own values from v with the same load,
+    // its address chosen arithmetically; a bf16 cache loads both)
+    constexpr bool VN = OWN && CBF;
+    Row4<CBF> kk[NB], vv[NB];
+    float4 vn[VN ? NB : 1];
+    auto load_pass = [&](int p0) {
+#pragma unroll
+      for (int bb = 0; bb < NB; ++bb) {
+        const int p = min(p0 + 4 * bb, p_hi - 1);
+        const size_t cr = ((size_t)p * a.kvh + j) * hd + dl;
+        kk[bb] = load_row4<CBF>(a.kc, cr);
+        if constexpr (OWN && !CBF) {
+          const float* vsrc = p >= start ? a.v + (size_t)(p - start) * kvw + (size_t)j * hd + dl
+                                         : reinterpret_cast<const float*>(a.vc) + cr;
+          vv[bb] = load_row4<CBF>(vsrc, 0);  // (CBF false here)
+        } else {
+          vv[bb] = load_row4<CBF>(a.vc, cr);
+        }
+        if constexpr (VN)
+          vn[bb] = *reinterpret_cast<const float4*>(a.v + (p >= start ? (size_t)(p - start) * kvw : 0) + (size_t)j * hd + dl);
+      }
+    };
+    const int p_first = p_lo + wave;
+    load_pass(p_first);
+
+    // queries of the G heads at once (thread d: dim d of every head): norms
+    // from one transposed lane reduction, RoPE at pos, 1/sqrt(hd)
+#pragma unroll
+    for (int g = 0; g < MAXG; ++g) {
+      xq[g] = in && g < G ? xq[g] : 0.f;
       sq[g] = xq[g] * xq[g];
     }
     const float r = rows8_sum(sq);
     if ((lane & 7) == 0) s_ss[wave][lane >> 3] = r;
     __syncthreads();
-    const float wq = in ? 1.f + load_scalar(a.qn_w, a.qn_dt, tid) : 0.f;
+    const float wq = in ? 1.f + elem_value(qnw, a.qn_w, a.qn_dt, dq) : 0.f;
 #pragma unroll
     for (int g = 0; g < MAXG; ++g) {
       const float tot = (s_ss[0][g] + s_ss[1][g]) + (s_ss[2][g] + s_ss[3][g]);
@@ -238,96 +307,117 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
 #pragma unroll
     for (int g = 0; g < MAXG; ++g)
       if (in && g < G) s_q[g * hd + tid] = xq[g] * scale;
-  }
-  // new keys of this chunk's positions (start .. pos), from k
-  const int u_lo = max(p_lo, start) - start, u_hi = p_hi - 1 - start;
-  for (int u = u_lo; u <= u_hi; ++u) {
-    const float kr = norm_rope(in ? a.k[(size_t)u * kvw + (size_t)j * hd + tid] : 0.f, a.kn_w, a.kn_dt, a,
-                               start + u, s_tmp, s_red);
-    if (in) s_knew[u * hd + tid] = kr;
-  }
-  // the chunk holding position pos writes token t's cache row of kv head j
-  if (c == nc - 1 && in) {
-    const size_t cr = ((size_t)pos * a.kvh + j) * hd + tid;
-    store1<CBF>(a.kc, cr, s_knew[t * hd + tid]);
-    store1<CBF>(a.vc, cr, a.v[(size_t)t * kvw + (size_t)j * hd + tid]);
-  }
-  __syncthreads();
-
-  const int d0 = lane * 4;
-  const bool lin = d0 < hd;
-  float4 q4[MAXG], acc[MAXG];
-  float m[MAXG], l[MAXG];
-#pragma unroll
-  for (int g = 0; g < MAXG; ++g) {
-    q4[g] = lin && g < G ? *reinterpret_cast<const float4*>(s_q + g * hd + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
-    acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-    m[g] = -INFINITY;
-    l[g] = 0.f;
-  }
-  for (int p0 = p_lo + wave; p0 < p_hi; p0 += 4 * NB) {
-    float4 kk[NB], vv[NB];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int p = min(p0 + 4 * b, p_hi - 1);
-      if (!lin) {
-        kk[b] = vv[b] = make_float4(0.f, 0.f, 0.f, 0.f);
-      } else if (p < start) {
-        const size_t cr = ((size_t)p * a.kvh + j) * hd + d0;
-        kk[b] = load4<CBF>(a.kc, cr);
-        vv[b] = load4<CBF>(a.vc, cr);
-      } else {
-        kk[b] = *reinterpret_cast<const float4*>(s_knew + (p - start) * hd + d0);
-        vv[b] = *reinterpret_cast<const float4*>(a.v + (size_t)(p - start) * kvw + (size_t)j * hd + d0);
+    if constexpr (OWN) {
+      // new keys of this chunk's positions (start .. pos), from k
+      const float wk = elem_value(knw, a.kn_w, a.kn_dt, dq);
+      for (int u = u_lo; u <= u_hi; ++u) {
+        const float kx = u == u_lo ? k_first : a.k[(size_t)u * kvw + (size_t)j * hd + dq];
+        const float kr = norm_rope(in ? kx : 0.f, wk, a, start + u, s_tmp, s_red);
+        if (in) s_knew[u * hd + tid] = kr;
+      }
+      // the chunk holding position pos writes token t's cache row of kv head j
+      if (c == nc - 1 && in) {
+        const size_t cr = ((size_t)pos * a.kvh + j) * hd + tid;
+        store1<CBF>(a.kc, cr, s_knew[t * hd + tid]);
+        store1<CBF>(a.vc, cr, a.v[(size_t)t * kvw + (size_t)j * hd + tid]);
       }
     }
+    __syncthreads();
+
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      if (p0 + 4 * b >= p_hi) break;
-      float d[MAXG];
+    for (int g = 0; g < MAXG; ++g) {
+      q4[g] = lin && g < G ? *reinterpret_cast<const float4*>(s_q + g * hd + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+      m[g] = -INFINITY;
+      l[g] = 0.f;
+    }
+    // passes of NB positions per wavefront (c*C + w, + 4, ..), the first one
+    // already loaded; the step's own keys and values are selected per
+    // position after the loads
+    for (int p0 = p_first; p0 < p_hi; p0 += 4 * NB) {
+      if (p0 != p_first) load_pass(p0);
+      // the pass's scores for every head (independent of each other), then
+      // per head one softmax step over the pass: one max, NB independent
+      // exponentials and one rescale of (m, l, acc), not a serial online
+      // update per position.  Positions past the chunk score -inf.
+      float sr[NB];  // lanes 8g ..: head g's score at position p0 + 4 bb
 #pragma unroll
-      for (int g = 0; g < MAXG; ++g)
-        d[g] = q4[g].x * kk[b].x + q4[g].y * kk[b].y + q4[g].z * kk[b].z + q4[g].w * kk[b].w;
-      const float sr = rows8_sum(d);  // lanes 8g ..: head g's score
+      for (int bb = 0; bb < NB; ++bb) {
+        float4 k4 = kk[bb].f4();
+        if constexpr (OWN) {
+          if (p0 + 4 * bb >= start && p0 + 4 * bb < p_hi)  // (uniform per wavefront)
+            k4 = *reinterpret_cast<const float4*>(s_knew + (p0 + 4 * bb - start) * hd + dl);
+        }
+        float d[MAXG];
+#pragma unroll
+        for (int g = 0; g < MAXG; ++g) d[g] = q4[g].x * k4.x + q4[g].y * k4.y + q4[g].z * k4.z + q4[g].w * k4.w;
+        sr[bb] = rows8_sum(d);
+      }
 #pragma unroll
       for (int g = 0; g < MAXG; ++g) {
         if (g >= G) break;
-        const float sg = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(sr), 8 * g));
-        const float mn = fmaxf(m[g], sg);
-        const float f = __expf(m[g] - mn), e = __expf(sg - mn);
-        l[g] = l[g] * f + e;
-        acc[g].x = acc[g].x * f + e * vv[b].x;
-        acc[g].y = acc[g].y * f + e * vv[b].y;
-        acc[g].z = acc[g].z * f + e * vv[b].z;
-        acc[g].w = acc[g].w * f + e * vv[b].w;
-        m[g] = mn;
+        float sc[NB];
+        float mx = m[g];
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+          sc[bb] = p0 + 4 * bb < p_hi ? __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(sr[bb]), 8 * g)) : -INFINITY;
+          mx = fmaxf(mx, sc[bb]);
+        }
+        const float f = __expf(m[g] - mx);  // (mx is finite: position p0 exists)
+        float es = 0.f;
+        float4 av = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int bb = 0; bb < NB; ++bb) {
+          const float e = __expf(sc[bb] - mx);
+          float4 v4 = vv[bb].f4();
+          if constexpr (VN) {
+            if (p0 + 4 * bb >= start) v4 = vn[bb];  // (uniform per wavefront)
+          }
+          es += e;
+          av.x = fmaf(e, v4.x, av.x);
+          av.y = fmaf(e, v4.y, av.y);
+          av.z = fmaf(e, v4.z, av.z);
+          av.w = fmaf(e, v4.w, av.w);
+        }
+        l[g] = l[g] * f + es;
+        acc[g].x = acc[g].x * f + av.x;
+        acc[g].y = acc[g].y * f + av.y;
+        acc[g].z = acc[g].z * f + av.z;
+        acc[g].w = acc[g].w * f + av.w;
+        m[g] = mx;
       }
     }
-  }
-  // merge the 4 wavefronts per head: one chunk (short contexts) writes the
-  // gated output directly; otherwise the chunk partial (m, l, acc[hd]) goes
-  // to the workspace
-  const int maxc = a.max_chunks;
-  for (int g = 0; g < G; ++g) {
-    if (lane == 0) {
-      s_m[wave][g] = m[g];
-      s_l[wave][g] = l[g];
+  };
+  if (p_hi - 1 >= start) body(std::true_type{});
+  else body(std::false_type{});
+  // merge the 4 wavefronts, every head in one pass (thread d: dim d): one
+  // chunk (short contexts) writes the gated output directly; otherwise the
+  // chunk partial (m, l, acc[hd]) goes to the workspace for attn_merge_kernel
+#pragma unroll
+  for (int g = 0; g < MAXG; ++g) {
+    if (g < G) {
+      if (lane == 0) {
+        s_m[wave][g] = m[g];
+        s_l[wave][g] = l[g];
+      }
+      if (lin) *reinterpret_cast<float4*>(&s_acc[wave][g][d0]) = acc[g];
     }
-    if (lin) *reinterpret_cast<float4*>(&s_acc[wave][d0]) = acc[g];
-    __syncthreads();
+  }
+  __syncthreads();
+  const int maxc = a.max_chunks;
+#pragma unroll
+  for (int g = 0; g < MAXG; ++g) {
+    if (g >= G) break;
     const float M = fmaxf(fmaxf(s_m[0][g], s_m[1][g]), fmaxf(s_m[2][g], s_m[3][g]));
     float L = 0.f, o = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
       const float f = s_m[w][g] == -INFINITY ? 0.f : __expf(s_m[w][g] - M);
       L += s_l[w][g] * f;
-      o += in ? s_acc[w][tid] * f : 0.f;
+      o += in ? s_acc[w][g][tid] * f : 0.f;
     }
     if (nc == 1) {
-      float gg = gate[0];
-#pragma unroll
-      for (int k = 1; k < MAXG; ++k) gg = g == k ? gate[k] : gg;
-      if (in) a.gated[(size_t)t * qw + (size_t)(hb + g) * hd + tid] = (o / L) * sigmoid(gg);
+      if (in) a.gated[(size_t)t * qw + (size_t)(hb + g) * hd + tid] = (o / L) * sigmoid(gate[g]);
     } else {
       float* part = a.part + ((size_t)(t * a.heads + hb + g) * maxc + c) * (hd + 2);
       if (in) part[2 + tid] = o;
@@ -336,70 +426,56 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
         part[1] = L;
       }
     }
-    __syncthreads();  // s_m / s_acc are rewritten for the next head
   }
-  if (nc == 1) return;
-  if (tid == 0) {
-    uint32_t* ticket = a.tickets + (t * a.kvh + j) * a.hsplit + hs;
-    const uint32_t arrived = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) + 1u;
-    s_last = arrived == (uint32_t)nc;
-    if (s_last) __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  if (!s_last) return;
-  // last arrival: merge the nc chunks.  Chunk statistics of every head go
-  // through LDS in one pass; then wavefront w merges heads w, w + 4 with 16-byte
-  // loads of 4 dims per lane, 8 chunks in flight.
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  for (int e = tid; e < G * nc; e += 256) {
-    const int g = e / nc, cc = e - g * nc;
-    const float* pc = a.part + ((size_t)(t * a.heads + hb + g) * maxc + cc) * (hd + 2);
-    s_cm2[g][cc] = pc[0];
-    s_cl2[g][cc] = pc[1];
-  }
-  __syncthreads();
-  if (tid < G) {
-    float M = -INFINITY;
-    for (int cc = 0; cc < nc; ++cc) M = fmaxf(M, s_cm2[tid][cc]);
-    float L = 0.f;
-    for (int cc = 0; cc < nc; ++cc) {
-      const float f = s_cm2[tid][cc] == -INFINITY ? 0.f : __expf(s_cm2[tid][cc] - M);
-      s_cm2[tid][cc] = f;
-      L += s_cl2[tid][cc] * f;
-    }
-    s_L[tid] = L;
-  }
-  __syncthreads();
-  for (int g = wave; g < G; g += 4) {
-    if (!lin) continue;
-    const size_t qb = (size_t)t * 2 * qw + (size_t)(hb + g) * 2 * hd + hd + d0;
-    const float4 gate = make_float4(a.qg[qb + 0], a.qg[qb + 1], a.qg[qb + 2], a.qg[qb + 3]);  // issued first
-    const float* base = a.part + (size_t)(t * a.heads + hb + g) * maxc * (hd + 2) + 2 + d0;
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int c0 = 0; c0 < nc; c0 += 8) {
-      float4 v[8];
+}
+
+// Merge of the chunk partials of (query head h, token t): thread d holds
+// dim d.  The partials' values are loaded at once (up to kAttnMaxChunks per
+// thread, clamped in range), the chunk statistics by the first nc threads
+// into LDS; the chunks are combined in chunk order against the largest
+// chunk maximum (as the split kernel combines its wavefronts), then gated.
+struct AttnMergeArgs {
+  const float* qg;
+  const float* part;
+  float* gated;
+  const int* start_dev;
+  int start, max_pos, T, heads, hd, chunk, max_chunks;
+};
+
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnMergeArgs a) {
+  __shared__ float s_mc[kAttnMaxChunks], s_lc[kAttnMaxChunks];
+  const int h = blockIdx.x, t = blockIdx.y, d = threadIdx.x;
+  const int hd = a.hd, dd = d < hd ? d : 0;
+  // Every partial row exists (max_chunks per head), so all loads are issued
+  // before the position is known; rows past the chunk count are dropped.
+  const float* base = a.part + (size_t)(t * a.heads + h) * a.max_chunks * (hd + 2);
+  float ov[kAttnMaxChunks];
 #pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const int cc = min(c0 + b, nc - 1);
-        const float* src = base + (size_t)cc * (hd + 2);
-        v[b] = make_float4(src[0], src[1], src[2], src[3]);
-      }
-#pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const float f = c0 + b < nc ? s_cm2[g][c0 + b] : 0.f;
-        o.x += v[b].x * f;
-        o.y += v[b].y * f;
-        o.z += v[b].z * f;
-        o.w += v[b].w * f;
-      }
-    }
-    const float inv = 1.f / s_L[g];
-    const size_t ob = (size_t)t * qw + (size_t)(hb + g) * hd + d0;
-    a.gated[ob + 0] = o.x * inv * sigmoid(gate.x);
-    a.gated[ob + 1] = o.y * inv * sigmoid(gate.y);
-    a.gated[ob + 2] = o.z * inv * sigmoid(gate.z);
-    a.gated[ob + 3] = o.w * inv * sigmoid(gate.w);
+  for (int c = 0; c < kAttnMaxChunks; ++c) ov[c] = base[(size_t)c * (hd + 2) + 2 + dd];
+  const float gate = a.qg[(size_t)t * 2 * a.heads * hd + (size_t)h * 2 * hd + hd + dd];
+  const int dc = min(d, kAttnMaxChunks - 1);
+  const float mc = base[(size_t)dc * (hd + 2)], lc = base[(size_t)dc * (hd + 2) + 1];
+  const int start = a.start_dev ? *a.start_dev : a.start;
+  if (start < 0 || start + a.T > a.max_pos) return;  // the split kernel wrote NaN outputs
+  const int pos = start + t, nc = (pos + a.chunk) / a.chunk;
+  if (nc == 1) return;  // the split kernel wrote the gated output itself
+  if (d < kAttnMaxChunks) {
+    s_mc[d] = mc;
+    s_lc[d] = lc;
   }
+  __syncthreads();
+  float M = -INFINITY;
+  for (int c = 0; c < nc; ++c) M = fmaxf(M, s_mc[c]);
+  float L = 0.f, o = 0.f;
+#pragma unroll
+  for (int c = 0; c < kAttnMaxChunks; ++c) {
+    if (c < nc) {
+      const float f = s_mc[c] == -INFINITY ? 0.f : __expf(s_mc[c] - M);
+      L += s_lc[c] * f;
+      o += ov[c] * f;
+    }
+  }
+  if (d < hd) a.gated[(size_t)t * a.heads * hd + (size_t)h * hd + d] = (o / L) * sigmoid(gate);
 }
 
 // Normalised projection of the attention inputs: rows of [Wq | Wk | Wv]
@@ -684,7 +760,6 @@ int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_w
   a.interleaved = rope_interleaved;
   a.gated = ws.gated;
   a.part = ws.part;
-  a.tickets = ws.tickets;
   // chunks of >= 32 positions, at most kAttnMaxChunks of them over the
   // positions the step can reach (the cache length when the position is
   // only known on the device)
@@ -704,6 +779,23 @@ int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_w
   else hipLaunchKernelGGL(attn_split_kernel<false>, grid, dim3(256), shm, s, a);
   st = check_launch("attn_split_kernel");
   if (st) return st;
+  if (nchunks > 1) {
+    AttnMergeArgs ma;
+    ma.qg = ws.qg;
+    ma.part = ws.part;
+    ma.gated = ws.gated;
+    ma.start_dev = start_position_device;
+    ma.start = start_position;
+    ma.max_pos = max_positions;
+    ma.T = tokens;
+    ma.heads = heads;
+    ma.hd = head_dim;
+    ma.chunk = a.chunk;
+    ma.max_chunks = kAttnMaxChunks;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)heads, (unsigned)tokens), dim3(256), 0, s, ma);
+    st = check_launch("attn_merge_kernel");
+    if (st) return st;
+  }
   AttnOutArgs o;
   o.gated = ws.gated;
   o.wo = o_proj;

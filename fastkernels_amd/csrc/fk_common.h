@@ -132,6 +132,22 @@ __device__ __forceinline__ void gather_raw(const void* p, size_t base, size_t st
   }
 }
 
+// Element i of a bf16 or fp32 vector whose dtype is a run-time code, in two
+// halves: elem_word() loads the aligned 32-bit word holding it with an
+// address chosen arithmetically (no branch, so the load does not make the
+// compiler wait for the loads before it), elem_value() decodes it where it
+// is used.  For bf16 the word may start up to 2 bytes before the element
+// (same aligned word, so the same page).
+__device__ __forceinline__ uint32_t elem_word(const void* p, int dtype, size_t i) {
+  const uintptr_t at = reinterpret_cast<uintptr_t>(p) + (dtype == FK_DTYPE_BF16 ? i * 2 : i * 4);
+  return *reinterpret_cast<const uint32_t*>(at & ~(uintptr_t)3);
+}
+__device__ __forceinline__ float elem_value(uint32_t w, const void* p, int dtype, size_t i) {
+  if (dtype != FK_DTYPE_BF16) return __uint_as_float(w);
+  const bool high = ((reinterpret_cast<uintptr_t>(p) + i * 2) & 2) != 0;
+  return __uint_as_float((high ? w >> 16 : w & 0xffffu) << 16);
+}
+
 template <bool BF>
 __device__ __forceinline__ float raw_value(uint32_t r) {
   return __uint_as_float(BF ? r << 16 : r);
@@ -406,15 +422,32 @@ struct WaitLimits {
   uint32_t poll;
   uint32_t spin;
 };
+// The header words as loaded, turned into limits where they are first
+// needed.  A kernel loads them before its other loads and calls limits()
+// late: the compiler makes the uniform words scalar right after the load
+// otherwise, and that wait (a round trip to the coherent level) would hold
+// back every load issued after it.  Loads retire in order, so the late
+// wait finds the header words long arrived.
+struct WaitHeader {
+  uint32_t epoch, set, err;
+  __device__ __forceinline__ WaitLimits limits() {
+    asm volatile("" : "+v"(epoch), "+v"(set), "+v"(err));
+    WaitLimits w;
+    w.tag = epoch + 1u;
+    w.poll = err ? 0u : set ? set - 1u : kPollLimit;
+    w.spin = err ? 0u : set ? set - 1u : kSpinLimit;
+    return w;
+  }
+};
+__device__ __forceinline__ WaitHeader load_wait_header(const uint32_t* header, int epoch_word) {
+  WaitHeader h;
+  h.epoch = load_coherent(&header[epoch_word]);
+  h.set = load_coherent(&header[14]);
+  h.err = load_coherent(&header[15]);
+  return h;
+}
 __device__ __forceinline__ WaitLimits wait_limits(const uint32_t* header, int epoch_word) {
-  const uint32_t epoch = load_coherent(&header[epoch_word]);
-  const uint32_t set = load_coherent(&header[14]);
-  const uint32_t err = load_coherent(&header[15]);
-  WaitLimits w;
-  w.tag = epoch + 1u;
-  w.poll = err ? 0u : set ? set - 1u : kPollLimit;
-  w.spin = err ? 0u : set ? set - 1u : kSpinLimit;
-  return w;
+  return load_wait_header(header, epoch_word).limits();
 }
 
 // Poisoned value of an output whose inputs a failed wait left invalid.

@@ -634,8 +634,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   const int T = a.T, H = VALU_A ? 2048 : a.H, C = a.C, V = a.V, R = a.R, Hv = a.Hv;
   const int NC = 2 * T;  // MFMA columns in use: (hi, lo) per token
   const int NCP = NC <= 2 ? 2 : NC <= 4 ? 4 : NC <= 8 ? 8 : 16;  // staging columns (power of two)
-  const WaitLimits wl = wait_limits(a.tw.tickets, kStepTicketEpoch);
-  const uint32_t tag = wl.tag, plim = wl.poll;
+  WaitHeader hdr = load_wait_header(a.tw.tickets, kStepTicketEpoch);  // (limits taken at the staging)
   const int n = lane & 15, g4 = lane >> 4;  // MFMA lane -> (column / A row, k group)
 
   // Roles.  Each value head runs on kStepHeadWGs workgroups at the end of
@@ -646,9 +645,9 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   const int head = is_head ? qb / kStepHeadWGs : 0, quarter = is_head ? qb % kStepHeadWGs : 0;
   const bool is_out = b < H / 16;
 
-  // The token chunks and the norm weight are loaded and staged before any
-  // weight load is issued: behind the 50 MB weight stream of every
-  // workgroup, their few lines would come back with the last weight tile.
+  // The token chunks and the norm weight are loaded before any weight load
+  // is issued: behind the 50 MB weight stream of every workgroup, their few
+  // lines would come back with the last weight tile.
   constexpr int XCH = NT * 2048 / 8 / 512;  // token chunks per thread at H <= 2048
   // H and V are powers of two (the host checks): indices split by shifts.
   const int lh = 31 - __builtin_clz((unsigned)H);
@@ -665,63 +664,9 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     }
   }
 
-  // ---- stage the normalised tokens -----------------------------------------
-  // MFMA path: bf16 hi/lo columns in s_xb [H/8 chunks][NCP][8] (bcol_slot);
-  // VALU path: fp32 in s_x [T][H].  Chunk q of thread tid is token-major
-  // chunk tid + 512 q; H % 512 == 0, so a wavefront's 64 chunks belong to one
-  // token and the sum of squares reduces in a fixed order.
-  uint16_t* s_xb = reinterpret_cast<uint16_t*>(s_dyn);
-  {
-#pragma unroll
-    for (int q = 0; q < XCH; ++q) {
-      const int idx8 = tid + q * 512;
-      if (idx8 < nchunk) {  // uniform per wavefront
-        float xv[8];
-        raw8_to_f32<BFX>(xr[q], xv);
-        float p = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) p = fmaf(xv[e], xv[e], p);
-        p = wave_sum(p);
-        if (lane == 0) s_part[idx8 >> cpt_sh][(idx8 & (cpt - 1)) >> 6] = p;
-      }
-    }
-    if (tid == 0) s_fail = 0;
-    if (tid < kStepTilesPerWG) s_tcnt[tid] = 0;
-    if (lane == 0) s_wtag[wave] = tag;
-    __syncthreads();
-    if (tid < T) {
-      float tot = 0.f;
-      for (int w = 0; w < (cpt >> 6); ++w) tot += s_part[tid][w];
-      s_rs[tid] = rsqrtf(tot / (float)H + a.eps);
-    }
-    if (tid == 0) store_tagged(a.tw.started + b, 0.f, s_wtag[kStepWaves - 1]);
-    __syncthreads();
-#pragma unroll
-    for (int q = 0; q < XCH; ++q) {
-      const int idx8 = tid + q * 512;
-      if (idx8 < nchunk) {
-        const int t = idx8 >> cpt_sh, k0 = (idx8 & (cpt - 1)) << 3;
-        float xv[8], nv[8], y[8];
-        raw8_to_f32<BFX>(xr[q], xv);
-        raw8_to_f32<true>(nr[q], nv);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = xv[e] * s_rs[t] * (1.0f + nv[e]);
-        if constexpr (VALU_A) {
-          float4* dst = reinterpret_cast<float4*>(reinterpret_cast<float*>(s_dyn) + (size_t)t * H + k0);
-          dst[0] = make_float4(y[0], y[1], y[2], y[3]);
-          dst[1] = make_float4(y[4], y[5], y[6], y[7]);
-        } else {
-          u32x4 vh, vl;
-          split_hi_lo8(y, vh, vl);
-          const int c = k0 >> 3;
-          *reinterpret_cast<u32x4*>(s_xb + (size_t)bcol_slot(c, 2 * t, NCP) * 8) = vh;
-          *reinterpret_cast<u32x4*>(s_xb + (size_t)bcol_slot(c, 2 * t + 1, NCP) * 8) = vl;
-        }
-      }
-    }
-    __syncthreads();
-  }
-
+  // The first weight tiles are issued right behind the token chunks: the
+  // staging below waits for the chunks only (loads retire in order), so the
+  // weight stream runs while the tokens are normalised and staged.
   // Conv taps (state and weights) of this workgroup's qkv rows, needed by
   // the first tile's epilogue on the VALU path, so issued before the tiles.
   uint32_t cwin_raw[8], cwk_raw[8];
@@ -787,6 +732,65 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
 #pragma unroll
   for (int i = 0; i < kStepTilesPerWG; ++i)
     if (i < kStepTilesAhead) issue_tile(i);
+
+  // ---- stage the normalised tokens -----------------------------------------
+  const WaitLimits wl = hdr.limits();
+  const uint32_t tag = wl.tag, plim = wl.poll;
+  // MFMA path: bf16 hi/lo columns in s_xb [H/8 chunks][NCP][8] (bcol_slot);
+  // VALU path: fp32 in s_x [T][H].  Chunk q of thread tid is token-major
+  // chunk tid + 512 q; H % 512 == 0, so a wavefront's 64 chunks belong to one
+  // token and the sum of squares reduces in a fixed order.
+  uint16_t* s_xb = reinterpret_cast<uint16_t*>(s_dyn);
+  {
+#pragma unroll
+    for (int q = 0; q < XCH; ++q) {
+      const int idx8 = tid + q * 512;
+      if (idx8 < nchunk) {  // uniform per wavefront
+        float xv[8];
+        raw8_to_f32<BFX>(xr[q], xv);
+        float p = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p = fmaf(xv[e], xv[e], p);
+        p = wave_sum(p);
+        if (lane == 0) s_part[idx8 >> cpt_sh][(idx8 & (cpt - 1)) >> 6] = p;
+      }
+    }
+    if (tid == 0) s_fail = 0;
+    if (tid < kStepTilesPerWG) s_tcnt[tid] = 0;
+    if (lane == 0) s_wtag[wave] = tag;
+    __syncthreads();
+    if (tid < T) {
+      float tot = 0.f;
+      for (int w = 0; w < (cpt >> 6); ++w) tot += s_part[tid][w];
+      s_rs[tid] = rsqrtf(tot / (float)H + a.eps);
+    }
+    if (tid == 0) store_tagged(a.tw.started + b, 0.f, s_wtag[kStepWaves - 1]);
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < XCH; ++q) {
+      const int idx8 = tid + q * 512;
+      if (idx8 < nchunk) {
+        const int t = idx8 >> cpt_sh, k0 = (idx8 & (cpt - 1)) << 3;
+        float xv[8], nv[8], y[8];
+        raw8_to_f32<BFX>(xr[q], xv);
+        raw8_to_f32<true>(nr[q], nv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = xv[e] * s_rs[t] * (1.0f + nv[e]);
+        if constexpr (VALU_A) {
+          float4* dst = reinterpret_cast<float4*>(reinterpret_cast<float*>(s_dyn) + (size_t)t * H + k0);
+          dst[0] = make_float4(y[0], y[1], y[2], y[3]);
+          dst[1] = make_float4(y[4], y[5], y[6], y[7]);
+        } else {
+          u32x4 vh, vl;
+          split_hi_lo8(y, vh, vl);
+          const int c = k0 >> 3;
+          *reinterpret_cast<u32x4*>(s_xb + (size_t)bcol_slot(c, 2 * t, NCP) * 8) = vh;
+          *reinterpret_cast<u32x4*>(s_xb + (size_t)bcol_slot(c, 2 * t + 1, NCP) * 8) = vl;
+        }
+      }
+    }
+    __syncthreads();
+  }
 
   // Small operands of later phases, fetched now so that no phase waits on a
   // dependent global load: the head's norm weight and decay parameters.

@@ -249,6 +249,41 @@ struct RouterArgs {
   MoeWs ws;
 };
 
+// Wave-wide reductions for the selection: DPP within each 16-lane row, then
+// the four row results read into scalar registers and combined there (a
+// uniform result, no lane swaps on the critical path of a lone wavefront).
+__device__ __forceinline__ uint32_t wave_max_u32_rows(uint32_t v) {
+  v = max(v, dpp_u32<kDppQuadXor1>(v));
+  v = max(v, dpp_u32<kDppQuadXor2>(v));
+  v = max(v, dpp_u32<kDppRowHalfMirror>(v));
+  v = max(v, dpp_u32<kDppRowMirror>(v));
+  const uint32_t r0 = __builtin_amdgcn_readlane(v, 0), r1 = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t r2 = __builtin_amdgcn_readlane(v, 32), r3 = __builtin_amdgcn_readlane(v, 48);
+  return max(max(r0, r1), max(r2, r3));
+}
+__device__ __forceinline__ float wave_max_rows(float v) {
+  v = fmaxf(v, __uint_as_float(dpp_u32<kDppQuadXor1>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<kDppQuadXor2>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<kDppRowHalfMirror>(__float_as_uint(v))));
+  v = fmaxf(v, __uint_as_float(dpp_u32<kDppRowMirror>(__float_as_uint(v))));
+  const float r0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+  const float r1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16));
+  const float r2 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32));
+  const float r3 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+__device__ __forceinline__ float wave_sum_rows(float v) {
+  v += __uint_as_float(dpp_u32<kDppQuadXor1>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppQuadXor2>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppRowHalfMirror>(__float_as_uint(v)));
+  v += __uint_as_float(dpp_u32<kDppRowMirror>(__float_as_uint(v)));
+  const float r0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+  const float r1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16));
+  const float r2 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32));
+  const float r3 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 // Softmax + top-k over logits held in registers (lane l holds experts
 // l + 64 j; -inf where l + 64 j >= E).  Candidate (p, j) of a lane becomes
 // the 32-bit key ((bits(p) + 1) << 2) | (3 - j): probabilities lie in [0, 1],
@@ -273,7 +308,7 @@ __device__ void topk_select_keys32_multi(float (&p)[NT][4], int E, int K, int la
     for (int j = 0; j < 4; ++j) m[i] = fmaxf(m[i], p[i][j]);
   }
 #pragma unroll
-  for (int i = 0; i < NT; ++i) m[i] = wave_max(m[i]);
+  for (int i = 0; i < NT; ++i) m[i] = wave_max_rows(m[i]);
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
     s[i] = 0.f;
@@ -285,7 +320,7 @@ __device__ void topk_select_keys32_multi(float (&p)[NT][4], int E, int K, int la
     }
   }
 #pragma unroll
-  for (int i = 0; i < NT; ++i) s[i] = wave_sum(s[i]);
+  for (int i = 0; i < NT; ++i) s[i] = wave_sum_rows(s[i]);
   uint32_t key[NT][4];
   auto cswap = [](uint32_t& a, uint32_t& b) {
     const uint32_t hi = a > b ? a : b, lo = a > b ? b : a;
@@ -312,7 +347,7 @@ __device__ void topk_select_keys32_multi(float (&p)[NT][4], int E, int K, int la
   for (int k = 0; k < K; ++k) {
 #pragma unroll
     for (int i = 0; i < NT; ++i) {
-      const uint32_t mk = wave_max_u32(key[i][0]);
+      const uint32_t mk = wave_max_u32_rows(key[i][0]);
       const int sel_lane = __ffsll((unsigned long long)__ballot(key[i][0] == mk)) - 1;
       const int sel = sel_lane + kWave * (int)(3 - (mk & 3u));
       const float mv = __uint_as_float((mk >> 2) - 1u);
@@ -455,7 +490,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(RouterArgs a) {
   __shared__ int s_bad;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int e = blockIdx.x * 4 + wave;
-  const uint32_t spin = wait_limits(a.ws.tickets, kTicketEpoch).spin;
+  WaitHeader hdr = load_wait_header(a.ws.tickets, kTicketEpoch);  // (limit taken at the barrier)
   const int nch = a.H >> 3;
   const int tile = (a.T + gridDim.y - 1) / gridDim.y;
   const int tb = blockIdx.y * tile;
@@ -530,6 +565,7 @@ __global__ __launch_bounds__(256) void moe_router_kernel(RouterArgs a) {
   const uint32_t G = gridDim.x * gridDim.y;
   publish_wait();
   __syncthreads();
+  const uint32_t spin = hdr.limits().spin;
   if (threadIdx.x == 0)
     s_bad = !grid_arrive_and_wait(&a.ws.tickets[kTicketRouterBarrier], G, &a.ws.tickets[kTicketError], spin);
   __syncthreads();
@@ -1594,46 +1630,121 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   }
 
   // ---------------- P3: routed gate/up (+ down-row prefetch) ---------------
-  // (wave-uniform: the down code branches on it and reduces across lanes
-  // with lane swaps, which read inactive lanes' stale registers; lanes past
-  // I load nothing and their dot products are zero)
-  const bool prefetch = U <= NPF && r_first < H;
-  Raw8<true> dr[NPF];
-  if (prefetch && lane * 8 < I) {
-#pragma unroll
-    for (int u = 0; u < NPF; ++u) {
-      if (u < U) dr[u] = load_raw8_stream<true>(f.dn, ((size_t)s_active[u] * H + r_first) * I + (size_t)lane * 8);
-      else dr[u].a = u32x4{0, 0, 0, 0};
-    }
-  }
   // Blocks of kFusedChunk consecutive intermediates of one expert per
   // workgroup, two per wavefront; each block leaves as one 128-byte line per
   // routed token.
   const int bpe = I / kFusedChunk, nblk = U * bpe;
-  for (int blk = b; blk < nblk; blk += G) {
-    const int u = blk / bpe, i0 = (blk - u * bpe) * kFusedChunk;
-    const int e = s_active[u], pa = s_aoff[u], np = s_aoff[u + 1] - pa;
-    const int ia = i0 + 2 * wave;
-    const char* we = reinterpret_cast<const char*>(f.gu) + (size_t)e * 2 * I * H * 2;
-    Raw8<true> ga[4], ua8[4], gb[4], ub8[4];
+  // (wave-uniform: the down code branches on it and reduces across lanes
+  // with lane swaps, which read inactive lanes' stale registers)
+  const bool prefetch = U <= NPF && r_first < H;
+  Raw8<true> dr[NPF];
+  if constexpr (ONE) {
+    // One token: each routed expert holds one pair (expert u at permuted
+    // position u).  The loads are issued in the order their data is needed,
+    // and loads return roughly in issue order: the token's chunks, the first
+    // block's gate/up rows, then this wavefront's 8 down rows.  Gate/up
+    // (32 MB over the grid) then completes before the down rows (16 MB), and
+    // the activation hand-off that follows gate/up overlaps the down stream.
+    // Every load is unconditional (clamped in range; unused lanes and slots
+    // are dropped where the values are used), so no branch makes the
+    // compiler wait for the loads before it.
+    Raw8<BFX> xt[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = lane + kWave * j;
-      if (c < nch) {
-        ga[j] = load_raw8_stream<true>(we, (size_t)ia * H + (size_t)c * 8);
-        gb[j] = load_raw8_stream<true>(we, (size_t)(ia + 1) * H + (size_t)c * 8);
-        ua8[j] = load_raw8_stream<true>(we, (size_t)(I + ia) * H + (size_t)c * 8);
-        ub8[j] = load_raw8_stream<true>(we, (size_t)(I + ia + 1) * H + (size_t)c * 8);
+    for (int j = 0; j < 4; ++j) xt[j] = load_raw8<BFX>(a.x, (size_t)min(lane + kWave * j, nch - 1) * 8);
+    const size_t dcol = (size_t)min(lane * 8, I - 8), drow = (size_t)min(r_first, H - 1);
+    auto issue_down = [&]() {
+#pragma unroll
+      for (int u = 0; u < NPF; ++u)
+        dr[u] = load_raw8_stream<true>(f.dn, ((size_t)s_active[min(u, U - 1)] * H + drow) * I + dcol);
+    };
+    // one block: its gate/up rows, then (first block only) the down rows
+    auto block = [&](int blk, bool first_blk) {
+      const int u = blk / bpe, i0 = (blk - u * bpe) * kFusedChunk;
+      const int ia = i0 + 2 * wave;
+      const char* we = reinterpret_cast<const char*>(f.gu) + (size_t)s_active[u] * 2 * I * H * 2;
+      Raw8<true> ga[4], ua8[4], gb[4], ub8[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const size_t c8 = (size_t)min(lane + kWave * j, nch - 1) * 8;
+        ga[j] = load_raw8_stream<true>(we, (size_t)ia * H + c8);
+        gb[j] = load_raw8_stream<true>(we, (size_t)(ia + 1) * H + c8);
+        ua8[j] = load_raw8_stream<true>(we, (size_t)(I + ia) * H + c8);
+        ub8[j] = load_raw8_stream<true>(we, (size_t)(I + ia + 1) * H + c8);
+      }
+      if (first_blk) issue_down();
+      float acc[4] = {0.f, 0.f, 0.f, 0.f};  // gate ia, up ia, gate ia + 1, up ia + 1
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (lane + kWave * j < nch) {
+          float x8[8], w8[8];
+          raw8_to_f32<BFX>(xt[j], x8);
+          raw8_to_f32<true>(ga[j], w8);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[0] = fmaf(w8[q], x8[q], acc[0]);
+          raw8_to_f32<true>(ua8[j], w8);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[1] = fmaf(w8[q], x8[q], acc[1]);
+          raw8_to_f32<true>(gb[j], w8);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[2] = fmaf(w8[q], x8[q], acc[2]);
+          raw8_to_f32<true>(ub8[j], w8);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[3] = fmaf(w8[q], x8[q], acc[3]);
+        }
+      }
+      // the four sums at once (lanes 16r ..: sum r)
+      const float rs = rows4_sum(acc);
+      const float g0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 0));
+      const float u0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 16));
+      const float g1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 32));
+      const float u1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 48));
+      if (lane == 0) {
+        s_chunk[0][2 * wave] = silu(g0) * u0;
+        s_chunk[0][2 * wave + 1] = silu(g1) * u1;
+      }
+      __syncthreads();
+      if (tid < kFusedChunk) store_tagged(a.ws.f_act + (size_t)u * I + i0 + tid, poison_if(bad, s_chunk[0][tid]), tag);
+      __syncthreads();
+    };
+    if (b < nblk) {
+      block(b, true);
+      for (int blk = b + G; blk < nblk; blk += G) block(blk, false);
+    } else {
+      issue_down();  // a workgroup without a gate/up block
+    }
+  } else {
+    if (prefetch && lane * 8 < I) {
+#pragma unroll
+      for (int u = 0; u < NPF; ++u) {
+        if (u < U) dr[u] = load_raw8_stream<true>(f.dn, ((size_t)s_active[u] * H + r_first) * I + (size_t)lane * 8);
+        else dr[u].a = u32x4{0, 0, 0, 0};
       }
     }
-    fused_gateup_item<BFX>(ga, ua8, a.x, H, lane, np, s_tok + pa, &s_chunk[0][2 * wave]);
-    fused_gateup_item<BFX>(gb, ub8, a.x, H, lane, np, s_tok + pa, &s_chunk[0][2 * wave + 1]);
-    __syncthreads();
-    if (tid < kFusedChunk * np) {
-      const int pp = tid / kFusedChunk, l = tid % kFusedChunk;
-      store_tagged(a.ws.f_act + (size_t)(pa + pp) * I + i0 + l, poison_if(bad, s_chunk[pp][l]), tag);
+    for (int blk = b; blk < nblk; blk += G) {
+      const int u = blk / bpe, i0 = (blk - u * bpe) * kFusedChunk;
+      const int e = s_active[u], pa = s_aoff[u], np = s_aoff[u + 1] - pa;
+      const int ia = i0 + 2 * wave;
+      const char* we = reinterpret_cast<const char*>(f.gu) + (size_t)e * 2 * I * H * 2;
+      Raw8<true> ga[4], ua8[4], gb[4], ub8[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = lane + kWave * j;
+        if (c < nch) {
+          ga[j] = load_raw8_stream<true>(we, (size_t)ia * H + (size_t)c * 8);
+          gb[j] = load_raw8_stream<true>(we, (size_t)(ia + 1) * H + (size_t)c * 8);
+          ua8[j] = load_raw8_stream<true>(we, (size_t)(I + ia) * H + (size_t)c * 8);
+          ub8[j] = load_raw8_stream<true>(we, (size_t)(I + ia + 1) * H + (size_t)c * 8);
+        }
+      }
+      fused_gateup_item<BFX>(ga, ua8, a.x, H, lane, np, s_tok + pa, &s_chunk[0][2 * wave]);
+      fused_gateup_item<BFX>(gb, ub8, a.x, H, lane, np, s_tok + pa, &s_chunk[0][2 * wave + 1]);
+      __syncthreads();
+      if (tid < kFusedChunk * np) {
+        const int pp = tid / kFusedChunk, l = tid % kFusedChunk;
+        store_tagged(a.ws.f_act + (size_t)(pa + pp) * I + i0 + l, poison_if(bad, s_chunk[pp][l]), tag);
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 
   // ---------------- P4: stage activations, down rows, combine --------------
@@ -1673,8 +1784,9 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       float acc = s_sg[0] * dot8_act_lds(sdr, s_act + (size_t)P * I, lane, I);
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
-        const float wt = u < U ? s_wpos[u] : 0.f;
-        acc = fmaf(wt, dot8_act_lds(dr[u], s_act + (size_t)(u < U ? u : 0) * I, lane, I), acc);
+        // (slots past U hold a repeated row: dropped, not multiplied by 0)
+        const float d = dot8_act_lds(dr[u], s_act + (size_t)(u < U ? u : 0) * I, lane, I);
+        acc = u < U ? fmaf(s_wpos[u], d, acc) : acc;
       }
       const float o = poison_if(bad_out, wave_sum(acc));
       if (lane == 0) {
@@ -1837,8 +1949,7 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   const int nrb = (E + 7) / 8, tu = a.tu;
   const int ub = blockIdx.x % nrb, tb = blockIdx.x / nrb;
   const int e = ub * 8 + wave, t0 = tb * tu, ntok = max(0, min(tu, T - t0));
-  const WaitLimits wl = wait_limits(a.ws.tickets, kTicketEpoch);
-  const uint32_t tag = wl.tag;
+  WaitHeader hdr = load_wait_header(a.ws.tickets, kTicketEpoch);  // (limits taken after the first loads)
   if (tid == 0) s_fail = 0;
 
   // ---- logits of rows 8ub.. for tokens t0 .. t0 + ntok - 1 ----------------
@@ -1852,13 +1963,13 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   Raw8<BFX> xr[TU][4];
   float wn[4][8];
   // bias of the row whose logits this thread applies it to: the wavefront's
-  // row, or (tiled) the row this thread stores (thread t*8 + l: row 8ub + l)
-  float bias = 0.f;
-  if (TILED) {
-    if (a.bias && tid < 8 * TU && ub * 8 + (tid & 7) < E) bias = load_scalar(a.bias, a.bias_dt, ub * 8 + (tid & 7));
-  } else if (a.bias && row) {
-    bias = load_scalar(a.bias, a.bias_dt, e);
-  }
+  // row, or (tiled) the row this thread stores (thread t*8 + l: row 8ub + l);
+  // its word is loaded after the rows (unconditionally: a missing bias reads
+  // the router weight and is dropped), decoded where it is added
+  const int brow = TILED ? min(ub * 8 + (tid & 7), E - 1) : erow;
+  const void* bsrc = a.bias ? a.bias : a.W;
+  const int bdt = a.bias ? a.bias_dt : FK_DTYPE_F32;
+  uint32_t bias_word;
   {
     Raw8<BFW> wr[4];
     Raw8<BFN> nr[4];
@@ -1871,6 +1982,7 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
         xr[t][j] = load_raw8<BFX>(a.x, (size_t)min(t0 + t, tlast) * H + (size_t)cc * 8);
       nr[j] = load_raw8<BFN>(a.nw, (size_t)cc * 8);
     }
+    bias_word = elem_word(bsrc, bdt, brow);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int c = lane + kWave * j;
@@ -1881,6 +1993,10 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
       for (int q = 0; q < 8; ++q) wn[j][q] = c < nch ? w8[q] * (a.off + n8[q]) : 0.f;
     }
   }
+  const bool bias_on = a.bias && (TILED ? tid < 8 * TU && ub * 8 + (tid & 7) < E : row);
+  const float bias = bias_on ? elem_value(bias_word, bsrc, bdt, brow) : 0.f;
+  const WaitLimits wl = hdr.limits();
+  const uint32_t tag = wl.tag;
   for (int tt = 0; tt < ntok; tt += TU) {
     const int nt = min(TU, ntok - tt);
     // next tile's tokens, fetched while this tile is computed (bf16 tokens;

@@ -92,3 +92,21 @@ def test_moe_layer_hidden_not_multiple_of_16(device, tokens):
     # H = 1032 = 8 * 129: an odd number of 8-element chunks per row through
     # the single-launch layer (T <= 2), the tagged router and the GEMV experts
     _check(device, 64, 1032, 128, tokens, seed=300 + tokens)
+
+
+@pytest.mark.parametrize("tokens", [1, 16])
+def test_router_bias_bf16_and_misaligned(device, tokens):
+    # a bf16 router bias, also as a view starting 2 bytes into its storage:
+    # the tagged router loads the aligned word holding each element
+    e, h = 256, 2048
+    w = _weights(e, h, 64, seed=400 + tokens)
+    x = wl.make_hidden(tokens, h, seed=401)
+    bias16 = wl.zipf_router_bias(e, seed=0).to(torch.bfloat16)
+    store = torch.zeros(e + 1, dtype=torch.bfloat16, device=device)
+    store[1:] = bias16.to(device)
+    for bd in (bias16.to(device), store[1:]):
+        logits, ids, wt = hip.hip_qwen36_batched_moe_router_decode(x.to(device), w[0].to(device), w[1].to(device),
+                                                                   top_k=K, router_bias=bd)
+        o_logits, _, _ = oracle.router(x, w[0], w[1], K, router_bias=bias16)
+        torch.testing.assert_close(logits.cpu(), o_logits, atol=1e-4, rtol=1e-4)
+        assert_routing_parity(logits, ids, wt, o_logits, K)
