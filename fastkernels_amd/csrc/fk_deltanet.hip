@@ -515,35 +515,39 @@ __global__ __launch_bounds__(256) void deltanet_out_kernel(OutArgs a) {
 // ---------------------------------------------------------------------------
 // Single-launch DeltaNet step (fk_deltanet_step for T <= 8, D = 128, bf16
 // weights).  One 512-thread workgroup per CU, grid capped at co-resident
-// capacity, three phases joined by launch-tagged words (the MoE layer's
-// protocol: value + 32-bit launch tag per 8-byte word, polled by consumers;
-// the epoch advances once every workgroup's started record carries the tag):
-//   A  projections: workgroup b owns row tiles b, b+G, .. (16 rows of the
-//      concatenated [qkv | z | a | b] weights); its 8 wavefronts split K and
-//      run v_mfma_f32_16x16x32_bf16 with the normalised tokens as bf16
-//      hi + lo columns (2 per token, so the fp32 activations keep ~16
-//      mantissa bits); partial tiles are summed through LDS.  The owner of
-//      a qkv row applies the causal conv + SiLU over the tokens and rolls
-//      the conv state.  Outputs leave as tagged 128-byte runs.
-//   B  one workgroup per value head: its fp32 state (prefetched into
-//      registers at the start, 32 per thread: thread (column j, quarter g)
-//      holds rows 32g..32g+31 of column j, so the four partial sums of a
-//      column sit in one lane quad and reduce with two DPP steps) runs the
-//      gated delta rule over the tokens; then the gated RMSNorm per token;
-//      normed values leave tagged.
-//   C  workgroup b < H/16 owns output rows 16b..16b+15: W_out tiles are
-//      fetched into registers after phase A, the normed values of every
-//      token are polled into LDS as bf16 hi + lo columns, and MFMA + an LDS
-//      sum over the 8 wavefronts give update (and hidden_out = x + update).
+// capacity, phases joined by launch-tagged words (the MoE layer's protocol:
+// value + 32-bit launch tag per 8-byte word, polled by consumers; the epoch
+// advances once every workgroup's started record carries the tag):
+//   A  projections: workgroup b owns row tiles b, b + G, b + 2G (16 rows of
+//      the concatenated [qkv | z] weights).  T <= 2: whole-row dot products
+//      on the VALU; T > 2: its 8 wavefronts split K and run
+//      v_mfma_f32_16x16x32_bf16 with the normalised tokens as bf16 hi + lo
+//      columns (2 per token, so the fp32 activations keep ~16 mantissa
+//      bits), partial tiles summed through LDS.  The owner of a qkv row
+//      applies the causal conv + SiLU over the tokens and rolls the conv
+//      state.  Outputs leave tagged.  A head workgroup (below) also computes
+//      its head's a and b logits from its own staged tokens.
+//   B  four workgroups per value head, a quarter of its value columns each:
+//      the fp32 state (prefetched into registers: thread (column jl, group
+//      g) holds rows 8g .. 8g + 7 of its column, the column sums reduce over
+//      16 lanes with DPP) runs the gated delta rule over the tokens; the
+//      gated values o * w * silu(z) and the quarter's sum of squares of o
+//      leave tagged.
+//   C1 unit (rb, ks): rows 128 rb .. + 128 of W_out restricted to the
+//      columns of a few heads (fetched into registers after phase A); it
+//      applies each head's RMSNorm scale (from the four quarter sums) while
+//      staging the gated values as hi + lo columns, runs the MFMAs and
+//      leaves partial sums tagged.
+//   C2 workgroup b < H / 16 sums the partials of rows 16b .. 16b + 15:
+//      update (and hidden_out = x + update).
 // ---------------------------------------------------------------------------
 constexpr int kStepMaxTokens = 8;
 constexpr int kStepWaves = 8;
 constexpr int kStepMaxGrid = 1024;
-constexpr int kStepTilesPerWG = 4;  // phase A row tiles per workgroup (host checks)
+constexpr int kStepTilesPerWG = 3;  // phase A row tiles per workgroup (host checks)
 constexpr int kStepD = 128;
 constexpr size_t kStepMixWords = (size_t)kStepMaxTokens * 8192;
 constexpr size_t kStepVWords = (size_t)kStepMaxTokens * 4096;
-constexpr size_t kStepHeadWords = (size_t)kStepMaxTokens * 64;
 constexpr size_t kStepPartWords = (size_t)8 * kStepMaxTokens * 2048;  // [V/512 <= 8][T][H <= 2048]
 constexpr int kStepHeadWGs = 4;  // workgroups per value head (value columns split four ways)
 constexpr int kStepQCols = kStepD / kStepHeadWGs;  // value columns per head workgroup
@@ -557,9 +561,7 @@ struct StepTagWs {
   uint32_t* tickets;  // [16] workspace header: epoch, poll bound, error flag (fk_host.h)
   uint64_t* mix;      // [T, C] conv'd qkv
   uint64_t* z;        // [T, V]
-  uint64_t* a;        // [T, Hv]
-  uint64_t* b;        // [T, Hv]
-  uint64_t* norm;     // [T, V] gated-RMSNorm output
+  uint64_t* norm;     // [T, V] gated values o * w * silu(z), before the RMSNorm scale
   uint64_t* started;  // [grid]
   // Polling hints: a tile's (a head's) tag is stored once its outputs are
   // stored.  A consumer waits on the few hints of its producers before it
@@ -623,10 +625,11 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   char* s_dyn = reinterpret_cast<char*>(s_dyn_v);
   __shared__ float s_rs[kStepMaxTokens];
   __shared__ float s_part[kStepMaxTokens][kStepWaves];  // [token][wavefront of that token]
-  __shared__ float s_sc[kStepMaxTokens][4];  // decay, beta (head workgroups)
+  __shared__ float s_sc[kStepMaxTokens][2];  // decay, beta (head workgroups)
   __shared__ uint32_t s_wtag[kStepWaves];
   __shared__ int s_fail;
   __shared__ int s_tcnt[kStepTilesPerWG];  // wavefronts done with each phase A tile (VALU path)
+  __shared__ float s_abp[kStepMaxTokens][kStepWaves][2];  // head workgroups: a and b logit parts [token][wavefront]
   // (the wavefront index is uniform: kept in a scalar register, so that
   // addresses derived from it stay scalar too)
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -663,6 +666,22 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       nr[q] = load_raw8<true>(a.nw, (size_t)(idx8 & (cpt - 1)) * 8);
     }
   }
+  // The a and b rows of a head workgroup's own head: each head computes its
+  // a and b logits while it stages the tokens (below), so that no head waits
+  // for other workgroups' a/b projections.  Thread tid takes chunk
+  // tid % (H / 8) of both rows (for every token it stages); every workgroup
+  // issues the loads, the others on the head-0 rows, unused: no branch
+  // around a load.
+  Raw8<true> war, wbr;
+  {
+    const size_t o = ((size_t)head * H + (size_t)((tid & ((H >> 3) - 1)) << 3));
+    war = load_raw8<true>(a.w[2], o);
+    wbr = load_raw8<true>(a.w[3], o);
+  }
+  // (kept ahead of the weight tiles: the scheduler would otherwise sink the
+  // a/b loads towards their use, behind the tiles, and the staging's wait
+  // for them would then wait for the tiles too)
+  __builtin_amdgcn_sched_barrier(0);
 
   // The first weight tiles are issued right behind the token chunks: the
   // staging below waits for the chunks only (loads retire in order), so the
@@ -700,7 +719,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
 #pragma unroll
   for (int i = 0; i < kStepTilesPerWG; ++i)
     if (b + i * G < ntiles) ntl = i + 1;
-  // The matrix boundaries C, C + V, C + V + Hv and R are multiples of 16
+  // The matrix boundary C and R = C + V are multiples of 16
   // (the host checks), so a tile lies in one matrix and the base address of
   // each load is uniform; the lane adds a fixed byte offset.  Every slot
   // issues its load: one outside the weights (past the last tile or past
@@ -713,10 +732,9 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   auto issue_tile = [&](int i) {
     const int tile = b + i * G;
     const int row0 = tile * 16;
-    const int wh = row0 < C ? 0 : row0 < C + V ? 1 : row0 < C + V + Hv ? 2 : 3;
-    const int r0 = row0 - (wh == 0 ? 0 : wh == 1 ? C : wh == 2 ? C + V : C + V + Hv);
-    const char* tp = reinterpret_cast<const char*>(wh == 0 ? a.w[0] : wh == 1 ? a.w[1] : wh == 2 ? a.w[2] : a.w[3]) +
-                     ((size_t)(tile < ntiles ? r0 : 0) << (lh + 1));
+    const bool zt = row0 >= C;
+    const char* tp = reinterpret_cast<const char*>(zt ? a.w[1] : a.w[0]) +
+                     ((size_t)(tile < ntiles ? row0 - (zt ? C : 0) : 0) << (lh + 1));
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const bool live = s < ks && tile < ntiles;
@@ -732,6 +750,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
 #pragma unroll
   for (int i = 0; i < kStepTilesPerWG; ++i)
     if (i < kStepTilesAhead) issue_tile(i);
+
 
   // ---- stage the normalised tokens -----------------------------------------
   const WaitLimits wl = hdr.limits();
@@ -776,6 +795,22 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         raw8_to_f32<true>(nr[q], nv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) y[e] = xv[e] * s_rs[t] * (1.0f + nv[e]);
+        if (is_head) {  // this chunk's share of the a and b logits of token t
+          float wa[8], wb[8], da = 0.f, db = 0.f;
+          raw8_to_f32<true>(war, wa);
+          raw8_to_f32<true>(wbr, wb);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            da = fmaf(wa[e], y[e], da);
+            db = fmaf(wb[e], y[e], db);
+          }
+          da = wave_sum(da);
+          db = wave_sum(db);
+          if (lane == 0) {
+            s_abp[t][(idx8 & (cpt - 1)) >> 6][0] = da;
+            s_abp[t][(idx8 & (cpt - 1)) >> 6][1] = db;
+          }
+        }
         if constexpr (VALU_A) {
           float4* dst = reinterpret_cast<float4*>(reinterpret_cast<float*>(s_dyn) + (size_t)t * H + k0);
           dst[0] = make_float4(y[0], y[1], y[2], y[3]);
@@ -880,16 +915,9 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
               for (int j = 0; j < 8; ++j)
                 if (j < a.KS) reinterpret_cast<uint16_t*>(a.next_conv)[(size_t)row * a.KS + j] = f32_to_bf16_bits(seq(T + j));
             } else {
-              // (one store site per destination: a destination chosen per
-              // lane would be read from the kernel arguments by a vector load)
 #pragma unroll
-              for (int t = 0; t < NT; ++t) {
-                if (t < T) {
-                  if (row < C + V) store_tagged(a.tw.z + (size_t)t * V + (row - C), v[t], tag);
-                  else if (row < C + V + Hv) store_tagged(a.tw.a + (size_t)t * Hv + (row - C - V), v[t], tag);
-                  else store_tagged(a.tw.b + (size_t)t * Hv + (row - C - V - Hv), v[t], tag);
-                }
-              }
+              for (int t = 0; t < NT; ++t)
+                if (t < T) store_tagged(a.tw.z + (size_t)t * V + (row - C), v[t], tag);
             }
           }
         }
@@ -982,12 +1010,8 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
           for (int j = 0; j < 8; ++j)
             if (j < a.KS) reinterpret_cast<uint16_t*>(a.next_conv)[(size_t)erow * a.KS + j] = f32_to_bf16_bits(sq[T + j]);
         }
-      } else if (erow < C + V) {  // one store site per destination (see the VALU path)
-        store_tagged(a.tw.z + (size_t)et * V + (erow - C), ev, tag);
-      } else if (erow < C + V + Hv) {
-        store_tagged(a.tw.a + (size_t)et * Hv + (erow - C - V), ev, tag);
       } else {
-        store_tagged(a.tw.b + (size_t)et * Hv + (erow - C - V - Hv), ev, tag);
+        store_tagged(a.tw.z + (size_t)et * V + (erow - C), ev, tag);
       }
     }
     __syncthreads();  // phases B and C reuse the dynamic LDS
@@ -1044,15 +1068,16 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   // ---- phase B: gated delta rule, a quarter of one value head ------------
   if (is_head) {
     // s_in: [T][kStepInPitch]: q[128], k[128], v[32], z[32] (this quarter's
-    // value columns), a, b; then s_o [T][32].
+    // value columns); then s_o [T][32].  a and b are this workgroup's own
+    // (s_abp).
     float* s_in = reinterpret_cast<float*>(s_dyn);
     float* s_o = s_in + (size_t)T * kStepInPitch;
     const int hq = head / (Hv / a.Hk);
-    constexpr int per_tok = 2 * kStepD + 2 * kStepQCols + 2;
+    constexpr int per_tok = 2 * kStepD + 2 * kStepQCols;
     const int n_in = T * per_tok;
     bool ok = true;
-    // Hints of the 22 tiles holding this quarter's q, k, v, z, a and b rows
-    // (one load per lane), then one read of the inputs.
+    // Hints of the 20 tiles holding this quarter's q, k, v and z rows (one
+    // load per lane), then one read of the inputs.
     if (wave == 0) {
       constexpr int TPB = kStepD / 16, TPQ = kStepQCols / 16;  // tiles per 128 rows, per quarter's 32 rows
       int tl = -1;
@@ -1062,10 +1087,6 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         const int l = lane - 2 * TPB;
         const int row0 = (l < TPQ ? 2 * a.Hk * kStepD : C) + head * kStepD + quarter * kStepQCols;
         tl = row0 / 16 + l % TPQ;
-      } else if (lane == 2 * TPB + 2 * TPQ) {
-        tl = (C + V + head) / 16;
-      } else if (lane == 2 * TPB + 2 * TPQ + 1) {
-        tl = (C + V + Hv + head) / 16;
       }
       uint64_t hw[1];
       const uint64_t* hs[1] = {tl >= 0 ? a.tw.hint_tile + tl : nullptr};
@@ -1092,9 +1113,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
           else if (r < 2 * kStepD) src = a.tw.mix + (size_t)t * C + (size_t)(a.Hk + hq) * kStepD + (r - kStepD);
           else if (r < 2 * kStepD + kStepQCols)
             src = a.tw.mix + (size_t)t * C + (size_t)(2 * a.Hk + head) * kStepD + quarter * kStepQCols + (r - 2 * kStepD);
-          else if (r < 2 * kStepD + 2 * kStepQCols)
-            src = a.tw.z + (size_t)t * V + (size_t)head * kStepD + quarter * kStepQCols + (r - 2 * kStepD - kStepQCols);
-          else src = (r == per_tok - 2 ? a.tw.a : a.tw.b) + (size_t)t * Hv + head;
+          else src = a.tw.z + (size_t)t * V + (size_t)head * kStepD + quarter * kStepQCols + (r - 2 * kStepD - kStepQCols);
           srcs[j] = src;
           dsti[j] = t * kStepInPitch + r;
         }
@@ -1122,7 +1141,11 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       k[lane] = k0 * kss;
       k[lane + 64] = k1 * kss;
       if (lane == 0) {
-        const float* ab = s_in + (size_t)t * kStepInPitch + per_tok - 2;
+        float ab[2] = {0.f, 0.f};  // the wavefront parts, in order
+        for (int w = 0; w < (cpt >> 6); ++w) {
+          ab[0] += s_abp[t][w][0];
+          ab[1] += s_abp[t][w][1];
+        }
         const float neg_a = -expf(raw_value<true>(alog[0]));
         const float gin = ab[0] + raw_value<true>(dtb1[0]);
         s_sc[t][0] = expf(neg_a * (fmaxf(gin, 0.f) + log1pf(expf(-fabsf(gin)))));
@@ -1167,33 +1190,20 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       if (sgr == 0) s_o[t * kStepQCols + sjl] = o;
     }
     __syncthreads();
-    // Gated RMSNorm: the quarters of a head exchange their sums of squares
-    // (tagged) and each normalises its own columns with the four sums added
-    // in quarter order, so all four use the same scale.
+    // Gated RMSNorm, its scale left to phase C: each quarter stores its
+    // columns gated but not yet scaled, o * w * silu(z), and its sum of
+    // squares of o; the phase C unit reading the head adds the four sums in
+    // quarter order and scales the head's columns as it stages them.
     if (wave < T) {
       const int t = wave;
       const float o = lane < kStepQCols ? s_o[t * kStepQCols + lane] : 0.f;
       const float ss = wave_sum(o * o);
-      if (lane == 0) {
-        store_tagged(a.tw.hss + ((size_t)head * kStepHeadWGs + quarter) * kStepMaxTokens + t, ss, tag);
-        uint64_t w[kStepHeadWGs];
-        const uint64_t* srcs[kStepHeadWGs];
-#pragma unroll
-        for (int q = 0; q < kStepHeadWGs; ++q) {
-          srcs[q] = a.tw.hss + ((size_t)head * kStepHeadWGs + q) * kStepMaxTokens + t;
-          w[q] = load_tagged(srcs[q]);
-        }
-        const bool hok = poll_tagged<kStepHeadWGs>(w, srcs, tag, plim);
-        if (!hok) s_fail = 1;
-        float tot = 0.f;
-#pragma unroll
-        for (int q = 0; q < kStepHeadWGs; ++q) tot += value_of(w[q]);
-        s_sc[t][2] = poison_if(!hok || bad_in, rsqrtf(tot / (float)kStepD + a.eps));
-      }
+      if (lane == 0)
+        store_tagged(a.tw.hss + ((size_t)head * kStepHeadWGs + quarter) * kStepMaxTokens + t, poison_if(bad_in, ss), tag);
       if (lane < kStepQCols) {
         const float zz = s_in[(size_t)t * kStepInPitch + 2 * kStepD + kStepQCols + lane];
         store_tagged(a.tw.norm + (size_t)t * V + (size_t)head * kStepD + quarter * kStepQCols + lane,
-                     o * s_sc[t][2] * raw_value<true>(lnw1[0]) * silu(zz), tag);
+                     poison_if(bad_in, o * raw_value<true>(lnw1[0]) * silu(zz)), tag);
       }
     }
     __syncthreads();
@@ -1218,24 +1228,32 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       if (!poll_tagged<1>(hw, hs, tag, plim)) s_fail = 1;
     }
     __syncthreads();
-    // The T * kcu inputs: one chunk of 8 consecutive columns per thread.
+    // The T * kcu inputs: one chunk of 8 consecutive columns per thread,
+    // with the four quarter sums of squares of the chunk's head and token.
     const int lcu = 31 - __builtin_clz((unsigned)kcu) - 3, cpu = 1 << lcu;  // chunks per token
     static_assert(kStepMaxTokens * 512 / 8 <= 512, "unit inputs exceed one chunk per thread");
     {
       const int t = tid >> lcu, c = tid & (cpu - 1);
+      const int hh = h0 + (c >> 4);  // (16 chunks per head)
       const bool live = t < T;
-      uint64_t w[8];
-      const uint64_t* srcs[8];
+      uint64_t w[8 + kStepHeadWGs];
+      const uint64_t* srcs[8 + kStepHeadWGs];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        srcs[e] = live ? a.tw.norm + (size_t)t * V + (size_t)uks * kcu + c * 8 + e : nullptr;
-        w[e] = srcs[e] ? load_tagged(srcs[e]) : 0ull;
-      }
-      ok = poll_tagged<8>(w, srcs, tag, plim);
+      for (int e = 0; e < 8; ++e) srcs[e] = live ? a.tw.norm + (size_t)t * V + (size_t)uks * kcu + c * 8 + e : nullptr;
+#pragma unroll
+      for (int q = 0; q < kStepHeadWGs; ++q)
+        srcs[8 + q] = live ? a.tw.hss + ((size_t)hh * kStepHeadWGs + q) * kStepMaxTokens + t : nullptr;
+#pragma unroll
+      for (int e = 0; e < 8 + kStepHeadWGs; ++e) w[e] = srcs[e] ? load_tagged(srcs[e]) : 0ull;
+      ok = poll_tagged<8 + kStepHeadWGs>(w, srcs, tag, plim);
       if (live) {
+        float tot = 0.f;
+#pragma unroll
+        for (int q = 0; q < kStepHeadWGs; ++q) tot += value_of(w[8 + q]);
+        const float scale = rsqrtf(tot / (float)kStepD + a.eps);
         float y[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = value_of(w[e]);
+        for (int e = 0; e < 8; ++e) y[e] = value_of(w[e]) * scale;
         u32x4 vh, vl;
         split_hi_lo8(y, vh, vl);
         *reinterpret_cast<u32x4*>(s_nb + (size_t)bcol_slot(c, 2 * t, NCP) * 8) = vh;
@@ -1396,8 +1414,6 @@ static size_t step_tag_layout(char* base, StepTagWs* tw) {
   tw->tickets = reinterpret_cast<uint32_t*>(take(16 * sizeof(uint32_t)));
   tw->mix = reinterpret_cast<uint64_t*>(take(kStepMixWords * 8));
   tw->z = reinterpret_cast<uint64_t*>(take(kStepVWords * 8));
-  tw->a = reinterpret_cast<uint64_t*>(take(kStepHeadWords * 8));
-  tw->b = reinterpret_cast<uint64_t*>(take(kStepHeadWords * 8));
   tw->norm = reinterpret_cast<uint64_t*>(take(kStepVWords * 8));
   tw->started = reinterpret_cast<uint64_t*>(take((size_t)kStepMaxGrid * 8));
   tw->hint_tile = reinterpret_cast<uint64_t*>(take((size_t)kStepTilesPerWG * kStepMaxGrid * 8));
@@ -1428,7 +1444,7 @@ static size_t step_ws_layout(int T, int Hk, int Hv, int D, char* base, StepWs* w
 // projections, conv state, conv weight, recurrent state, out projection,
 // gated-norm weight, a_log, dt_bias).
 static bool step_fused_eligible(int T, int H, int Hk, int Hv, int D, const int* dt, int G) {
-  const int C = (2 * Hk + Hv) * D, V = Hv * D, R = C + V + 2 * Hv;
+  const int C = (2 * Hk + Hv) * D, V = Hv * D, R = C + V;
   bool dtypes_ok = dt[5] == FK_DTYPE_F32;
   for (int i = 1; i < 10; ++i)
     if (i != 5 && dt[i] != FK_DTYPE_BF16) dtypes_ok = false;
@@ -1699,7 +1715,7 @@ int fk_deltanet_step(const void* hidden, const void* input_norm_weight, const vo
     sa.Hv = value_heads;
     sa.C = conv_dim;
     sa.V = value_heads * head_dim;
-    sa.R = conv_dim + sa.V + 2 * value_heads;
+    sa.R = conv_dim + sa.V;  // a and b: computed by the head workgroups
     sa.KS = kernel_size;
     sa.eps = eps;
     sa.update = update;
