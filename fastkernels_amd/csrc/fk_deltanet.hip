@@ -552,6 +552,7 @@ constexpr size_t kStepPartWords = (size_t)8 * kStepMaxTokens * 2048;  // [V/512 
 constexpr int kStepHeadWGs = 4;  // workgroups per value head (value columns split four ways)
 constexpr int kStepQCols = kStepD / kStepHeadWGs;  // value columns per head workgroup
 constexpr int kStepInPitch = 2 * kStepD + 2 * kStepQCols + 4;  // head workgroup inputs per token (q, k, v, z, a, b, pad)
+constexpr int kStepHssPitch = 64 * kStepHeadWGs;  // (head, quarter) words per token
 constexpr int kStepTilesAhead = 2;  // phase A weight tiles in flight per wavefront
 constexpr int kStepTicketEpoch = kWorkspaceEpochWord;
 constexpr int kStepTicketError = kWorkspaceErrorWord;
@@ -570,7 +571,7 @@ struct StepTagWs {
   // outputs still carry their own tags and are re-read until they do.
   uint64_t* hint_tile;  // [kStepTilesPerWG * kStepMaxGrid]
   uint64_t* hint_head;  // [64 * kStepHeadWGs] per head workgroup
-  uint64_t* hss;        // [64 * kStepHeadWGs][kStepMaxTokens] head quarters' sums of squares
+  uint64_t* hss;        // [kStepMaxTokens][kStepHssPitch] head quarters' sums of squares
   uint64_t* part;       // [V / 512][T][H] phase C partial sums
 };
 
@@ -1199,7 +1200,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       const float o = lane < kStepQCols ? s_o[t * kStepQCols + lane] : 0.f;
       const float ss = wave_sum(o * o);
       if (lane == 0)
-        store_tagged(a.tw.hss + ((size_t)head * kStepHeadWGs + quarter) * kStepMaxTokens + t, poison_if(bad_in, ss), tag);
+        store_tagged(a.tw.hss + (size_t)t * kStepHssPitch + head * kStepHeadWGs + quarter, poison_if(bad_in, ss), tag);
       if (lane < kStepQCols) {
         const float zz = s_in[(size_t)t * kStepInPitch + 2 * kStepD + kStepQCols + lane];
         store_tagged(a.tw.norm + (size_t)t * V + (size_t)head * kStepD + quarter * kStepQCols + lane,
@@ -1228,32 +1229,47 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       if (!poll_tagged<1>(hw, hs, tag, plim)) s_fail = 1;
     }
     __syncthreads();
-    // The T * kcu inputs: one chunk of 8 consecutive columns per thread,
-    // with the four quarter sums of squares of the chunk's head and token.
-    const int lcu = 31 - __builtin_clz((unsigned)kcu) - 3, cpu = 1 << lcu;  // chunks per token
+    // The T * kcu inputs, read coalesced (thread tid: words tid + 512 j of
+    // the unit's [T][kcu] block) with the quarter sums of squares of its
+    // heads, into LDS; then thread (t, c) scales the 8 columns of chunk c of
+    // token t by their head's RMSNorm factor and stages them as hi + lo.
+    const int lkcu = 31 - __builtin_clz((unsigned)kcu), lcu = lkcu - 3, cpu = 1 << lcu;  // chunks per token
     static_assert(kStepMaxTokens * 512 / 8 <= 512, "unit inputs exceed one chunk per thread");
+    float* s_val = reinterpret_cast<float*>(s_dyn + (size_t)kcu * NCP * 2);  // [T][kcu]
+    float* s_hss = s_val + (size_t)T * kcu;                                  // [T][nh * 4]
+    {
+      const int nhq = nh * kStepHeadWGs;
+      uint64_t w[NT + 1];
+      const uint64_t* srcs[NT + 1];
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const int g = tid + 512 * j, t = g >> lkcu;
+        srcs[j] = t < T ? a.tw.norm + (size_t)t * V + (size_t)uks * kcu + (g & (kcu - 1)) : nullptr;
+      }
+      {
+        const int t = tid / nhq, hq = tid - t * nhq;
+        srcs[NT] = t < T ? a.tw.hss + (size_t)t * kStepHssPitch + h0 * kStepHeadWGs + hq : nullptr;
+      }
+#pragma unroll
+      for (int j = 0; j <= NT; ++j) w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+      ok = poll_tagged<NT + 1>(w, srcs, tag, plim);
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        if (srcs[j]) s_val[tid + 512 * j] = value_of(w[j]);
+      if (srcs[NT]) s_hss[tid] = value_of(w[NT]);
+    }
+    __syncthreads();
     {
       const int t = tid >> lcu, c = tid & (cpu - 1);
-      const int hh = h0 + (c >> 4);  // (16 chunks per head)
-      const bool live = t < T;
-      uint64_t w[8 + kStepHeadWGs];
-      const uint64_t* srcs[8 + kStepHeadWGs];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) srcs[e] = live ? a.tw.norm + (size_t)t * V + (size_t)uks * kcu + c * 8 + e : nullptr;
-#pragma unroll
-      for (int q = 0; q < kStepHeadWGs; ++q)
-        srcs[8 + q] = live ? a.tw.hss + ((size_t)hh * kStepHeadWGs + q) * kStepMaxTokens + t : nullptr;
-#pragma unroll
-      for (int e = 0; e < 8 + kStepHeadWGs; ++e) w[e] = srcs[e] ? load_tagged(srcs[e]) : 0ull;
-      ok = poll_tagged<8 + kStepHeadWGs>(w, srcs, tag, plim);
-      if (live) {
+      if (t < T) {
         float tot = 0.f;
 #pragma unroll
-        for (int q = 0; q < kStepHeadWGs; ++q) tot += value_of(w[8 + q]);
+        for (int q = 0; q < kStepHeadWGs; ++q) tot += s_hss[t * nh * kStepHeadWGs + (c >> 4) * kStepHeadWGs + q];
         const float scale = rsqrtf(tot / (float)kStepD + a.eps);
-        float y[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) y[e] = value_of(w[e]) * scale;
+        const float4* vp = reinterpret_cast<const float4*>(s_val + (size_t)t * kcu + c * 8);
+        const float4 v0 = vp[0], v1 = vp[1];
+        float y[8] = {v0.x * scale, v0.y * scale, v0.z * scale, v0.w * scale,
+                      v1.x * scale, v1.y * scale, v1.z * scale, v1.w * scale};
         u32x4 vh, vl;
         split_hi_lo8(y, vh, vl);
         *reinterpret_cast<u32x4*>(s_nb + (size_t)bcol_slot(c, 2 * t, NCP) * 8) = vh;
@@ -1418,7 +1434,7 @@ static size_t step_tag_layout(char* base, StepTagWs* tw) {
   tw->started = reinterpret_cast<uint64_t*>(take((size_t)kStepMaxGrid * 8));
   tw->hint_tile = reinterpret_cast<uint64_t*>(take((size_t)kStepTilesPerWG * kStepMaxGrid * 8));
   tw->hint_head = reinterpret_cast<uint64_t*>(take((size_t)64 * kStepHeadWGs * 8));
-  tw->hss = reinterpret_cast<uint64_t*>(take((size_t)64 * kStepHeadWGs * kStepMaxTokens * 8));
+  tw->hss = reinterpret_cast<uint64_t*>(take((size_t)kStepMaxTokens * kStepHssPitch * 8));
   tw->part = reinterpret_cast<uint64_t*>(take(kStepPartWords * 8));
   return off;
 }
@@ -1460,7 +1476,9 @@ static size_t step_fused_lds(int T, int H, int V) {
                red = ((size_t)kStepWaves * kStepTilesPerWG * 16 * nc + kStepTilesPerWG * 16 * 16) * 4;
   const size_t pa = T <= 2 ? (size_t)T * H * 4 : (size_t)H * ncp * 2 + (tile > red ? tile : red);
   const size_t pb = ((size_t)T * kStepInPitch + (size_t)T * kStepQCols) * 4;
-  const size_t pc = (size_t)(V < 512 ? V : 512) * ncp * 2;
+  const size_t kcu = V < 512 ? V : 512;
+  // phase C: the unit's staging [kcu/8][ncp][8] bf16, values [T][kcu], sums of squares [T][16]
+  const size_t pc = kcu * ncp * 2 + ((size_t)T * kcu + (size_t)T * 4 * kStepHeadWGs) * 4;
   return pa > pb ? (pa > pc ? pa : pc) : (pb > pc ? pb : pc);
 }
 
