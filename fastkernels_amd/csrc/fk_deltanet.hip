@@ -1068,14 +1068,12 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
 
   // ---- phase B: gated delta rule, a quarter of one value head ------------
   if (is_head) {
-    // s_in: [T][kStepInPitch]: q[128], k[128], v[32], z[32] (this quarter's
-    // value columns); then s_o [T][32].  a and b are this workgroup's own
-    // (s_abp).
+    // s_in: [T][kStepInPitch]: q[128], k[128] (normalised), v[32], z[32]
+    // (this quarter's value columns); then s_o [T][32].  a and b are this
+    // workgroup's own (s_abp).
     float* s_in = reinterpret_cast<float*>(s_dyn);
     float* s_o = s_in + (size_t)T * kStepInPitch;
     const int hq = head / (Hv / a.Hk);
-    constexpr int per_tok = 2 * kStepD + 2 * kStepQCols;
-    const int n_in = T * per_tok;
     bool ok = true;
     // Hints of the 20 tiles holding this quarter's q, k, v and z rows (one
     // load per lane), then one read of the inputs.
@@ -1095,57 +1093,38 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       if (!poll_tagged<1>(hw, hs, tag, plim)) s_fail = 1;
     }
     __syncthreads();
-    // one batch of tagged loads in flight covers every input (T <= NT)
-    constexpr int BB = NT <= 2 ? 2 : 6;
-    static_assert(BB * 512 >= NT * per_tok, "head inputs exceed one poll batch");
-    {
-      uint64_t w[BB];
-      const uint64_t* srcs[BB];
-      int dsti[BB];
-#pragma unroll
-      for (int j = 0; j < BB; ++j) {
-        const int idx = tid + j * 512;
-        srcs[j] = nullptr;
-        dsti[j] = -1;
-        if (idx < n_in) {
-          const int t = idx / per_tok, r = idx - t * per_tok;
-          const uint64_t* src;
-          if (r < kStepD) src = a.tw.mix + (size_t)t * C + (size_t)hq * kStepD + r;
-          else if (r < 2 * kStepD) src = a.tw.mix + (size_t)t * C + (size_t)(a.Hk + hq) * kStepD + (r - kStepD);
-          else if (r < 2 * kStepD + kStepQCols)
-            src = a.tw.mix + (size_t)t * C + (size_t)(2 * a.Hk + head) * kStepD + quarter * kStepQCols + (r - 2 * kStepD);
-          else src = a.tw.z + (size_t)t * V + (size_t)head * kStepD + quarter * kStepQCols + (r - 2 * kStepD - kStepQCols);
-          srcs[j] = src;
-          dsti[j] = t * kStepInPitch + r;
-        }
-        w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
-      }
-      ok = poll_tagged<BB>(w, srcs, tag, plim);
-#pragma unroll
-      for (int j = 0; j < BB; ++j)
-        if (dsti[j] >= 0) s_in[dsti[j]] = value_of(w[j]);
-    }
-    if (!ok) s_fail = 1;
-    __syncthreads();
-    // inputs incomplete (a failed wait): the head's outputs and state are NaN
-    const bool bad_in = s_fail;
-    // Per token (wave t): l2-normalise q (times D^-1/2) and k in place; decay and beta.
+    // Wavefront t < T reads token t's inputs (lane: q and k rows lane and
+    // lane + 64, and v (lanes < 32) or z of this quarter's columns), l2-
+    // normalises q (times D^-1/2) and k with two wavefront sums and stages
+    // them; its lane 0 computes the token's decay and beta from the a/b
+    // logit parts (in wavefront order).
     if (wave < T) {
       const int t = wave;
-      float* q = s_in + (size_t)t * kStepInPitch;
-      float* k = q + kStepD;
-      const float q0 = q[lane], q1 = q[lane + 64], k0 = k[lane], k1 = k[lane + 64];
+      const uint64_t* mrow = a.tw.mix + (size_t)t * C;
+      const uint64_t* qrow = mrow + (size_t)hq * kStepD;
+      const uint64_t* krow = mrow + (size_t)(a.Hk + hq) * kStepD;
+      const uint64_t* srcs[5] = {
+          qrow + lane, qrow + lane + 64, krow + lane, krow + lane + 64,
+          lane < kStepQCols ? mrow + (size_t)(2 * a.Hk + head) * kStepD + quarter * kStepQCols + lane
+                            : a.tw.z + (size_t)t * V + (size_t)head * kStepD + quarter * kStepQCols + (lane - kStepQCols)};
+      uint64_t w[5];
+#pragma unroll
+      for (int j = 0; j < 5; ++j) w[j] = load_tagged(srcs[j]);
+      ok = poll_tagged<5>(w, srcs, tag, plim);
+      const float q0 = value_of(w[0]), q1 = value_of(w[1]), k0 = value_of(w[2]), k1 = value_of(w[3]);
       const float sq = wave_sum(q0 * q0 + q1 * q1), sk = wave_sum(k0 * k0 + k1 * k1);
       const float qs = rsqrtf(sq + a.eps) * rsqrtf((float)kStepD), kss = rsqrtf(sk + a.eps);
-      q[lane] = q0 * qs;
-      q[lane + 64] = q1 * qs;
-      k[lane] = k0 * kss;
-      k[lane + 64] = k1 * kss;
+      float* tin = s_in + (size_t)t * kStepInPitch;
+      tin[lane] = q0 * qs;
+      tin[lane + 64] = q1 * qs;
+      tin[kStepD + lane] = k0 * kss;
+      tin[kStepD + lane + 64] = k1 * kss;
+      tin[2 * kStepD + lane] = value_of(w[4]);  // v[32] then z[32]
       if (lane == 0) {
-        float ab[2] = {0.f, 0.f};  // the wavefront parts, in order
-        for (int w = 0; w < (cpt >> 6); ++w) {
-          ab[0] += s_abp[t][w][0];
-          ab[1] += s_abp[t][w][1];
+        float ab[2] = {0.f, 0.f};
+        for (int q = 0; q < (cpt >> 6); ++q) {
+          ab[0] += s_abp[t][q][0];
+          ab[1] += s_abp[t][q][1];
         }
         const float neg_a = -expf(raw_value<true>(alog[0]));
         const float gin = ab[0] + raw_value<true>(dtb1[0]);
@@ -1153,42 +1132,62 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         s_sc[t][1] = 1.f / (1.f + expf(-ab[1]));
       }
     }
+    if (!ok) s_fail = 1;
     __syncthreads();
+    // inputs incomplete (a failed wait): the head's outputs and state are NaN
+    const bool bad_in = s_fail;
     // Recurrence: lanes 16 jl' .. 16 jl' + 15 of a wavefront share a value
-    // column; each holds 8 rows and the column sums reduce over the 16 lanes.
+    // column; each holds 8 rows of the state and the column sums reduce over
+    // the 16 lanes.  The next token's q, k and v are read from LDS while the
+    // current one runs.
     float S[8];
 #pragma unroll
     for (int m = 0; m < 8; ++m) S[m] = raw_value<false>(S_raw[m]);
-    for (int t = 0; t < T; ++t) {
-      const float decay = s_sc[t][0], beta = s_sc[t][1];
+    auto load_tok = [&](int t, float (&k8)[8], float (&q8)[8], float& v) {
       const float* tin = s_in + (size_t)t * kStepInPitch;
-      float kn[8], qn[8];
-      {
-        const float4* k4 = reinterpret_cast<const float4*>(tin + kStepD + sgr * 8);
-        const float4* q4 = reinterpret_cast<const float4*>(tin + sgr * 8);
+      const float4* k4 = reinterpret_cast<const float4*>(tin + kStepD + sgr * 8);
+      const float4* q4 = reinterpret_cast<const float4*>(tin + sgr * 8);
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          const float4 kk = k4[m], qq = q4[m];
-          kn[4 * m] = kk.x; kn[4 * m + 1] = kk.y; kn[4 * m + 2] = kk.z; kn[4 * m + 3] = kk.w;
-          qn[4 * m] = qq.x; qn[4 * m + 1] = qq.y; qn[4 * m + 2] = qq.z; qn[4 * m + 3] = qq.w;
+      for (int m = 0; m < 2; ++m) {
+        const float4 kk = k4[m], qq = q4[m];
+        k8[4 * m] = kk.x; k8[4 * m + 1] = kk.y; k8[4 * m + 2] = kk.z; k8[4 * m + 3] = kk.w;
+        q8[4 * m] = qq.x; q8[4 * m + 1] = qq.y; q8[4 * m + 2] = qq.z; q8[4 * m + 3] = qq.w;
+      }
+      v = tin[2 * kStepD + sjl];
+    };
+    float kc[8], qc[8], vc;
+    load_tok(0, kc, qc, vc);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      if (t < T) {
+        const float decay = s_sc[t][0], beta = s_sc[t][1];
+        float kx[8], qx[8], vx = 0.f;
+        if (t + 1 < T) load_tok(t + 1, kx, qx, vx);
+        float part = 0.f;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          S[m] *= decay;
+          part = fmaf(S[m], kc[m], part);
+        }
+        const float ksum = row16_sum(part);
+        const float delta = (vc - ksum) * beta;
+        float op = 0.f;
+#pragma unroll
+        for (int m = 0; m < 8; ++m) {
+          S[m] = fmaf(kc[m], delta, S[m]);
+          op = fmaf(S[m], qc[m], op);
+        }
+        const float o = row16_sum(op);
+        if (sgr == 0) s_o[t * kStepQCols + sjl] = o;
+        if (t + 1 < T) {
+#pragma unroll
+          for (int m = 0; m < 8; ++m) {
+            kc[m] = kx[m];
+            qc[m] = qx[m];
+          }
+          vc = vx;
         }
       }
-      float part = 0.f;
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        S[m] *= decay;
-        part = fmaf(S[m], kn[m], part);
-      }
-      const float ksum = row16_sum(part);
-      const float delta = (tin[2 * kStepD + sjl] - ksum) * beta;
-      float op = 0.f;
-#pragma unroll
-      for (int m = 0; m < 8; ++m) {
-        S[m] = fmaf(kn[m], delta, S[m]);
-        op = fmaf(S[m], qn[m], op);
-      }
-      const float o = row16_sum(op);
-      if (sgr == 0) s_o[t * kStepQCols + sjl] = o;
     }
     __syncthreads();
     // Gated RMSNorm, its scale left to phase C: each quarter stores its
