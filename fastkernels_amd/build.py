@@ -1,6 +1,7 @@
 """Build libfastkernels_hip.so (the gfx950 HIP kernels + C ABI) in-tree.
 
-Usage: ``python -m fastkernels_amd.build`` (or ``fastkernels_amd.build.build()``).
+Usage: ``python -m fastkernels_amd.build`` (or ``fastkernels_amd.build.build()``);
+``--timeline`` builds the diagnostic phase-timeline variant alongside.
 Each ``csrc/*.hip`` file is compiled to an object with hipcc for
 ``--offload-arch=gfx950`` and the objects are linked into
 ``fastkernels_amd/libfastkernels_hip.so``.  Compilation runs on a machine
@@ -22,6 +23,7 @@ CSRC = PACKAGE_DIR / "csrc"
 INCLUDE = REPO_ROOT / "include"
 LIB_NAME = "libfastkernels_hip.so"
 LIB_PATH = PACKAGE_DIR / LIB_NAME
+TIMELINE_LIB_PATH = PACKAGE_DIR / "libfastkernels_hip_timeline.so"
 BUILD_DIR = PACKAGE_DIR / "_build"
 ARCH = "gfx950"
 
@@ -69,18 +71,26 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
-    """Compile every kernel source and link the shared library; returns its path."""
+def build(verbose: bool = False, jobs: int | None = None, timeline: bool = False) -> Path:
+    """Compile every kernel source and link the shared library; returns its path.
+
+    ``timeline=True`` builds the diagnostic variant instead: the single-launch
+    kernels record per-phase wall-clock markers (``-DFK_TIMELINE``) into
+    ``libfastkernels_hip_timeline.so``, read by ``python -m
+    fastkernels_amd.timeline``.  The product library is left untouched."""
 
     hipcc = _hipcc()
-    BUILD_DIR.mkdir(exist_ok=True)
+    build_dir = BUILD_DIR / "timeline" if timeline else BUILD_DIR
+    out_path = TIMELINE_LIB_PATH if timeline else LIB_PATH
+    build_dir.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
+    extra = ["-DFK_TIMELINE"] if timeline else []
 
     def compile_one(src: Path) -> Path:
-        obj = BUILD_DIR / (src.stem + ".o")
-        cmd = [hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
+        obj = build_dir / (src.stem + ".o")
+        cmd = [hipcc, *HIPCC_FLAGS, *extra, f"-I{INCLUDE}", "-c", str(src), "-o", str(obj)]
         if verbose:
             print(" ".join(cmd))
         _run(cmd)
@@ -90,15 +100,15 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
         objs = list(pool.map(compile_one, srcs))
 
-    tmp = LIB_PATH.with_name(LIB_NAME + ".tmp")
+    tmp = out_path.with_name(out_path.name + ".tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     if verbose:
         print(" ".join(cmd))
     _run(cmd)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out_path)
+    return out_path
 
 
 if __name__ == "__main__":
-    path = build(verbose="-v" in sys.argv)
+    path = build(verbose="-v" in sys.argv, timeline="--timeline" in sys.argv)
     print(path)

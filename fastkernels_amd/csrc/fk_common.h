@@ -477,4 +477,50 @@ __device__ __forceinline__ float sigmoid(float g) { return 1.0f / (1.0f + __expf
 
 __host__ __device__ constexpr size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// ---------------------------------------------------------------------------
+// Phase timeline of the single-launch kernels, in diagnostic builds only
+// (-DFK_TIMELINE: `python -m fastkernels_amd.build --timeline` builds them
+// into a library of their own).  FK_TIMELINE_DECL opens a kernel's marker
+// registers; FK_MARK(k) keeps the wall clock (100 MHz) at marker k in the
+// calling thread; FK_TIMELINE_COMMIT(unit, row) stores thread 0's markers in
+// row `row` (one per workgroup) of the translation unit's device buffer,
+// declared with FK_TIMELINE_BUFFER(unit) and read by the host through
+// fk_timeline_read_<unit> / fk_timeline_clear_<unit>.  In ordinary builds
+// they all expand to nothing.
+constexpr int kTimelineMarks = 16;
+constexpr int kTimelineRows = 1024;
+#ifdef FK_TIMELINE
+#define FK_TIMELINE_DECL unsigned long long fk_tl_[fk::kTimelineMarks] = {}
+#define FK_MARK(k) (fk_tl_[(k)] = wall_clock64())
+#define FK_TIMELINE_COMMIT(unit, row)                                                     \
+  do {                                                                                    \
+    if (threadIdx.x == 0 && (row) < fk::kTimelineRows)                                    \
+      for (int i_ = 0; i_ < fk::kTimelineMarks; ++i_)                                     \
+        fk_tl_buf_##unit[(size_t)(row) * fk::kTimelineMarks + i_] = fk_tl_[i_];           \
+  } while (0)
+#define FK_TIMELINE_BUFFER(unit)                                                                          \
+  static __device__ unsigned long long fk_tl_buf_##unit[fk::kTimelineRows * fk::kTimelineMarks];          \
+  extern "C" int fk_timeline_read_##unit(void* host, size_t bytes) {                                     \
+    if (!host || bytes > sizeof(fk_tl_buf_##unit)) return FK_ERR_INVALID;                                 \
+    return hipMemcpyFromSymbol(host, HIP_SYMBOL(fk_tl_buf_##unit), bytes, 0, hipMemcpyDeviceToHost) ==    \
+                   hipSuccess                                                                             \
+               ? FK_OK                                                                                    \
+               : FK_ERR_LAUNCH;                                                                           \
+  }                                                                                                       \
+  extern "C" int fk_timeline_clear_##unit() {                                                            \
+    static const unsigned long long zeros[fk::kTimelineRows * fk::kTimelineMarks] = {};                  \
+    return hipMemcpyToSymbol(HIP_SYMBOL(fk_tl_buf_##unit), zeros, sizeof(zeros), 0, hipMemcpyHostToDevice) == \
+                   hipSuccess                                                                             \
+               ? FK_OK                                                                                    \
+               : FK_ERR_LAUNCH;                                                                           \
+  }
+#else
+#define FK_TIMELINE_DECL \
+  do {                   \
+  } while (0)
+#define FK_MARK(k) ((void)0)
+#define FK_TIMELINE_COMMIT(unit, row) ((void)0)
+#define FK_TIMELINE_BUFFER(unit)
+#endif
+
 }  // namespace fk

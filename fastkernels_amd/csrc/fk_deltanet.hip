@@ -618,8 +618,12 @@ __device__ __forceinline__ float row16_sum(float v) {
 // has the dtype of the model's own decode: bf16 weights, norm weights, conv
 // state and decay parameters, fp32 recurrent state (the host sends other
 // combinations to the staged kernels).
+FK_TIMELINE_BUFFER(deltanet_step)
+
 template <bool BFX, int NT>
 __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
+  FK_TIMELINE_DECL;
+  FK_MARK(0);  // (timeline markers: diagnostic builds only)
   // T <= 2 (and H = 2048, which the host checks): phase A on the VALU.
   constexpr bool VALU_A = NT <= 2;
   extern __shared__ float4 s_dyn_v[];
@@ -753,6 +757,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     if (i < kStepTilesAhead) issue_tile(i);
 
 
+  FK_MARK(1);
   // ---- stage the normalised tokens -----------------------------------------
   const WaitLimits wl = hdr.limits();
   const uint32_t tag = wl.tag, plim = wl.poll;
@@ -1021,6 +1026,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   }
   }
 
+  FK_MARK(2);
   // ---- W_out for phase C, fetched while the heads run --------------------
   // Phase C is split over K.  Unit (rb, ks), on workgroup b = rb * nks + ks,
   // multiplies rows 128 rb .. + 128 of W_out, restricted to the columns
@@ -1134,6 +1140,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     }
     if (!ok) s_fail = 1;
     __syncthreads();
+    FK_MARK(3);
     // inputs incomplete (a failed wait): the head's outputs and state are NaN
     const bool bad_in = s_fail;
     // Recurrence: lanes 16 jl' .. 16 jl' + 15 of a wavefront share a value
@@ -1190,6 +1197,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       }
     }
     __syncthreads();
+    FK_MARK(4);
     // Gated RMSNorm, its scale left to phase C: each quarter stores its
     // columns gated but not yet scaled, o * w * silu(z), and its sum of
     // squares of o; the phase C unit reading the head adds the four sums in
@@ -1208,6 +1216,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     }
     __syncthreads();
     if (tid == 0) store_tagged(a.tw.hint_head + qb, 0.f, tag);
+    FK_MARK(5);
     {
       const size_t base = ((size_t)head * kStepD + (size_t)sgr * 8) * kStepD + jcol;
 #pragma unroll
@@ -1278,6 +1287,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     if (!ok) s_fail = 1;
     __syncthreads();
     const bool bad_unit = s_fail;
+    FK_MARK(6);
     f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
@@ -1299,6 +1309,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     }
   }
 
+  FK_MARK(7);
   // ---- phase C2: rows 16b..16b+15 = sum of the nks unit partials ----------
   if (is_out) {
     // (nks partials per thread: polled directly, few enough not to need hints)
@@ -1318,6 +1329,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       for (int j = 0; j < 8; ++j)
         if (j < nks) v += value_of(w[j]);
       v = poison_if(!pok, v);
+      FK_MARK(8);
       const size_t o = (size_t)t * H + b * 16 + r;
       a.update[o] = v;
       if (a.hidden_out) a.hidden_out[o] = raw_value<BFX>(xres[0]) + v;
@@ -1326,6 +1338,8 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   if (tid == 0 && s_fail)
     __hip_atomic_fetch_or(&a.tw.tickets[kStepTicketError], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
                           __HIP_MEMORY_SCOPE_AGENT);
+  FK_MARK(9);
+  FK_TIMELINE_COMMIT(deltanet_step, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------

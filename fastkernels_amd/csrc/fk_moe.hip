@@ -1340,6 +1340,8 @@ __device__ __forceinline__ void fused_tables(int id, float wt, int P, int K, int
 // ONE: compiled for a single token (T == 1): 8 prefetched down rows (one per
 // routed expert) and straight-line down code, which keeps the kernel within
 // the register budget of two workgroups' waves per SIMD.
+FK_TIMELINE_BUFFER(moe_fused)
+
 template <bool BFX, bool ONE>
 __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   constexpr int NPF = ONE ? 8 : kFusedPrefetch;
@@ -1371,6 +1373,8 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   bool have_tag = false;
   if (tid == 0) s_fail = 0;
   __syncthreads();
+  FK_TIMELINE_DECL;
+  FK_MARK(0);  // (timeline markers: diagnostic builds only)
 
   // ---------------- P1: router rows, shared gate/up, shared gate -----------
   // Units of 8 items, one per wavefront: router rows 8u.. (u < nrb), shared
@@ -1526,6 +1530,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
     }
     __syncthreads();
   }
+  FK_MARK(1);
   if (!have_tag) {
     const WaitLimits wl = wait_limits(a.ws.tickets, kTicketEpoch);
     tag = wl.tag;
@@ -1563,10 +1568,12 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
     }
     const bool ok = poll_tagged<NJE>(w, srcs, tag, plim);
     if (!ok) s_fail = 1;
+    FK_MARK(2);
     float p[NJE];
 #pragma unroll
     for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
     topk_select_regs<NJE>(p, E, K, lane, tk_id, tk_w);
+    FK_MARK(3);
     // (after a failed wait the logits may be stale: ids stay in range and
     // every output of this workgroup is poisoned below)
     if (!ok) tk_id = min(max(tk_id, 0), E - 1);
@@ -1622,6 +1629,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   const bool bad = s_fail;
   if (b == 0 && tid == 0 && !bad) store_coherent(&a.ws.tickets[kTicketEpoch], tag);
   const int U = s_nact;
+  FK_MARK(4);
   if (b == 0) {
     for (int j = tid; j < P; j += 512) {
       a.ids_out[j] = s_ids[j];
@@ -1747,6 +1755,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
     }
   }
 
+  FK_MARK(5);
   // ---------------- P4: stage activations, down rows, combine --------------
   // Every workgroup polls all activations (and the shared gates) into LDS,
   // kFusedStage tagged loads in flight per thread.
@@ -1770,6 +1779,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   __syncthreads();
   const bool bad_out = s_fail;
   if (tid == 0 && bad_out) __hip_atomic_fetch_or(err, FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  FK_MARK(6);
 
   // Down rows: each lane accumulates, per token, the gate- and routing-
   // weighted partial dots of every expert on its 8 columns; one wave sum per
@@ -1842,6 +1852,8 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       }
     }
   }
+  FK_MARK(7);
+  FK_TIMELINE_COMMIT(moe_fused, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------

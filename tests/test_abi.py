@@ -31,6 +31,20 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.fk_abi_version() == 1
 
 
+def test_product_library_carries_no_timeline_markers():
+    # the per-phase timeline exists only in the -DFK_TIMELINE diagnostic build
+    lib = _lib.load()
+    for unit in ("moe_fused", "deltanet_step"):
+        assert not hasattr(lib, f"fk_timeline_read_{unit}"), unit
+
+
+def test_timeline_markers_have_names():
+    from fastkernels_amd import timeline
+
+    assert [len(v[1]) for v in timeline.MARKERS.values()] == [8, 10]
+    assert all(len(names) <= 16 for _, names in timeline.MARKERS.values())  # kTimelineMarks
+
+
 def test_status_strings():
     assert _lib.status_string(_lib.FK_OK) == "ok"
     assert "workspace" in _lib.status_string(_lib.FK_ERR_WORKSPACE)
