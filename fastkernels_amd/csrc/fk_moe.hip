@@ -41,7 +41,7 @@ constexpr int kDownRows = 4 * kDownRowsPerWave;  // down rows per workgroup
 
 struct MoeWs {
   uint32_t* tickets;    // [16] arrival counters; [kTicketEpoch] = fused launch epoch
-  // Single-launch layer (T <= 2) and small-batch router (T <= 32): tagged hand-off words in
+  // Single-launch layer (T = 1) and small-batch router (T <= 32): tagged hand-off words in
   // a fixed-size region, so that no offset depends on the problem shape
   // (fk_moe_router / fk_moe_align lay the workspace out without I and H).
   uint64_t* f_logits;   // [T, E] router logits (capacity 256 * 256)
@@ -1190,8 +1190,10 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Single-launch MoE layer for small batches (T <= 2, H <= 2048, I <= 512,
-// E <= 256, bf16 router and expert weights, shared expert present).
+// Single-launch MoE layer for one token (T = 1, H <= 2048, I <= 512,
+// E <= 256, bf16 router and expert weights, shared expert present).  From
+// two tokens on the tagged router and the expert kernels are faster (T = 2:
+// 33.0 against 35.0 µs in this kernel).
 //
 // 512-thread workgroups, one per CU (grid capped at the co-resident
 // capacity).  Item q of every phase goes to wavefront (q / G) of workgroup
@@ -1199,15 +1201,15 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertArgs a) {
 //   P1  router logits (one expert row per item) and, overlapped, the shared
 //       expert's gate/up + SwiGLU (one intermediate per item) and its gate;
 //       each wavefront then prefetches its shared down row
-//   P2  every workgroup polls the logits of every token, computes the top-k
-//       (one wavefront per token) and the routing tables in LDS
+//   P2  every workgroup polls the token's logits and computes the top-k in
+//       one wavefront, whose lanes then hold the routing tables (expert u at
+//       position u, selection order)
 //   P3  routed gate/up + SwiGLU (one expert intermediate = 2 rows per item);
-//       each wavefront first prefetches its down row of every routed expert
-//       (U <= 16), so down weights stream concurrently with gate/up
+//       each wavefront then prefetches its down row of every routed expert,
+//       so down weights stream while the activations are handed off
 //   P4  every workgroup polls all activations into LDS; down: one output row
-//       per item, per-pair dots, then out[t] = sum_k w[t,k] y[pos(t,k)] +
-//       g_t y[shared t] (slot order, as the multi-launch combine) and
-//       layer_out = x + out.
+//       per item, out = g y[shared] + sum_k w_k y[k] (slot order, as the
+//       multi-launch combine) and layer_out = x + out.
 // Arithmetic order matches the multi-launch kernels, so both paths give
 // bitwise-identical results.
 //
@@ -1222,11 +1224,10 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertArgs a) {
 // Tags are 32-bit: a word left untouched for exactly 2^32 launches on one
 // workspace would read as current.
 // ---------------------------------------------------------------------------
-constexpr int kFusedMaxTokens = 2;  // from 3 tokens on, the tagged router + expert kernels are faster
+constexpr int kFusedMaxTokens = 1;  // from 2 tokens on, the tagged router + expert kernels are faster
 constexpr int kFusedMaxPairs = kFusedMaxTokens * 8;
 constexpr int kFusedWaves = 8;
 constexpr int kFusedMaxExperts = 256;
-constexpr int kFusedPrefetch = 16;
 constexpr int kFusedStage = 12;  // tagged loads in flight per thread while staging activations
 constexpr int kFusedChunk = 16;  // routed items per workgroup block: 16 tagged words = one 128-byte line
 static_assert(kFusedLogitWords >= (size_t)kFusedMaxTokens * kFusedMaxExperts, "fused logit region too small");
@@ -1302,55 +1303,17 @@ __device__ __forceinline__ float dot8_act_lds(const Raw8<true>& w, const float* 
   return d;
 }
 
-// Routing tables of P <= 32 (token, slot) pairs held one per lane of a
-// wavefront (pair l = t*K + k: expert id, routing weight).  Pair l goes to
-// permuted position rank_l = #{m : id_m < id_l or (id_m == id_l and m < l)}
-// (stable); it heads its expert's run when no earlier pair has its id, and
-// the run's index among the routed experts is the number of distinct
-// smaller ids.
-__device__ __forceinline__ void fused_tables(int id, float wt, int P, int K, int lane, int* s_tok, float* s_wpos,
-                                             int* s_active, int* s_aoff, int* s_nact) {
-  const int myid = lane < P ? id : 0x7fffffff;
-  int rank = 0, dups = 0;
-  uint32_t smaller = 0;  // bit m: id_m < id_l
-  for (int m = 0; m < P; ++m) {
-    const int v = __builtin_amdgcn_readlane(myid, m);
-    rank += (v < myid) | ((v == myid) & (m < lane));
-    dups += (v == myid) & (m < lane);
-    smaller |= (uint32_t)(v < myid) << m;
-  }
-  const bool head = lane < P && dups == 0;
-  const uint64_t heads = __ballot(head);
-  const int u = __popc(smaller & (uint32_t)heads);
-  if (lane < P) {
-    s_tok[rank] = lane / K;
-    s_wpos[rank] = wt;
-  }
-  if (head) {
-    s_active[u] = myid;
-    s_aoff[u] = rank;
-  }
-  if (lane == 0) {
-    const int nu = __popcll(heads);
-    *s_nact = nu;
-    s_aoff[nu] = P;
-  }
-}
-
-// ONE: compiled for a single token (T == 1): 8 prefetched down rows (one per
-// routed expert) and straight-line down code, which keeps the kernel within
-// the register budget of two workgroups' waves per SIMD.
+// One token: 8 prefetched down rows (one per routed expert) and straight-
+// line down code, which keeps the kernel within the register budget of two
+// workgroups' waves per SIMD.
 FK_TIMELINE_BUFFER(moe_fused)
 
-template <bool BFX, bool ONE>
+template <bool BFX>
 __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
-  constexpr int NPF = ONE ? 8 : kFusedPrefetch;
-  constexpr int NTOK = ONE ? 1 : kFusedMaxTokens;
+  constexpr int NPF = 8;  // prefetched down rows per wavefront: one per routed expert
   __shared__ __align__(16) int s_ids[kFusedMaxPairs];
   __shared__ float s_w[kFusedMaxPairs];
-  __shared__ int s_tok[kFusedMaxPairs];         // permuted position -> token
-  __shared__ int s_active[kFusedMaxPairs];      // routed experts, ascending
-  __shared__ int s_aoff[kFusedMaxPairs + 1];    // first permuted position of each (P at U)
+  __shared__ int s_active[kFusedMaxPairs];      // routed experts, selection order
   __shared__ int s_nact;
   __shared__ int s_fail;
   __shared__ uint32_t s_wtag[kFusedWaves];
@@ -1363,7 +1326,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   const int G = gridDim.x, b = blockIdx.x;
   const int NW = G * kFusedWaves;
   const int q0 = wave * G + b;
-  const int T = ONE ? 1 : a.T, H = a.H, E = a.E, K = a.K, I = f.I, P = T * K;
+  const int T = 1, H = a.H, E = a.E, K = a.K, I = f.I, P = K;
   const int nch = H >> 3;
   uint32_t* err = &a.ws.tickets[kTicketError];
   // The launch tag (epoch + 1) is loaded after the wavefront's P1 weight
@@ -1392,7 +1355,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
         // between them (a load whose dtype is tested at run time would wait
         // for every load before it).
         Raw8<true> wr[4], nr[4];
-        Raw8<BFX> xr[4];  // token 0 (the only one when ONE) rides with the weights
+        Raw8<BFX> xr[4];  // the token rides with the weights
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int cc = min(lane + kWave * j, nch - 1);
@@ -1417,32 +1380,22 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
           for (int qq = 0; qq < 8; ++qq) wn[j][qq] = c < nch ? w8[qq] * (a.off + n8[qq]) : 0.f;
         }
         const float bias = a.bias ? load_scalar(a.bias, a.bias_dt, e) : 0.f;
-#pragma unroll 1
-        for (int t = 0; t < NTOK; ++t) {
-          if (t < T) {
-            if (t > 0) {
+        float ss = 0.f, d = 0.f;
 #pragma unroll
-              for (int j = 0; j < 4; ++j)
-                xr[j] = load_raw8<BFX>(a.x, (size_t)t * H + (size_t)min(lane + kWave * j, nch - 1) * 8);
-            }
-            float ss = 0.f, d = 0.f;
+        for (int j = 0; j < 4; ++j) {
+          const bool in = lane + kWave * j < nch;
+          float x8[8];
+          raw8_to_f32<BFX>(xr[j], x8);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const bool in = lane + kWave * j < nch;
-              float x8[8];
-              raw8_to_f32<BFX>(xr[j], x8);
-#pragma unroll
-              for (int qq = 0; qq < 8; ++qq) {
-                const float xv = in ? x8[qq] : 0.f;
-                ss = fmaf(xv, xv, ss);
-                d = fmaf(xv, wn[j][qq], d);
-              }
-            }
-            ss = wave_sum(ss);
-            d = wave_sum(d);
-            mine = lane == t ? d * rsqrtf(ss / (float)H + a.eps) + bias : mine;
+          for (int qq = 0; qq < 8; ++qq) {
+            const float xv = in ? x8[qq] : 0.f;
+            ss = fmaf(xv, xv, ss);
+            d = fmaf(xv, wn[j][qq], d);
           }
         }
+        ss = wave_sum(ss);
+        d = wave_sum(d);
+        mine = d * rsqrtf(ss / (float)H + a.eps) + bias;
       }
       if (lane < T) s_chunk[lane][wave] = mine;
     } else if (unit < nrb + nsb) {
@@ -1491,26 +1444,16 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
 #pragma unroll
         for (int qq = 0; qq < 8; ++qq) g8[j][qq] = (f.sg && c < nch) ? g8[j][qq] : 0.f;
       }
-#pragma unroll 1
-      for (int t = 0; t < NTOK; ++t) {
-        if (t < T) {
-          if (t > 0) {
+      float d = 0.f;
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-              xr[j] = load_raw8<BFX>(a.x, (size_t)t * H + (size_t)min(lane + kWave * j, nch - 1) * 8);
-          }
-          float d = 0.f;
+      for (int j = 0; j < 4; ++j) {
+        float x8[8];
+        raw8_to_f32<BFX>(xr[j], x8);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float x8[8];
-            raw8_to_f32<BFX>(xr[j], x8);
-#pragma unroll
-            for (int qq = 0; qq < 8; ++qq) d = fmaf(x8[qq], g8[j][qq], d);
-          }
-          d = wave_sum(d);
-          if (lane == 0) s_chunk[t][0] = f.sg ? sigmoid(d) : 1.f;
-        }
+        for (int qq = 0; qq < 8; ++qq) d = fmaf(x8[qq], g8[j][qq], d);
       }
+      d = wave_sum(d);
+      if (lane == 0) s_chunk[0][0] = f.sg ? sigmoid(d) : 1.f;
     }
     __syncthreads();
     if (tid < 8 * T) {
@@ -1598,30 +1541,17 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       if (!poll_tagged<kChunk>(w, srcs, tag, plim)) s_fail = 1;
     }
   }
-  if (ONE) {
-    // One token: the top-k wavefront holds the K pairs in its lanes, each a
-    // distinct expert, so the tables are the selection itself (expert u at
-    // permuted position u, selection order) with no sort.
-    if (wave == 0) {
-      if (lane < K) {
-        s_active[lane] = tk_id;
-        s_aoff[lane] = lane;
-        s_wpos[lane] = tk_w;
-        s_tok[lane] = 0;
-      }
-      if (lane == 0) {
-        s_aoff[K] = K;
-        s_nact = K;
-      }
+  // One token: the top-k wavefront holds the K pairs in its lanes, each a
+  // distinct expert, so the tables are the selection itself (expert u at
+  // permuted position u, selection order) with no sort.
+  if (wave == 0) {
+    if (lane < K) {
+      s_active[lane] = tk_id;
+      s_wpos[lane] = tk_w;
     }
-    __syncthreads();
-  } else {
-    __syncthreads();
-    if (wave == 0)
-      fused_tables(lane < P ? s_ids[lane] : 0, lane < P ? s_w[lane] : 0.f, P, K, lane, s_tok, s_wpos, s_active,
-                   s_aoff, &s_nact);
-    __syncthreads();
+    if (lane == 0) s_nact = K;
   }
+  __syncthreads();
   // A failed wait poisons every later output of the workgroup.  Workgroup 0
   // advances the epoch only when every workgroup has read it (all started
   // records carry this launch's tag): otherwise a late workgroup would take
@@ -1646,7 +1576,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   // with lane swaps, which read inactive lanes' stale registers)
   const bool prefetch = U <= NPF && r_first < H;
   Raw8<true> dr[NPF];
-  if constexpr (ONE) {
+  {
     // One token: each routed expert holds one pair (expert u at permuted
     // position u).  The loads are issued in the order their data is needed,
     // and loads return roughly in issue order: the token's chunks, the first
@@ -1720,39 +1650,6 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
     } else {
       issue_down();  // a workgroup without a gate/up block
     }
-  } else {
-    if (prefetch && lane * 8 < I) {
-#pragma unroll
-      for (int u = 0; u < NPF; ++u) {
-        if (u < U) dr[u] = load_raw8_stream<true>(f.dn, ((size_t)s_active[u] * H + r_first) * I + (size_t)lane * 8);
-        else dr[u].a = u32x4{0, 0, 0, 0};
-      }
-    }
-    for (int blk = b; blk < nblk; blk += G) {
-      const int u = blk / bpe, i0 = (blk - u * bpe) * kFusedChunk;
-      const int e = s_active[u], pa = s_aoff[u], np = s_aoff[u + 1] - pa;
-      const int ia = i0 + 2 * wave;
-      const char* we = reinterpret_cast<const char*>(f.gu) + (size_t)e * 2 * I * H * 2;
-      Raw8<true> ga[4], ua8[4], gb[4], ub8[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = lane + kWave * j;
-        if (c < nch) {
-          ga[j] = load_raw8_stream<true>(we, (size_t)ia * H + (size_t)c * 8);
-          gb[j] = load_raw8_stream<true>(we, (size_t)(ia + 1) * H + (size_t)c * 8);
-          ua8[j] = load_raw8_stream<true>(we, (size_t)(I + ia) * H + (size_t)c * 8);
-          ub8[j] = load_raw8_stream<true>(we, (size_t)(I + ia + 1) * H + (size_t)c * 8);
-        }
-      }
-      fused_gateup_item<BFX>(ga, ua8, a.x, H, lane, np, s_tok + pa, &s_chunk[0][2 * wave]);
-      fused_gateup_item<BFX>(gb, ub8, a.x, H, lane, np, s_tok + pa, &s_chunk[0][2 * wave + 1]);
-      __syncthreads();
-      if (tid < kFusedChunk * np) {
-        const int pp = tid / kFusedChunk, l = tid % kFusedChunk;
-        store_tagged(a.ws.f_act + (size_t)(pa + pp) * I + i0 + l, poison_if(bad, s_chunk[pp][l]), tag);
-      }
-      __syncthreads();
-    }
   }
 
   FK_MARK(5);
@@ -1781,53 +1678,29 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   if (tid == 0 && bad_out) __hip_atomic_fetch_or(err, FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   FK_MARK(6);
 
-  // Down rows: each lane accumulates, per token, the gate- and routing-
-  // weighted partial dots of every expert on its 8 columns; one wave sum per
-  // token gives out[t, r].
+  // Down rows: each lane accumulates the gate- and routing-weighted partial
+  // dots of the shared and every routed expert on its 8 columns (shared
+  // first, then the routed experts in selection order, as the multi-launch
+  // combine); one wave sum gives out[r].
   const float* s_sg = s_act + n_act;
   for (int r = q0; r < H; r += NW) {
     const bool first = r == r_first;
-    if (ONE && first && prefetch) {
-      // One token, down rows prefetched: expert u sits at permuted position
-      // u; unused slots have zero rows and zero weight, so the code has no
-      // branches and every LDS read can be issued at once.
-      float acc = s_sg[0] * dot8_act_lds(sdr, s_act + (size_t)P * I, lane, I);
+    float acc;
+    if (first && prefetch) {
+      // Down rows prefetched: expert u sits at permuted position u; the code
+      // has no branches and every LDS read can be issued at once.
+      acc = s_sg[0] * dot8_act_lds(sdr, s_act + (size_t)P * I, lane, I);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < NPF; ++u) {
         // (slots past U hold a repeated row: dropped, not multiplied by 0)
         const float d = dot8_act_lds(dr[u], s_act + (size_t)(u < U ? u : 0) * I, lane, I);
         acc = u < U ? fmaf(s_wpos[u], d, acc) : acc;
       }
-      const float o = poison_if(bad_out, wave_sum(acc));
-      if (lane == 0) {
-        f.out[r] = o;
-        if (f.layer_out) f.layer_out[r] = raw_value<BFX>(x_first_raw[0]) + o;
-      }
-      continue;
-    }
-    float acc[kFusedMaxTokens];
-    {
+    } else {
       Raw8<true> w;
       if (first) w = sdr;
       else if (lane * 8 < I) w = load_raw8_stream<true>(f.sdn, (size_t)r * I + (size_t)lane * 8);
-#pragma unroll
-      for (int tt = 0; tt < kFusedMaxTokens; ++tt)
-        acc[tt] = tt < T ? s_sg[tt] * dot8_act_lds(w, s_act + (size_t)(P + tt) * I, lane, I) : 0.f;
-    }
-    auto add_expert = [&](const Raw8<true>& w, int u) {
-      for (int pos = s_aoff[u]; pos < s_aoff[u + 1]; ++pos) {
-        const float d = dot8_act_lds(w, s_act + (size_t)pos * I, lane, I);
-        const int t = s_tok[pos];
-        const float wt = s_wpos[pos];
-#pragma unroll
-        for (int tt = 0; tt < kFusedMaxTokens; ++tt) acc[tt] = tt == t ? fmaf(wt, d, acc[tt]) : acc[tt];
-      }
-    };
-    if (!ONE && first && prefetch) {
-#pragma unroll
-      for (int u = 0; u < NPF; ++u)
-        if (u < U) add_expert(dr[u], u);
-    } else {
+      acc = s_sg[0] * dot8_act_lds(w, s_act + (size_t)P * I, lane, I);
       for (int u0 = 0; u0 < U; u0 += 8) {
         Raw8<true> wb8[8];
 #pragma unroll
@@ -1836,20 +1709,14 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
             wb8[v] = load_raw8_stream<true>(f.dn, ((size_t)s_active[u0 + v] * H + r) * I + (size_t)lane * 8);
 #pragma unroll
         for (int v = 0; v < 8; ++v)
-          if (u0 + v < U) add_expert(wb8[v], u0 + v);
+          if (u0 + v < U) acc = fmaf(s_wpos[u0 + v], dot8_act_lds(wb8[v], s_act + (size_t)(u0 + v) * I, lane, I), acc);
       }
     }
-#pragma unroll
-    for (int tt = 0; tt < kFusedMaxTokens; ++tt) {
-      if (tt < T) {
-        const float o = poison_if(bad_out, wave_sum(acc[tt]));
-        if (lane == tt) {
-          const size_t off = (size_t)tt * H + r;
-          f.out[off] = o;
-          if (f.layer_out)
-            f.layer_out[off] = (first ? raw_value<BFX>(x_first_raw[0]) : load_scalar(a.x, BFX ? FK_DTYPE_BF16 : FK_DTYPE_F32, off)) + o;
-        }
-      }
+    const float o = poison_if(bad_out, wave_sum(acc));
+    if (lane == 0) {
+      f.out[r] = o;
+      if (f.layer_out)
+        f.layer_out[r] = (first ? raw_value<BFX>(x_first_raw[0]) : load_scalar(a.x, BFX ? FK_DTYPE_BF16 : FK_DTYPE_F32, r)) + o;
     }
   }
   FK_MARK(7);
@@ -2219,11 +2086,11 @@ static bool fused_eligible(int T, int H, int I, int E, int K, int router_dt, int
 
 constexpr size_t kFusedMaxDynLds = ((size_t)(kFusedMaxPairs + kFusedMaxTokens) * 512 + kFusedMaxTokens) * sizeof(float);
 
-template <bool BX, bool ONE>
+template <bool BX>
 static int launch_fused_t(const FusedArgs& fa, hipStream_t stream) {
   static int cap_cache[64] = {0};
   static bool attr_set[64] = {false};
-  auto kernel = moe_fused_kernel<BX, ONE>;
+  auto kernel = moe_fused_kernel<BX>;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(FK_ERR_LAUNCH, "no current HIP device");
   if (!attr_set[dev]) {
@@ -2625,10 +2492,8 @@ int fk_moe_layer(const void* hidden, int hidden_dtype, const void* norm_weight, 
     fa.I = intermediate;
     fa.out = moe_out;
     fa.layer_out = layer_out;
-    const bool one = tokens == 1;
-    if (hidden_dtype == FK_DTYPE_BF16)
-      return one ? launch_fused_t<true, true>(fa, as_stream(stream)) : launch_fused_t<true, false>(fa, as_stream(stream));
-    return one ? launch_fused_t<false, true>(fa, as_stream(stream)) : launch_fused_t<false, false>(fa, as_stream(stream));
+    if (hidden_dtype == FK_DTYPE_BF16) return launch_fused_t<true>(fa, as_stream(stream));
+    return launch_fused_t<false>(fa, as_stream(stream));
   }
   st = fk_moe_router(hidden, hidden_dtype, norm_weight, norm_dtype, router_weight, router_dtype, router_bias,
                      bias_dtype, tokens, hidden_size, num_experts, top_k, eps, norm_offset, logits, topk_ids,

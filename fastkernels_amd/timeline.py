@@ -7,7 +7,7 @@ Usage, on a GPU, after ``python -m fastkernels_amd.build --timeline``::
 
 It loads ``libfastkernels_hip_timeline.so``: the same kernels compiled with
 ``-DFK_TIMELINE``, in which thread 0 of every workgroup of
-``moe_fused_kernel`` (the MoE layer at T <= 2) and ``deltanet_step_kernel``
+``moe_fused_kernel`` (the MoE layer at T = 1) and ``deltanet_step_kernel``
 keeps the wall clock (100 MHz) at each phase boundary.  Steps run in steady
 state: 16 back-to-back steps over 4 weight sets are captured as one HIP graph
 and replayed; the markers are cleared and the graph replayed once more, so the

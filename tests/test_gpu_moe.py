@@ -271,7 +271,7 @@ def test_moe_layer_deterministic(device, real_gpu):
 def test_moe_layer_fp32_hidden(device, real_cpu, real_gpu, tokens):
     # the real-weight runner feeds fp32 hidden (bench/qwen36_full_decode.py:152),
     # and a layer stack feeds each layer the previous layer's fp32 output:
-    # single-launch (T <= 2), GEMV (T = 8) and T >= 64 expert paths
+    # single-launch (T = 1), GEMV (T = 8) and T >= 64 expert paths
     x = wl.make_hidden(tokens, H, seed=9, dtype=torch.float32)
     lh, moe, logits, ids, w = hip.hip_qwen36_batched_moe_layer_decode(x.to(device), *_moe_args(real_gpu), top_k=K)
     ref = oracle.routed_experts(x, ids.cpu(), w.cpu(), real_cpu["expert_gate_up_weight"], real_cpu["expert_down_weight"])
@@ -357,7 +357,7 @@ def test_fused_layer_repeated_calls_stay_consistent(device, real_gpu):
 @pytest.mark.parametrize("tokens", [1, 2, 5])
 def test_moe_layer_reduced_shapes(device, shape, tokens):
     # Smaller expert counts and intermediate sizes through every small-T
-    # path (single launch at T = 1 and 2, router + GEMV experts at T = 5).
+    # path (single launch at T = 1, router + GEMV experts at T = 2 and 5).
     # I < 512 leaves lanes of the single-launch kernel's down rows idle,
     # which must not change its lane reductions.
     e, h, i = shape

@@ -90,7 +90,7 @@ def test_moe_layer_beyond_256_tokens(device, e, h, i, tokens):
 @pytest.mark.parametrize("tokens", [1, 2, 16, 64])
 def test_moe_layer_hidden_not_multiple_of_16(device, tokens):
     # H = 1032 = 8 * 129: an odd number of 8-element chunks per row through
-    # the single-launch layer (T <= 2), the tagged router and the GEMV experts
+    # the single-launch layer (T = 1), the tagged router and the GEMV experts
     _check(device, 64, 1032, 128, tokens, seed=300 + tokens)
 
 
