@@ -87,6 +87,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [P, I, P, I, P, P, P, P, P, P, I, I, I, I, I, c_float, P, P, P],
     ),
+    "fk_synthetic_attention": (
+        c_int,
+        [P, I, P, P, I, P, P, P, P, P, I, I, I, I, I, I, I, I, c_float, P, P],
+    ),
 }
 
 _lock = threading.Lock()

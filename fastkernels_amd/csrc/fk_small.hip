@@ -238,6 +238,139 @@ __global__ __launch_bounds__(256) void synthetic_deltanet_kernel(SynDnArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Synthetic grouped-query attention (one token, one workgroup).  Semantics of
+// reference_qwen36_attention_decode (reference/qwen36_decode.py:174-209),
+// rounded where triton_synthetic_qwen36_attention_decode
+// (kernels/triton/qwen36_attention.py:852-998) stores its intermediates:
+// q, k and v are projected in fp32 from the plain-weight RMSNorm and held in
+// the hidden dtype; RoPE (interleaved pairs, angle position / 10^4^(2i/r))
+// turns q (held in the hidden dtype) and k; the new k and v rows go to row
+// `position` of the caches (cache dtype); every query head attends over
+// cache rows 0..position of its kv head (softmax of q.k / sqrt(head_dim));
+// out = x + W_o attended, attended held in the hidden dtype.
+// ---------------------------------------------------------------------------
+constexpr int kSynAttnMax = 128;  // hidden, query and kv widths, cache rows
+
+struct SynAttnArgs {
+  const void* x;
+  int x_dt;
+  void* kc;
+  void* vc;
+  int c_dt;
+  const void* nw;
+  const void* qw;
+  const void* kw;
+  const void* vw;
+  const void* ow;
+  int w_dt;
+  int H, heads, kvh, hd, rope_dim, pos;
+  float eps;
+  void* out;
+};
+
+__device__ __forceinline__ float round_to_dtype(int dtype, float v) {
+  return dtype == FK_DTYPE_BF16 ? bf16_bits_to_f32(f32_to_bf16_bits(v)) : v;
+}
+
+__global__ __launch_bounds__(256) void synthetic_attention_kernel(SynAttnArgs a) {
+  __shared__ float s_x[kSynAttnMax], s_xn[kSynAttnMax], s_p[3 * kSynAttnMax];  // s_p: q | k | v (hidden dtype)
+  __shared__ float s_q[kSynAttnMax], s_k[kSynAttnMax], s_v[kSynAttnMax], s_att[kSynAttnMax];
+  __shared__ float s_red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int QW = a.heads * a.hd, KW = a.kvh * a.hd, P = a.pos + 1;
+  float ss = 0.f;
+  for (int h = tid; h < a.H; h += 256) {
+    const float v = load_scalar(a.x, a.x_dt, h);
+    s_x[h] = v;
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) s_red[wave] = ss;
+  __syncthreads();
+  const float rs = rsqrtf((s_red[0] + s_red[1] + s_red[2] + s_red[3]) / (float)a.H + a.eps);
+  for (int h = tid; h < a.H; h += 256) s_xn[h] = s_x[h] * rs * load_scalar(a.nw, a.w_dt, h);
+  __syncthreads();
+  // q | k | v rows, held in the hidden dtype
+  for (int r = tid; r < QW + 2 * KW; r += 256) {
+    const void* w = r < QW ? a.qw : r < QW + KW ? a.kw : a.vw;
+    const int row = r < QW ? r : r < QW + KW ? r - QW : r - QW - KW;
+    float acc = 0.f;
+    for (int h = 0; h < a.H; ++h) acc = fmaf(load_scalar(w, a.w_dt, (size_t)row * a.H + h), s_xn[h], acc);
+    s_p[r] = round_to_dtype(a.x_dt, acc);
+  }
+  __syncthreads();
+  // RoPE on q and k; the new k and v rows into the caches
+  int rot = a.rope_dim < a.hd ? a.rope_dim : a.hd;
+  rot -= rot % 2;
+  for (int i = tid; i < QW + KW; i += 256) {
+    const bool isq = i < QW;
+    const int j = isq ? i : i - QW, dim = j % a.hd;
+    const float* src = isq ? s_p : s_p + QW;
+    float v = src[j];
+    if (dim < rot) {
+      const float pair = src[j - dim + (dim ^ 1)];
+      const float ang = (float)a.pos / expf(logf(10000.0f) * ((float)(dim & ~1) / (float)rot));
+      const float c = cosf(ang), sn = sinf(ang);
+      v = (dim & 1) ? pair * sn + v * c : v * c - pair * sn;
+    }
+    if (isq) {
+      s_q[j] = round_to_dtype(a.x_dt, v);
+    } else {
+      s_k[j] = round_to_dtype(a.c_dt, v);
+      const float vv = s_p[QW + KW + j];
+      s_v[j] = round_to_dtype(a.c_dt, vv);
+      store_scalar(a.kc, a.c_dt, (size_t)a.pos * KW + j, v);
+      store_scalar(a.vc, a.c_dt, (size_t)a.pos * KW + j, vv);
+    }
+  }
+  __syncthreads();
+  // Wavefront w takes query heads w, w + 4, ...; lane l positions l, l + 64
+  // (the new row from LDS, older rows from the cache).
+  const float scale = rsqrtf((float)a.hd);
+  const int group = a.heads / a.kvh;
+  for (int h = wave; h < a.heads; h += 4) {
+    const int kv = h / group;
+    float sc[2], e[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = lane + 64 * u;
+      sc[u] = -INFINITY;
+      if (t < P) {
+        float d = 0.f;
+        for (int dd = 0; dd < a.hd; ++dd) {
+          const float kvl = t == a.pos ? s_k[kv * a.hd + dd] : load_scalar(a.kc, a.c_dt, (size_t)t * KW + kv * a.hd + dd);
+          d = fmaf(kvl, s_q[h * a.hd + dd], d);
+        }
+        sc[u] = d * scale;
+      }
+    }
+    const float m = wave_max(fmaxf(sc[0], sc[1]));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) e[u] = lane + 64 * u < P ? expf(sc[u] - m) : 0.f;
+    const float den = wave_sum(e[0] + e[1]);
+    for (int dd = 0; dd < a.hd; ++dd) {
+      float part = 0.f;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int t = lane + 64 * u;
+        if (t < P) {
+          const float vl = t == a.pos ? s_v[kv * a.hd + dd] : load_scalar(a.vc, a.c_dt, (size_t)t * KW + kv * a.hd + dd);
+          part = fmaf(e[u] / den, vl, part);
+        }
+      }
+      part = wave_sum(part);
+      if (lane == 0) s_att[h * a.hd + dd] = round_to_dtype(a.x_dt, part);
+    }
+  }
+  __syncthreads();
+  for (int h = tid; h < a.H; h += 256) {
+    float d = 0.f;
+    for (int j = 0; j < QW; ++j) d = fmaf(load_scalar(a.ow, a.w_dt, (size_t)h * QW + j), s_att[j], d);
+    store_scalar(a.out, a.x_dt, h, s_x[h] + d);
+  }
+}
+
 }  // namespace fk
 
 using namespace fk;
@@ -381,6 +514,47 @@ int fk_synthetic_deltanet(const void* hidden, int hidden_dtype, const void* stat
   da.s_out = state_out;
   hipLaunchKernelGGL(synthetic_deltanet_kernel, dim3(1), dim3(256), 0, as_stream(stream), da);
   return check_launch("synthetic_deltanet_kernel");
+}
+
+int fk_synthetic_attention(const void* hidden, int hidden_dtype, void* key_cache, void* value_cache, int cache_dtype,
+                           const void* norm_weight, const void* q_weight, const void* k_weight, const void* v_weight,
+                           const void* out_weight, int weight_dtype, int hidden_size, int attention_heads,
+                           int kv_heads, int head_dim, int rope_dim, int position, int max_positions, float eps,
+                           void* out, void* stream) {
+  if (!is_float_dtype(hidden_dtype) || !is_float_dtype(cache_dtype) || !is_float_dtype(weight_dtype))
+    return fail(FK_ERR_DTYPE, "synthetic attention tensors must be f32 or bf16");
+  if (hidden_size < 1 || attention_heads < 1 || kv_heads < 1 || head_dim < 1 || max_positions < 1)
+    return fail(FK_ERR_INVALID, "synthetic attention sizes must be positive");
+  if (attention_heads % kv_heads != 0) return fail(FK_ERR_INVALID, "attention_heads must be a multiple of kv_heads");
+  if (position < 0 || position >= max_positions) return fail(FK_ERR_INVALID, "position must be in [0, max_positions)");
+  if (hidden_size > kSynAttnMax || attention_heads * head_dim > kSynAttnMax || kv_heads * head_dim > kSynAttnMax ||
+      max_positions > kSynAttnMax)
+    return fail(FK_ERR_UNSUPPORTED, "synthetic attention widths and cache length must be <= %d", kSynAttnMax);
+  if (!hidden || !key_cache || !value_cache || !norm_weight || !q_weight || !k_weight || !v_weight || !out_weight ||
+      !out)
+    return fail(FK_ERR_INVALID, "synthetic attention pointers must be non-NULL");
+  SynAttnArgs sa;
+  sa.x = hidden;
+  sa.x_dt = hidden_dtype;
+  sa.kc = key_cache;
+  sa.vc = value_cache;
+  sa.c_dt = cache_dtype;
+  sa.nw = norm_weight;
+  sa.qw = q_weight;
+  sa.kw = k_weight;
+  sa.vw = v_weight;
+  sa.ow = out_weight;
+  sa.w_dt = weight_dtype;
+  sa.H = hidden_size;
+  sa.heads = attention_heads;
+  sa.kvh = kv_heads;
+  sa.hd = head_dim;
+  sa.rope_dim = rope_dim < 0 ? 0 : rope_dim;
+  sa.pos = position;
+  sa.eps = eps;
+  sa.out = out;
+  hipLaunchKernelGGL(synthetic_attention_kernel, dim3(1), dim3(256), 0, as_stream(stream), sa);
+  return check_launch("synthetic_attention_kernel");
 }
 
 }  // extern "C"

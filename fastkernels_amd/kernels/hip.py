@@ -54,6 +54,8 @@ __all__ = [
     "hip_synthetic_qwen36_moe_decode",
     "hip_synthetic_qwen36_deltanet_decode",
     "hip_synthetic_qwen36_deltanet_moe_decode",
+    "hip_synthetic_qwen36_attention_decode",
+    "hip_synthetic_qwen36_attention_moe_decode",
     "workspace_status",
     "TRITON_ALIASES",
 ]
@@ -1135,6 +1137,77 @@ def hip_synthetic_qwen36_deltanet_moe_decode(hidden, state, layer, *, qk_heads, 
         layer["expert_down_weight"], layer["shared_gate_up_weight"], layer["shared_down_weight"], top_k=top_k,
     )
     return hidden, next_state
+
+
+def hip_synthetic_qwen36_attention_decode(
+    hidden, key_cache, value_cache, norm_weight, q_weight, k_weight, v_weight, out_weight,
+    *, position: int, attention_heads: int, kv_heads: int, head_dim: int, rope_dim: int, eps: float = 1e-6,
+    fuse_project_rope: bool = False, copy_cache: bool = True,
+):
+    """One-token synthetic grouped-query attention: `(hidden', key_cache', value_cache')`
+    (reference qwen36_attention.py:852-998).  `copy_cache=False` updates the
+    caches in place and returns them; `fuse_project_rope` selects a launch
+    shape in the reference and changes nothing here (one launch either way)."""
+
+    _require_lib()
+    if hidden.ndim != 1:
+        raise ValueError("hidden must have shape [hidden_size]")
+    if key_cache.ndim != 3 or value_cache.ndim != 3:
+        raise ValueError("key/value caches must have shape [positions, kv_heads, head_dim]")
+    if not hidden.is_cuda or not key_cache.is_cuda or not value_cache.is_cuda:
+        raise ValueError("hidden and caches must be CUDA tensors")
+    if key_cache.shape != value_cache.shape:
+        raise ValueError("key and value caches must have the same shape")
+    if tuple(key_cache.shape[1:]) != (kv_heads, head_dim):
+        raise ValueError("cache shape does not match kv_heads/head_dim")
+    if position >= key_cache.shape[0]:
+        raise ValueError("position exceeds cache length")
+    hidden_size = hidden.shape[0]
+    q_width, kv_width, max_positions = attention_heads * head_dim, kv_heads * head_dim, key_cache.shape[0]
+    if hidden_size > 128 or q_width > 128 or kv_width > 128 or max_positions > 128:
+        raise ValueError("prototype synthetic Qwen3.6 attention kernel only supports tiny synthetic shapes")
+    if position < 0:
+        raise ValueError("position must be >= 0")
+    if attention_heads % kv_heads != 0:
+        raise ValueError("attention_heads must be a multiple of kv_heads")
+    if key_cache.dtype != value_cache.dtype:
+        raise ValueError("key and value caches must share a dtype")
+    ws = [_dense(t) for t in (norm_weight, q_weight, k_weight, v_weight, out_weight)]
+    if len({t.dtype for t in ws}) != 1:
+        raise ValueError("synthetic attention weights must share a dtype")
+    x = _dense(hidden)
+    if copy_cache:
+        kc, vc = key_cache.clone(), value_cache.clone()
+    else:
+        if not key_cache.is_contiguous() or not value_cache.is_contiguous():
+            raise ValueError("copy_cache=False needs contiguous caches")
+        kc, vc = key_cache, value_cache
+    out = torch.empty_like(x)
+    _lib.call(
+        "fk_synthetic_attention",
+        x.data_ptr(), _fcode(x, "hidden"), kc.data_ptr(), vc.data_ptr(), _fcode(kc, "key_cache"),
+        *[t.data_ptr() for t in ws], _fcode(ws[0], "weights"), hidden_size, attention_heads, kv_heads, head_dim,
+        rope_dim, position, max_positions, float(eps), out.data_ptr(), _stream(x.device),
+    )
+    return out, kc, vc
+
+
+def hip_synthetic_qwen36_attention_moe_decode(
+    hidden, key_cache, value_cache, layer, *, position: int, attention_heads: int, kv_heads: int, head_dim: int,
+    rope_dim: int, top_k: int, copy_cache: bool = True,
+):
+    """Synthetic Attention -> MoE layer (reference qwen36_layer.py:346-384)."""
+
+    hidden, next_key_cache, next_value_cache = hip_synthetic_qwen36_attention_decode(
+        hidden, key_cache, value_cache, layer["norm_weight"], layer["q_weight"], layer["k_weight"],
+        layer["v_weight"], layer["out_weight"], position=position, attention_heads=attention_heads,
+        kv_heads=kv_heads, head_dim=head_dim, rope_dim=rope_dim, copy_cache=copy_cache,
+    )
+    hidden = hip_synthetic_qwen36_moe_decode(
+        hidden, layer["norm_weight"], layer["router_weight"], layer["expert_gate_up_weight"],
+        layer["expert_down_weight"], layer["shared_gate_up_weight"], layer["shared_down_weight"], top_k=top_k,
+    )
+    return hidden, next_key_cache, next_value_cache
 
 
 # Reference name -> HIP implementation, for import-level drop-in switching.

@@ -369,6 +369,26 @@ int fk_synthetic_deltanet(const void* hidden, int hidden_dtype,
                           int head_dim, int value_dim_per_head, float eps,
                           void* hidden_out, void* state_out, void* stream);
 
+/* One-token synthetic grouped-query attention: xn = RMSNorm(x) * w;
+ * q, k, v = W xn (held in hidden_dtype); RoPE on q and k (interleaved pairs,
+ * angle position / 10000^(2i / r), r = min(rope_dim, head_dim) rounded down
+ * to even); k and v written to row `position` of the caches ([max_positions,
+ * kv_heads, head_dim], cache_dtype, updated in place); each query head
+ * attends over rows 0..position of its kv head; out = x + W_o attended, in
+ * hidden_dtype.  Limits: widths and max_positions <= 128.
+ * Replaces triton_synthetic_qwen36_attention_decode
+ * (qwen36_attention.py:852-998; the caller copies the caches first when it
+ * wants them untouched, as the reference's copy_cache=True does). */
+int fk_synthetic_attention(const void* hidden, int hidden_dtype,
+                           void* key_cache, void* value_cache, int cache_dtype,
+                           const void* norm_weight, const void* q_weight,
+                           const void* k_weight, const void* v_weight,
+                           const void* out_weight, int weight_dtype,
+                           int hidden_size, int attention_heads, int kv_heads,
+                           int head_dim, int rope_dim, int position,
+                           int max_positions, float eps, void* out,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -35,6 +35,10 @@ Pinning (what checks each function against something other than itself):
                       with expanded kv heads and an offset causal mask; one
                       position gives the value row; cache rows outside the
                       step untouched
+  synthetic attention float64 restatement with RoPE as complex
+                      multiplication and torch scaled_dot_product_attention
+                      over expanded kv heads; caller's caches untouched, rows
+                      other than the step's unchanged
 No function is left "parity unpinned" at the north-star tolerances; the only
 unpinned behaviours are torch.topk's tie order (replaced here by the
 documented lower-id rule) and cross-version bf16 rounding of the synthetic

@@ -39,6 +39,8 @@ __all__ = [
     "attention_moe_layer",
     "synthetic_moe_decode",
     "synthetic_deltanet_decode",
+    "synthetic_attention_decode",
+    "synthetic_rope",
 ]
 
 
@@ -591,3 +593,50 @@ def synthetic_deltanet_decode(
     recurrent = (q.unsqueeze(-1) * new_state).sum(dim=-2) * gate
     out = recurrent.reshape(-1) @ layer["out_weight"].transpose(-1, -2)
     return hidden + out, new_state
+
+
+def synthetic_rope(values: Any, position: int, rope_dim: int) -> Any:
+    """Interleaved-pair RoPE of the synthetic oracle (reference/qwen36_decode.py:37-56):
+    pairs (2i, 2i + 1) of the first min(rope_dim, head_dim) (even) dims turn by
+    position / 10000^(2i / r); cos and sin are cast to the values' dtype."""
+
+    r = min(rope_dim, values.shape[-1]) if rope_dim > 0 else 0
+    r -= r % 2
+    if r == 0:
+        return values
+    ang = position / (10000.0 ** (torch.arange(0, r, 2, dtype=torch.float32) / r))
+    cos, sin = torch.cos(ang).to(values.dtype), torch.sin(ang).to(values.dtype)
+    out = values.clone()
+    even, odd = values[..., :r:2], values[..., 1:r:2]
+    out[..., :r:2] = even * cos - odd * sin
+    out[..., 1:r:2] = even * sin + odd * cos
+    return out
+
+
+def synthetic_attention_decode(
+    hidden: Any, key_cache: Any, value_cache: Any, layer: dict[str, Any], *, attention_heads: int, kv_heads: int,
+    head_dim: int, rope_dim: int, position: int, eps: float = 1e-6
+) -> tuple[Any, Any, Any]:
+    """One-token grouped-query attention of the synthetic oracle
+    (reference/qwen36_decode.py:174-209), in the input dtype: plain-weight
+    RMSNorm, q/k/v projections, RoPE on q and k, the new k and v rows written
+    at `position` of copies of the caches, softmax(q.k / sqrt(head_dim)) over
+    rows 0..position of each query head's kv head, `hidden + W_o attended`."""
+
+    x = rms_norm_plain(hidden, layer["norm_weight"], eps)
+    q = (x @ layer["q_weight"].transpose(-1, -2)).reshape(attention_heads, head_dim)
+    k = (x @ layer["k_weight"].transpose(-1, -2)).reshape(kv_heads, head_dim)
+    v = (x @ layer["v_weight"].transpose(-1, -2)).reshape(kv_heads, head_dim)
+    q, k = synthetic_rope(q, position, rope_dim), synthetic_rope(k, position, rope_dim)
+    kc, vc = key_cache.clone(), value_cache.clone()
+    kc[position] = k
+    vc[position] = v
+    keys, values = kc[: position + 1], vc[: position + 1]
+    group = attention_heads // kv_heads
+    heads = []
+    for h in range(attention_heads):
+        scores = (keys[:, h // group] @ q[h]) * (1.0 / head_dim**0.5)
+        heads.append(torch.softmax(scores, dim=-1) @ values[:, h // group])
+    attended = torch.stack(heads).reshape(-1)
+    return hidden + attended @ layer["out_weight"].transpose(-1, -2), kc, vc
+

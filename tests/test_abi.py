@@ -45,6 +45,49 @@ def test_timeline_markers_have_names():
     assert all(len(names) <= 16 for _, names in timeline.MARKERS.values())  # kTimelineMarks
 
 
+# The names of the reference operator package (fastkernels.kernels.triton
+# __all__, kernels/triton/__init__.py:37-62): a host switched to this package
+# finds every one of them.
+REFERENCE_OPERATORS = [
+    "triton_expert_histogram", "triton_fused_swiglu", "triton_qwen36_batched_attention_decode",
+    "triton_qwen36_batched_attention_moe_layer_decode", "triton_qwen36_batched_attention_project",
+    "triton_qwen36_batched_deltanet_conv", "triton_qwen36_batched_deltanet_moe_layer_decode",
+    "triton_qwen36_batched_deltanet_project", "triton_qwen36_batched_deltanet_recurrent_output",
+    "triton_qwen36_batched_moe_decode", "triton_qwen36_batched_moe_layer_decode",
+    "triton_qwen36_batched_moe_router_decode", "triton_qwen36_batched_routed_experts_decode",
+    "triton_qwen36_batched_routed_shared_experts_decode", "triton_qwen36_moe_decode",
+    "triton_qwen36_moe_router_decode", "triton_qwen36_routed_experts_decode",
+    "triton_qwen36_routed_shared_experts_decode", "triton_qwen36_single_expert_mlp_decode",
+    "triton_synthetic_qwen36_attention_decode", "triton_synthetic_qwen36_attention_moe_decode",
+    "triton_synthetic_qwen36_deltanet_decode", "triton_synthetic_qwen36_deltanet_moe_decode",
+    "triton_synthetic_qwen36_moe_decode",
+]
+
+
+def test_every_reference_operator_name_is_exported():
+    assert len(REFERENCE_OPERATORS) == 24
+    assert set(REFERENCE_OPERATORS) == set(hip.TRITON_ALIASES)
+    for name in REFERENCE_OPERATORS:
+        assert getattr(hip, name) is hip.TRITON_ALIASES[name], name
+    # the reference's own test module imports these names in one statement
+    ns: dict = {}
+    exec("from fastkernels_amd.kernels.hip import " + ", ".join(REFERENCE_OPERATORS), ns)
+    assert all(name in ns for name in REFERENCE_OPERATORS)
+
+
+def test_synthetic_attention_rejects_like_the_reference():
+    # reference qwen36_attention.py:875-893: checked in this order, before any GPU work
+    kc = torch.zeros(8, 2, 4)
+    args = (torch.zeros(16), kc, kc, None, None, None, None, None)
+    kw = dict(position=2, attention_heads=4, kv_heads=2, head_dim=4, rope_dim=4)
+    with pytest.raises(ValueError, match="hidden must have shape"):
+        hip.hip_synthetic_qwen36_attention_decode(torch.zeros(2, 16), *args[1:], **kw)
+    with pytest.raises(ValueError, match="key/value caches must have shape"):
+        hip.hip_synthetic_qwen36_attention_decode(args[0], torch.zeros(8, 8), kc, *args[3:], **kw)
+    with pytest.raises(ValueError, match="CUDA tensors"):
+        hip.hip_synthetic_qwen36_attention_decode(*args, **kw)
+
+
 def test_status_strings():
     assert _lib.status_string(_lib.FK_OK) == "ok"
     assert "workspace" in _lib.status_string(_lib.FK_ERR_WORKSPACE)
@@ -178,24 +221,6 @@ def test_attention_validation():
         hip.hip_qwen36_batched_attention_decode(x, kc, kc.clone(), *args, **kw)
     with pytest.raises(ValueError, match="weight must have shape"):
         hip.hip_qwen36_batched_attention_project(x, torch.zeros(16), torch.zeros(32, 8), args[2], args[3])
-
-
-def test_triton_aliases_cover_reference_hot_path_names():
-    expected = {
-        "triton_expert_histogram", "triton_fused_swiglu", "triton_qwen36_batched_moe_decode",
-        "triton_qwen36_batched_deltanet_moe_layer_decode", "triton_qwen36_batched_deltanet_conv",
-        "triton_qwen36_batched_deltanet_project", "triton_qwen36_batched_deltanet_recurrent_output",
-        "triton_qwen36_batched_moe_layer_decode", "triton_qwen36_batched_moe_router_decode",
-        "triton_qwen36_batched_routed_experts_decode", "triton_qwen36_batched_routed_shared_experts_decode",
-        "triton_qwen36_moe_decode", "triton_qwen36_moe_router_decode", "triton_qwen36_routed_experts_decode",
-        "triton_qwen36_routed_shared_experts_decode", "triton_qwen36_single_expert_mlp_decode",
-        "triton_synthetic_qwen36_deltanet_decode", "triton_synthetic_qwen36_deltanet_moe_decode",
-        "triton_synthetic_qwen36_moe_decode", "triton_qwen36_batched_attention_project",
-        "triton_qwen36_batched_attention_decode", "triton_qwen36_batched_attention_moe_layer_decode",
-    }
-    assert expected == set(hip.TRITON_ALIASES)
-    for name in expected:
-        assert getattr(hip, name) is hip.TRITON_ALIASES[name]
 
 
 def test_product_package_does_not_import_oracle():

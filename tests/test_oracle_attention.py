@@ -114,3 +114,66 @@ def test_attention_single_position_returns_the_value_row():
     att = nvc[0].repeat_interleave(HEADS // KVH, dim=0)[None]  # softmax over one position is 1
     ref = (att.reshape(1, -1) * torch.sigmoid(gate.reshape(1, -1))) @ w["wo"].t()
     torch.testing.assert_close(upd, ref, atol=1e-5, rtol=1e-5)
+
+
+# ---------------------------------------------------------------------------
+# The synthetic (tiny-spec) attention block: oracle.synthetic_rope and
+# oracle.synthetic_attention_decode (reference/qwen36_decode.py:37-56,174-209)
+# ---------------------------------------------------------------------------
+def _complex_rope64(x, position, rope_dim):
+    """Interleaved RoPE as multiplication of (even + i odd) by e^{i p theta_j},
+    theta_j = 10000^(-2j / r), in float64."""
+
+    r = min(rope_dim, x.shape[-1])
+    r -= r % 2
+    x = x.double()
+    out = x.clone()
+    if r == 0:
+        return out
+    z = torch.complex(x[..., :r:2], x[..., 1:r:2])
+    theta = 10000.0 ** (-torch.arange(0, r, 2, dtype=torch.float64) / r)
+    z = z * torch.polar(torch.ones_like(theta), position * theta)
+    out[..., :r:2], out[..., 1:r:2] = z.real, z.imag
+    return out
+
+
+@pytest.mark.parametrize("rope_dim", [0, 3, 4, 6])
+def test_synthetic_rope_is_complex_multiplication(rope_dim):
+    x = torch.randn(3, 6, generator=torch.Generator().manual_seed(3))
+    assert torch.equal(oracle.synthetic_rope(x, 0, rope_dim), x)
+    for p in (1, 5, 77):
+        torch.testing.assert_close(oracle.synthetic_rope(x, p, rope_dim).double(), _complex_rope64(x, p, rope_dim),
+                                   rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("position", [0, 2, 7])
+def test_synthetic_attention_decode_matches_sdpa_restatement(position):
+    g = torch.Generator().manual_seed(10 + position)
+    H, heads, kvh, hd, rd, P = 16, 4, 2, 4, 4, 8
+    layer = dict(norm_weight=1 + 0.2 * torch.randn(H, generator=g), q_weight=0.3 * torch.randn(heads * hd, H, generator=g),
+                 k_weight=0.3 * torch.randn(kvh * hd, H, generator=g), v_weight=0.3 * torch.randn(kvh * hd, H, generator=g),
+                 out_weight=0.3 * torch.randn(H, heads * hd, generator=g))
+    x = torch.randn(H, generator=g)
+    kc, vc = torch.randn(P, kvh, hd, generator=g), torch.randn(P, kvh, hd, generator=g)
+    kc0, vc0 = kc.clone(), vc.clone()
+    out, nkc, nvc = oracle.synthetic_attention_decode(x, kc, vc, layer, attention_heads=heads, kv_heads=kvh,
+                                                      head_dim=hd, rope_dim=rd, position=position)
+    assert torch.equal(kc, kc0) and torch.equal(vc, vc0)  # the inputs are not touched
+    # independent float64 restatement: RMSNorm by its formula, RoPE as complex
+    # multiplication, attention by the library's SDPA over expanded kv heads
+    x64 = x.double()
+    xn = x64 / torch.sqrt((x64 * x64).mean() + 1e-6) * layer["norm_weight"].double()
+    q = _complex_rope64((layer["q_weight"].double() @ xn).reshape(heads, hd), position, rd)
+    k = _complex_rope64((layer["k_weight"].double() @ xn).reshape(kvh, hd), position, rd)
+    v = (layer["v_weight"].double() @ xn).reshape(kvh, hd)
+    keys, vals = kc0.double().clone(), vc0.double().clone()
+    keys[position], vals[position] = k, v
+    K = keys[: position + 1].permute(1, 0, 2).repeat_interleave(heads // kvh, dim=0)  # [heads, t, hd]
+    V = vals[: position + 1].permute(1, 0, 2).repeat_interleave(heads // kvh, dim=0)
+    att = F.scaled_dot_product_attention(q[:, None, :], K, V)[:, 0, :].reshape(-1)
+    ref = x64 + layer["out_weight"].double() @ att
+    torch.testing.assert_close(out.double(), ref, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(nkc[position].double(), k, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(nvc[position].double(), v, rtol=1e-5, atol=1e-5)
+    rows = [t for t in range(P) if t != position]
+    assert torch.equal(nkc[rows], kc0[rows]) and torch.equal(nvc[rows], vc0[rows])
