@@ -197,6 +197,19 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   const bool in = tid < hd;
   float* s_q = reinterpret_cast<float*>(s_dyn);
   float* s_knew = s_q + MAXG * hd;
+  // The queries, gates and norm weights do not depend on the position: they
+  // are loaded before it, so the position's round trip overlaps theirs.
+  float xq[MAXG], sq[MAXG];
+  float gate[MAXG];  // this thread's gate values (used at the end)
+  const int dq = in ? tid : 0;
+#pragma unroll
+  for (int g = 0; g < MAXG; ++g) {
+    const size_t qb = (size_t)t * 2 * qw + (size_t)(hb + min(g, G - 1)) * 2 * hd + dq;
+    xq[g] = a.qg[qb];
+    gate[g] = a.qg[qb + hd];
+  }
+  const uint32_t qnw = elem_word(a.qn_w, a.qn_dt, dq);
+  const uint32_t knw = elem_word(a.kn_w, a.kn_dt, dq);
   const int start = a.start_dev ? *a.start_dev : a.start;
   if (start < 0 || start + a.T > a.max_pos) {
     // a run-time position past the cache: no cache access, NaN outputs
@@ -209,15 +222,14 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   if (c >= nc) return;
   const int p_lo = c * C, p_hi = min(p_lo + C, pos + 1);
 
-  // Loads first, in the order their data is used: the queries (and gates),
-  // then this wavefront's first pass of cached rows, which arrive while the
-  // queries are normalised and rotated.  Every load is unconditional
+  // Loads first, in the order their data is used: the queries (and gates,
+  // above), then this wavefront's first pass of cached rows, which arrive
+  // while the queries are normalised and rotated.  Every load is unconditional
   // (clamped in range, unused values dropped after): a load under a
   // condition makes the compiler wait for the loads before it.
   const int d0 = lane * 4;
   const bool lin = d0 < hd;
   const int dl = lin ? d0 : 0;  // (idle lanes read dim 0)
-  float gate[MAXG];  // this thread's gate values, loaded with the queries (used at the end)
   float4 q4[MAXG], acc[MAXG];
   float m[MAXG], l[MAXG];
   // OWN: the chunk holds some of the step's own positions (start ..), whose
@@ -225,17 +237,7 @@ __global__ __launch_bounds__(256) void attn_split_kernel(AttnArgs a) {
   // are stale and are read only to keep the loads unconditional.
   auto body = [&](auto own_tag) {
     constexpr bool OWN = decltype(own_tag)::value;
-    float xq[MAXG], sq[MAXG];
-    const int dq = in ? tid : 0;
-#pragma unroll
-    for (int g = 0; g < MAXG; ++g) {
-      const size_t qb = (size_t)t * 2 * qw + (size_t)(hb + min(g, G - 1)) * 2 * hd + dq;
-      xq[g] = a.qg[qb];
-      gate[g] = a.qg[qb + hd];
-    }
-    const uint32_t qnw = elem_word(a.qn_w, a.qn_dt, dq);
-    // the key norm weight and the first own position's k (OWN chunks)
-    const uint32_t knw = elem_word(a.kn_w, a.kn_dt, dq);
+    // the first own position's k (OWN chunks)
     const int u_lo = max(p_lo, start) - start, u_hi = p_hi - 1 - start;
     const float k_first = a.k[(size_t)(OWN ? u_lo : 0) * kvw + (size_t)j * hd + dq];
     // (an fp32 cache takes the step's own values from v with the same load,
