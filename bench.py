@@ -33,6 +33,7 @@ import time
 
 METRIC = "µs per MoE layer decode step at batch 1/16/128; achieved HBM TB/s vs peak"
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+GRAPH_WARM_REPLAYS = 2  # untimed replays of each captured graph before the timed one
 REFERENCE_A100_T1_US = 181.5  # real_moe_ms 0.1815 ms, A100 (reference docs/modal.md:1053)
 
 
@@ -252,8 +253,13 @@ def main() -> int:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         # replay() launches on the current stream: make it the timed stream.
+        # Two untimed replays first (the first uploads the graph; the one
+        # after it still runs ~3% slow at T=16 while the 13 GB of rotating
+        # weight sets are first touched through the graph), then exactly
+        # `steps` steps timed in one replay.
         with torch.cuda.stream(stream):
-            graph.replay()  # upload + warm
+            for _ in range(GRAPH_WARM_REPLAYS):
+                graph.replay()
             stream.synchronize()
             start.record(stream)
             graph.replay()
@@ -577,6 +583,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "graph_warm_replays": GRAPH_WARM_REPLAYS,
         "ms_per_step": round(ms_per_step, 6),
         "higher_is_better": False,
         "scaling": "weak",

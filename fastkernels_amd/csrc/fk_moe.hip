@@ -1815,6 +1815,8 @@ __device__ void build_routing_tables_masks(const int* s_ids, const uint32_t* s_m
 // rows and the storing threads apply the scale (same expression, so both
 // give the same logits).  Dynamic LDS: workgroup 0's ids [T*K] and token
 // masks [E * ceil(T/32)] (sized by the host for this T).
+FK_TIMELINE_BUFFER(moe_router)
+
 template <bool BFW, bool BFX, bool BFN, bool TILED>
 __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   constexpr int TU = kTagRouterTile;
@@ -1830,6 +1832,8 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   const int e = ub * 8 + wave, t0 = tb * tu, ntok = max(0, min(tu, T - t0));
   WaitHeader hdr = load_wait_header(a.ws.tickets, kTicketEpoch);  // (limits taken after the first loads)
   if (tid == 0) s_fail = 0;
+  FK_TIMELINE_DECL;
+  FK_MARK(0);  // (timeline markers: diagnostic builds only)
 
   // ---- logits of rows 8ub.. for tokens t0 .. t0 + ntok - 1 ----------------
   // Every load of the row is issued with the first tile's tokens, before the
@@ -1958,6 +1962,7 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
       }
     }
     __syncthreads();  // s_chunk is rewritten by the next tile
+    if (tt == 0) FK_MARK(1);
     if (more) {
 #pragma unroll
       for (int t = 0; t < TU; ++t)
@@ -1970,6 +1975,7 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
     }
   }
 
+  FK_MARK(2);
   // ---- top-k of tokens blockIdx.x, blockIdx.x + grid, .. ------------------
   if (wave == 0) {
     constexpr int NJE = kFusedMaxExperts / kWave;
@@ -2008,6 +2014,8 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
     if (tid == 0 && s_fail)
       __hip_atomic_fetch_or(&a.ws.tickets[kTicketError], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
                             __HIP_MEMORY_SCOPE_AGENT);
+    FK_MARK(3);
+    FK_TIMELINE_COMMIT(moe_router, blockIdx.x);
     return;
   }
 
@@ -2050,7 +2058,10 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
     else __hip_atomic_fetch_or(&a.ws.tickets[kTicketError], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
   }
+  FK_MARK(4);
   build_routing_tables_masks(s_ids, s_mask, T, K, E, a.ws, s_off);
+  FK_MARK(5);
+  FK_TIMELINE_COMMIT(moe_router, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------

@@ -4,11 +4,14 @@ Usage, on a GPU, after ``python -m fastkernels_amd.build --timeline``::
 
     python -m fastkernels_amd.timeline moe --tokens 1
     python -m fastkernels_amd.timeline deltanet --tokens 8
+    python -m fastkernels_amd.timeline router --tokens 128 --zipf
 
 It loads ``libfastkernels_hip_timeline.so``: the same kernels compiled with
 ``-DFK_TIMELINE``, in which thread 0 of every workgroup of
-``moe_fused_kernel`` (the MoE layer at T = 1) and ``deltanet_step_kernel``
-keeps the wall clock (100 MHz) at each phase boundary.  Steps run in steady
+``moe_fused_kernel`` (the MoE layer at T = 1), ``moe_router_tagged_kernel``
+(the router stage from two tokens on; the layer's router stage alone is
+timed) and ``deltanet_step_kernel`` keeps the wall clock (100 MHz) at each
+phase boundary.  Steps run in steady
 state: 16 back-to-back steps over 4 weight sets are captured as one HIP graph
 and replayed; the markers are cleared and the graph replayed once more, so the
 recorded step is the last of 16 that follow one another on the stream.  The
@@ -39,6 +42,17 @@ MARKERS = {
             "down rows and combine written (end)",
         ],
     ),
+    "router": (
+        "moe_router",
+        [
+            "workgroup start",
+            "first tile of logits stored",
+            "every tile of logits stored",
+            "top-k done, ids published (workgroups < T; the others end here)",
+            "workgroup 0: every id polled, epoch advanced",
+            "workgroup 0: routing tables built",
+        ],
+    ),
     "deltanet": (
         "deltanet_step",
         [
@@ -63,6 +77,7 @@ def parse_args(argv=None) -> argparse.Namespace:
     p.add_argument("--tokens", type=int, default=1)
     p.add_argument("--steps", type=int, default=16)
     p.add_argument("--weight-sets", type=int, default=4)
+    p.add_argument("--zipf", action="store_true", help="router: the config-2 Zipf router bias")
     return p.parse_args(argv)
 
 
@@ -118,23 +133,31 @@ def main(argv=None) -> int:
             "shared_expert_gate_weight": rnd(H),
         }
 
+    bias = wl.zipf_router_bias(E, seed=0).to(dev) if args.zipf else None
     plans = []
     for r in range(R):
-        if args.kernel == "moe":
-            p = MoeLayerPlan(moe_set(r), T, top_k=spec.num_routed_experts)
+        if args.kernel in ("moe", "router"):
+            p = MoeLayerPlan(moe_set(r), T, top_k=spec.num_routed_experts, router_bias=bias)
         else:
             p = DeltaNetStepPlan(wl.make_deltanet_weights(spec, seed=2000 + r, device=dev), T, spec)
         p.hidden.copy_(wl.make_hidden(T, spec.hidden_size, seed=50 + r).to(dev))
         plans.append(p)
     stream = torch.cuda.Stream(dev)
+
+    def step(p):
+        if args.kernel == "router":
+            p.run_router(stream)
+        else:
+            p.run(stream)
+
     with torch.cuda.stream(stream):
         for i in range(2 * R):
-            plans[i % R].run(stream)
+            step(plans[i % R])
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
         for i in range(args.steps):
-            plans[i % R].run(stream)
+            step(plans[i % R])
     with torch.cuda.stream(stream):
         graph.replay()
         stream.synchronize()
