@@ -340,12 +340,15 @@ def main() -> int:
         steps = args.steps
         for r in range(nsets):
             w = wl.make_attention_weights(spec, seed=3000 + r, device=dev)
-            # every run advances the position: room for warmup + capture-time + timed steps
-            ap = AttentionStepPlan(w, tokens, spec, max_positions=context + (args.warmup + 2 * steps + 8) * tokens,
+            # every run advances the position: room for the warmup, untimed and timed replays
+            ap = AttentionStepPlan(w, tokens, spec,
+                                   max_positions=context + (args.warmup + (GRAPH_WARM_REPLAYS + 1) * steps + 8) * tokens,
                                    start_position=context)
             ap.hidden.copy_(wl.make_hidden(tokens, H, seed=70 + r).to(dev))
             aplans.append(ap)
         ms = timed_graph([p.run for p in aplans], steps, args.warmup)
+        for p in aplans:
+            p.check_device(stream)
         nbytes = wl.attention_step_bytes(tokens, context, spec)
         return {
             "tokens": tokens,

@@ -13,7 +13,8 @@
 //   cache[start + t] = (k, v); o_h = softmax(q_h . K_j[0..p] / sqrt(hd)) V_j[0..p]
 //   update = (o * sigmoid(gate)) Wo^T;  hidden_out = x + update
 //
-// Kernels (four launches per step):
+// Kernels: T <= 4 at the shapes attn_step_chunks accepts (the model's) run
+// as one launch, attn_step_kernel (below); other steps as four launches:
 //   attn_proj_kernel  RMSNorm folded into a GEMV over [Wq | Wk | Wv] (9216
 //                     rows at the model shape); H > 2048 takes the shared
 //                     normalized projection kernel of fk_deltanet.hip
@@ -63,29 +64,6 @@ struct AttnArgs {
 
 constexpr int kAttnMaxKvHeads = 64;
 constexpr int kAttnMaxChunks = 64;  // position chunks per (token, kv head): the merge reads at most this many
-
-struct AttnWs {
-  float* qg;
-  float* k;
-  float* v;
-  float* gated;
-  float* part;
-};
-
-static size_t attn_ws_layout(int T, int heads, int kvh, int hd, char* base, AttnWs* ws) {
-  size_t off = 0;
-  auto take = [&](size_t bytes) {
-    size_t at = off;
-    off = align_up(off + bytes, 256);
-    return base ? reinterpret_cast<float*>(base + at) : nullptr;
-  };
-  ws->qg = take((size_t)T * heads * 2 * hd * 4);
-  ws->k = take((size_t)T * kvh * hd * 4);
-  ws->v = take((size_t)T * kvh * hd * 4);
-  ws->gated = take((size_t)T * heads * hd * 4);
-  ws->part = take((size_t)T * heads * kAttnMaxChunks * (hd + 2) * 4);
-  return off;
-}
 
 template <bool BF>
 __device__ __forceinline__ float4 load4(const void* p, size_t i) {
@@ -636,6 +614,844 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
   if (a.advance && blockIdx.x == 0 && threadIdx.x == 0) *a.advance += a.T;
 }
 
+// ---------------------------------------------------------------------------
+// Single-launch attention step (fk_attention_decode for T <= 4 at the shapes
+// attn_step_eligible accepts; the model's: hidden 2048, 16 query and 2 kv
+// heads of 256, bf16 weights).  One 512-thread workgroup per CU, grid capped
+// at the co-resident capacity; phases joined by launch-tagged words (value +
+// 32-bit launch tag per 8-byte word, polled by the consumers, as in the MoE
+// layer and the DeltaNet step).  The attention units first wait on one hint
+// word per phase A workgroup (their inputs come from most of the grid while
+// it still streams); the later consumers poll their inputs directly:
+//   A   projections: the R rows of [Wq | Wk | Wv] split evenly over the grid
+//       (36 per workgroup at the model shape, 4 or 5 per wavefront), each a
+//       whole-row dot product with the tokens x * (1 + w) staged in LDS,
+//       times the token's rsqrt(mean(x^2) + eps); outputs leave tagged.
+//   B   attention unit (t, j, hs, c), one per workgroup at the model shape:
+//       query heads hs * 4 .. + 4 of kv head j for token t over chunk c of
+//       its positions 0 .. start + t (split evenly over nch chunks at run
+//       time; the chunk's first cached rows are fetched before phase A's
+//       weight rows and staged in LDS after it).  RoPE angles are computed
+//       once per position; wavefronts 0-3 normalise and rotate the queries,
+//       4-7 the step's own keys, recomputed from k (its own values come from
+//       v: no dependence on another workgroup's cache write); 8 wavefronts
+//       each keep an online softmax over their positions, merged through
+//       LDS.  The chunk's (max, sum, weighted values) per head leave tagged,
+//       and the chunk holding position start + t writes that token's cache
+//       rows of kv head j.
+//   M   merge unit (t, h, ds) on the last workgroups: dims 64 ds .. + 64 of
+//       head h over the nch chunks, times sigmoid(gate); leaves the gated
+//       values tagged.
+//   C1  unit (rb, ks) on the first workgroups: rows 128 rb .. + 128 of Wo
+//       restricted to columns 512 ks .. + 512 (fetched into registers when
+//       the unit's attention role is done) against the gated values of
+//       every token; partial sums leave tagged.
+//   C2  workgroup b < H / 16: rows 16 b .. + 16 = the sum of the K / 512
+//       partials (update), hidden_out = x + update.
+// The last workgroup keeps the epoch: once every workgroup has stored its
+// started word (after reading the epoch and the position) it advances the
+// epoch and, with a device-held position, the position by T.
+// ---------------------------------------------------------------------------
+constexpr int kAsWaves = 8;
+constexpr int kAsThreads = 64 * kAsWaves;
+constexpr int kAsMaxTokens = 4;
+constexpr int kAsMaxGrid = 512;
+constexpr int kAsMaxRows = 5;      // phase A rows per wavefront
+constexpr int kAsMaxChunks = 64;   // attention units per (token, kv head)
+constexpr int kAsMDims = 64;       // head dims per merge unit
+constexpr int kAsKcu = 512;        // Wo columns per C1 unit
+constexpr int kAsRb = 128;         // Wo rows per C1 unit (16 per wavefront)
+constexpr int kAsTile = 24;        // cached positions per LDS tile of an attention unit
+constexpr int kAsKvLoads = 2 * kAsTile * (kAttnMaxHeadDim / 4) / kAsThreads;  // 4-element loads per thread per tile
+constexpr int kAsMaxH = 2048;
+constexpr int kAsMaxG = 8;         // query heads per kv head
+constexpr int kAsGu = 4;           // query heads per attention unit
+// dynamic LDS: phase B's [4][hd] x 2 (queries), [4][hd] x 3 (own keys raw
+// and final, own values) and a tile of cached rows [kAsTile][hd] x 2 (k, v;
+// the softmax states [8 wavefronts][4][hd] reuse it); phase A's [T][H] and
+// C1's [T][512] are smaller
+constexpr size_t kAsMaxLds = (size_t)(2 * kAsGu + 3 * kAsMaxTokens + 2 * kAsTile) * kAttnMaxHeadDim * 4;
+static_assert(kAsWaves * kAsGu <= 2 * kAsTile, "the softmax states must fit in the row tile");
+static_assert(kAsMaxTokens * kAsMaxH * 4 <= kAsMaxLds, "phase A's tokens must fit in the LDS");
+
+struct AttnTagWs {
+  uint32_t* tickets;  // [16] workspace header (epoch, poll bound, error word)
+  uint64_t* started;  // [kAsMaxGrid]
+  uint64_t* hint_a;   // [kAsMaxGrid] phase A, per workgroup
+  uint64_t* qkv;      // [T][R] projected (q_h | gate_h) pairs, k, v
+  uint64_t* part;     // [T][heads][kAsMaxChunks][hd + 2] chunk (max, sum, weighted values)
+  uint64_t* gated;    // [T][K]
+  uint64_t* cpart;    // [K / 512][T][H] C1 partial sums
+};
+
+struct AttnStepArgs {
+  const void* x;
+  const void* nw;
+  int nw_dt;
+  const void* wq;  // bf16 [2K, H]: rows 2 hd h .. + hd = q_h, the next hd = gate_h
+  const void* wk;  // bf16 [kvh hd, H]
+  const void* wv;
+  const void* wo;  // bf16 [H, K]
+  const void* qn_w;
+  const void* kn_w;
+  int qn_dt, kn_dt;
+  void* kc;  // [max_pos, kvh, hd]
+  void* vc;
+  int* start_dev;
+  int start, max_pos;
+  int T, H, heads, kvh, hd, rope_dim, interleaved, nch;
+  float theta_log2, eps, qk_eps;
+  float* update;
+  float* hidden_out;
+  AttnTagWs tw;
+};
+
+// Phase A row split: workgroup b holds rows b * base + min(b, rem) .. (base
+// + 1 rows for b < rem, base after); returns the workgroup holding row r.
+__device__ __forceinline__ int as_wg_of_row(int r, int R, int G) {
+  const int base = R / G, rem = R % G, cut = rem * (base + 1);
+  return r < cut ? r / (base + 1) : rem + (r - cut) / base;
+}
+
+// RoPE of the 4 dims d0 .. d0 + 3 of a normalised head row in LDS (dims >=
+// rope_dim unchanged); cs[i] = (cos, sin) of pair i's angle at the row's
+// position, p * theta^(-2i / rope_dim) as the split kernel computes it.
+__device__ __forceinline__ float4 as_rope4(const float* row, int d0, const float2* cs, const AttnStepArgs& a) {
+  float y[4] = {row[d0], row[d0 + 1], row[d0 + 2], row[d0 + 3]};
+  const int rd = a.rope_dim;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int d = d0 + e;
+    if (d < rd) {
+      int i, partner;
+      float sign;
+      if (a.interleaved) {
+        i = d >> 1;
+        partner = d ^ 1;
+        sign = (d & 1) ? 1.f : -1.f;
+      } else {
+        const int h2 = rd >> 1;
+        i = d < h2 ? d : d - h2;
+        partner = d < h2 ? d + h2 : d - h2;
+        sign = d < h2 ? -1.f : 1.f;
+      }
+      y[e] = y[e] * cs[i].x + sign * row[partner] * cs[i].y;
+    }
+  }
+  return make_float4(y[0], y[1], y[2], y[3]);
+}
+
+// RMSNorm(1 + w) over hd of one head row in LDS, held 4 dims per lane by one
+// wavefront (w: the lane's 4 norm-weight words); written back in place.
+__device__ __forceinline__ void as_norm_row(float* row, int d0, bool lin, int hd, float eps, const uint32_t (&w)[4],
+                                            const void* wp, int wdt) {
+  float4 x4 = lin ? *reinterpret_cast<const float4*>(row + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
+  const float ss = wave_sum(x4.x * x4.x + x4.y * x4.y + x4.z * x4.z + x4.w * x4.w);
+  const float r = rsqrtf(ss / (float)hd + eps);
+  if (lin) {
+    x4.x *= r * (1.f + elem_value(w[0], wp, wdt, d0));
+    x4.y *= r * (1.f + elem_value(w[1], wp, wdt, d0 + 1));
+    x4.z *= r * (1.f + elem_value(w[2], wp, wdt, d0 + 2));
+    x4.w *= r * (1.f + elem_value(w[3], wp, wdt, d0 + 3));
+    *reinterpret_cast<float4*>(row + d0) = x4;
+  }
+}
+
+// Workgroup barrier for LDS hand-offs only: waits for the wavefront's LDS
+// operations, not its global stores (__syncthreads() also waits until every
+// global store is acknowledged, which would hold back each hint word by a
+// memory round trip).  Every exchange between the wavefronts of
+// attn_step_kernel goes through LDS; other workgroups read its global words
+// by their tags.
+__device__ __forceinline__ void as_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// elem_word through a global-address-space pointer (a global load, not a
+// flat one, which would also count against the LDS wait counter).
+__device__ __forceinline__ uint32_t as_elem_word(const void* p, int dtype, size_t i) {
+  const uintptr_t at = reinterpret_cast<uintptr_t>(p) + (dtype == FK_DTYPE_BF16 ? i * 2 : i * 4);
+  return *reinterpret_cast<const __attribute__((address_space(1))) uint32_t*>(at & ~(uintptr_t)3);
+}
+
+FK_TIMELINE_BUFFER(attn_step)
+
+template <bool BFX, bool CBF>
+__global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
+  FK_TIMELINE_DECL;
+  FK_MARK(0);  // (timeline markers: diagnostic builds only)
+  extern __shared__ float4 s_dyn_v[];
+  float* s_dyn = reinterpret_cast<float*>(s_dyn_v);
+  __shared__ float s_part[kAsWaves][kAsMaxTokens];
+  __shared__ float s_rs[kAsMaxTokens];
+  __shared__ float s_m[kAsWaves][kAsGu], s_l[kAsWaves][kAsGu], s_f[kAsWaves][kAsGu], s_ML[kAsGu][2];
+  __shared__ float2 s_cs[1 + kAsMaxTokens][kAttnMaxHeadDim / 2];  // RoPE (cos, sin): the queries', the own keys'
+
+  __shared__ float s_fc[kAsMaxChunks];
+  __shared__ float s_L;
+  __shared__ float s_mo[kAsWaves][kAsMDims];
+  __shared__ int s_fail, s_kfail;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = gridDim.x, b = blockIdx.x;
+  const int T = a.T, H = a.H, hd = a.hd, heads = a.heads, kvh = a.kvh, Gq = heads / kvh;
+  const int K = heads * hd, Rq = 2 * K, Rk = kvh * hd, R = Rq + 2 * Rk;
+  const int nch = a.nch, nds = hd / kAsMDims, nks = K / kAsKcu, nchk = H >> 3;
+  const int hd_sh = 31 - __builtin_clz(hd);  // (hd is a power of two: the host checks)
+  // The workspace header and the position are loaded first.  The position
+  // stays in a vector register (a scalar copy would make the compiler wait
+  // for it at once); its first use, the cached-row addresses, comes after
+  // the weight rows are issued, and the loads retire in order, so that wait
+  // holds back nothing else.
+  WaitHeader hdr = load_wait_header(a.tw.tickets, kWorkspaceEpochWord);
+  int start_ld = a.start_dev ? load_coherent(a.start_dev) : a.start;
+
+  // Roles: attention units and merge units on the last workgroups (at the
+  // model shape every workgroup is an attention unit), C1 units and C2 rows
+  // on the first; a workgroup runs its roles in the order B, M, C1, C2.
+  const int hsplit = Gq > kAsGu ? Gq / kAsGu : 1, Gu = Gq / hsplit;  // units per kv head and token, heads per unit
+  const int n_att = T * kvh * hsplit * nch, att0 = G - n_att;
+  const int n_m = T * heads * nds, m0 = G - n_m;
+  const int n_c1 = (H / kAsRb) * nks;
+  const bool is_att = b >= att0, is_m = b >= m0, is_c1 = b < n_c1, is_out = b < H / 16;
+  const int au = is_att ? b - att0 : 0;
+  const int ac = au % nch, ahs = (au / nch) % hsplit, aj = (au / (nch * hsplit)) % kvh, at = au / (nch * hsplit * kvh);
+  const int hb = aj * Gq + ahs * Gu;  // the unit's first query head
+  const int d0 = lane * 4;
+  const bool lin = d0 < hd;
+  const int dl = lin ? d0 : 0;
+
+  // ---- loads, in the order their data is used ----------------------------
+  // tokens (chunk q = tid + 512 i of the T * H / 8) and the norm weight
+  constexpr int XCH = kAsMaxTokens * kAsMaxH / 8 / kAsThreads;
+  Raw8<BFX> xr[XCH];
+  uint32_t nwr[XCH][8];
+#pragma unroll
+  for (int i = 0; i < XCH; ++i) {
+    const int q = tid + i * kAsThreads, qc = q < T * nchk ? q : 0;
+    xr[i] = load_raw8<BFX>(a.x, (size_t)qc * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) nwr[i][e] = as_elem_word(a.nw, a.nw_dt, (size_t)(qc % nchk) * 8 + e);
+  }
+  // q/k norm weights of this lane's dims, residual inputs of the C2 rows
+  uint32_t qnr[4], knr[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    qnr[e] = as_elem_word(a.qn_w, a.qn_dt, dl + e);
+    knr[e] = as_elem_word(a.kn_w, a.kn_dt, dl + e);
+  }
+  uint32_t xres[1];
+  gather_raw<BFX>(a.x, is_out && tid < 16 * T ? (size_t)(tid >> 4) * H + b * 16 + (tid & 15) : 0, 0, 1, xres);
+  // phase A rows of this wavefront: rlo .. rlo + rn - 1 (rn >= 1; the
+  // unused row slots repeat the last row)
+  const int rbase = R / G, rrem = R % G;
+  const int wlo = b * rbase + min(b, rrem), wn = rbase + (b < rrem ? 1 : 0);
+  const int vb = wn / kAsWaves, vr = wn % kAsWaves;
+  const int rlo = wlo + wave * vb + min(wave, vr), rn = vb + (wave < vr ? 1 : 0);
+  Raw8<true> wt[kAsMaxRows][4];
+#pragma unroll
+  for (int i = 0; i < kAsMaxRows; ++i) {
+    const int row = rlo + (i < rn ? i : rn - 1);
+    const uint16_t* wp = row < Rq        ? reinterpret_cast<const uint16_t*>(a.wq) + (size_t)row * H
+                         : row < Rq + Rk ? reinterpret_cast<const uint16_t*>(a.wk) + (size_t)(row - Rq) * H
+                                         : reinterpret_cast<const uint16_t*>(a.wv) + (size_t)(row - Rq - Rk) * H;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wt[i][j] = load_raw8_stream<true>(wp, (size_t)min(lane + kWave * j, nchk - 1) * 8);
+  }
+  // the unit's first tile of cached rows (clamped in range, so every
+  // workgroup issues it), staged in LDS after phase A
+  asm volatile("" : "+v"(start_ld));  // (the position's wait: here, not at its load)
+  const int start = start_ld;
+  const bool bad_pos = start < 0 || start + T > a.max_pos;
+  const int apos = start + at, an = bad_pos ? 0 : apos + 1;  // positions 0 .. apos
+  const int aC = (an + nch - 1) / nch;
+  const int p_lo = min(ac * aC, an), p_hi = min(p_lo + aC, an);
+  // Cached rows of an attention unit, a tile of kAsTile positions from pt at
+  // a time: load u = tid + 512 i covers 4 dims (quad u % (hd / 4)) of row
+  // u / (hd / 4) of [k rows | v rows]; positions past the chunk repeat its
+  // last one (clamped in range).
+  const int qsh = hd_sh - 2;
+  Row4<CBF> kvr[kAsKvLoads];
+  auto issue_tile = [&](int pt) {
+#pragma unroll
+    for (int i = 0; i < kAsKvLoads; ++i) {
+      const int u = tid + i * kAsThreads, row = u >> qsh, qd = u & ((1 << qsh) - 1);
+      const bool isv = row >= kAsTile;
+      const int p = max(min(pt + (isv ? row - kAsTile : row), p_hi - 1), 0);
+      const size_t cr = ((size_t)p * kvh + aj) * hd + 4 * qd;
+      kvr[i] = load_row4<CBF>(isv ? a.vc : a.kc, row < 2 * kAsTile ? cr : 0);
+    }
+  };
+  auto stage_tile = [&](float* s_kt) {  // [2 * kAsTile][hd] as fp32: k rows, then v rows
+#pragma unroll
+    for (int i = 0; i < kAsKvLoads; ++i) {
+      const int u = tid + i * kAsThreads;
+      if ((u >> qsh) < 2 * kAsTile) *reinterpret_cast<float4*>(s_kt + 4 * u) = kvr[i].f4();
+    }
+  };
+  issue_tile(p_lo);
+  FK_MARK(1);
+
+  // ---- stage the tokens: s_x[t][c] = x * (1 + w), s_rs[t] -----------------
+  const WaitLimits wl = hdr.limits();
+  const uint32_t tag = wl.tag, plim = wl.poll;
+  float* s_x = s_dyn;
+  {
+    float ssp[kAsMaxTokens] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < XCH; ++i) {
+      const int q = tid + i * kAsThreads;
+      if (q < T * nchk) {  // (uniform per wavefront: nchk is a multiple of 64)
+        const int t = q / nchk, c = q - t * nchk;
+        float x8[8];
+        raw8_to_f32<BFX>(xr[i], x8);
+        float p = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          p = fmaf(x8[e], x8[e], p);
+          x8[e] *= 1.f + elem_value(nwr[i][e], a.nw, a.nw_dt, (size_t)c * 8 + e);
+        }
+#pragma unroll
+        for (int u = 0; u < kAsMaxTokens; ++u) ssp[u] += u == t ? p : 0.f;
+        float4* dst = reinterpret_cast<float4*>(s_x + (size_t)t * H + c * 8);
+        dst[0] = make_float4(x8[0], x8[1], x8[2], x8[3]);
+        dst[1] = make_float4(x8[4], x8[5], x8[6], x8[7]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kAsMaxTokens; ++u) {
+      if (u < T) {
+        const float s = wave_sum(ssp[u]);
+        if (lane == 0) s_part[wave][u] = s;
+      }
+    }
+    if (tid == 0) {
+      s_fail = 0;
+      s_kfail = 0;
+    }
+    as_sync();
+    if (tid < T) {
+      float tot = 0.f;
+#pragma unroll
+      for (int w = 0; w < kAsWaves; ++w) tot += s_part[w][tid];
+      s_rs[tid] = rsqrtf(tot / (float)H + a.eps);
+    }
+    as_sync();
+  }
+
+  // ---- phase A: row dot products, every token --------------------------
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int i = 0; i < kAsMaxRows; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) asm volatile("" : "+v"(wt[i][j].a));  // rows converted where used, per token
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (kWave * j < nchk) {  // (uniform)
+        const float4* xp = reinterpret_cast<const float4*>(s_x + (size_t)t * H + (lane + kWave * j) * 8);
+        const float4 xa = xp[0], xb = xp[1];
+        const float x8[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+        for (int i = 0; i < kAsMaxRows; ++i) {
+          float w8[8];
+          raw8_to_f32<true>(wt[i][j], w8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[i] = fmaf(w8[e], x8[e], acc[i]);
+        }
+      }
+    }
+    const float v = rows8_sum(acc) * s_rs[t];  // lanes 8i ..: row i
+    const int ri = lane >> 3;
+    if ((lane & 7) == 0 && ri < rn) store_tagged(a.tw.qkv + (size_t)t * R + rlo + ri, v, tag);
+  }
+  as_sync();  // every wavefront's outputs are stored before the hint; phase B reuses the LDS
+  if (tid == 0) {
+    store_tagged(a.tw.hint_a + b, 0.f, tag);
+    store_tagged(a.tw.started + b, (float)start, tag);  // (after the epoch and position loads)
+  }
+  FK_MARK(2);
+
+
+  // ---- phase B: attention unit (at, aj, ahs, ac) ---------------------------
+  if (is_att) {
+    float* s_q = s_dyn;                            // [Gu][hd] raw, then normalised
+    float* s_qf = s_q + kAsGu * hd;                // [Gu][hd] rotated and scaled
+    float* s_kr = s_qf + kAsGu * hd;               // [4][hd] own keys raw, then normalised
+    float* s_kf = s_kr + kAsMaxTokens * hd;        // [4][hd] own keys rotated
+    float* s_vn = s_kf + kAsMaxTokens * hd;        // [4][hd] own values
+    float* s_kt = s_vn + kAsMaxTokens * hd;        // [2][kAsTile][hd] cached k, v rows of a tile
+    float* s_acc = s_kt;                           // [waves][Gu][hd] after the last tile
+    // own positions of the chunk: o_lo .. p_hi - 1, tokens u_lo ..
+    const int o_lo = max(p_lo, start), n_own = p_hi > o_lo ? p_hi - o_lo : 0, u_lo = o_lo - start;
+    {
+      // hints of the phase A workgroups holding the q rows of heads hb ..
+      // hb + Gu - 1 and the k and v rows of kv head aj
+      const int q_lo = as_wg_of_row(2 * hd * hb, R, G), q_hi = as_wg_of_row(2 * hd * (hb + Gu) - 1, R, G);
+      const int k_lo = as_wg_of_row(Rq + aj * hd, R, G), k_hi = as_wg_of_row(Rq + aj * hd + hd - 1, R, G);
+      const int v_lo = as_wg_of_row(Rq + Rk + aj * hd, R, G), v_hi = as_wg_of_row(Rq + Rk + aj * hd + hd - 1, R, G);
+      const int nq = q_hi - q_lo + 1, nk = k_hi - k_lo + 1, nv = v_hi - v_lo + 1;
+      uint64_t hw[2];
+      const uint64_t* hs[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid + i * kAsThreads;
+        const int w = e < nq ? q_lo + e : e < nq + nk ? k_lo + e - nq : e < nq + nk + nv ? v_lo + e - nq - nk : -1;
+        hs[i] = w >= 0 ? a.tw.hint_a + w : nullptr;
+        hw[i] = hs[i] ? load_tagged(hs[i]) : 0ull;
+      }
+      if (!poll_tagged<2>(hw, hs, tag, plim)) s_fail = 1;
+    }
+    // RoPE angles, once per position: slot 0 the queries' (apos), slot
+    // 1 + s own key s's (o_lo + s); entry i of a slot is pair i's (cos, sin)
+    {
+      const int npair = a.rope_dim >> 1;  // (<= 128)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int e = tid + k * kAsThreads, slot = e >> 7, i = e & 127;
+        if (i < npair && slot <= n_own) {
+          const float inv_freq = exp2f(-(float)(2 * i) / (float)a.rope_dim * a.theta_log2);
+          float sn, cs;
+          sincosf((float)(slot == 0 ? apos : o_lo + slot - 1) * inv_freq, &sn, &cs);
+          s_cs[slot][i] = make_float2(cs, sn);
+        }
+      }
+    }
+    as_sync();
+    {
+      // token at's queries of heads hb .. (word e = g * hd + d), the own
+      // tokens' k and v (word e = s * hd + d)
+      uint64_t w[6];
+      const uint64_t* srcs[6];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid + i * kAsThreads, s = e >> hd_sh, d = e & (hd - 1);
+        srcs[i] = e < Gu * hd ? a.tw.qkv + (size_t)at * R + (size_t)(hb + s) * 2 * hd + d : nullptr;
+        const uint64_t* kr = a.tw.qkv + (size_t)(u_lo + s) * R + Rq + (size_t)aj * hd + d;
+        srcs[2 + i] = s < n_own ? kr : nullptr;
+        srcs[4 + i] = s < n_own ? kr + Rk : nullptr;
+      }
+#pragma unroll
+      for (int i = 0; i < 6; ++i) w[i] = srcs[i] ? load_tagged(srcs[i]) : 0ull;
+      if (!poll_tagged<6>(w, srcs, tag, plim)) s_fail = 1;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int e = tid + i * kAsThreads;
+        if (srcs[i]) s_q[e] = value_of(w[i]);
+        if (srcs[2 + i]) {
+          s_kr[e] = value_of(w[2 + i]);
+          s_vn[e] = value_of(w[4 + i]);
+        }
+      }
+    }
+    as_sync();
+    FK_MARK(3);
+    const bool bad = s_fail || bad_pos;
+    // head norms: wavefront g < 4 query head hb + g, wavefront 4 + s own key s
+    if (wave < Gu) as_norm_row(s_q + wave * hd, dl, lin, hd, a.qk_eps, qnr, a.qn_w, a.qn_dt);
+    if (wave >= kAsGu && wave - kAsGu < n_own)
+      as_norm_row(s_kr + (wave - kAsGu) * hd, dl, lin, hd, a.qk_eps, knr, a.kn_w, a.kn_dt);
+    as_sync();
+    FK_MARK(10);
+    // RoPE, and the queries' 1/sqrt(hd)
+    if (wave < Gu && lin) {
+      const float scale = rsqrtf((float)hd);
+      float4 y = as_rope4(s_q + wave * hd, d0, s_cs[0], a);
+      y.x *= scale;
+      y.y *= scale;
+      y.z *= scale;
+      y.w *= scale;
+      *reinterpret_cast<float4*>(s_qf + wave * hd + d0) = y;
+    }
+    if (wave >= kAsGu && wave - kAsGu < n_own && lin) {
+      const int s = wave - kAsGu;
+      *reinterpret_cast<float4*>(s_kf + s * hd + d0) = as_rope4(s_kr + s * hd, d0, s_cs[1 + s], a);
+    }
+    as_sync();
+    FK_MARK(11);
+    float4 q4[kAsGu], acc[kAsGu];
+    float m[kAsGu], l[kAsGu];
+#pragma unroll
+    for (int g = 0; g < kAsGu; ++g) {
+      q4[g] = lin && g < Gu ? *reinterpret_cast<const float4*>(s_qf + g * hd + d0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+      m[g] = -INFINITY;
+      l[g] = 0.f;
+    }
+    // tiles of kAsTile positions (the first fetched before phase A): staged
+    // in LDS, then wavefront w takes positions pt + w, + 8, ..; per head one
+    // softmax step over its positions of the tile.  The step's own
+    // positions read the recomputed keys and the values from v.
+    constexpr int PPW = kAsTile / kAsWaves;  // positions per wavefront per tile
+    for (int pt = p_lo; pt < p_hi; pt += kAsTile) {
+      if (pt != p_lo) {
+        as_sync();  // every wavefront is done with the previous tile
+        issue_tile(pt);
+      }
+      stage_tile(s_kt);
+      as_sync();
+      FK_MARK(12);
+      const float* s_vt = s_kt + kAsTile * hd;
+      const int pend = min(pt + kAsTile, p_hi);
+      float sr[PPW];  // lanes 16g ..: head g's score at position pt + w + 8 bb
+#pragma unroll
+      for (int bb = 0; bb < PPW; ++bb) {
+        const int p = min(pt + wave + kAsWaves * bb, pend - 1);  // (positions past the tile: scored -inf below)
+        const float* kp = p >= o_lo ? s_kf + (p - o_lo) * hd : s_kt + (p - pt) * hd;  // (uniform)
+        const float4 k4 = *reinterpret_cast<const float4*>(kp + dl);
+        float d[kAsGu];
+#pragma unroll
+        for (int g = 0; g < kAsGu; ++g) d[g] = q4[g].x * k4.x + q4[g].y * k4.y + q4[g].z * k4.z + q4[g].w * k4.w;
+        sr[bb] = rows4_sum(d);
+      }
+#pragma unroll
+      for (int g = 0; g < kAsGu; ++g) {
+        if (g >= Gu) break;
+        float sc[PPW];
+        float mx = m[g];
+#pragma unroll
+        for (int bb = 0; bb < PPW; ++bb) {
+          sc[bb] = pt + wave + kAsWaves * bb < pend
+                       ? __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(sr[bb]), 16 * g))
+                       : -INFINITY;
+          mx = fmaxf(mx, sc[bb]);
+        }
+        if (mx == -INFINITY) continue;  // (uniform: no position of this wavefront in the tile)
+        const float f = __expf(m[g] - mx);
+        float es = 0.f;
+        float4 av = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int bb = 0; bb < PPW; ++bb) {
+          const int p = min(pt + wave + kAsWaves * bb, pend - 1);
+          const float e = __expf(sc[bb] - mx);
+          const float* vp = p >= o_lo ? s_vn + (p - o_lo) * hd : s_vt + (p - pt) * hd;  // (uniform)
+          const float4 v4 = *reinterpret_cast<const float4*>(vp + dl);
+          es += e;
+          av.x = fmaf(e, v4.x, av.x);
+          av.y = fmaf(e, v4.y, av.y);
+          av.z = fmaf(e, v4.z, av.z);
+          av.w = fmaf(e, v4.w, av.w);
+        }
+        l[g] = l[g] * f + es;
+        acc[g].x = acc[g].x * f + av.x;
+        acc[g].y = acc[g].y * f + av.y;
+        acc[g].z = acc[g].z * f + av.z;
+        acc[g].w = acc[g].w * f + av.w;
+        m[g] = mx;
+      }
+    }
+    as_sync();  // the softmax states reuse the row tile
+    FK_MARK(13);
+    // the wavefronts' states merged per (head, dim): per-wavefront factors
+    // exp(m_w - M) once, then the chunk partial (max, sum, weighted values)
+    // leaves tagged
+#pragma unroll
+    for (int g = 0; g < kAsGu; ++g) {
+      if (g < Gu) {
+        if (lane == 0) {
+          s_m[wave][g] = m[g];
+          s_l[wave][g] = l[g];
+        }
+        if (lin) *reinterpret_cast<float4*>(s_acc + ((size_t)wave * Gu + g) * hd + d0) = acc[g];
+      }
+    }
+    as_sync();
+    if (tid < kAsWaves * kAsGu) {
+      const int w = tid / kAsGu, g = tid - w * kAsGu;
+      if (g < Gu) {
+        float M = s_m[0][g];
+#pragma unroll
+        for (int v = 1; v < kAsWaves; ++v) M = fmaxf(M, s_m[v][g]);
+        s_f[w][g] = s_m[w][g] == -INFINITY ? 0.f : __expf(s_m[w][g] - M);
+        if (w == 0) {
+          float L = 0.f;
+#pragma unroll
+          for (int v = 0; v < kAsWaves; ++v) L += s_m[v][g] == -INFINITY ? 0.f : s_l[v][g] * __expf(s_m[v][g] - M);
+          s_ML[g][0] = M;
+          s_ML[g][1] = L;
+        }
+      }
+    }
+    as_sync();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + i * kAsThreads;
+      if (e < Gu * hd) {
+        const int g = e >> hd_sh, d = e & (hd - 1);
+        float o = 0.f;
+#pragma unroll
+        for (int w = 0; w < kAsWaves; ++w) o = fmaf(s_acc[((size_t)w * Gu + g) * hd + d], s_f[w][g], o);
+        uint64_t* pp = a.tw.part + (((size_t)at * heads + hb + g) * kAsMaxChunks + ac) * (hd + 2);
+        store_tagged(pp + 2 + d, poison_if(bad, o), tag);
+        if (d == 0) {
+          store_tagged(pp, poison_if(bad, s_ML[g][0]), tag);
+          store_tagged(pp + 1, poison_if(bad, s_ML[g][1]), tag);
+        }
+      }
+    }
+    // the first unit of the chunk holding position apos writes token at's
+    // cache rows of kv head aj (after its partials: nothing waits for these)
+    if (!bad_pos && ahs == 0 && apos >= p_lo && apos < p_hi && tid < hd) {
+      const int s = apos - o_lo;
+      const size_t cr = ((size_t)apos * kvh + aj) * hd + tid;
+      store1<CBF>(a.kc, cr, poison_if(bad, s_kf[s * hd + tid]));
+      store1<CBF>(a.vc, cr, poison_if(bad, s_vn[s * hd + tid]));
+    }
+    as_sync();  // (the LDS is reused by the next role)
+    FK_MARK(14);
+  }
+  FK_MARK(4);
+
+  // ---- phase M: merge unit (mt, mh, mds) -----------------------------------
+  if (is_m) {
+    const int mu = b - m0, mt = mu / (heads * nds), mh = (mu / nds) % heads, mds = mu % nds;
+    // (the partials are polled directly: the attention units are done
+    // streaming by now, and a wait on their hint words first would cost a
+    // memory round trip more)
+    // thread (wavefront cg, lane dd): dim 64 mds + dd of chunks cg, cg + 8, ..;
+    // wavefront 0 also the chunk statistics (lane c) and the gate (lane dd)
+    const uint64_t* pbase = a.tw.part + ((size_t)mt * heads + mh) * kAsMaxChunks * (hd + 2);
+    uint64_t w[kAsMaxChunks / kAsWaves];
+    const uint64_t* srcs[kAsMaxChunks / kAsWaves];
+#pragma unroll
+    for (int k = 0; k < kAsMaxChunks / kAsWaves; ++k) {
+      const int c = wave + kAsWaves * k;
+      srcs[k] = c < nch ? pbase + (size_t)c * (hd + 2) + 2 + mds * kAsMDims + lane : nullptr;
+      w[k] = srcs[k] ? load_tagged(srcs[k]) : 0ull;
+    }
+    uint64_t st[3];
+    const uint64_t* ss[3] = {nullptr, nullptr, nullptr};
+    if (wave == 0) {
+      ss[0] = lane < nch ? pbase + (size_t)lane * (hd + 2) : nullptr;
+      ss[1] = lane < nch ? pbase + (size_t)lane * (hd + 2) + 1 : nullptr;
+      ss[2] = a.tw.qkv + (size_t)mt * R + (size_t)mh * 2 * hd + hd + mds * kAsMDims + lane;
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) st[i] = ss[i] ? load_tagged(ss[i]) : 0ull;
+    bool ok = poll_tagged<kAsMaxChunks / kAsWaves>(w, srcs, tag, plim);
+    ok = poll_tagged<3>(st, ss, tag, plim) && ok;
+    if (!ok) s_fail = 1;
+    if (wave == 0) {
+      const float mc = lane < nch ? value_of(st[0]) : -INFINITY, lc = lane < nch ? value_of(st[1]) : 0.f;
+      const float M = wave_max(mc);
+      const float fc = mc == -INFINITY ? 0.f : __expf(mc - M);
+      const float L = wave_sum(fc * lc);
+      s_fc[lane] = fc;
+      if (lane == 0) s_L = L;
+    }
+    as_sync();
+    float o = 0.f;
+#pragma unroll
+    for (int k = 0; k < kAsMaxChunks / kAsWaves; ++k)
+      if (srcs[k]) o = fmaf(s_fc[wave + kAsWaves * k], value_of(w[k]), o);
+    s_mo[wave][lane] = o;
+    as_sync();
+    if (wave == 0) {
+      float tot = 0.f;
+#pragma unroll
+      for (int cg = 0; cg < kAsWaves; ++cg) tot += s_mo[cg][lane];
+      const float gv = tot / s_L * sigmoid(value_of(st[2]));
+      store_tagged(a.tw.gated + (size_t)mt * K + (size_t)mh * hd + mds * kAsMDims + lane, poison_if(s_fail != 0, gv), tag);
+    }
+    as_sync();  // (the LDS is reused by the next role)
+  }
+  FK_MARK(5);
+
+  // ---- phase C1: unit (urb, uks) -------------------------------------------
+  if (is_c1) {
+    // Wo block first: a unit without an attention or merge role gets here
+    // right after phase A, so its rows arrive while it waits for the merges
+    const int urb = b / nks, uks = b - urb * nks;
+    u32x4 wo[16];
+    {
+      const uint16_t* wp = reinterpret_cast<const uint16_t*>(a.wo) + (size_t)(urb * kAsRb + wave * 16) * K +
+                           (size_t)uks * kAsKcu + lane * 8;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) wo[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wp + (size_t)r * K));
+    }
+    float* s_g = s_dyn;  // [T][512] gated values of the unit's columns (polled directly)
+    {
+      uint64_t w[kAsMaxTokens];
+      const uint64_t* srcs[kAsMaxTokens];
+#pragma unroll
+      for (int t = 0; t < kAsMaxTokens; ++t) {
+        srcs[t] = t < T ? a.tw.gated + (size_t)t * K + (size_t)uks * kAsKcu + tid : nullptr;
+        w[t] = srcs[t] ? load_tagged(srcs[t]) : 0ull;
+      }
+      if (!poll_tagged<kAsMaxTokens>(w, srcs, tag, plim)) s_fail = 1;
+#pragma unroll
+      for (int t = 0; t < kAsMaxTokens; ++t)
+        if (t < T) s_g[t * kAsKcu + tid] = value_of(w[t]);
+    }
+    as_sync();
+    FK_MARK(6);
+    const bool bad = s_fail != 0;
+    for (int t = 0; t < T; ++t) {
+      const float4* gp = reinterpret_cast<const float4*>(s_g + t * kAsKcu + lane * 8);
+      const float4 ga = gp[0], gb = gp[1];
+      const float g8[8] = {ga.x, ga.y, ga.z, ga.w, gb.x, gb.y, gb.z, gb.w};
+      float lo[8], hi[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        Raw8<true> r0, r1;
+        r0.a = wo[r];
+        r1.a = wo[r + 8];
+        float w0[8], w1[8];
+        raw8_to_f32<true>(r0, w0);
+        raw8_to_f32<true>(r1, w1);
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          s0 = fmaf(w0[e], g8[e], s0);
+          s1 = fmaf(w1[e], g8[e], s1);
+        }
+        lo[r] = s0;
+        hi[r] = s1;
+      }
+      const float vlo = rows8_sum(lo), vhi = rows8_sum(hi);  // lanes 8i ..: rows i and 8 + i
+      if ((lane & 7) == 0) {
+        const size_t o = ((size_t)uks * T + t) * H + (size_t)urb * kAsRb + wave * 16 + (lane >> 3);
+        store_tagged(a.tw.cpart + o, poison_if(bad, vlo), tag);
+        store_tagged(a.tw.cpart + o + 8, poison_if(bad, vhi), tag);
+      }
+    }
+  }
+  FK_MARK(7);
+
+  // ---- phase C2: rows 16b .. 16b + 15 = sum of the nks unit partials -------
+  if (is_out && tid < 16 * T) {
+    // (nks <= 8 partials per thread, polled directly)
+    const int r = tid & 15, t = tid >> 4;
+    uint64_t w[8];
+    const uint64_t* srcs[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      srcs[j] = j < nks ? a.tw.cpart + ((size_t)j * T + t) * H + b * 16 + r : nullptr;
+      w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+    }
+    const bool pok = poll_tagged<8>(w, srcs, tag, plim);
+    if (!pok) s_fail = 1;
+    float v = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < nks) v += value_of(w[j]);
+    v = poison_if(!pok, v);
+    const size_t o = (size_t)t * H + b * 16 + r;
+    a.update[o] = v;
+    if (a.hidden_out) a.hidden_out[o] = raw_value<BFX>(xres[0]) + v;
+  }
+  FK_MARK(8);
+
+  // ---- epoch keeper ----------------------------------------------------------
+  if (b == G - 1) {
+    uint64_t w[1];
+    const uint64_t* srcs[1] = {tid < G ? a.tw.started + tid : nullptr};
+    w[0] = srcs[0] ? load_tagged(srcs[0]) : 0ull;
+    if (!poll_tagged<1>(w, srcs, tag, plim)) s_kfail = 1;
+    as_sync();
+    // (not after a failed wait: a workgroup that has not read the epoch and
+    // the position yet would take the next launch's; the error word poisons
+    // later launches)
+    if (tid == 0 && !s_kfail) {
+      store_coherent(&a.tw.tickets[kWorkspaceEpochWord], tag);
+      if (a.start_dev) store_coherent(a.start_dev, start + T);
+    }
+  }
+  as_sync();
+  if (tid == 0 && (s_fail || s_kfail))
+    __hip_atomic_fetch_or(&a.tw.tickets[kWorkspaceErrorWord], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
+  FK_MARK(9);
+  FK_TIMELINE_COMMIT(attn_step, blockIdx.x);
+}
+
+// Attention workspace: the single-launch step's tagged region first (its
+// 16-word header at offset 0 serves fk_workspace_status; the other words
+// exist for T <= kAsMaxTokens only), then the staged launches' buffers.
+struct AttnWs {
+  AttnTagWs tw;
+  float* qg;
+  float* k;
+  float* v;
+  float* gated;
+  float* part;
+};
+
+static size_t attn_ws_layout(int T, int heads, int kvh, int hd, char* base, AttnWs* ws) {
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = off;
+    off = align_up(off + bytes, 256);
+    return base ? base + at : nullptr;
+  };
+  const bool one = T <= kAsMaxTokens;
+  const size_t K = (size_t)heads * hd, R = 2 * K + 2 * (size_t)kvh * hd;
+  auto words = [&](size_t n) { return reinterpret_cast<uint64_t*>(take(one ? n * 8 : 0)); };
+  ws->tw.tickets = reinterpret_cast<uint32_t*>(take(16 * sizeof(uint32_t)));
+  ws->tw.started = words(kAsMaxGrid);
+  ws->tw.hint_a = words(kAsMaxGrid);
+  ws->tw.qkv = words((size_t)T * R);
+  ws->tw.part = words((size_t)T * heads * kAsMaxChunks * (hd + 2));
+  ws->tw.gated = words((size_t)T * K);
+  ws->tw.cpart = words((K + kAsKcu - 1) / kAsKcu * T * kAsMaxH);
+  auto floats = [&](size_t n) { return reinterpret_cast<float*>(take(n * 4)); };
+  ws->qg = floats((size_t)T * heads * 2 * hd);
+  ws->k = floats((size_t)T * kvh * hd);
+  ws->v = floats((size_t)T * kvh * hd);
+  ws->gated = floats((size_t)T * heads * hd);
+  ws->part = floats((size_t)T * heads * kAttnMaxChunks * (hd + 2));
+  return off;
+}
+
+// Single-launch step: chunks per (token, kv head, group of 4 query heads)
+// on a grid of G workgroups (every workgroup an attention unit when that
+// allows 64 chunks or fewer), or 0 when the shape is not one the kernel
+// handles.
+static int attn_step_chunks(int T, int H, int heads, int kvh, int hd, int weight_dt, int G) {
+  if (weight_dt != FK_DTYPE_BF16 || T < 1 || T > kAsMaxTokens || G < 1 || G > kAsMaxGrid) return 0;
+  if (H < 512 || H > kAsMaxH || H % 512 || hd < kAsMDims || hd > kAttnMaxHeadDim || (hd & (hd - 1))) return 0;
+  if (heads < 1 || kvh < 1 || heads % kvh || heads / kvh > kAsMaxG) return 0;
+  const int Gq = heads / kvh, hsplit = Gq > kAsGu ? Gq / kAsGu : 1;
+  if (Gq > kAsGu && Gq % kAsGu) return 0;
+  const int K = heads * hd, R = 2 * K + 2 * kvh * hd;
+  if (K % kAsKcu || K > 4096) return 0;
+  if (R / G < kAsWaves || (R + G - 1) / G > kAsWaves * kAsMaxRows) return 0;  // 1 .. kAsMaxRows rows per wavefront
+  const int n_c1 = (H / kAsRb) * (K / kAsKcu), n_m = T * heads * (hd / kAsMDims);
+  if (n_c1 > G || H / 16 > G || n_m > G) return 0;
+  int nch = G / (T * kvh * hsplit);
+  if (nch > kAsMaxChunks) nch = kAsMaxChunks;
+  return nch > 0 ? nch : 0;
+}
+
+// Grid of the single-launch step (one workgroup per CU, capped at the
+// co-resident capacity), or 0 when the device cannot host it.
+template <bool BX, bool CB>
+static int attn_step_grid() {
+  static int cap_cache[64] = {0};
+  static int attr_ok[64] = {0};  // 0 unknown, 1 set, -1 refused
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (attr_ok[dev] == 0)
+    attr_ok[dev] = hipFuncSetAttribute(reinterpret_cast<const void*>(attn_step_kernel<BX, CB>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kAsMaxLds) == hipSuccess
+                       ? 1
+                       : -1;
+  if (attr_ok[dev] < 0) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const int cap = resident_capacity(attn_step_kernel<BX, CB>, kAsThreads, kAsMaxLds, cap_cache);
+  const int cus = device_cus();
+  const int G = cap < cus ? cap : cus;
+  return G > kAsMaxGrid ? kAsMaxGrid : G;
+}
+
+static int attn_step_grid_for(bool bx, bool cb) {
+  if (bx) return cb ? attn_step_grid<true, true>() : attn_step_grid<true, false>();
+  return cb ? attn_step_grid<false, true>() : attn_step_grid<false, false>();
+}
+
 static int check_attn_shape(int tokens, int hidden_size, int heads, int kv_heads, int head_dim, int rope_dim) {
   if (tokens < 1 || tokens > kAttnMaxTokens) return fail(FK_ERR_UNSUPPORTED, "tokens must be in [1, %d]", kAttnMaxTokens);
   if (hidden_size < 8 || hidden_size % 8 || hidden_size > 4096)
@@ -720,6 +1536,7 @@ int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_w
                         float* hidden_out, void* workspace, size_t workspace_bytes, void* stream) {
   int st = check_attn_shape(tokens, hidden_size, heads, kv_heads, head_dim, rope_dim);
   if (st) return st;
+  if (max_positions < 1) return fail(FK_ERR_INVALID, "max_positions must be positive");
   if (!start_position_device && (start_position < 0 || start_position + tokens > max_positions))
     return fail(FK_ERR_INVALID, "decode positions [%d, %d) exceed the cache length %d", start_position,
                 start_position + tokens, max_positions);
@@ -735,6 +1552,55 @@ int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_w
     return fail(FK_ERR_WORKSPACE, "attention workspace needs %zu bytes (got %zu)", need, workspace_bytes);
   attn_ws_layout(tokens, heads, kv_heads, head_dim, reinterpret_cast<char*>(workspace), &ws);
   const hipStream_t s = as_stream(stream);
+  const int rd = rope_dim < head_dim ? rope_dim : head_dim;
+  if (!is_float_dtype(hidden_dtype) || !is_float_dtype(norm_dtype) || !is_float_dtype(weight_dtype))
+    return fail(FK_ERR_DTYPE, "projection inputs must be f32 or bf16");
+  if (!hidden || !norm_weight || !q_proj || !k_proj || !v_proj)
+    return fail(FK_ERR_INVALID, "projection pointers must be non-NULL");
+  if (!aligned16(hidden) || !aligned16(norm_weight) || !aligned16(q_proj) || !aligned16(k_proj) || !aligned16(v_proj))
+    return fail(FK_ERR_ALIGNMENT, "hidden, norm_weight and projection weights must be 16-byte aligned");
+  if (tokens <= kAsMaxTokens) {
+    const bool bx = hidden_dtype == FK_DTYPE_BF16, cb = cache_dtype == FK_DTYPE_BF16;
+    const int G = attn_step_grid_for(bx, cb);
+    const int nch = attn_step_chunks(tokens, hidden_size, heads, kv_heads, head_dim, weight_dtype, G);
+    if (nch > 0) {
+      AttnStepArgs sa;
+      sa.x = hidden;
+      sa.nw = norm_weight;
+      sa.nw_dt = norm_dtype;
+      sa.wq = q_proj;
+      sa.wk = k_proj;
+      sa.wv = v_proj;
+      sa.wo = o_proj;
+      sa.qn_w = q_norm_weight;
+      sa.kn_w = k_norm_weight;
+      sa.qn_dt = sa.kn_dt = qk_norm_dtype;
+      sa.kc = key_cache;
+      sa.vc = value_cache;
+      sa.start_dev = const_cast<int*>(start_position_device);
+      sa.start = start_position;
+      sa.max_pos = max_positions;
+      sa.T = tokens;
+      sa.H = hidden_size;
+      sa.heads = heads;
+      sa.kvh = kv_heads;
+      sa.hd = head_dim;
+      sa.rope_dim = rd - rd % 2;
+      sa.interleaved = rope_interleaved;
+      sa.nch = nch;
+      sa.theta_log2 = log2f(rope_theta);
+      sa.eps = eps;
+      sa.qk_eps = qk_eps;
+      sa.update = update;
+      sa.hidden_out = hidden_out;
+      sa.tw = ws.tw;
+      if (bx && cb) hipLaunchKernelGGL((attn_step_kernel<true, true>), dim3(G), dim3(kAsThreads), kAsMaxLds, s, sa);
+      else if (bx) hipLaunchKernelGGL((attn_step_kernel<true, false>), dim3(G), dim3(kAsThreads), kAsMaxLds, s, sa);
+      else if (cb) hipLaunchKernelGGL((attn_step_kernel<false, true>), dim3(G), dim3(kAsThreads), kAsMaxLds, s, sa);
+      else hipLaunchKernelGGL((attn_step_kernel<false, false>), dim3(G), dim3(kAsThreads), kAsMaxLds, s, sa);
+      return check_launch("attn_step_kernel");
+    }
+  }
   st = fk_attention_project(hidden, hidden_dtype, norm_weight, norm_dtype, q_proj, k_proj, v_proj, weight_dtype,
                             tokens, hidden_size, 2 * heads * head_dim, kv_heads * head_dim, eps, 1.0f, ws.qg, ws.k,
                             ws.v, stream);
@@ -755,7 +1621,6 @@ int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_w
   a.heads = heads;
   a.kvh = kv_heads;
   a.hd = head_dim;
-  const int rd = rope_dim < head_dim ? rope_dim : head_dim;
   a.rope_dim = rd - rd % 2;
   a.theta_log2 = log2f(rope_theta);
   a.eps = qk_eps;

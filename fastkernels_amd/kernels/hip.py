@@ -119,7 +119,7 @@ def _workspace(kind: str, device: torch.device, nbytes: int) -> torch.Tensor:
 
 
 # Workspaces whose kernels wait on other workgroups (bounded waits, error word).
-_POLLING_KINDS = ("moe", "deltanet_step")
+_POLLING_KINDS = ("moe", "deltanet_step", "attention")
 
 
 def workspace_status(device: Any = None, *, clear: bool = True) -> None:

@@ -222,9 +222,10 @@ class AttentionStepPlan:
     """One gated full-attention decode step of `tokens` rows + residual.
 
     The plan owns the KV caches ([max_positions, kv_heads, head_dim]) and a
-    device int32 `position`; every run decodes at that position and its last
-    kernel advances it by `tokens`, so a step captured once in a HIP graph decodes
-    successive positions on replay.  `set_position()` rewinds it.
+    device int32 `position`; every run decodes at that position and advances
+    it by `tokens` once every workgroup has read it, so a step captured once
+    in a HIP graph decodes successive positions on replay.  `set_position()`
+    rewinds it.
     """
 
     def __init__(
@@ -288,3 +289,9 @@ class AttentionStepPlan:
             sp.attention_head_dim, sp.rope_dim, float(sp.rope_theta), self.interleaved, self.eps, self.eps,
             self.update.data_ptr(), self.hidden_out.data_ptr(), self.workspace.data_ptr(), self.workspace.numel(), s,
         )
+
+    def check_device(self, stream: torch.cuda.Stream | None = None) -> None:
+        _check_device(self.workspace, self.device, stream)
+
+    def set_poll_limit(self, limit: int | None, stream: torch.cuda.Stream | None = None) -> None:
+        _set_poll_limit(self.workspace, self.device, limit, stream)

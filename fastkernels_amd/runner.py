@@ -219,7 +219,7 @@ class ResidentDecodeRunner:
 
     def check_device(self, stream: torch.cuda.Stream | None = None) -> None:
         for pair, moe in zip(self.mixers, self.moes):
-            if isinstance(pair[0], DeltaNetStepPlan):
-                pair[0].check_device(stream)
+            pair[0].check_device(stream)
+            if pair[1] is not pair[0]:
                 pair[1].check_device(stream)
             moe.check_device(stream)

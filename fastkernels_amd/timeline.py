@@ -5,12 +5,14 @@ Usage, on a GPU, after ``python -m fastkernels_amd.build --timeline``::
     python -m fastkernels_amd.timeline moe --tokens 1
     python -m fastkernels_amd.timeline deltanet --tokens 8
     python -m fastkernels_amd.timeline router --tokens 128 --zipf
+    python -m fastkernels_amd.timeline attention --tokens 1 --context 1024
 
 It loads ``libfastkernels_hip_timeline.so``: the same kernels compiled with
 ``-DFK_TIMELINE``, in which thread 0 of every workgroup of
 ``moe_fused_kernel`` (the MoE layer at T = 1), ``moe_router_tagged_kernel``
 (the router stage from two tokens on; the layer's router stage alone is
-timed) and ``deltanet_step_kernel`` keeps the wall clock (100 MHz) at each
+timed), ``deltanet_step_kernel`` and ``attn_step_kernel`` (the attention step
+after ``--context`` cached positions) keeps the wall clock (100 MHz) at each
 phase boundary.  Steps run in steady
 state: 16 back-to-back steps over 4 weight sets are captured as one HIP graph
 and replayed; the markers are cleared and the graph replayed once more, so the
@@ -53,6 +55,26 @@ MARKERS = {
             "workgroup 0: routing tables built",
         ],
     ),
+    "attention": (
+        "attn_step",
+        [
+            "workgroup start",
+            "weight rows issued",
+            "A: projection rows stored (hint, started)",
+            "B: attention inputs read",
+            "B: chunk partial stored",
+            "M: gated values stored",
+            "C1: gated values read",
+            "C1: partial sums stored",
+            "C2: output rows written",
+            "end",
+            "B: q and own-key norms",
+            "B: RoPE",
+            "B: row tile staged",
+            "B: softmax over the chunk done",
+            "B: wavefronts merged, partials stored",
+        ],
+    ),
     "deltanet": (
         "deltanet_step",
         [
@@ -78,6 +100,7 @@ def parse_args(argv=None) -> argparse.Namespace:
     p.add_argument("--steps", type=int, default=16)
     p.add_argument("--weight-sets", type=int, default=4)
     p.add_argument("--zipf", action="store_true", help="router: the config-2 Zipf router bias")
+    p.add_argument("--context", type=int, default=1024, help="attention: cached positions before the step")
     return p.parse_args(argv)
 
 
@@ -95,7 +118,7 @@ def main(argv=None) -> int:
     import torch
 
     from fastkernels_amd import workloads as wl
-    from fastkernels_amd.plan import DeltaNetStepPlan, MoeLayerPlan
+    from fastkernels_amd.plan import AttentionStepPlan, DeltaNetStepPlan, MoeLayerPlan
     from fastkernels_amd.spec import qwen36_35b_a3b_spec
 
     if not torch.cuda.is_available():
@@ -138,6 +161,10 @@ def main(argv=None) -> int:
     for r in range(R):
         if args.kernel in ("moe", "router"):
             p = MoeLayerPlan(moe_set(r), T, top_k=spec.num_routed_experts, router_bias=bias)
+        elif args.kernel == "attention":
+            # room for every run of the warmup, the capture's replays and the marked replay
+            p = AttentionStepPlan(wl.make_attention_weights(spec, seed=3000 + r, device=dev), T, spec,
+                                  max_positions=args.context + (4 * args.steps + 8) * T, start_position=args.context)
         else:
             p = DeltaNetStepPlan(wl.make_deltanet_weights(spec, seed=2000 + r, device=dev), T, spec)
         p.hidden.copy_(wl.make_hidden(T, spec.hidden_size, seed=50 + r).to(dev))

@@ -57,15 +57,16 @@ const char* fk_status_string(int status);
 const char* fk_last_error_detail(void);
 
 /* Device error word of a workspace of fk_moe_router / fk_moe_align /
- * fk_moe_experts / fk_moe_layer or fk_deltanet_step.  Those kernels hand
- * values between workgroups and assume that every workgroup of a launch is
- * resident at once (the host caps their grids at the device's co-resident
- * capacity); each wait is bounded.  A wait that runs out (another process
- * or stream holding CUs for long) sets the error word, the kernel ends
- * normally and the outputs its workgroups produced from incomplete inputs
- * are NaN (routing weights, MoE outputs, DeltaNet update and recurrent
- * state).  While the word stays set, every later call on the workspace
- * gives NaN outputs.  This call synchronises `stream`, then returns FK_OK
+ * fk_moe_experts / fk_moe_layer, fk_deltanet_step or fk_attention_decode.
+ * Those kernels hand values between workgroups and assume that every
+ * workgroup of a launch is resident at once (the host caps their grids at
+ * the device's co-resident capacity); each wait is bounded.  A wait that
+ * runs out (another process or stream holding CUs for long) sets the error
+ * word, the kernel ends normally and the outputs its workgroups produced
+ * from incomplete inputs are NaN (routing weights, MoE outputs, DeltaNet
+ * update and recurrent state, attention update and the step's cache rows).
+ * While the word stays set, every later call on the workspace gives NaN
+ * outputs.  This call synchronises `stream`, then returns FK_OK
  * or FK_ERR_DEVICE; `clear` != 0 also resets the word (stream-ordered),
  * after which calls give valid outputs again.
  * No counterpart in the reference: its Triton kernels never wait on another
@@ -242,7 +243,12 @@ size_t fk_attention_workspace_bytes(int tokens, int heads, int kv_heads, int hea
  * place of start_position and advanced by `tokens` at the end of the step,
  * so one captured HIP graph decodes successive positions; a value with
  * start + tokens past max_positions gives NaN updates and leaves the caches
- * untouched.
+ * untouched.  For tokens <= 4 with bf16 weights, hidden_size a multiple of
+ * 512 up to 2048, head_dim a power of two in [64, 256], heads / kv_heads <=
+ * 8 (a multiple of 4 above 4) and heads * head_dim a multiple of 512 (the
+ * model's shapes) this is one launch whose workgroups hand values to each
+ * other (the workspace then also carries the error word of
+ * fk_workspace_status); other calls run four launches.
  * Replaces triton_qwen36_batched_attention_decode (qwen36_attention.py:448-577)
  * and the residual add of triton_qwen36_batched_attention_moe_layer_decode
  * (qwen36_layer.py:109-201). */

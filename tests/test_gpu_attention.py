@@ -124,3 +124,106 @@ def test_attention_moe_layer_matches_oracle(device, attn_cpu, attn_gpu):
     o_logits = oracle.router(h, moe["norm_weight"], moe["router_weight"], K)[0]
     if assert_routing_parity(logits, ids, weights, o_logits, K) == 0:
         assert torch.equal(ids.cpu(), want[7])
+
+
+# The single-launch step (T <= 4 at these shapes) splits each token's
+# positions over its attention units at run time and stages the cached rows
+# in tiles of 40 per unit: long contexts take several tiles per unit, and a
+# step's own positions fall in the last unit(s).
+@pytest.mark.parametrize("cache_dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("tokens,start", [(1, 1023), (4, 60), (3, 2000), (2, 1300)])
+def test_attention_decode_long_contexts_match_oracle(device, attn_cpu, attn_gpu, cache_dtype, tokens, start):
+    print(f"attention long context cache={cache_dtype} tokens={tokens} start={start}", flush=True)
+    x, kc, vc = _inputs(tokens, start, cache_dtype, seed=17)
+    upd, nkc, nvc = hip.hip_qwen36_batched_attention_decode(
+        x.to(device), kc.to(device), vc.to(device), *_args(attn_gpu), start_position=start, **KW)
+    o_upd, o_kc, o_vc = oracle.attention_update(
+        x, kc, vc, *_args(attn_cpu), start_position=start, heads=HEADS, kv_heads=KVH, head_dim=HD, rope_dim=RD,
+        rope_theta=THETA, interleaved=True)
+    torch.testing.assert_close(upd.cpu(), o_upd, **tol(torch.bfloat16))
+    new = slice(start, start + tokens)
+    torch.testing.assert_close(nkc[new].float().cpu(), o_kc[new].float(), **tol(torch.bfloat16))
+    torch.testing.assert_close(nvc[new].float().cpu(), o_vc[new].float(), **tol(torch.bfloat16))
+    for c, ref in ((nkc, kc), (nvc, vc)):
+        assert torch.equal(c[:start].cpu(), ref[:start]) and torch.equal(c[start + tokens:].cpu(), ref[start + tokens:])
+
+
+def _plan(attn_gpu, tokens, max_positions, start, hidden_dtype=torch.bfloat16):
+    from fastkernels_amd.plan import AttentionStepPlan
+    from fastkernels_amd.spec import qwen36_35b_a3b_spec
+
+    w = dict(attn_gpu)
+    return AttentionStepPlan(w, tokens, qwen36_35b_a3b_spec(), max_positions=max_positions, start_position=start,
+                             hidden_dtype=hidden_dtype)
+
+
+@pytest.mark.parametrize("hidden_dtype", [torch.bfloat16, torch.float32])
+def test_attention_plan_graph_replays_decode_successive_positions(device, attn_cpu, attn_gpu, hidden_dtype):
+    # one captured step replayed three times == three eager steps (bit for
+    # bit): the device-held position advances once per step, inside the
+    # launch; the last step also matches the oracle run over the same cache
+    print(f"attention plan graph replay hidden={hidden_dtype}", flush=True)
+    tokens, start, maxp = 1, 37, 48
+    g = torch.Generator().manual_seed(23)
+    kc0 = torch.randn(maxp, KVH, HD, generator=g) * 0.5
+    vc0 = torch.randn(maxp, KVH, HD, generator=g) * 0.5
+    xs = [torch.randn(tokens, H, generator=g).to(hidden_dtype) for _ in range(3)]
+    eager, graphed = _plan(attn_gpu, tokens, maxp, start, hidden_dtype), _plan(attn_gpu, tokens, maxp, start, hidden_dtype)
+    for p in (eager, graphed):
+        p.key_cache.copy_(kc0.to(device))
+        p.value_cache.copy_(vc0.to(device))
+    stream = torch.cuda.Stream(device)
+    with torch.cuda.stream(stream):
+        graphed.hidden.copy_(xs[0].to(device))
+        graphed.run(stream)  # (warm: the first call sets the kernel's attributes)
+        graphed.set_position(start)
+        graphed.key_cache.copy_(kc0.to(device))
+        graphed.value_cache.copy_(vc0.to(device))
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        graphed.run(stream)
+    outs = []
+    for s in range(3):
+        eager.hidden.copy_(xs[s].to(device))
+        eager.run()
+        torch.cuda.synchronize()
+        a = eager.hidden_out.clone()
+        with torch.cuda.stream(stream):
+            graphed.hidden.copy_(xs[s].to(device))
+            graph.replay()
+        stream.synchronize()
+        assert torch.equal(a, graphed.hidden_out), f"step {s}"
+        outs.append(a)
+    assert int(graphed.position.item()) == start + 3 and int(eager.position.item()) == start + 3
+    assert torch.equal(eager.key_cache, graphed.key_cache) and torch.equal(eager.value_cache, graphed.value_cache)
+    # the oracle's third step over the cache the first two left
+    kc, vc = kc0.clone(), vc0.clone()
+    for s in range(3):
+        o_upd, kc, vc = oracle.attention_update(
+            xs[s], kc, vc, *_args(attn_cpu), start_position=start + s, heads=HEADS, kv_heads=KVH, head_dim=HD,
+            rope_dim=RD, rope_theta=THETA, interleaved=True)
+        torch.testing.assert_close(outs[s].cpu(), xs[s].float() + o_upd, **tol(torch.bfloat16))
+    eager.check_device()
+    graphed.check_device()
+
+
+def test_attention_plan_position_past_the_cache_gives_nan(device, attn_gpu):
+    # a device-held position whose step would pass the cache: NaN update,
+    # caches untouched, no wait flagged; a valid position afterwards decodes
+    plan = _plan(attn_gpu, 2, 8, 7)
+    g = torch.Generator().manual_seed(29)
+    plan.key_cache.copy_(torch.randn(8, KVH, HD, generator=g).to(device))
+    plan.value_cache.copy_(torch.randn(8, KVH, HD, generator=g).to(device))
+    plan.hidden.copy_(torch.randn(2, H, generator=g).to(torch.bfloat16).to(device))
+    kc, vc = plan.key_cache.clone(), plan.value_cache.clone()
+    plan.run()
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(plan.update).all())
+    assert torch.equal(plan.key_cache, kc) and torch.equal(plan.value_cache, vc)
+    plan.check_device()
+    plan.set_position(6)
+    plan.run()
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(plan.update).all())
+    plan.check_device()

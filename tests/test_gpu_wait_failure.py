@@ -116,3 +116,45 @@ def test_operator_workspace_status_reports_and_clears(device, small_moe):
     again = hip.hip_qwen36_batched_moe_decode(x, *args, top_k=8)[0]
     hip.workspace_status(device)
     assert torch.equal(again, good)
+
+
+@pytest.mark.parametrize("tokens", [1, 4])
+def test_attention_step_wait_failure_is_poisoned_and_flagged(device, tokens):
+    # the single-launch attention step (T <= 4): every wait gives up at once
+    # -> NaN update and hidden_out, the step's own cache rows NaN, the
+    # position not advanced, the flag set; after clearing, the step at the
+    # same position equals the untouched run bit for bit
+    from fastkernels_amd.plan import AttentionStepPlan
+
+    print(f"attention wait failure tokens={tokens}", flush=True)
+    start, maxp = 21, 32
+    plan = AttentionStepPlan(wl.make_attention_weights(SPEC, seed=36, device=device), tokens, SPEC,
+                             max_positions=maxp, start_position=start)
+    g = torch.Generator().manual_seed(37)
+    plan.key_cache.copy_(torch.randn(maxp, SPEC.attention_kv_heads, SPEC.attention_head_dim, generator=g).to(device))
+    plan.value_cache.copy_(torch.randn(maxp, SPEC.attention_kv_heads, SPEC.attention_head_dim, generator=g).to(device))
+    plan.hidden.copy_(wl.make_hidden(tokens, SPEC.hidden_size, seed=38).to(device))
+    own = slice(start, start + tokens)
+    plan.run()
+    plan.check_device()
+    good = [plan.update.clone(), plan.hidden_out.clone(), plan.key_cache.clone()]
+    assert all(bool(torch.isfinite(t).all()) for t in good)
+    assert int(plan.position.item()) == start + tokens
+    plan.set_poll_limit(0)
+    plan.set_position(start)
+    plan.run()
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(plan.update).all()) and bool(torch.isnan(plan.hidden_out).all())
+    assert bool(torch.isnan(plan.key_cache[own]).all())
+    assert torch.equal(plan.key_cache[:start], good[2][:start])
+    assert int(plan.position.item()) == start  # (the epoch keeper's wait failed too)
+    plan.set_poll_limit(None)
+    plan.run()
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(plan.update).all())
+    _expect_device_error(plan)
+    plan.set_position(start)
+    plan.run()
+    plan.check_device()
+    for a, b in zip([plan.update, plan.hidden_out, plan.key_cache], good):
+        assert torch.equal(a, b)
