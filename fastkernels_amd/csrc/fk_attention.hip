@@ -757,18 +757,6 @@ __device__ __forceinline__ void as_norm_row(float* row, int d0, bool lin, int hd
   }
 }
 
-// Workgroup barrier for LDS hand-offs only: waits for the wavefront's LDS
-// operations, not its global stores (__syncthreads() also waits until every
-// global store is acknowledged, which would hold back each hint word by a
-// memory round trip).  Every exchange between the wavefronts of
-// attn_step_kernel goes through LDS; other workgroups read its global words
-// by their tags.
-__device__ __forceinline__ void as_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 // elem_word through a global-address-space pointer (a global load, not a
 // flat one, which would also count against the LDS wait counter).
 __device__ __forceinline__ uint32_t as_elem_word(const void* p, int dtype, size_t i) {
@@ -930,14 +918,14 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
       s_fail = 0;
       s_kfail = 0;
     }
-    as_sync();
+    lds_barrier();
     if (tid < T) {
       float tot = 0.f;
 #pragma unroll
       for (int w = 0; w < kAsWaves; ++w) tot += s_part[w][tid];
       s_rs[tid] = rsqrtf(tot / (float)H + a.eps);
     }
-    as_sync();
+    lds_barrier();
   }
 
   // ---- phase A: row dot products, every token --------------------------
@@ -966,7 +954,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
     const int ri = lane >> 3;
     if ((lane & 7) == 0 && ri < rn) store_tagged(a.tw.qkv + (size_t)t * R + rlo + ri, v, tag);
   }
-  as_sync();  // every wavefront's outputs are stored before the hint; phase B reuses the LDS
+  lds_barrier();  // every wavefront's outputs are stored before the hint; phase B reuses the LDS
   if (tid == 0) {
     store_tagged(a.tw.hint_a + b, 0.f, tag);
     store_tagged(a.tw.started + b, (float)start, tag);  // (after the epoch and position loads)
@@ -1018,7 +1006,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
         }
       }
     }
-    as_sync();
+    lds_barrier();
     {
       // token at's queries of heads hb .. (word e = g * hd + d), the own
       // tokens' k and v (word e = s * hd + d)
@@ -1045,14 +1033,14 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
         }
       }
     }
-    as_sync();
+    lds_barrier();
     FK_MARK(3);
     const bool bad = s_fail || bad_pos;
     // head norms: wavefront g < 4 query head hb + g, wavefront 4 + s own key s
     if (wave < Gu) as_norm_row(s_q + wave * hd, dl, lin, hd, a.qk_eps, qnr, a.qn_w, a.qn_dt);
     if (wave >= kAsGu && wave - kAsGu < n_own)
       as_norm_row(s_kr + (wave - kAsGu) * hd, dl, lin, hd, a.qk_eps, knr, a.kn_w, a.kn_dt);
-    as_sync();
+    lds_barrier();
     FK_MARK(10);
     // RoPE, and the queries' 1/sqrt(hd)
     if (wave < Gu && lin) {
@@ -1068,7 +1056,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
       const int s = wave - kAsGu;
       *reinterpret_cast<float4*>(s_kf + s * hd + d0) = as_rope4(s_kr + s * hd, d0, s_cs[1 + s], a);
     }
-    as_sync();
+    lds_barrier();
     FK_MARK(11);
     float4 q4[kAsGu], acc[kAsGu];
     float m[kAsGu], l[kAsGu];
@@ -1086,11 +1074,11 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
     constexpr int PPW = kAsTile / kAsWaves;  // positions per wavefront per tile
     for (int pt = p_lo; pt < p_hi; pt += kAsTile) {
       if (pt != p_lo) {
-        as_sync();  // every wavefront is done with the previous tile
+        lds_barrier();  // every wavefront is done with the previous tile
         issue_tile(pt);
       }
       stage_tile(s_kt);
-      as_sync();
+      lds_barrier();
       FK_MARK(12);
       const float* s_vt = s_kt + kAsTile * hd;
       const int pend = min(pt + kAsTile, p_hi);
@@ -1141,7 +1129,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
         m[g] = mx;
       }
     }
-    as_sync();  // the softmax states reuse the row tile
+    lds_barrier();  // the softmax states reuse the row tile
     FK_MARK(13);
     // the wavefronts' states merged per (head, dim): per-wavefront factors
     // exp(m_w - M) once, then the chunk partial (max, sum, weighted values)
@@ -1156,7 +1144,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
         if (lin) *reinterpret_cast<float4*>(s_acc + ((size_t)wave * Gu + g) * hd + d0) = acc[g];
       }
     }
-    as_sync();
+    lds_barrier();
     if (tid < kAsWaves * kAsGu) {
       const int w = tid / kAsGu, g = tid - w * kAsGu;
       if (g < Gu) {
@@ -1173,7 +1161,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
         }
       }
     }
-    as_sync();
+    lds_barrier();
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int e = tid + i * kAsThreads;
@@ -1198,7 +1186,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
       store1<CBF>(a.kc, cr, poison_if(bad, s_kf[s * hd + tid]));
       store1<CBF>(a.vc, cr, poison_if(bad, s_vn[s * hd + tid]));
     }
-    as_sync();  // (the LDS is reused by the next role)
+    lds_barrier();  // (the LDS is reused by the next role)
     FK_MARK(14);
   }
   FK_MARK(4);
@@ -1240,13 +1228,13 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
       s_fc[lane] = fc;
       if (lane == 0) s_L = L;
     }
-    as_sync();
+    lds_barrier();
     float o = 0.f;
 #pragma unroll
     for (int k = 0; k < kAsMaxChunks / kAsWaves; ++k)
       if (srcs[k]) o = fmaf(s_fc[wave + kAsWaves * k], value_of(w[k]), o);
     s_mo[wave][lane] = o;
-    as_sync();
+    lds_barrier();
     if (wave == 0) {
       float tot = 0.f;
 #pragma unroll
@@ -1254,7 +1242,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
       const float gv = tot / s_L * sigmoid(value_of(st[2]));
       store_tagged(a.tw.gated + (size_t)mt * K + (size_t)mh * hd + mds * kAsMDims + lane, poison_if(s_fail != 0, gv), tag);
     }
-    as_sync();  // (the LDS is reused by the next role)
+    lds_barrier();  // (the LDS is reused by the next role)
   }
   FK_MARK(5);
 
@@ -1284,7 +1272,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
       for (int t = 0; t < kAsMaxTokens; ++t)
         if (t < T) s_g[t * kAsKcu + tid] = value_of(w[t]);
     }
-    as_sync();
+    lds_barrier();
     FK_MARK(6);
     const bool bad = s_fail != 0;
     for (int t = 0; t < T; ++t) {
@@ -1349,7 +1337,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
     const uint64_t* srcs[1] = {tid < G ? a.tw.started + tid : nullptr};
     w[0] = srcs[0] ? load_tagged(srcs[0]) : 0ull;
     if (!poll_tagged<1>(w, srcs, tag, plim)) s_kfail = 1;
-    as_sync();
+    lds_barrier();
     // (not after a failed wait: a workgroup that has not read the epoch and
     // the position yet would take the next launch's; the error word poisons
     // later launches)
@@ -1358,7 +1346,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
       if (a.start_dev) store_coherent(a.start_dev, start + T);
     }
   }
-  as_sync();
+  lds_barrier();
   if (tid == 0 && (s_fail || s_kfail))
     __hip_atomic_fetch_or(&a.tw.tickets[kWorkspaceErrorWord], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
                           __HIP_MEMORY_SCOPE_AGENT);

@@ -450,6 +450,18 @@ __device__ __forceinline__ WaitLimits wait_limits(const uint32_t* header, int ep
   return load_wait_header(header, epoch_word).limits();
 }
 
+// Workgroup barrier for hand-offs through LDS only: waits for the
+// wavefront's LDS operations, not for its global stores (__syncthreads()
+// also waits until every global store of the wavefront is acknowledged, a
+// memory round trip).  For kernels whose wavefronts exchange data through
+// LDS alone while their global words go to other workgroups, which read
+// them by their launch tags.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Poisoned value of an output whose inputs a failed wait left invalid.
 __device__ __forceinline__ float poison_if(bool bad, float v) { return bad ? __builtin_nanf("") : v; }
 
