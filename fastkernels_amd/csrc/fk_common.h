@@ -392,6 +392,27 @@ __device__ __forceinline__ bool poll_tagged(uint64_t (&w)[N], const uint64_t* co
   return false;
 }
 
+// poll_tagged over a contiguous run: word j of this thread is
+// base[first + stride * j] when first + stride * j < n (else no word); the
+// addresses are recomputed per round instead of held in registers.
+template <int N>
+__device__ __forceinline__ bool poll_run(uint64_t (&w)[N], const uint64_t* base, int first, int stride, int n,
+                                         uint32_t tag, uint32_t limit) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) w[j] = first + stride * j < n ? load_tagged(base + first + stride * j) : 0ull;
+  for (uint32_t i = 0; i < limit; ++i) {
+    bool ready = true;
+#pragma unroll
+    for (int j = 0; j < N; ++j) ready = ready && (first + stride * j >= n || tag_of(w[j]) == tag);
+    if (ready) return true;
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (first + stride * j < n && tag_of(w[j]) != tag) w[j] = load_tagged(base + first + stride * j);
+  }
+  return false;
+}
+
 // Grid-wide barrier for kernels whose grid the host has capped at the number
 // of co-resident workgroups.  Called by one thread per workgroup after the
 // workgroup's publishing stores have been waited for.  The wait is bounded

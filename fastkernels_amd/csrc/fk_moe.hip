@@ -1724,6 +1724,470 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
 }
 
 // ---------------------------------------------------------------------------
+// A run of MoE layers at one token in one launch (fk_moe_stack_decode): layer
+// l's input is layer l-1's layer_out, as in the resident layer stack.  Each
+// layer runs the phases of moe_fused_kernel with the same arithmetic in the
+// same order, so its outputs equal a chain of fk_moe_layer calls bit for bit:
+//   X   the layer's input in LDS (fp32): layer 0's converted from the
+//       caller's tokens, a later layer's polled from the previous layer's
+//       tagged outputs by every workgroup
+//   P1  router rows, shared gate/up rows and the shared gate, in units of 8
+//       rows (one per wavefront), at most one unit per workgroup; a unit's
+//       weight rows for layer l + 1 are fetched during layer l's down phase
+//   P2  every workgroup polls the logits and selects the top-k itself
+//   P3  routed gate/up blocks, the wavefront's 8 down rows fetched behind them
+//   P4  activations polled into LDS, down rows, combine and residual; the
+//       layer output also leaves as tagged words for the next layer
+// The launch epoch is kept as in the single-launch layer (once per launch).
+// Per-layer tagged words: logits [E], activations [(K + 1) I], the shared
+// gate [1], the layer output [H] (kStackLayerWords per layer).
+// ---------------------------------------------------------------------------
+constexpr int kStackMaxH = 2048;
+constexpr int kStackMaxLayers = 64;  // layers per launch (descriptors staged in LDS)
+static_assert(sizeof(fk_moe_stack_layer) == 13 * 8, "descriptor: 13 pointers");
+constexpr size_t kStackLayerWords = 256 + 9 * 512 + 64 + kStackMaxH;  // logits, activations, gate (padded), output
+constexpr size_t kStackMaxDynLds = ((size_t)kStackMaxH + 9 * 512 + 4) * sizeof(float);
+
+struct StackArgs {
+  const void* x0;
+  const fk_moe_stack_layer* layers;
+  int L, bias_dt, H, I, E, K;
+  float eps, off;
+  uint32_t* tickets;   // workspace header (epoch, poll bound, error word)
+  uint64_t* started;   // [kFusedMaxGrid]
+  uint64_t* words;     // [L][kStackLayerWords]
+};
+
+// The layer descriptors live in device memory, so the compiler cannot tell
+// that their pointers address global memory: without these casts every
+// access through them would be a flat access (which also counts against the
+// LDS wait counter).  Elements are bf16 unless stated.
+typedef const __attribute__((address_space(1))) u32x4 g_u32x4;
+__device__ __forceinline__ u32x4 g_row16(const void* base, size_t elem) {
+  return *(g_u32x4*)((const __attribute__((address_space(1))) char*)base + elem * 2);
+}
+__device__ __forceinline__ u32x4 g_row16_nt(const void* base, size_t elem) {
+  return __builtin_nontemporal_load((g_u32x4*)((const __attribute__((address_space(1))) char*)base + elem * 2));
+}
+__device__ __forceinline__ float g_scalar(const void* p, int dtype, size_t i) {
+  const __attribute__((address_space(1))) char* c = (const __attribute__((address_space(1))) char*)p;
+  return dtype == FK_DTYPE_BF16 ? __uint_as_float((uint32_t)((const __attribute__((address_space(1))) uint16_t*)c)[i] << 16)
+                                : ((const __attribute__((address_space(1))) float*)c)[i];
+}
+template <class T>
+__device__ __forceinline__ void g_store(T* p, size_t i, T v) {
+  ((__attribute__((address_space(1))) T*)p)[i] = v;
+}
+__device__ __forceinline__ void bf16x8_to_f32(const u32x4& v, float out[8]) {
+  Raw8<true> r;
+  r.a = v;
+  r.b = u32x4{0, 0, 0, 0};
+  raw8_to_f32<true>(r, out);
+}
+
+FK_TIMELINE_BUFFER(moe_stack)
+
+template <bool BFX0>
+__global__ __launch_bounds__(512) void moe_stack_kernel(StackArgs sa) {
+  constexpr int NPF = 8;  // prefetched down rows per wavefront: one per routed expert
+  __shared__ int s_ids[8];
+  __shared__ float s_w[8];
+  __shared__ int s_active[8];  // routed experts, selection order
+  __shared__ float s_wpos[8];  // their routing weights
+  __shared__ int s_fail;
+  __shared__ uint32_t s_wtag[kFusedWaves];
+  __shared__ float s_chunk[kFusedChunk];
+  __shared__ uint64_t s_desc_w[kStackMaxLayers * 13];  // the layer descriptors
+  extern __shared__ float4 s_dyn_v[];
+  float* s_x = reinterpret_cast<float*>(s_dyn_v);  // [H] the layer's input
+  float* s_act = s_x + kStackMaxH;                  // [(K + 1) I] activations, then the shared gate
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = gridDim.x, b = blockIdx.x;
+  const int NW = G * kFusedWaves;  // (>= H, the host checks: one down row per wavefront)
+  const int H = sa.H, E = sa.E, K = sa.K, I = sa.I, L = sa.L, P = K;
+  const int nch = H >> 3;
+  const int nrb = (E + 7) / 8, nsb = I / 8, nunits = nrb + nsb + 1;
+  const bool has_unit = b < nunits;
+  const int unit = b;
+  uint32_t* err = &sa.tickets[kTicketError];
+  WaitHeader hdr = load_wait_header(sa.tickets, kTicketEpoch);
+  if (tid == 0) s_fail = 0;
+  FK_TIMELINE_DECL;
+  FK_MARK(0);  // (timeline markers: diagnostic builds only)
+
+  // P1 weight rows of this workgroup's unit: router row (pa) + norm weight
+  // (pb), or shared gate row (pa) + up row (pb), or the shared gate (pa; the
+  // norm weight when there is none: a valid address, products dropped).
+  // Clamped in range and unconditional within the unit's kind.
+  u32x4 pa[4], pb[4];
+  auto issue_unit = [&](const fk_moe_stack_layer& lyr) {
+    // one source and row per kind, then the same eight loads for every kind
+    const void* src_a;
+    const void* src_b;
+    size_t row_a, row_b;
+    if (unit < nrb) {
+      src_a = lyr.router_weight;
+      row_a = (size_t)min(unit * 8 + wave, E - 1) * H;
+      src_b = lyr.norm_weight;
+      row_b = 0;
+    } else if (unit < nrb + nsb) {
+      const int i = (unit - nrb) * 8 + wave;
+      src_a = src_b = lyr.shared_gate_up;
+      row_a = (size_t)i * H;
+      row_b = (size_t)(I + i) * H;
+    } else {
+      src_a = src_b = lyr.shared_gate ? lyr.shared_gate : lyr.norm_weight;
+      row_a = row_b = 0;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const size_t cc = (size_t)min(lane + kWave * j, nch - 1) * 8;
+      pa[j] = g_row16(src_a, row_a + cc);
+      pb[j] = g_row16(src_b, row_b + cc);
+    }
+  };
+  // The descriptors are read once into LDS: read from global memory where a
+  // phase needs them, they would be vector loads (the kernel writes global
+  // memory, so the compiler cannot serve them from the scalar cache), each
+  // waited for on the spot.
+  {
+    const __attribute__((address_space(1))) uint64_t* gd = (const __attribute__((address_space(1))) uint64_t*)sa.layers;
+    for (int w = tid; w < L * 13; w += 512) s_desc_w[w] = gd[w];
+  }
+  __syncthreads();
+  const fk_moe_stack_layer* s_desc = reinterpret_cast<const fk_moe_stack_layer*>(s_desc_w);
+  if (has_unit) issue_unit(s_desc[0]);
+  // layer 0's input into LDS (chunk tid of the H / 8, threads tid < nch)
+  {
+    const Raw8<BFX0> x0r = load_raw8<BFX0>(sa.x0, (size_t)min(tid, nch - 1) * 8);
+    if (tid < nch) {
+      float x8[8];
+      raw8_to_f32<BFX0>(x0r, x8);
+      float4* d = reinterpret_cast<float4*>(s_x + tid * 8);
+      d[0] = make_float4(x8[0], x8[1], x8[2], x8[3]);
+      d[1] = make_float4(x8[4], x8[5], x8[6], x8[7]);
+    }
+  }
+  const WaitLimits wl = hdr.limits();
+  const uint32_t tag = wl.tag, plim = wl.poll;
+
+  for (int l = 0; l < L; ++l) {
+    // The thread index, made opaque once per layer: per-lane addresses
+    // derived from it are recomputed in each layer instead of being hoisted
+    // out of the loop and held in registers across all of it.
+    int tid_l = threadIdx.x;
+    asm volatile("" : "+v"(tid_l));
+    const int tid = tid_l, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int q0 = wave * G + b;
+    FK_MARK(1);
+    const fk_moe_stack_layer& ly = s_desc[l];
+    uint64_t* f_logits = sa.words + (size_t)l * kStackLayerWords;
+    uint64_t* f_act = f_logits + 256;
+    uint64_t* f_sgate = f_act + 9 * 512;
+    uint64_t* f_x = f_sgate + 64;
+    // ---- X: the layer's input into LDS (layer 0's: before the loop) -------
+    if (l > 0) {
+      const uint64_t* px = sa.words + (size_t)(l - 1) * kStackLayerWords + 256 + 9 * 512 + 64;
+      uint64_t w[kStackMaxH / 512];
+      if (!poll_run<kStackMaxH / 512>(w, px, tid, 512, H, tag, plim)) s_fail = 1;
+#pragma unroll
+      for (int j = 0; j < kStackMaxH / 512; ++j)
+        if (tid + 512 * j < H) s_x[tid + 512 * j] = value_of(w[j]);
+    }
+    __syncthreads();
+    FK_MARK(2);
+
+    // ---- P1: this workgroup's unit (as moe_fused_kernel, x from LDS) -----
+    if (has_unit) {
+      float mine = 0.f;
+      if (unit < nrb) {
+        const int e = unit * 8 + wave;
+        if (e < E) {
+          float wn[4][8];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int c = lane + kWave * j;
+            float w8[8], n8[8];
+            bf16x8_to_f32(pb[j], n8);
+            bf16x8_to_f32(pa[j], w8);
+#pragma unroll
+            for (int qq = 0; qq < 8; ++qq) wn[j][qq] = c < nch ? w8[qq] * (sa.off + n8[qq]) : 0.f;
+          }
+          const float bias = ly.router_bias ? g_scalar(ly.router_bias, sa.bias_dt, e) : 0.f;
+          float ss = 0.f, d = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int c = lane + kWave * j;
+            const bool in = c < nch;
+            const float4* xp = reinterpret_cast<const float4*>(s_x + (size_t)min(c, nch - 1) * 8);
+            const float4 xa = xp[0], xb = xp[1];
+            const float x8[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+            for (int qq = 0; qq < 8; ++qq) {
+              const float xv = in ? x8[qq] : 0.f;
+              ss = fmaf(xv, xv, ss);
+              d = fmaf(xv, wn[j][qq], d);
+            }
+          }
+          ss = wave_sum(ss);
+          d = wave_sum(d);
+          mine = d * rsqrtf(ss / (float)H + sa.eps) + bias;
+        }
+      } else if (unit < nrb + nsb) {
+        float g = 0.f, u = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = lane + kWave * j;
+          if (c < nch) {
+            float a8[8], b8[8];
+            const float4* xp = reinterpret_cast<const float4*>(s_x + (size_t)c * 8);
+            const float4 xa = xp[0], xb = xp[1];
+            const float x8[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            bf16x8_to_f32(pa[j], a8);
+            bf16x8_to_f32(pb[j], b8);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+              g = fmaf(a8[q], x8[q], g);
+              u = fmaf(b8[q], x8[q], u);
+            }
+          }
+        }
+        g = wave_sum(g);
+        u = wave_sum(u);
+        mine = silu(g) * u;
+      } else if (wave == 0) {
+        float g8[4][8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = lane + kWave * j;
+          bf16x8_to_f32(pa[j], g8[j]);
+#pragma unroll
+          for (int qq = 0; qq < 8; ++qq) g8[j][qq] = (ly.shared_gate && c < nch) ? g8[j][qq] : 0.f;
+        }
+        float d = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float4* xp = reinterpret_cast<const float4*>(s_x + (size_t)min(lane + kWave * j, nch - 1) * 8);
+          const float4 xa = xp[0], xb = xp[1];
+          const float x8[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+          for (int qq = 0; qq < 8; ++qq) d = fmaf(x8[qq], g8[j][qq], d);
+        }
+        d = wave_sum(d);
+        mine = ly.shared_gate ? sigmoid(d) : 1.f;
+      }
+      if (lane == 0) s_chunk[wave] = mine;
+      __syncthreads();
+      if (tid < 8) {
+        const float v = s_chunk[tid];
+        if (unit < nrb) {
+          const int e = unit * 8 + tid;
+          if (e < E) {
+            g_store(ly.logits, (size_t)e, v);
+            store_tagged(f_logits + e, v, tag);
+          }
+        } else if (unit < nrb + nsb) {
+          store_tagged(f_act + (size_t)P * I + (unit - nrb) * 8 + tid, v, tag);
+        } else if (tid == 0) {
+          store_tagged(f_sgate, v, tag);
+        }
+      }
+    }
+    if (l == 0) {
+      // started record (every wavefront has used the epoch it read)
+      if (lane == 0) s_wtag[wave] = tag;
+      __syncthreads();
+      if (tid == 0) store_tagged(sa.started + b, __uint_as_float(s_wtag[kFusedWaves - 1]), tag);
+    }
+    FK_MARK(3);
+    // this wavefront's shared down row
+    const int r_first = q0;
+    Raw8<true> sdr;
+    sdr.a = g_row16_nt(ly.shared_down, (size_t)min(r_first, H - 1) * I + (size_t)min(lane * 8, I - 8));
+    sdr.b = u32x4{0, 0, 0, 0};
+
+    // ---- P2: top-k in every workgroup ------------------------------------
+    if (wave == 0) {
+      constexpr int NJE = kFusedMaxExperts / kWave;
+      uint64_t w[NJE];
+      const uint64_t* srcs[NJE];
+#pragma unroll
+      for (int j = 0; j < NJE; ++j) {
+        const int ex = lane + kWave * j;
+        srcs[j] = ex < E ? f_logits + ex : nullptr;
+        w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+      }
+      const bool ok = poll_tagged<NJE>(w, srcs, tag, plim);
+      if (!ok) s_fail = 1;
+      float p[NJE];
+#pragma unroll
+      for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
+      int tk_id = 0;
+      float tk_w = 0.f;
+      topk_select_regs<NJE>(p, E, K, lane, tk_id, tk_w);
+      if (!ok) tk_id = min(max(tk_id, 0), E - 1);
+      if (lane < K) {
+        s_ids[lane] = tk_id;
+        s_w[lane] = tk_w;
+        s_active[lane] = tk_id;
+        s_wpos[lane] = tk_w;
+      }
+    } else if (l == 0 && b == 0) {
+      // workgroup 0: every workgroup of the launch has read the epoch
+      constexpr int kChunk = 4;
+      const int nthr = (kFusedWaves - 1) * kWave;
+      for (int base = tid - kWave; base < G; base += kChunk * nthr) {
+        uint64_t w[kChunk];
+        const uint64_t* srcs[kChunk];
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+          const int r = base + j * nthr;
+          srcs[j] = r < G ? sa.started + r : nullptr;
+          w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+        }
+        if (!poll_tagged<kChunk>(w, srcs, tag, plim)) s_fail = 1;
+      }
+    }
+    __syncthreads();
+    const bool bad = s_fail;
+    if (l == 0 && b == 0 && tid == 0 && !bad) store_coherent(&sa.tickets[kTicketEpoch], tag);
+    if (b == 0 && tid < K) {
+      g_store(ly.topk_ids, (size_t)tid, (int64_t)s_ids[tid]);
+      g_store(ly.topk_weights, (size_t)tid, poison_if(bad, s_w[tid]));
+    }
+    FK_MARK(4);
+
+    // ---- P3: routed gate/up (+ down-row prefetch) --------------------------
+    const int U = K, bpe = I / kFusedChunk, nblk = U * bpe;
+    const bool prefetch = r_first < H;
+    Raw8<true> dr[NPF];
+#pragma unroll
+    for (int u = 0; u < NPF; ++u) dr[u].b = u32x4{0, 0, 0, 0};
+    {
+      const void* gu = ly.gate_up;
+      const void* dn = ly.down;
+      const size_t dcol = (size_t)min(lane * 8, I - 8), drow = (size_t)min(r_first, H - 1);
+      auto issue_down = [&]() {
+#pragma unroll
+        for (int u = 0; u < NPF; ++u)
+          dr[u].a = g_row16_nt(dn, ((size_t)s_active[min(u, U - 1)] * H + drow) * I + dcol);
+      };
+      auto block = [&](int blk, bool first_blk) {
+        const int u = blk / bpe, i0 = (blk - u * bpe) * kFusedChunk;
+        const int ia = i0 + 2 * wave;
+        const size_t we = (size_t)s_active[u] * 2 * I * H;  // (elements)
+        u32x4 ga[4], ua8[4], gb[4], ub8[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const size_t c8 = (size_t)min(lane + kWave * j, nch - 1) * 8;
+          ga[j] = g_row16_nt(gu, we + (size_t)ia * H + c8);
+          gb[j] = g_row16_nt(gu, we + (size_t)(ia + 1) * H + c8);
+          ua8[j] = g_row16_nt(gu, we + (size_t)(I + ia) * H + c8);
+          ub8[j] = g_row16_nt(gu, we + (size_t)(I + ia + 1) * H + c8);
+        }
+        if (first_blk) issue_down();
+        float acc[4] = {0.f, 0.f, 0.f, 0.f};  // gate ia, up ia, gate ia + 1, up ia + 1
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int c = lane + kWave * j;
+          if (c < nch) {
+            float w8[8];
+            const float4* xp = reinterpret_cast<const float4*>(s_x + (size_t)c * 8);
+            const float4 xa = xp[0], xb = xp[1];
+            const float x8[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            bf16x8_to_f32(ga[j], w8);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc[0] = fmaf(w8[q], x8[q], acc[0]);
+            bf16x8_to_f32(ua8[j], w8);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc[1] = fmaf(w8[q], x8[q], acc[1]);
+            bf16x8_to_f32(gb[j], w8);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc[2] = fmaf(w8[q], x8[q], acc[2]);
+            bf16x8_to_f32(ub8[j], w8);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc[3] = fmaf(w8[q], x8[q], acc[3]);
+          }
+        }
+        const float rs = rows4_sum(acc);
+        const float g0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 0));
+        const float u0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 16));
+        const float g1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 32));
+        const float u1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 48));
+        if (lane == 0) {
+          s_chunk[2 * wave] = silu(g0) * u0;
+          s_chunk[2 * wave + 1] = silu(g1) * u1;
+        }
+        __syncthreads();
+        if (tid < kFusedChunk) store_tagged(f_act + (size_t)u * I + i0 + tid, poison_if(bad, s_chunk[tid]), tag);
+        __syncthreads();
+      };
+      if (b < nblk) {
+        block(b, true);
+        for (int blk = b + G; blk < nblk; blk += G) block(blk, false);
+      } else {
+        issue_down();
+      }
+    }
+    FK_MARK(5);
+
+    // ---- P4: activations, next layer's unit rows, down rows, combine -----
+    // ((K + 1) I <= 9 * 512 activations: 9 words per thread; the shared gate
+    // by thread 0)
+    const int n_act = (P + 1) * I;
+    bool stage_ok;
+    {
+      uint64_t w[9];
+      stage_ok = poll_run<9>(w, f_act, tid, 512, n_act, tag, plim);
+#pragma unroll
+      for (int j = 0; j < 9; ++j)
+        if (tid + 512 * j < n_act) s_act[tid + 512 * j] = value_of(w[j]);
+      if (tid == 0) {
+        uint64_t g[1];
+        stage_ok = poll_run<1>(g, f_sgate, 0, 1, 1, tag, plim) && stage_ok;
+        s_act[n_act] = value_of(g[0]);
+      }
+    }
+    if (!stage_ok) s_fail = 1;
+    __syncthreads();
+    const bool bad_out = s_fail;
+    // the next layer's unit rows: issued after the activation polls (a
+    // wavefront's loads retire in order, so rows issued before them would
+    // hold the polls back); they arrive during the down rows and the next
+    // layer's input hand-off
+    if (l + 1 < L && has_unit) issue_unit(s_desc[l + 1]);
+    FK_MARK(6);
+    const float* s_sg = s_act + n_act;
+    for (int r = q0; r < H; r += NW) {
+      const bool first = r == r_first;
+      float acc;
+      if (first && prefetch) {
+        acc = s_sg[0] * dot8_act_lds(sdr, s_act + (size_t)P * I, lane, I);
+#pragma unroll
+        for (int u = 0; u < NPF; ++u) {
+          const float d = dot8_act_lds(dr[u], s_act + (size_t)(u < U ? u : 0) * I, lane, I);
+          acc = u < U ? fmaf(s_wpos[u], d, acc) : acc;
+        }
+      } else {
+        // (not reached at the host-checked shapes: every row is a first row)
+        acc = 0.f;
+      }
+      const float o = poison_if(bad_out, wave_sum(acc));
+      if (lane == 0) {
+        const float lo = s_x[r] + o;
+        g_store(ly.moe_out, (size_t)r, o);
+        g_store(ly.layer_out, (size_t)r, lo);
+        store_tagged(f_x + r, lo, tag);
+      }
+    }
+    __syncthreads();  // s_x and s_act are reused by the next layer
+    FK_MARK(7);
+  }
+  if (tid == 0 && s_fail) __hip_atomic_fetch_or(err, FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  FK_TIMELINE_COMMIT(moe_stack, blockIdx.x);
+}
+
+// ---------------------------------------------------------------------------
 // Router without grid barrier (T <= 256, E <= 256, H <= 2048).
 //
 // Workgroup (ub, tb) computes the logits of expert rows 8ub.. (one per
@@ -2120,6 +2584,36 @@ static int launch_fused_t(const FusedArgs& fa, hipStream_t stream) {
   return check_launch("moe_fused_kernel");
 }
 
+// Single-launch run of layers (T = 1): shapes the kernel handles on a grid
+// of G workgroups (every P1 unit on its own workgroup, one down row per
+// wavefront).
+static bool stack_eligible(int H, int I, int E, int K, int G) {
+  const int nunits = (E + 7) / 8 + I / 8 + 1;
+  return H >= 8 && H <= kStackMaxH && H % 8 == 0 && I >= kFusedChunk && I <= 512 && I % kFusedChunk == 0 && E >= 1 &&
+         E <= kFusedMaxExperts && K >= 1 && K <= 8 && K <= E && nunits <= G && G * kFusedWaves >= H && G <= kFusedMaxGrid;
+}
+
+template <bool BX>
+static int stack_grid() {
+  static int cap_cache[64] = {0};
+  const int cap = resident_capacity(moe_stack_kernel<BX>, 512, kStackMaxDynLds, cap_cache);
+  const int cus = device_cus();
+  return cap < cus ? cap : cus;  // one workgroup per CU
+}
+
+static size_t stack_ws_layout(int L, char* base, uint32_t** tickets, uint64_t** started, uint64_t** words) {
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = off;
+    off = align_up(off + bytes, 256);
+    return base ? base + at : nullptr;
+  };
+  *tickets = reinterpret_cast<uint32_t*>(take(16 * sizeof(uint32_t)));
+  *started = reinterpret_cast<uint64_t*>(take((size_t)kFusedMaxGrid * 8));
+  *words = reinterpret_cast<uint64_t*>(take((size_t)L * kStackLayerWords * 8));
+  return off;
+}
+
 template <bool BW, bool BX, int NJ, int NJE>
 static int launch_router_t(const RouterArgs& ra, hipStream_t stream) {
   static int cap_cache[64] = {0};
@@ -2514,6 +3008,53 @@ int fk_moe_layer(const void* hidden, int hidden_dtype, const void* norm_weight, 
                                    shared_gate_dtype, tokens, hidden_size, intermediate, num_experts, top_k,
                                    moe_out, layer_out, ws);
   return launch_experts(ea, expert_dtype, as_stream(stream));
+}
+
+size_t fk_moe_stack_workspace_bytes(int num_layers, int num_experts, int top_k, int intermediate, int hidden_size) {
+  if (num_layers < 1 || num_experts < 1 || top_k < 1 || intermediate < 1 || hidden_size < 1) return 0;
+  uint32_t* t;
+  uint64_t *s, *w;
+  return stack_ws_layout(num_layers, nullptr, &t, &s, &w);
+}
+
+int fk_moe_stack_decode(const void* hidden, int hidden_dtype, const fk_moe_stack_layer* layers, int num_layers,
+                        int bias_dtype, int hidden_size, int intermediate, int num_experts, int top_k, float eps,
+                        float norm_offset, void* workspace, size_t workspace_bytes, void* stream) {
+  if (num_layers < 1) return fail(FK_ERR_INVALID, "num_layers must be positive");
+  if (num_layers > kStackMaxLayers)
+    return fail(FK_ERR_UNSUPPORTED, "num_layers must be <= %d per call (chain longer runs through layer_out)",
+                kStackMaxLayers);
+  if (!hidden || !layers) return fail(FK_ERR_INVALID, "hidden and layers must be non-NULL");
+  if (!is_float_dtype(hidden_dtype) || !is_float_dtype(bias_dtype))
+    return fail(FK_ERR_DTYPE, "hidden and router bias must be f32 or bf16");
+  if (!aligned16(hidden)) return fail(FK_ERR_ALIGNMENT, "hidden must be 16-byte aligned");
+  const bool bx = hidden_dtype == FK_DTYPE_BF16;
+  const int G = bx ? stack_grid<true>() : stack_grid<false>();
+  if (!stack_eligible(hidden_size, intermediate, num_experts, top_k, G))
+    return fail(FK_ERR_UNSUPPORTED,
+                "fk_moe_stack_decode: hidden_size <= %d (multiple of 8), intermediate <= 512 (multiple of %d), "
+                "num_experts <= %d, top_k <= 8 on a grid of %d workgroups",
+                kStackMaxH, kFusedChunk, kFusedMaxExperts, G);
+  StackArgs sa;
+  const size_t need = stack_ws_layout(num_layers, nullptr, &sa.tickets, &sa.started, &sa.words);
+  if (!workspace || workspace_bytes < need)
+    return fail(FK_ERR_WORKSPACE, "stack workspace needs %zu bytes (got %zu)", need, workspace_bytes);
+  stack_ws_layout(num_layers, reinterpret_cast<char*>(workspace), &sa.tickets, &sa.started, &sa.words);
+  sa.x0 = hidden;
+  sa.layers = layers;
+  sa.L = num_layers;
+  sa.bias_dt = bias_dtype;
+  sa.H = hidden_size;
+  sa.I = intermediate;
+  sa.E = num_experts;
+  sa.K = top_k;
+  sa.eps = eps;
+  sa.off = norm_offset;
+  const size_t shm = kStackMaxDynLds;
+  const hipStream_t s = as_stream(stream);
+  if (bx) hipLaunchKernelGGL(moe_stack_kernel<true>, dim3(G), dim3(512), shm, s, sa);
+  else hipLaunchKernelGGL(moe_stack_kernel<false>, dim3(G), dim3(512), shm, s, sa);
+  return check_launch("moe_stack_kernel");
 }
 
 int fk_moe_layer_noalloc(const void* hidden, int hidden_dtype, const void* norm_weight, int norm_dtype,
