@@ -565,10 +565,11 @@ struct StepTagWs {
   uint64_t* norm;     // [T, V] gated values o * w * silu(z), before the RMSNorm scale
   uint64_t* started;  // [grid]
   // Polling hints: a tile's (a head's) tag is stored once its outputs are
-  // stored.  A consumer waits on the few hints of its producers before it
-  // reads their outputs, instead of spinning on every output word (which
-  // floods the memory system while the producers still stream).  The
-  // outputs still carry their own tags and are re-read until they do.
+  // stored.  From three tokens on, a consumer waits on the few hints of its
+  // producers before it reads their outputs, instead of spinning on every
+  // output word (which floods the memory system while the producers still
+  // stream).  The outputs still carry their own tags and are re-read until
+  // they do.
   uint64_t* hint_tile;  // [kStepTilesPerWG * kStepMaxGrid]
   uint64_t* hint_head;  // [64 * kStepHeadWGs] per head workgroup
   uint64_t* hss;        // [kStepMaxTokens][kStepHssPitch] head quarters' sums of squares
@@ -1081,9 +1082,11 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     float* s_o = s_in + (size_t)T * kStepInPitch;
     const int hq = head / (Hv / a.Hk);
     bool ok = true;
-    // Hints of the 20 tiles holding this quarter's q, k, v and z rows (one
-    // load per lane), then one read of the inputs.
-    if (wave == 0) {
+    // From three tokens on: hints of the 20 tiles holding this quarter's q,
+    // k, v and z rows (one load per lane), then one read of the inputs.  At
+    // one or two tokens the inputs are polled directly (a round trip fewer;
+    // the few words re-read while the last tiles stream cost less than it).
+    if (NT > 2 && wave == 0) {
       constexpr int TPB = kStepD / 16, TPQ = kStepQCols / 16;  // tiles per 128 rows, per quarter's 32 rows
       int tl = -1;
       if (lane < 2 * TPB) {
@@ -1230,7 +1233,11 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     uint16_t* s_nb = reinterpret_cast<uint16_t*>(s_dyn);  // [kcu/8][NCP][8] bf16 (bcol_slot)
     const int h0 = uks * (kcu / kStepD), nh = kcu / kStepD;  // heads of the unit's columns
     bool ok = true;
-    if (wave == 0) {  // the head workgroups of those heads
+    // From three tokens on, the hints of the head workgroups of those heads
+    // first; at one or two tokens the inputs are polled directly (-0.45 us
+    // at T = 1; at T = 8 the units re-read 8x the words while the heads
+    // still run, +0.65 us).
+    if (NT > 2 && wave == 0) {
       uint64_t hw[1];
       const uint64_t* hs[1] = {lane < nh * kStepHeadWGs ? a.tw.hint_head + h0 * kStepHeadWGs + lane : nullptr};
       hw[0] = hs[0] ? load_tagged(hs[0]) : 0ull;

@@ -1578,12 +1578,14 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   Raw8<true> dr[NPF];
   {
     // One token: each routed expert holds one pair (expert u at permuted
-    // position u).  The loads are issued in the order their data is needed,
-    // and loads return roughly in issue order: the token's chunks, the first
-    // block's gate/up rows, then this wavefront's 8 down rows.  Gate/up
-    // (32 MB over the grid) then completes before the down rows (16 MB), and
-    // the activation hand-off that follows gate/up overlaps the down stream.
-    // Every load is unconditional (clamped in range; unused lanes and slots
+    // position u).  The token's chunks and the first block's gate/up rows are
+    // issued first; this wavefront's 8 down rows only once the block's
+    // activations are stored.  Loads in flight together are served
+    // interleaved, whatever their issue order: with the down rows (16 MB
+    // over the grid) issued right behind the gate/up rows (32 MB), gate/up
+    // completed ~1 us later, and the activation hand-off that follows it is
+    // on the critical path while the down stream is not (it overlaps the
+    // hand-off).  Every load is unconditional (clamped in range; unused lanes and slots
     // are dropped where the values are used), so no branch makes the
     // compiler wait for the loads before it.
     Raw8<BFX> xt[4];
@@ -1609,7 +1611,6 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
         ua8[j] = load_raw8_stream<true>(we, (size_t)(I + ia) * H + c8);
         ub8[j] = load_raw8_stream<true>(we, (size_t)(I + ia + 1) * H + c8);
       }
-      if (first_blk) issue_down();
       float acc[4] = {0.f, 0.f, 0.f, 0.f};  // gate ia, up ia, gate ia + 1, up ia + 1
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -1642,6 +1643,7 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       }
       __syncthreads();
       if (tid < kFusedChunk) store_tagged(a.ws.f_act + (size_t)u * I + i0 + tid, poison_if(bad, s_chunk[0][tid]), tag);
+      if (first_blk) issue_down();
       __syncthreads();
     };
     if (b < nblk) {
@@ -2085,7 +2087,6 @@ __global__ __launch_bounds__(512) void moe_stack_kernel(StackArgs sa) {
           ua8[j] = g_row16_nt(gu, we + (size_t)(I + ia) * H + c8);
           ub8[j] = g_row16_nt(gu, we + (size_t)(I + ia + 1) * H + c8);
         }
-        if (first_blk) issue_down();
         float acc[4] = {0.f, 0.f, 0.f, 0.f};  // gate ia, up ia, gate ia + 1, up ia + 1
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -2120,6 +2121,7 @@ __global__ __launch_bounds__(512) void moe_stack_kernel(StackArgs sa) {
         }
         __syncthreads();
         if (tid < kFusedChunk) store_tagged(f_act + (size_t)u * I + i0 + tid, poison_if(bad, s_chunk[tid]), tag);
+        if (first_blk) issue_down();  // (after the gate/up rows are in, as in moe_fused_kernel)
         __syncthreads();
       };
       if (b < nblk) {
