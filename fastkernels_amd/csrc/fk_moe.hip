@@ -110,13 +110,18 @@ static size_t moe_ws_layout(int T, int K, int E, int I, int H, char* base, MoeWs
 // Routing tables (histogram, offsets, stable permutation, active experts).
 // Runs inside one workgroup of NWV wavefronts; `s_ids` holds the P clamped ids.
 // ---------------------------------------------------------------------------
+// Inclusive prefix sum over the wavefront: within each 16-lane row by DPP
+// row shifts (lanes shifted in from outside the row read 0), then each row
+// adds the totals of the rows below it (read from lanes 15, 31 and 47).
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int d = 1; d < kWave; d <<= 1) {
-    int o = __shfl_up(v, d, kWave);
-    if (lane >= d) v += o;
-  }
-  return v;
+  v += (int)dpp_u32<0x111>((uint32_t)v);  // row_shr:1
+  v += (int)dpp_u32<0x112>((uint32_t)v);  // row_shr:2
+  v += (int)dpp_u32<0x114>((uint32_t)v);  // row_shr:4
+  v += (int)dpp_u32<0x118>((uint32_t)v);  // row_shr:8
+  const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31),
+            r2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = lane >> 4;
+  return v + (row == 0 ? 0 : row == 1 ? r0 : row == 2 ? r0 + r1 : r0 + r1 + r2);
 }
 
 // Deterministic, parallel stable counting sort of the P pairs by expert.
@@ -2194,22 +2199,30 @@ __global__ __launch_bounds__(512) void moe_stack_kernel(StackArgs sa) {
 //
 // Workgroup (ub, tb) computes the logits of expert rows 8ub.. (one per
 // wavefront) for tokens tu*tb .. tu*tb + tu - 1 (tu from 2 to 32, the
-// smallest whose grid is co-resident), in tiles of 4 tokens: the row and the
-// first tile's tokens are loaded together, each later tile is fetched while
-// the previous one is computed, and every tile leaves as one tagged run per
-// token (the launch-tag protocol of the single-launch layer, same epoch
-// counter).  Workgroup b then polls the logits of tokens b, b + grid, .. and
-// computes each top-k with one wavefront (a selection is issue-bound, so the
-// tokens go to different CUs), writes the token's ids and weights, and
-// publishes the ids as tagged words.  Workgroup 0 polls the T*K ids,
-// advances the epoch (the ids of every token carry this launch's tag, so
-// every workgroup has written logits with it and has read the epoch) and
-// builds the routing tables for the expert stage.  Same arithmetic as
+// smallest whose grid is co-resident), in tiles of TU tokens (2 when a
+// workgroup has 2, else 4): the row and the first tile's tokens are loaded
+// together, each later tile is fetched while the previous one is computed,
+// and every tile leaves as one tagged run per token (the launch-tag protocol
+// of the single-launch layer, same epoch counter).
+// Up to 8 tokens, workgroup 0 then polls every logit and selects every
+// token itself (one token per wavefront).  From 9 tokens on, workgroup b
+// polls the logits of tokens b, b + grid, .. and computes each top-k with
+// one wavefront (a selection is issue-bound, so the tokens go to different
+// CUs), writes the token's ids and weights, and publishes the ids as tagged
+// words; workgroup 0 polls the T*K ids.  Either way workgroup 0 then
+// advances the epoch (the words it polled carry this launch's tag, so every
+// workgroup has written logits with it and has read the epoch) and builds
+// the routing tables for the expert stage.  Same arithmetic as
 // moe_router_kernel, so both give identical logits and ids.
 // ---------------------------------------------------------------------------
 constexpr int kTagRouterMaxTokens = 256;
 constexpr int kTagRouterTile = 4;       // tokens per tile of the logits loop
 constexpr int kTagRouterMaxPerWg = 32;  // most tokens per workgroup
+// Up to this many tokens workgroup 0 selects them all, one token per
+// wavefront.  (Two per wavefront, up to 16 tokens, measured no faster at
+// T = 16 than the selections spread over 16 workgroups: a selection is
+// VALU-bound, and eight wavefronts share one CU's four SIMDs.)
+constexpr int kTagRouterSelfTokens = kFusedWaves;
 constexpr int kMaskWords = kTagRouterMaxTokens / 32;
 static_assert(kFusedSelWords >= (size_t)kTagRouterMaxTokens * 8, "router selection region too small");
 static_assert(kFusedLogitWords >= (size_t)kTagRouterMaxTokens * kFusedMaxExperts, "router logit region too small");
@@ -2283,9 +2296,9 @@ __device__ void build_routing_tables_masks(const int* s_ids, const uint32_t* s_m
 // masks [E * ceil(T/32)] (sized by the host for this T).
 FK_TIMELINE_BUFFER(moe_router)
 
-template <bool BFW, bool BFX, bool BFN, bool TILED>
+template <bool BFW, bool BFX, bool BFN, bool TILED, int TU>
 __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
-  constexpr int TU = kTagRouterTile;
+  static_assert(TU <= kTagRouterTile && (!TILED || TU == kTagRouterTile), "tile of tokens");
   extern __shared__ int s_dyn_ids[];
   __shared__ int s_off[kFusedMaxExperts];
   __shared__ float s_chunk[TU][8];
@@ -2442,6 +2455,67 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   }
 
   FK_MARK(2);
+  const int nmw = (T + 31) >> 5;
+  int* s_ids = s_dyn_ids;
+  uint32_t* s_mask = reinterpret_cast<uint32_t*>(s_dyn_ids + T * K);  // [E][nmw]
+  if (T <= kTagRouterSelfTokens) {
+    // ---- few tokens: workgroup 0 selects every token itself ----------------
+    // (wavefront w: token w), with no hand-off of the ids through memory.  Its logits polls cover every workgroup's logits, so they also
+    // show that every workgroup has read the epoch.
+    if (blockIdx.x != 0) {
+      if (tid == 0 && s_fail)
+        __hip_atomic_fetch_or(&a.ws.tickets[kTicketError], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
+      FK_MARK(3);
+      FK_TIMELINE_COMMIT(moe_router, blockIdx.x);
+      return;
+    }
+    for (int i = tid; i < E * nmw; i += kFusedWaves * kWave) s_mask[i] = 0u;
+    constexpr int NJE = kFusedMaxExperts / kWave;
+    const int t = wave;
+    uint64_t w[NJE];
+    const uint64_t* srcs[NJE];
+#pragma unroll
+    for (int j = 0; j < NJE; ++j) {
+      const int ex = lane + kWave * j;
+      srcs[j] = t < T && ex < E ? a.ws.f_logits + (size_t)t * E + ex : nullptr;
+      w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
+    }
+    const bool ok = poll_tagged<NJE>(w, srcs, tag, wl.poll);
+    int id = 0;
+    float wt = 0.f;
+    if (t < T) {
+      float p[NJE];
+#pragma unroll
+      for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
+      topk_select_regs<NJE>(p, E, K, lane, id, wt);
+    }
+    __syncthreads();  // s_mask cleared
+    if (t < T && lane < K) {
+      // (after a failed wait: stale logits, ids kept in range, weights poisoned)
+      const int sid = ok ? id : min(max(id, 0), E - 1);
+      const float swt = poison_if(!ok, wt);
+      const int j = t * K + lane;
+      a.ids_out[j] = sid;
+      a.w_out[j] = swt;
+      a.ws.ids32[j] = sid;
+      a.ws.wts[j] = swt;
+      s_ids[j] = sid;
+      atomicOr(&s_mask[sid * nmw + (t >> 5)], 1u << (t & 31));
+    }
+    if (!ok) s_fail = 1;
+    __syncthreads();
+    if (tid == 0) {
+      if (!s_fail) store_coherent(&a.ws.tickets[kTicketEpoch], tag);
+      else __hip_atomic_fetch_or(&a.ws.tickets[kTicketError], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+    }
+    FK_MARK(4);
+    build_routing_tables_masks(s_ids, s_mask, T, K, E, a.ws, s_off);
+    FK_MARK(5);
+    FK_TIMELINE_COMMIT(moe_router, blockIdx.x);
+    return;
+  }
   // ---- top-k of tokens blockIdx.x, blockIdx.x + grid, .. ------------------
   if (wave == 0) {
     constexpr int NJE = kFusedMaxExperts / kWave;
@@ -2486,9 +2560,6 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   }
 
   // ---- workgroup 0: every token's ids, epoch, routing tables --------------
-  const int nmw = (T + 31) >> 5;
-  int* s_ids = s_dyn_ids;
-  uint32_t* s_mask = reinterpret_cast<uint32_t*>(s_dyn_ids + T * K);  // [E][nmw]
   for (int i = tid; i < E * nmw; i += kFusedWaves * kWave) s_mask[i] = 0u;
   __syncthreads();
   const int P = T * K;  // <= 2048: up to 4 ids per thread
@@ -2650,12 +2721,15 @@ static int launch_router_tagged_t(const RouterArgs& ra_in, hipStream_t stream) {
   };
   // (capacities are taken at the largest dynamic LDS, T = 256)
   constexpr size_t kMaxShm = ((size_t)kTagRouterMaxTokens * 8 + (size_t)kFusedMaxExperts * kMaskWords) * 4;
-  const int cap1 = resident_capacity(moe_router_tagged_kernel<BW, BX, BN, false>, 512, kMaxShm, cap_cache[0]);
+  const int cap1 = resident_capacity(moe_router_tagged_kernel<BW, BX, BN, false, kTagRouterTile>, 512, kMaxShm, cap_cache[0]);
   ra.tu = pick(cap1);
   int cap = cap1;
-  auto kernel = moe_router_tagged_kernel<BW, BX, BN, false>;
+  // (a two-token tile issues only two tokens' loads; its register budget is
+  // within the four-token tile's, so cap1 holds for it)
+  auto kernel = ra.tu <= 2 ? moe_router_tagged_kernel<BW, BX, BN, false, 2>
+                           : moe_router_tagged_kernel<BW, BX, BN, false, kTagRouterTile>;
   if (ra.tu > kTagRouterTile) {
-    kernel = moe_router_tagged_kernel<BW, BX, BN, true>;
+    kernel = moe_router_tagged_kernel<BW, BX, BN, true, kTagRouterTile>;
     cap = resident_capacity(kernel, 512, kMaxShm, cap_cache[1]);
     ra.tu = pick(cap);
   }
