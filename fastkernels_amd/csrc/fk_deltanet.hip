@@ -891,7 +891,37 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
           }
           // the lane holding the row's conv taps finishes the row
           if (lane == 2 * i + rr) {
-            if (row < C) {
+            if (row < C && a.KS == 4) {
+              // The model's kernel size: the window entries are known at
+              // compile time (the general form below selects every entry
+              // through run-time compares, ~800 instructions per row that
+              // every wavefront issues).  Same products in the same order.
+              float sq[4 + NT], wk[4];
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                sq[j] = raw_value<true>(cwin_raw[j]);
+                wk[j] = raw_value<true>(cwk_raw[j]);
+              }
+#pragma unroll
+              for (int t = 0; t < NT; ++t) sq[4 + t] = v[t];
+#pragma unroll
+              for (int t = 0; t < NT; ++t) {
+                if (t < T) {
+                  float cv = 0.f;
+#pragma unroll
+                  for (int j = 0; j < 4; ++j) cv = fmaf(wk[j], sq[t + 1 + j], cv);
+                  store_tagged(a.tw.mix + (size_t)t * C + row, silu(cv), tag);
+                }
+              }
+              // the next state: entries T .. T + 3
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                float e = sq[j];
+#pragma unroll
+                for (int tt = 1; tt <= NT; ++tt) e = T == tt ? sq[tt + j] : e;
+                reinterpret_cast<uint16_t*>(a.next_conv)[(size_t)row * 4 + j] = f32_to_bf16_bits(e);
+              }
+            } else if (row < C) {
               // causal conv + SiLU: token t's window is entries t + 1 .. t + KS
               // of [conv state (KS) | tokens]
               float st[8], wk[8];
