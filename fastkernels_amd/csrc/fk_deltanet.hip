@@ -564,12 +564,13 @@ struct StepTagWs {
   uint64_t* z;        // [T, V]
   uint64_t* norm;     // [T, V] gated values o * w * silu(z), before the RMSNorm scale
   uint64_t* started;  // [grid]
-  // Polling hints: a tile's (a head's) tag is stored once its outputs are
-  // stored.  From three tokens on, a consumer waits on the few hints of its
-  // producers before it reads their outputs, instead of spinning on every
-  // output word (which floods the memory system while the producers still
-  // stream).  The outputs still carry their own tags and are re-read until
-  // they do.
+  // Polling hints (from three tokens on; at one or two tokens the consumers
+  // poll the outputs directly and no tile hint is stored): a tile's (a
+  // head's) tag is stored once its outputs are stored.  A consumer waits on
+  // the few hints of its producers before it reads their outputs, instead of
+  // spinning on every output word (which floods the memory system while the
+  // producers still stream).  The outputs still carry their own tags and are
+  // re-read until they do.
   uint64_t* hint_tile;  // [kStepTilesPerWG * kStepMaxGrid]
   uint64_t* hint_head;  // [64 * kStepHeadWGs] per head workgroup
   uint64_t* hss;        // [kStepMaxTokens][kStepHssPitch] head quarters' sums of squares
@@ -634,7 +635,6 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   __shared__ float s_sc[kStepMaxTokens][2];  // decay, beta (head workgroups)
   __shared__ uint32_t s_wtag[kStepWaves];
   __shared__ int s_fail;
-  __shared__ int s_tcnt[kStepTilesPerWG];  // wavefronts done with each phase A tile (VALU path)
   __shared__ float s_abp[kStepMaxTokens][kStepWaves][2];  // head workgroups: a and b logit parts [token][wavefront]
   // (the wavefront index is uniform: kept in a scalar register, so that
   // addresses derived from it stay scalar too)
@@ -782,7 +782,6 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       }
     }
     if (tid == 0) s_fail = 0;
-    if (tid < kStepTilesPerWG) s_tcnt[tid] = 0;
     if (lane == 0) s_wtag[wave] = tag;
     __syncthreads();
     if (tid < T) {
@@ -867,6 +866,16 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         xk[t][p][0] = u0.x; xk[t][p][1] = u0.y; xk[t][p][2] = u0.z; xk[t][p][3] = u0.w;
         xk[t][p][4] = u1.x; xk[t][p][5] = u1.y; xk[t][p][6] = u1.z; xk[t][p][7] = u1.w;
       }
+    // Results of the row this lane finishes (lane 2i + rr: row rr of tile i),
+    // stored after the last tile: a store between two tiles' loads would be
+    // waited for with them (stores share the loads' in-order counter;
+    // -1 us at T = 1).  (A kernel size other than 4 takes the general form
+    // below, which stores at once.)
+    float o_val[NT];
+    uint32_t o_nc[2] = {0u, 0u};
+    int o_row = 0, o_kind = 0;  // 1: a qkv row (conv'd, and its next conv state), 2: a z row
+#pragma unroll
+    for (int t = 0; t < NT; ++t) o_val[t] = 0.f;
 #pragma unroll
     for (int i = 0; i < kStepTilesPerWG; ++i) {
       if (i < ntl) {  // uniform per workgroup
@@ -906,21 +915,24 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
               for (int t = 0; t < NT; ++t) sq[4 + t] = v[t];
 #pragma unroll
               for (int t = 0; t < NT; ++t) {
-                if (t < T) {
-                  float cv = 0.f;
+                float cv = 0.f;
 #pragma unroll
-                  for (int j = 0; j < 4; ++j) cv = fmaf(wk[j], sq[t + 1 + j], cv);
-                  store_tagged(a.tw.mix + (size_t)t * C + row, silu(cv), tag);
-                }
+                for (int j = 0; j < 4; ++j) cv = fmaf(wk[j], sq[t + 1 + j], cv);
+                o_val[t] = silu(cv);
               }
               // the next state: entries T .. T + 3
+              uint32_t nb[4];
 #pragma unroll
               for (int j = 0; j < 4; ++j) {
                 float e = sq[j];
 #pragma unroll
                 for (int tt = 1; tt <= NT; ++tt) e = T == tt ? sq[tt + j] : e;
-                reinterpret_cast<uint16_t*>(a.next_conv)[(size_t)row * 4 + j] = f32_to_bf16_bits(e);
+                nb[j] = f32_to_bf16_bits(e);
               }
+              o_nc[0] = nb[0] | (nb[1] << 16);
+              o_nc[1] = nb[2] | (nb[3] << 16);
+              o_row = row;
+              o_kind = 1;
             } else if (row < C) {
               // causal conv + SiLU: token t's window is entries t + 1 .. t + KS
               // of [conv state (KS) | tokens]
@@ -953,18 +965,29 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
                 if (j < a.KS) reinterpret_cast<uint16_t*>(a.next_conv)[(size_t)row * a.KS + j] = f32_to_bf16_bits(seq(T + j));
             } else {
 #pragma unroll
-              for (int t = 0; t < NT; ++t)
-                if (t < T) store_tagged(a.tw.z + (size_t)t * V + (row - C), v[t], tag);
+              for (int t = 0; t < NT; ++t) o_val[t] = v[t];
+              o_row = row;
+              o_kind = 2;
             }
           }
         }
-        // the last wavefront done with tile i stores its hint (every
-        // wavefront's stores of the tile are issued before its count)
-        if (lane == 0 && __hip_atomic_fetch_add(&s_tcnt[i], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
-                             kStepWaves - 1)
-          store_tagged(a.tw.hint_tile + b + i * G, 0.f, tag);
       }
       if (i + kStepTilesAhead < kStepTilesPerWG) issue_tile(i + kStepTilesAhead);
+    }
+    // (no tile hints: at T <= 2 the heads poll their inputs directly)
+    if (o_kind == 1) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        if (t < T) store_tagged(a.tw.mix + (size_t)t * C + o_row, o_val[t], tag);
+      uint16_t* nc = reinterpret_cast<uint16_t*>(a.next_conv) + (size_t)o_row * 4;
+      nc[0] = (uint16_t)o_nc[0];
+      nc[1] = (uint16_t)(o_nc[0] >> 16);
+      nc[2] = (uint16_t)o_nc[1];
+      nc[3] = (uint16_t)(o_nc[1] >> 16);
+    } else if (o_kind == 2) {
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+        if (t < T) store_tagged(a.tw.z + (size_t)t * V + (o_row - C), o_val[t], tag);
     }
     __syncthreads();  // phases B and C reuse the dynamic LDS
   } else {
