@@ -758,7 +758,6 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     if (i < kStepTilesAhead) issue_tile(i);
 
 
-  FK_MARK(1);
   // ---- stage the normalised tokens -----------------------------------------
   const WaitLimits wl = hdr.limits();
   const uint32_t tag = wl.tag, plim = wl.poll;
@@ -832,6 +831,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     }
     __syncthreads();
   }
+  FK_MARK(1);
 
   // Small operands of later phases, fetched now so that no phase waits on a
   // dependent global load: the head's norm weight and decay parameters.

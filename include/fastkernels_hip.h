@@ -201,7 +201,9 @@ size_t fk_moe_stack_workspace_bytes(int num_layers, int num_experts, int top_k, 
  * fk_moe_layer's (fk_workspace_status); zero-fill it once.
  * No counterpart in the reference: its 40-layer stack
  * is 40 calls of triton_qwen36_batched_moe_layer_decode
- * (qwen36_expert.py:1312-1350), which this replaces for T = 1. */
+ * (qwen36_expert.py:1312-1350), which this replaces for T = 1.  On MI355X
+ * it measures slower than one fk_moe_layer launch per layer (every
+ * workgroup reads each layer's outputs before the next layer starts). */
 int fk_moe_stack_decode(const void* hidden, int hidden_dtype, const fk_moe_stack_layer* layers,
                         int num_layers, int bias_dtype, int hidden_size, int intermediate,
                         int num_experts, int top_k, float eps, float norm_offset,
