@@ -767,17 +767,35 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   // token and the sum of squares reduces in a fixed order.
   uint16_t* s_xb = reinterpret_cast<uint16_t*>(s_dyn);
   {
+    if constexpr (XCH == 4) {
+      // the four chunks' sums of squares in one transposed reduction (lane
+      // 16q holds chunk q's sum)
+      float p4[4];
 #pragma unroll
-    for (int q = 0; q < XCH; ++q) {
-      const int idx8 = tid + q * 512;
-      if (idx8 < nchunk) {  // uniform per wavefront
+      for (int q = 0; q < 4; ++q) {
         float xv[8];
         raw8_to_f32<BFX>(xr[q], xv);
         float p = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) p = fmaf(xv[e], xv[e], p);
-        p = wave_sum(p);
-        if (lane == 0) s_part[idx8 >> cpt_sh][(idx8 & (cpt - 1)) >> 6] = p;
+        p4[q] = tid + q * 512 < nchunk ? p : 0.f;
+      }
+      const float ps = rows4_sum(p4);
+      const int base = (tid & ~63) + (lane >> 4) * 512;
+      if ((lane & 15) == 0 && base < nchunk) s_part[base >> cpt_sh][(base & (cpt - 1)) >> 6] = ps;
+    } else {
+#pragma unroll
+      for (int q = 0; q < XCH; ++q) {
+        const int idx8 = tid + q * 512;
+        if (idx8 < nchunk) {  // uniform per wavefront
+          float xv[8];
+          raw8_to_f32<BFX>(xr[q], xv);
+          float p = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) p = fmaf(xv[e], xv[e], p);
+          p = wave_sum(p);
+          if (lane == 0) s_part[idx8 >> cpt_sh][(idx8 & (cpt - 1)) >> 6] = p;
+        }
       }
     }
     if (tid == 0) s_fail = 0;
@@ -790,6 +808,11 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     }
     if (tid == 0) store_tagged(a.tw.started + b, 0.f, s_wtag[kStepWaves - 1]);
     __syncthreads();
+    // (four chunks: the head workgroups' a and b logit parts of all four in
+    // one transposed reduction, lane 8i holding part i = 2 q + (a: 0, b: 1))
+    float dab[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dab[i] = 0.f;
 #pragma unroll
     for (int q = 0; q < XCH; ++q) {
       const int idx8 = tid + q * 512;
@@ -800,7 +823,18 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         raw8_to_f32<true>(nr[q], nv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) y[e] = xv[e] * s_rs[t] * (1.0f + nv[e]);
-        if (is_head) {  // this chunk's share of the a and b logits of token t
+        if (XCH == 4 && is_head) {
+          float wa[8], wb[8], da = 0.f, db = 0.f;
+          raw8_to_f32<true>(war, wa);
+          raw8_to_f32<true>(wbr, wb);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            da = fmaf(wa[e], y[e], da);
+            db = fmaf(wb[e], y[e], db);
+          }
+          dab[(2 * q) & 7] = da;
+          dab[(2 * q + 1) & 7] = db;
+        } else if (is_head) {  // this chunk's share of the a and b logits of token t
           float wa[8], wb[8], da = 0.f, db = 0.f;
           raw8_to_f32<true>(war, wa);
           raw8_to_f32<true>(wbr, wb);
@@ -828,6 +862,11 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
           *reinterpret_cast<u32x4*>(s_xb + (size_t)bcol_slot(c, 2 * t + 1, NCP) * 8) = vl;
         }
       }
+    }
+    if (XCH == 4 && is_head) {
+      const float ab = rows8_sum(dab);
+      const int i = lane >> 3, base = (tid & ~63) + (i >> 1) * 512;
+      if ((lane & 7) == 0 && base < nchunk) s_abp[base >> cpt_sh][(base & (cpt - 1)) >> 6][i & 1] = ab;
     }
     __syncthreads();
   }
