@@ -684,8 +684,21 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     war = load_raw8<true>(a.w[2], o);
     wbr = load_raw8<true>(a.w[3], o);
   }
+  // Small operands of phase B, fetched with the tokens, ahead of the weight
+  // tiles: the head's norm weight and decay parameters, and (head
+  // workgroups) the head quarter's state: thread (jl, g) holds rows
+  // 8g .. 8g + 7 of value column jcol = quarter * 32 + jl.  Issued after the
+  // staging instead, they sat between the tiles' loads, and the waits for
+  // the tiles (counted over both paths) waited for them too.
+  uint32_t lnw1[1], alog[1], dtb1[1];
+  gather_raw<true>(a.lnw, quarter * kStepQCols + (lane & (kStepQCols - 1)), 0, 1, lnw1);
+  gather_raw<true>(a.a_log, is_head ? head : 0, 0, 1, alog);
+  gather_raw<true>(a.dt_bias, is_head ? head : 0, 0, 1, dtb1);
+  const int sjl = tid >> 4, sgr = tid & 15, jcol = quarter * kStepQCols + sjl;
+  uint32_t S_raw[8];
+  if (is_head) gather_raw<false>(a.rec_state, ((size_t)head * kStepD + (size_t)sgr * 8) * kStepD + jcol, kStepD, 8, S_raw);
   // (kept ahead of the weight tiles: the scheduler would otherwise sink the
-  // a/b loads towards their use, behind the tiles, and the staging's wait
+  // a/b and state loads towards their use, behind the tiles, and the waits
   // for them would then wait for the tiles too)
   __builtin_amdgcn_sched_barrier(0);
 
@@ -871,22 +884,6 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     __syncthreads();
   }
   FK_MARK(1);
-
-  // Small operands of later phases, fetched now so that no phase waits on a
-  // dependent global load: the head's norm weight and decay parameters.
-  uint32_t lnw1[1], alog[1], dtb1[1];
-  gather_raw<true>(a.lnw, quarter * kStepQCols + (lane & (kStepQCols - 1)), 0, 1, lnw1);
-  gather_raw<true>(a.a_log, is_head ? head : 0, 0, 1, alog);
-  gather_raw<true>(a.dt_bias, is_head ? head : 0, 0, 1, dtb1);
-
-  // Head workgroups: prefetch the state.  Thread (jl, g) holds rows
-  // 8g .. 8g + 7 of value column jcol = quarter * 32 + jl.  Issued after the
-  // weight tiles: the waits below are counted over every path, so head-only
-  // loads in front of them would make the other workgroups wait for more of
-  // their weight tiles.
-  const int sjl = tid >> 4, sgr = tid & 15, jcol = quarter * kStepQCols + sjl;
-  uint32_t S_raw[8];
-  if (is_head) gather_raw<false>(a.rec_state, ((size_t)head * kStepD + (size_t)sgr * 8) * kStepD + jcol, kStepD, 8, S_raw);
 
   if constexpr (VALU_A) {
     // ---- phase A (T <= 2): whole-row dot products on the VALU --------------
