@@ -620,9 +620,10 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
 // heads of 256, bf16 weights).  One 512-thread workgroup per CU, grid capped
 // at the co-resident capacity; phases joined by launch-tagged words (value +
 // 32-bit launch tag per 8-byte word, polled by the consumers, as in the MoE
-// layer and the DeltaNet step).  The attention units first wait on one hint
-// word per phase A workgroup (their inputs come from most of the grid while
-// it still streams); the later consumers poll their inputs directly:
+// layer and the DeltaNet step).  Every consumer polls its inputs directly
+// (waiting on hint words of its producers first cost a memory round trip
+// more; the attention units' first round is in flight while they compute
+// the RoPE angles):
 //   A   projections: the R rows of [Wq | Wk | Wv] split evenly over the grid
 //       (36 per workgroup at the model shape, 4 or 5 per wavefront), each a
 //       whole-row dot product with the tokens x * (1 + w) staged in LDS,
@@ -677,7 +678,6 @@ static_assert(kAsMaxTokens * kAsMaxH * 4 <= kAsMaxLds, "phase A's tokens must fi
 struct AttnTagWs {
   uint32_t* tickets;  // [16] workspace header (epoch, poll bound, error word)
   uint64_t* started;  // [kAsMaxGrid]
-  uint64_t* hint_a;   // [kAsMaxGrid] phase A, per workgroup
   uint64_t* qkv;      // [T][R] projected (q_h | gate_h) pairs, k, v
   uint64_t* part;     // [T][heads][kAsMaxChunks][hd + 2] chunk (max, sum, weighted values)
   uint64_t* gated;    // [T][K]
@@ -954,11 +954,8 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
     const int ri = lane >> 3;
     if ((lane & 7) == 0 && ri < rn) store_tagged(a.tw.qkv + (size_t)t * R + rlo + ri, v, tag);
   }
-  lds_barrier();  // every wavefront's outputs are stored before the hint; phase B reuses the LDS
-  if (tid == 0) {
-    store_tagged(a.tw.hint_a + b, 0.f, tag);
-    store_tagged(a.tw.started + b, (float)start, tag);  // (after the epoch and position loads)
-  }
+  lds_barrier();  // phase B reuses the LDS
+  if (tid == 0) store_tagged(a.tw.started + b, (float)start, tag);  // (after the epoch and position loads)
   FK_MARK(2);
 
 
@@ -973,24 +970,21 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
     float* s_acc = s_kt;                           // [waves][Gu][hd] after the last tile
     // own positions of the chunk: o_lo .. p_hi - 1, tokens u_lo ..
     const int o_lo = max(p_lo, start), n_own = p_hi > o_lo ? p_hi - o_lo : 0, u_lo = o_lo - start;
-    {
-      // hints of the phase A workgroups holding the q rows of heads hb ..
-      // hb + Gu - 1 and the k and v rows of kv head aj
-      const int q_lo = as_wg_of_row(2 * hd * hb, R, G), q_hi = as_wg_of_row(2 * hd * (hb + Gu) - 1, R, G);
-      const int k_lo = as_wg_of_row(Rq + aj * hd, R, G), k_hi = as_wg_of_row(Rq + aj * hd + hd - 1, R, G);
-      const int v_lo = as_wg_of_row(Rq + Rk + aj * hd, R, G), v_hi = as_wg_of_row(Rq + Rk + aj * hd + hd - 1, R, G);
-      const int nq = q_hi - q_lo + 1, nk = k_hi - k_lo + 1, nv = v_hi - v_lo + 1;
-      uint64_t hw[2];
-      const uint64_t* hs[2];
+    // token at's queries of heads hb .. (word e = g * hd + d), the own
+    // tokens' k and v (word e = s * hd + d), polled directly (their first
+    // round of loads in flight while the RoPE angles are computed)
+    uint64_t w[6];
+    const uint64_t* srcs[6];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int e = tid + i * kAsThreads;
-        const int w = e < nq ? q_lo + e : e < nq + nk ? k_lo + e - nq : e < nq + nk + nv ? v_lo + e - nq - nk : -1;
-        hs[i] = w >= 0 ? a.tw.hint_a + w : nullptr;
-        hw[i] = hs[i] ? load_tagged(hs[i]) : 0ull;
-      }
-      if (!poll_tagged<2>(hw, hs, tag, plim)) s_fail = 1;
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + i * kAsThreads, s = e >> hd_sh, d = e & (hd - 1);
+      srcs[i] = e < Gu * hd ? a.tw.qkv + (size_t)at * R + (size_t)(hb + s) * 2 * hd + d : nullptr;
+      const uint64_t* kr = a.tw.qkv + (size_t)(u_lo + s) * R + Rq + (size_t)aj * hd + d;
+      srcs[2 + i] = s < n_own ? kr : nullptr;
+      srcs[4 + i] = s < n_own ? kr + Rk : nullptr;
     }
+#pragma unroll
+    for (int i = 0; i < 6; ++i) w[i] = srcs[i] ? load_tagged(srcs[i]) : 0ull;
     // RoPE angles, once per position: slot 0 the queries' (apos), slot
     // 1 + s own key s's (o_lo + s); entry i of a slot is pair i's (cos, sin)
     {
@@ -1006,31 +1000,14 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
         }
       }
     }
-    lds_barrier();
-    {
-      // token at's queries of heads hb .. (word e = g * hd + d), the own
-      // tokens' k and v (word e = s * hd + d)
-      uint64_t w[6];
-      const uint64_t* srcs[6];
+    if (!poll_tagged<6>(w, srcs, tag, plim)) s_fail = 1;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int e = tid + i * kAsThreads, s = e >> hd_sh, d = e & (hd - 1);
-        srcs[i] = e < Gu * hd ? a.tw.qkv + (size_t)at * R + (size_t)(hb + s) * 2 * hd + d : nullptr;
-        const uint64_t* kr = a.tw.qkv + (size_t)(u_lo + s) * R + Rq + (size_t)aj * hd + d;
-        srcs[2 + i] = s < n_own ? kr : nullptr;
-        srcs[4 + i] = s < n_own ? kr + Rk : nullptr;
-      }
-#pragma unroll
-      for (int i = 0; i < 6; ++i) w[i] = srcs[i] ? load_tagged(srcs[i]) : 0ull;
-      if (!poll_tagged<6>(w, srcs, tag, plim)) s_fail = 1;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int e = tid + i * kAsThreads;
-        if (srcs[i]) s_q[e] = value_of(w[i]);
-        if (srcs[2 + i]) {
-          s_kr[e] = value_of(w[2 + i]);
-          s_vn[e] = value_of(w[4 + i]);
-        }
+    for (int i = 0; i < 2; ++i) {
+      const int e = tid + i * kAsThreads;
+      if (srcs[i]) s_q[e] = value_of(w[i]);
+      if (srcs[2 + i]) {
+        s_kr[e] = value_of(w[2 + i]);
+        s_vn[e] = value_of(w[4 + i]);
       }
     }
     lds_barrier();
@@ -1194,9 +1171,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
   // ---- phase M: merge unit (mt, mh, mds) -----------------------------------
   if (is_m) {
     const int mu = b - m0, mt = mu / (heads * nds), mh = (mu / nds) % heads, mds = mu % nds;
-    // (the partials are polled directly: the attention units are done
-    // streaming by now, and a wait on their hint words first would cost a
-    // memory round trip more)
+    // (the partials are polled directly, as every input of this kernel)
     // thread (wavefront cg, lane dd): dim 64 mds + dd of chunks cg, cg + 8, ..;
     // wavefront 0 also the chunk statistics (lane c) and the gate (lane dd)
     const uint64_t* pbase = a.tw.part + ((size_t)mt * heads + mh) * kAsMaxChunks * (hd + 2);
@@ -1378,7 +1353,6 @@ static size_t attn_ws_layout(int T, int heads, int kvh, int hd, char* base, Attn
   auto words = [&](size_t n) { return reinterpret_cast<uint64_t*>(take(one ? n * 8 : 0)); };
   ws->tw.tickets = reinterpret_cast<uint32_t*>(take(16 * sizeof(uint32_t)));
   ws->tw.started = words(kAsMaxGrid);
-  ws->tw.hint_a = words(kAsMaxGrid);
   ws->tw.qkv = words((size_t)T * R);
   ws->tw.part = words((size_t)T * heads * kAsMaxChunks * (hd + 2));
   ws->tw.gated = words((size_t)T * K);

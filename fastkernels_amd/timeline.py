@@ -76,7 +76,7 @@ MARKERS = {
         [
             "workgroup start",
             "weight rows issued",
-            "A: projection rows stored (hint, started)",
+            "A: projection rows stored (started)",
             "B: attention inputs read",
             "B: chunk partial stored",
             "M: gated values stored",
