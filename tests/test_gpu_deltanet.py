@@ -165,6 +165,28 @@ def test_step_single_launch_matches_oracle(device, real_dn, tokens):
     torch.testing.assert_close(plan.next_conv_state.cpu().float(), conv.float(), atol=1e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("tokens", [1, 2, 5])
+def test_step_single_launch_other_conv_kernel_size(device, real_dn, tokens):
+    # A conv kernel size other than the model's 4 (here 3) takes the general
+    # causal-conv epilogue of the single launch: at T <= 2 the window entries
+    # selected through run-time compares, above from the LDS sequence.
+    from fastkernels_amd.plan import DeltaNetStepPlan
+
+    dn = dict(real_dn)
+    dn["conv_state"] = real_dn["conv_state"][:, :3].contiguous()
+    dn["conv1d_weight"] = real_dn["conv1d_weight"][..., :3].contiguous()
+    x = wl.make_hidden(tokens, REAL.hidden_size, seed=90 + tokens)
+    plan = DeltaNetStepPlan(_to(dn, device), tokens, REAL)
+    plan.hidden.copy_(x.to(device))
+    plan.run()
+    plan.check_device()
+    update, conv, state = oracle.deltanet_update(x, dn["conv_state"], dn["recurrent_state"], dn, **_dims(REAL))
+    assert plan.next_conv_state.shape[1] == 3
+    torch.testing.assert_close(plan.update.cpu(), update, **tol(torch.bfloat16))
+    torch.testing.assert_close(plan.next_recurrent_state.cpu(), state, atol=1e-3, rtol=1e-3)
+    torch.testing.assert_close(plan.next_conv_state.cpu().float(), conv.float(), atol=1e-2, rtol=1e-2)
+
+
 @pytest.mark.parametrize("tokens", [1, 2, 5, 8])
 def test_step_single_launch_matches_staged_kernels(device, real_dn, tokens):
     # Same step through the staged operator kernels (fp32 VALU GEMVs).
