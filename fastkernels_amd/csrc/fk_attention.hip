@@ -631,8 +631,8 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
 //   B   attention unit (t, j, hs, c), one per workgroup at the model shape:
 //       query heads hs * 4 .. + 4 of kv head j for token t over chunk c of
 //       its positions 0 .. start + t (split evenly over nch chunks at run
-//       time; the chunk's first cached rows are fetched before phase A's
-//       weight rows and staged in LDS after it).  RoPE angles are computed
+//       time; the chunk's first cached rows are fetched with the unit's
+//       inputs and staged in LDS after the norms).  RoPE angles are computed
 //       once per position; wavefronts 0-3 normalise and rotate the queries,
 //       4-7 the step's own keys, recomputed from k (its own values come from
 //       v: no dependence on another workgroup's cache write); 8 wavefronts
@@ -847,8 +847,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) wt[i][j] = load_raw8_stream<true>(wp, (size_t)min(lane + kWave * j, nchk - 1) * 8);
   }
-  // the unit's first tile of cached rows (clamped in range, so every
-  // workgroup issues it), staged in LDS after phase A
+  // the unit's chunk (its first tile of cached rows is issued in phase B)
   asm volatile("" : "+v"(start_ld));  // (the position's wait: here, not at its load)
   const int start = start_ld;
   const bool bad_pos = start < 0 || start + T > a.max_pos;
@@ -878,7 +877,6 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
       if ((u >> qsh) < 2 * kAsTile) *reinterpret_cast<float4*>(s_kt + 4 * u) = kvr[i].f4();
     }
   };
-  issue_tile(p_lo);
   FK_MARK(1);
 
   // ---- stage the tokens: s_x[t][c] = x * (1 + w), s_rs[t] -----------------
@@ -985,6 +983,11 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < 6; ++i) w[i] = srcs[i] ? load_tagged(srcs[i]) : 0ull;
+    // The unit's first tile of cached rows, behind the first round of its
+    // inputs and staged after the norms and RoPE.  (Issued behind the phase
+    // A weight rows instead, it was waited for with them: the attention
+    // units then ended phase A last, 1.4 us later at ctx 1024.)
+    issue_tile(p_lo);
     // RoPE angles, once per position: slot 0 the queries' (apos), slot
     // 1 + s own key s's (o_lo + s); entry i of a slot is pair i's (cos, sin)
     {
