@@ -1036,6 +1036,14 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   const int pitch = 2 * H + 16;
   char* s_tile = s_dyn + (size_t)H * NCP * 2;
   {
+    // the tokens' B operands of this wavefront's K range, the same for every
+    // tile: read from LDS once (the staging ends with a barrier)
+    u32x4 bvr[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int c = (wave * kw + s * 32 + g4 * 8) >> 3;
+      bvr[s] = s < ks && n < NC ? *reinterpret_cast<const u32x4*>(s_xb + (size_t)bcol_slot(c, n, NCP) * 8) : u32x4{0, 0, 0, 0};
+    }
     f32x4_t acc[kStepTilesPerWG];
 #pragma unroll
     for (int i = 0; i < kStepTilesPerWG; ++i) {
@@ -1053,10 +1061,8 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
           if (s < ks) {
             const int k = wave * kw + s * 32 + g4 * 8;
             const u32x4 wv = *reinterpret_cast<const u32x4*>(s_tile + n * pitch + k * 2);
-            const int c = k >> 3;
-            const u32x4 bv = n < NC ? *reinterpret_cast<const u32x4*>(s_xb + (size_t)bcol_slot(c, n, NCP) * 8) : u32x4{0, 0, 0, 0};
             acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wv),
-                                                             __builtin_bit_cast(bf16x8_t, bv), acc[i], 0, 0, 0);
+                                                             __builtin_bit_cast(bf16x8_t, bvr[s]), acc[i], 0, 0, 0);
           }
         }
         __syncthreads();
