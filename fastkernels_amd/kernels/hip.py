@@ -195,7 +195,8 @@ def hip_qwen36_moe_align(topk_ids: Any, num_experts: int, topk_weights: Any | No
     `perm[p]` is the flat pair index `t*K + k` at permuted position `p`, with
     pairs sorted stably by (expert, token, slot); `inverse` is its inverse and
     `offsets` the exclusive prefix sum of `counts`.  The reference has no
-    permutation; `counts` equals `triton_expert_histogram`.
+    stable token permutation of its own (its expert kernels stream the
+    weights per (token, slot)); `counts` equals `triton_expert_histogram`.
     """
 
     _require_lib()
