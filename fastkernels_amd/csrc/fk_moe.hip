@@ -1345,66 +1345,68 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   FK_MARK(0);  // (timeline markers: diagnostic builds only)
 
   // ---------------- P1: router rows, shared gate/up, shared gate -----------
-  // Units of 8 items, one per wavefront: router rows 8u.. (u < nrb), shared
-  // intermediates 8(u - nrb).. (u < nrb + nsb), then the shared gate.  A
-  // unit's results go through LDS and leave as contiguous tagged runs.
-  const int nrb = (E + 7) / 8, nsb = I / 8, nunits = nrb + nsb + 1;
-  for (int unit = b; unit < nunits; unit += G) {
-    if (unit < nrb) {
-      const int e = unit * 8 + wave;
-      float mine = 0.f;
-      if (e < E) {
-        // All loads of the row (weights, token 0, the bf16 norm weight) are
-        // issued before the first use: indices are clamped in range and
-        // out-of-range chunks are zeroed afterwards, so there is no branch
-        // between them (a load whose dtype is tested at run time would wait
-        // for every load before it).
-        Raw8<true> wr[4], nr[4];
-        Raw8<BFX> xr[4];  // the token rides with the weights
+  // Item q (router rows 0..E-1, shared intermediates E..E+I-1, then the
+  // shared gate) goes to wavefront q / G of workgroup q % G: every workgroup
+  // holds one router row (its wavefront 0 at E <= G), so the logits land one
+  // row's latency after launch instead of behind rows queued on a few CUs.
+  // Each wavefront publishes its own result as one tagged word.
+  const int nitems = E + I + 1;
+  for (int q = q0; q < nitems; q += NW) {
+    if (q < E) {
+      const int e = q;
+      // All loads of the row (weights, token 0, the bf16 norm weight) are
+      // issued before the first use: indices are clamped in range and
+      // out-of-range chunks are zeroed afterwards, so there is no branch
+      // between them (a load whose dtype is tested at run time would wait
+      // for every load before it).
+      Raw8<true> wr[4], nr[4];
+      Raw8<BFX> xr[4];  // the token rides with the weights
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int cc = min(lane + kWave * j, nch - 1);
-          wr[j] = load_raw8<true>(a.W, (size_t)e * H + (size_t)cc * 8);
-          xr[j] = load_raw8<BFX>(a.x, (size_t)cc * 8);
-          nr[j] = load_raw8<true>(a.nw, (size_t)cc * 8);
-        }
-        {
-          const WaitLimits wl = wait_limits(a.ws.tickets, kTicketEpoch);
-          tag = wl.tag;
-          plim = wl.poll;
-        }
-        have_tag = true;
-        float wn[4][8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int c = lane + kWave * j;
-          float w8[8], n8[8];
-          raw8_to_f32<true>(nr[j], n8);
-          raw8_to_f32<true>(wr[j], w8);
-#pragma unroll
-          for (int qq = 0; qq < 8; ++qq) wn[j][qq] = c < nch ? w8[qq] * (a.off + n8[qq]) : 0.f;
-        }
-        const float bias = a.bias ? load_scalar(a.bias, a.bias_dt, e) : 0.f;
-        float ss = 0.f, d = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bool in = lane + kWave * j < nch;
-          float x8[8];
-          raw8_to_f32<BFX>(xr[j], x8);
-#pragma unroll
-          for (int qq = 0; qq < 8; ++qq) {
-            const float xv = in ? x8[qq] : 0.f;
-            ss = fmaf(xv, xv, ss);
-            d = fmaf(xv, wn[j][qq], d);
-          }
-        }
-        ss = wave_sum(ss);
-        d = wave_sum(d);
-        mine = d * rsqrtf(ss / (float)H + a.eps) + bias;
+      for (int j = 0; j < 4; ++j) {
+        const int cc = min(lane + kWave * j, nch - 1);
+        wr[j] = load_raw8<true>(a.W, (size_t)e * H + (size_t)cc * 8);
+        xr[j] = load_raw8<BFX>(a.x, (size_t)cc * 8);
+        nr[j] = load_raw8<true>(a.nw, (size_t)cc * 8);
       }
-      if (lane < T) s_chunk[lane][wave] = mine;
-    } else if (unit < nrb + nsb) {
-      const int i = (unit - nrb) * 8 + wave;
+      {
+        const WaitLimits wl = wait_limits(a.ws.tickets, kTicketEpoch);
+        tag = wl.tag;
+        plim = wl.poll;
+      }
+      have_tag = true;
+      float wn[4][8];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = lane + kWave * j;
+        float w8[8], n8[8];
+        raw8_to_f32<true>(nr[j], n8);
+        raw8_to_f32<true>(wr[j], w8);
+#pragma unroll
+        for (int qq = 0; qq < 8; ++qq) wn[j][qq] = c < nch ? w8[qq] * (a.off + n8[qq]) : 0.f;
+      }
+      const float bias = a.bias ? load_scalar(a.bias, a.bias_dt, e) : 0.f;
+      float ss = 0.f, d = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool in = lane + kWave * j < nch;
+        float x8[8];
+        raw8_to_f32<BFX>(xr[j], x8);
+#pragma unroll
+        for (int qq = 0; qq < 8; ++qq) {
+          const float xv = in ? x8[qq] : 0.f;
+          ss = fmaf(xv, xv, ss);
+          d = fmaf(xv, wn[j][qq], d);
+        }
+      }
+      ss = wave_sum(ss);
+      d = wave_sum(d);
+      const float v = d * rsqrtf(ss / (float)H + a.eps) + bias;
+      if (lane == 0) {
+        a.logits[e] = v;
+        store_tagged(a.ws.f_logits + e, v, tag);
+      }
+    } else if (q < E + I) {
+      const int i = q - E;
       Raw8<true> wg[4], wu[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -1420,9 +1422,11 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
         plim = wl.poll;
       }
       have_tag = true;
+      // (lane 0 writes the value to its wavefront's LDS slot and reads it back)
       fused_gateup_item<BFX>(wg, wu, a.x, H, lane, T, nullptr, &s_chunk[0][wave]);
-    } else if (wave == 0) {
-      // Shared-expert gate of every token: one row like the router's, loads
+      if (lane == 0) store_tagged(a.ws.f_act + (size_t)P * I + i, s_chunk[0][wave], tag);
+    } else {
+      // Shared-expert gate of the token: one row like the router's, loads
       // issued together as there.
       // (the gate weight is bf16 here; a NULL gate reads the norm weight, a
       // valid address, and the products are dropped)
@@ -1458,25 +1462,8 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
         for (int qq = 0; qq < 8; ++qq) d = fmaf(x8[qq], g8[j][qq], d);
       }
       d = wave_sum(d);
-      if (lane == 0) s_chunk[0][0] = f.sg ? sigmoid(d) : 1.f;
+      if (lane == 0) store_tagged(a.ws.f_sgate, f.sg ? sigmoid(d) : 1.f, tag);
     }
-    __syncthreads();
-    if (tid < 8 * T) {
-      const int t = tid >> 3, l = tid & 7;
-      const float v = s_chunk[t][l];
-      if (unit < nrb) {
-        const int e = unit * 8 + l;
-        if (e < E) {
-          a.logits[(size_t)t * E + e] = v;
-          store_tagged(a.ws.f_logits + (size_t)t * E + e, v, tag);
-        }
-      } else if (unit < nrb + nsb) {
-        store_tagged(a.ws.f_act + (size_t)(P + t) * I + (unit - nrb) * 8 + l, v, tag);
-      } else if (l == 0) {
-        store_tagged(a.ws.f_sgate + t, v, tag);
-      }
-    }
-    __syncthreads();
   }
   FK_MARK(1);
   if (!have_tag) {

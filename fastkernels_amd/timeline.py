@@ -118,6 +118,7 @@ def parse_args(argv=None) -> argparse.Namespace:
     p.add_argument("--zipf", action="store_true", help="router: the config-2 Zipf router bias")
     p.add_argument("--context", type=int, default=1024, help="attention: cached positions before the step")
     p.add_argument("--layers", type=int, default=8, help="stack: layers per run")
+    p.add_argument("--dump", default=None, help="also write every workgroup's marker times (µs) to this CSV file")
     return p.parse_args(argv)
 
 
@@ -234,6 +235,13 @@ def main(argv=None) -> int:
         v = [(w[k] - t0) / 100.0 for w in wgs if w[k] != 0]
         if v:
             print(f"| {k}: {name} | {len(v)} | {min(v):.2f} | {sum(v) / len(v):.2f} | {max(v):.2f} |")
+    if args.dump:
+        with open(args.dump, "w") as fh:
+            fh.write("workgroup," + ",".join(f"m{k}" for k in range(len(names))) + "\n")
+            for i in range(rows):
+                w = buf[i * marks : (i + 1) * marks]
+                if w[0] != 0:
+                    fh.write(f"{i}," + ",".join(f"{(w[k] - t0) / 100.0:.2f}" if w[k] else "" for k in range(len(names))) + "\n")
     return 0
 
 
