@@ -22,7 +22,9 @@ and replayed; the markers are cleared and the graph replayed once more, so the
 recorded step is the last of 16 that follow one another on the stream.  The
 report gives, per marker, the number of workgroups that passed it and the
 min / mean / max time after the earliest workgroup start, in microseconds, as
-a markdown table.  The markers perturb the code a little (a few registers and
+a markdown table; ``--dump PATH`` also writes every workgroup's marker
+times to a CSV file (one row per workgroup), for spreads by role.  The
+markers perturb the code a little (a few registers and
 stores): the totals read a few tenths of a microsecond above the product
 build's.
 """
