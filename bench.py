@@ -185,7 +185,7 @@ def main() -> int:
     import torch
 
     from fastkernels_amd import workloads as wl
-    from fastkernels_amd.plan import AttentionStepPlan, DeltaNetStepPlan, MoeLayerPlan, MoeStackPlan
+    from fastkernels_amd.plan import AttentionStepPlan, DeltaNetStepPlan, MoeLayerPlan
     from fastkernels_amd.spec import qwen36_35b_a3b_spec
 
     if not torch.cuda.is_available():
@@ -449,38 +449,6 @@ def main() -> int:
             "hbm_frac": round(nbytes / (us_layer * 1e-6) / (HBM_PEAK_GBS * 1e9), 4),
             "launches_per_step": layers,
         }
-        if tokens == 1 and layers <= 64:
-            # the same run as one launch (fk_moe_stack_decode; its outputs equal
-            # the per-layer chain's bit for bit, tests/test_gpu_stack.py)
-            # (graph replays: the per-layer launches stay the line's figure when
-            # they are faster; without a graph every step is issued from the
-            # host, where one call per run saves the other calls' issue time)
-            sp = MoeStackPlan(lsets, top_k=K, hidden=lplans[0].hidden)
-            ms1 = timed_graph([sp.run], steps, 2)
-            sp.check_device(stream)
-
-            def eager_ms(fn, n=8):
-                with torch.cuda.stream(stream):
-                    fn(stream)
-                    stream.synchronize()
-                    t0 = time.perf_counter()
-                    for _ in range(n):
-                        fn(stream)
-                    stream.synchronize()
-                return (time.perf_counter() - t0) * 1e3 / n
-
-            res["single_launch"] = {
-                "us_per_layer_step": round(ms1 * 1e3 / layers, 3),
-                "us_per_stack_step": round(ms1 * 1e3, 3),
-                "eager_us_per_stack_step": round(eager_ms(sp.run) * 1e3, 1),
-                "per_layer_launches_eager_us_per_stack_step": round(eager_ms(step) * 1e3, 1),
-                "note": "fk_moe_stack_decode: the run of layers as one launch, outputs equal to the per-layer "
-                        "launches bit for bit; eager = steps issued from the host without a graph",
-            }
-            sp.check_device(stream)
-            for lp in lplans:
-                lp.check_device(stream)
-            del sp
         del lplans
         torch.cuda.synchronize()
         return res

@@ -48,8 +48,6 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [P, I, P, P, I, P, P, P, I, I, I, I, I, I, P, P, P, c_size_t, P],
     ),
-    "fk_moe_stack_workspace_bytes": (c_size_t, [I, I, I, I, I]),
-    "fk_moe_stack_decode": (c_int, [P, I, P, I, I, I, I, I, I, c_float, c_float, P, c_size_t, P]),
     "fk_moe_layer": (
         c_int,
         [P, I, P, I, P, I, P, I, P, P, I, P, P, P, I, I, I, I, I, I, c_float, c_float, P, P, P, P, P, P, c_size_t, P],

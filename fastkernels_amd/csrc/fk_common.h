@@ -392,6 +392,23 @@ __device__ __forceinline__ bool poll_tagged(uint64_t (&w)[N], const uint64_t* co
   return false;
 }
 
+// One tagged word whose first read `w` is already issued: its value once it
+// carries `tag`.  The common case (the word was stored before the first read)
+// is one compare with no loop, so the compiler waits for exactly that load;
+// otherwise the word is re-read (every read checked before the next) until
+// it carries the tag or `limit` rounds have passed, which clears `ok`.
+__device__ __forceinline__ float settle_tagged(uint64_t w, const uint64_t* src, uint32_t tag, uint32_t limit,
+                                               bool& ok) {
+  if (tag_of(w) == tag) return value_of(w);
+  for (uint32_t i = 0; i < limit; ++i) {
+    __builtin_amdgcn_s_sleep(1);
+    w = load_tagged(src);
+    if (tag_of(w) == tag) return value_of(w);
+  }
+  ok = false;
+  return value_of(w);
+}
+
 // poll_tagged over a contiguous run: word j of this thread is
 // base[first + stride * j] when first + stride * j < n (else no word); the
 // addresses are recomputed per round instead of held in registers.

@@ -49,6 +49,7 @@ struct MoeWs {
   uint64_t* f_sgate;    // [T] shared-expert gates
   uint64_t* f_started;  // [grid] one tagged record per workgroup of the launch (capacity 1024)
   uint64_t* f_sel;      // [T, K] tagged router: expert ids chosen per token (capacity 256 * 8)
+  uint64_t* f_y;        // [K, H] single-launch layer: each routed slot's down-projection outputs (capacity 8 * 2048)
   int32_t* counts;      // [E]
   int32_t* offsets;     // [E+1] exclusive prefix of counts
   int32_t* perm;        // [P] permuted position -> pair index t*K+k
@@ -73,6 +74,7 @@ constexpr size_t kFusedLogitWords = 256 * 256;  // tagged router: T <= 256
 constexpr size_t kFusedActWords = (2 * 8 + 2) * 512;
 constexpr size_t kFusedGateWords = 2;
 constexpr size_t kFusedSelWords = 256 * 8;  // tagged router: T <= 256, K <= 8
+constexpr size_t kFusedYWords = 8 * 2048;   // single-launch layer: K <= 8, H <= 2048
 
 // Regions sized by I or H come last: fk_moe_router and fk_moe_align lay the
 // workspace out with I = H = 0 and must find the routing tables where
@@ -91,6 +93,7 @@ static size_t moe_ws_layout(int T, int K, int E, int I, int H, char* base, MoeWs
   ws->f_sgate = reinterpret_cast<uint64_t*>(take(kFusedGateWords * 8));
   ws->f_started = reinterpret_cast<uint64_t*>(take((size_t)kFusedMaxGrid * 8));
   ws->f_sel = reinterpret_cast<uint64_t*>(take(kFusedSelWords * 8));
+  ws->f_y = reinterpret_cast<uint64_t*>(take(kFusedYWords * 8));
   ws->counts = reinterpret_cast<int32_t*>(take((size_t)E * 4));
   ws->offsets = reinterpret_cast<int32_t*>(take((size_t)(E + 1) * 4));
   ws->perm = reinterpret_cast<int32_t*>(take(P * 4));
@@ -302,9 +305,10 @@ __device__ __forceinline__ float wave_sum_rows(float v) {
 // sum of the selected probabilities in selection order.
 // NT tokens at once (token i in p[i]): the tokens' chains are independent,
 // so their reductions interleave instead of running back to back.
+// Softmax of NT tokens' logits and their 32-bit keys (the prologue of the
+// selections below): p[i][j] becomes the probability of expert l + 64 j.
 template <int NT>
-__device__ void topk_select_keys32_multi(float (&p)[NT][4], int E, int K, int lane, int (&out_id)[NT],
-                                         float (&out_w)[NT]) {
+__device__ __forceinline__ void softmax_keys32(float (&p)[NT][4], int E, int lane, uint32_t (&key)[NT][4]) {
   float m[NT], s[NT];
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
@@ -326,7 +330,18 @@ __device__ void topk_select_keys32_multi(float (&p)[NT][4], int E, int K, int la
   }
 #pragma unroll
   for (int i = 0; i < NT; ++i) s[i] = wave_sum_rows(s[i]);
-  uint32_t key[NT][4];
+#pragma unroll
+  for (int i = 0; i < NT; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      p[i][j] = p[i][j] / s[i];
+      key[i][j] = lane + kWave * j < E ? ((__float_as_uint(p[i][j]) + 1u) << 2) | (uint32_t)(3 - j) : 0u;
+    }
+}
+
+// The K rounds of the selection on the keys of softmax_keys32.
+template <int NT>
+__device__ void select_rounds32(uint32_t (&key)[NT][4], int K, int lane, int (&out_id)[NT], float (&out_w)[NT]) {
   auto cswap = [](uint32_t& a, uint32_t& b) {
     const uint32_t hi = a > b ? a : b, lo = a > b ? b : a;
     a = hi;
@@ -336,9 +351,6 @@ __device__ void topk_select_keys32_multi(float (&p)[NT][4], int E, int K, int la
   int my_id[NT];
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      key[i][j] = lane + kWave * j < E ? ((__float_as_uint(p[i][j] / s[i]) + 1u) << 2) | (uint32_t)(3 - j) : 0u;
     // Sort the lane's keys descending (keys are distinct within a lane).
     cswap(key[i][0], key[i][1]);
     cswap(key[i][2], key[i][3]);
@@ -372,6 +384,131 @@ __device__ void topk_select_keys32_multi(float (&p)[NT][4], int E, int K, int la
   for (int i = 0; i < NT; ++i) {
     out_id[i] = my_id[i];
     out_w[i] = my_v[i] / denom[i];
+  }
+}
+
+template <int NT>
+__device__ void topk_select_keys32_multi(float (&p)[NT][4], int E, int K, int lane, int (&out_id)[NT],
+                                         float (&out_w)[NT]) {
+  uint32_t key[NT][4];
+  softmax_keys32<NT>(p, E, lane, key);
+  select_rounds32<NT>(key, K, lane, out_id, out_w);
+}
+
+// LDS of topk_select_ranked (one wavefront's).
+struct TopkLds {
+  uint64_t cand[kWave];
+};
+
+// Order-preserving 32-bit key of a logit (-0 folded into +0, so equal
+// logits have equal keys), and back.  0 is left for "no expert" (only a
+// negative NaN with every payload bit set would map there; it takes 1).
+__device__ __forceinline__ uint32_t logit_key(float l) {
+  const uint32_t u = __float_as_uint(l + 0.0f);
+  const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return k ? k : 1u;
+}
+__device__ __forceinline__ float key_logit(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// Top-k of one token for E <= 256 (lane l holds the logits of experts
+// l + 64 j, j < 4; any value where l + 64 j >= E) without K dependent
+// wavefront maxima.  The softmax is increasing, so the experts are selected
+// on their logits, in (logit desc, expert id asc) order: equal logits are
+// equal probabilities and go to the lower id.  (Two different logits can
+// round to one probability; which of them the reference takes is rounding,
+// not its tie rule.)
+//  1. threshold: tau = the smallest of the eight 8-lane groups' maximum
+//     32-bit keys.  The eight group maxima are eight experts with key >=
+//     tau, so each of the top K <= 8 has key >= tau (with a group holding no
+//     expert, tau = 0 and every expert is a candidate).  The same chain of
+//     lane swaps gives the largest key, the top logit.
+//  2. rank: the candidates are compacted into LDS (ballot prefix counts)
+//     with distinct 64-bit keys key << 32 | ~id, one per lane; a candidate's
+//     rank is the number of larger keys, and rank r < K is selection r.
+// More than 64 candidates (many equal logits) take K rounds of wavefront
+// maxima of the same 64-bit keys instead.  Weights: w_k = e_k / sum_j e_j,
+// e_j = exp(l_j - l_max) over the K selected logits (the renormalised
+// softmax probabilities: the softmax denominator cancels), the sum over the
+// selected lanes in a fixed lane order.  Selection r is written to
+// sel_id[r] and sel_w[r] (the caller's LDS, visible after its barrier).
+__device__ void topk_select_ranked(const float (&l)[4], int E, int K, int lane, TopkLds* lds, int* sel_id,
+                                   float* sel_w) {
+  uint32_t key[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) key[j] = lane + kWave * j < E ? logit_key(l[j]) : 0u;
+  uint32_t gm = max(max(key[0], key[1]), max(key[2], key[3]));
+  gm = max(gm, dpp_u32<kDppQuadXor1>(gm));
+  gm = max(gm, dpp_u32<kDppQuadXor2>(gm));
+  gm = max(gm, dpp_u32<kDppRowHalfMirror>(gm));
+  const uint32_t gmo = dpp_u32<kDppRowMirror>(gm);
+  uint32_t tau = min(gm, gmo), top = max(gm, gmo);
+  tau = min(tau, xor16_u32(tau));
+  top = max(top, xor16_u32(top));
+  tau = min(tau, xor32_u32(tau));
+  top = max(top, xor32_u32(top));
+  const float lmax = key_logit(top);
+  bool c[4];
+  int pos[4];
+  int C = 0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    c[j] = key[j] != 0u && key[j] >= tau;
+    const uint64_t mask = __ballot(c[j]);
+    pos[j] = C + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+    C += __popcll(mask);
+  }
+  C = __builtin_amdgcn_readfirstlane(C);
+  uint64_t mine = 0;  // this lane's selection or candidate (64-bit key)
+  int rank = K;       // its position, K: none
+  if (C > kWave) {
+    // K rounds: each takes the largest remaining 64-bit key of the wavefront.
+    uint64_t k64[4];
+    uint64_t head = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      k64[j] = key[j] ? ((uint64_t)key[j] << 32) | (uint32_t)~(lane + kWave * j) : 0ull;
+      head = max_u64(head, k64[j]);
+    }
+    for (int k = 0; k < K; ++k) {
+      const uint64_t mk = wave_max_u64(head);
+      if (head == mk) {
+        head = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          k64[j] = k64[j] == mk ? 0ull : k64[j];
+          head = max_u64(head, k64[j]);
+        }
+      }
+      if (lane == k) {
+        mine = mk;
+        rank = k;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (c[j]) lds->cand[pos[j]] = ((uint64_t)key[j] << 32) | (uint32_t)~(lane + kWave * j);
+    if (lane >= C) lds->cand[lane] = 0ull;  // pads the last group of eight
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    mine = lds->cand[lane];
+    int r = 0;
+    for (int i = 0; i < C; i += 8) {
+      uint64_t kk[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) kk[q] = lds->cand[i + q];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) r += (int)(kk[q] > mine);
+    }
+    rank = lane < C ? r : K;
+  }
+  const bool sel = rank < K;
+  const float e = expf(key_logit((uint32_t)(mine >> 32)) - lmax);
+  const float denom = wave_sum(sel ? e : 0.f);
+  if (sel) {
+    sel_id[rank] = min(max((int)~(uint32_t)mine, 0), E - 1);
+    sel_w[rank] = e / denom;
   }
 }
 
@@ -1195,35 +1332,45 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Single-launch MoE layer for one token (T = 1, H <= 2048, I <= 512,
-// E <= 256, bf16 router and expert weights, shared expert present).  From
-// two tokens on the tagged router and the expert kernels are faster (T = 2:
-// 33.0 against 35.0 µs in this kernel).
+// Single-launch MoE layer for one token (T = 1, H <= 2048 with H % 8 == 0,
+// I <= 512 with I % 16 == 0, E <= 256, K <= 8, bf16 router and expert
+// weights, shared expert present).  From two tokens on the tagged router and
+// the expert kernels are faster.
 //
-// 512-thread workgroups, one per CU (grid capped at the co-resident
-// capacity).  Item q of every phase goes to wavefront (q / G) of workgroup
-// (q % G), so consecutive items land on different CUs.
-//   P1  router logits (one expert row per item) and, overlapped, the shared
-//       expert's gate/up + SwiGLU (one intermediate per item) and its gate;
-//       each wavefront then prefetches its shared down row
-//   P2  every workgroup polls the token's logits and computes the top-k in
-//       one wavefront, whose lanes then hold the routing tables (expert u at
-//       position u, selection order)
-//   P3  routed gate/up + SwiGLU (one expert intermediate = 2 rows per item);
-//       each wavefront then prefetches its down row of every routed expert,
-//       so down weights stream while the activations are handed off
-//   P4  every workgroup polls all activations into LDS; down: one output row
-//       per item, out = g y[shared] + sum_k w_k y[k] (slot order, as the
-//       multi-launch combine) and layer_out = x + out.
-// Arithmetic order matches the multi-launch kernels, so both paths give
-// bitwise-identical results.
+// 512-thread workgroups, one per CU (grid G capped at the co-resident
+// capacity).  Item q of P1 goes to wavefront q / G of workgroup q % G, so
+// consecutive items land on different CUs.
+//   P1  router logits (one expert row per item; every workgroup holds one
+//       row, so the logits land one row's latency after the launch) and,
+//       overlapped, the shared expert's gate/up + SwiGLU (one intermediate
+//       per item) and its gate: routing-independent weights that stream
+//       while the logits are handed off
+//   P2  every workgroup polls the logits and selects the top-k itself
+//       (topk_select_ranked, one wavefront), which writes the routing table
+//       (expert of slot u, selection order) into LDS
+//   P3  routed gate/up: workgroup b takes block b (16 consecutive
+//       intermediates of one slot, two per wavefront); each intermediate
+//       leaves as one tagged word.  Then its down item is issued: 64 rows of
+//       one slot's down matrix (8 per wavefront, 64 KB), and one shared down
+//       row per wavefront for its output rows 8 b .. 8 b + 7
+//   P4  the workgroup polls its down item's slot activations (512 words, one
+//       per thread: the 32 workgroups of that slot, not the whole grid) and
+//       the shared ones, applies its 64 rows (lanes 8 j .. 8 j + 7 end with
+//       row j) and publishes y[slot][row] as tagged words
+//   P5  it polls the K slots' y of its 8 output rows (64 words) and writes
+//       out = sum_k w_k y_k + g sh in the multi-launch combine's order
+//       (routed slots in selection order, then the gated shared expert,
+//       moe_combine_kernel) and layer_out = x + out.
+// Every workgroup thus polls 512 + 512 + 64 words after its gate/up block
+// instead of all 4,608 activations: polls that run while the weight stream
+// is still in flight slow it down.
 //
 // Hand-offs carry a launch tag instead of using barriers: every value that
-// crosses workgroups (logits, activations, shared gates) is written as a
+// crosses workgroups (logits, activations, shared gate) is written as a
 // tagged word (store_tagged) and polled until it carries this launch's tag,
 // so a consumer waits only for the values it reads.  The tag is
 // epoch + 1, where the epoch is a workspace counter that every wavefront
-// reads at its start; each wavefront posts a started record with its tag,
+// reads at its start; each workgroup posts a started record with its tag,
 // and workgroup 0 advances the epoch once every record of this launch is
 // there (so no wavefront can read the advanced epoch in the same launch).
 // Tags are 32-bit: a word left untouched for exactly 2^32 launches on one
@@ -1233,7 +1380,6 @@ constexpr int kFusedMaxTokens = 1;  // from 2 tokens on, the tagged router + exp
 constexpr int kFusedMaxPairs = kFusedMaxTokens * 8;
 constexpr int kFusedWaves = 8;
 constexpr int kFusedMaxExperts = 256;
-constexpr int kFusedStage = 12;  // tagged loads in flight per thread while staging activations
 constexpr int kFusedChunk = 16;  // routed items per workgroup block: 16 tagged words = one 128-byte line
 static_assert(kFusedLogitWords >= (size_t)kFusedMaxTokens * kFusedMaxExperts, "fused logit region too small");
 static_assert(kFusedActWords >= (size_t)(kFusedMaxPairs + kFusedMaxTokens) * 512, "fused activation region too small");
@@ -1252,46 +1398,6 @@ struct FusedArgs {
   float* layer_out;
 };
 
-// Gate row i and up row I+i of one expert (bf16, H <= 2048: 4 chunks per
-// lane) against the tokens toks[0..npairs) (token p when toks is NULL);
-// lane 0 writes silu(g)*u of the p-th token to out[p * kFusedChunk].
-template <bool BFX>
-__device__ __forceinline__ void fused_gateup_item(const Raw8<true> (&wg)[4], const Raw8<true> (&wu)[4], const void* x,
-                                                  int H, int lane, int npairs, const int* toks, float* out) {
-  const int nch = H >> 3;
-  for (int pp = 0; pp < npairs; ++pp) {
-    const int t = toks ? toks[pp] : pp;
-    // bf16 tokens: the four chunks are loaded together (clamped in range),
-    // so a token costs one round trip, not one per chunk (fp32 chunks are
-    // loaded one at a time, which keeps the registers within budget)
-    Raw8<BFX> xr[BFX ? 4 : 1];
-    if constexpr (BFX) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) xr[j] = load_raw8<BFX>(x, (size_t)t * H + (size_t)min(lane + kWave * j, nch - 1) * 8);
-    }
-    float g = 0.f, u = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = lane + kWave * j;
-      if (c < nch) {
-        float x8[8], a8[8], b8[8];
-        if constexpr (BFX) raw8_to_f32<BFX>(xr[j], x8);
-        else load8_f32<BFX>(x, (size_t)t * H + (size_t)c * 8, x8);
-        raw8_to_f32<true>(wg[j], a8);
-        raw8_to_f32<true>(wu[j], b8);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          g = fmaf(a8[q], x8[q], g);
-          u = fmaf(b8[q], x8[q], u);
-        }
-      }
-    }
-    g = wave_sum(g);
-    u = wave_sum(u);
-    if (lane == 0) out[pp * kFusedChunk] = silu(g) * u;
-  }
-}
-
 // Down-row chunk (8 bf16) of this lane against the activation row staged in LDS.
 __device__ __forceinline__ float dot8_act_lds(const Raw8<true>& w, const float* act_row, int lane, int I) {
   float d = 0.f;
@@ -1308,30 +1414,120 @@ __device__ __forceinline__ float dot8_act_lds(const Raw8<true>& w, const float* 
   return d;
 }
 
-// One token: 8 prefetched down rows (one per routed expert) and straight-
-// line down code, which keeps the kernel within the register budget of two
-// workgroups' waves per SIMD.
+
+// Gate/up rows of NI intermediates (bf16, H <= 2048: 4 chunks per lane)
+// against the token's chunks xt; act[i] = silu(gate_i . x) * (up_i . x),
+// the same in every lane.  Every row load is issued before the first
+// product (addresses clamped in range, so no load is conditional);
+// after_issue() runs right behind the loads.
+template <bool BFX, int NI, class AfterIssue>
+__device__ __forceinline__ void fused_gu_rows(const Raw8<BFX> (&xt)[4], const char* const (&gate)[NI],
+                                              const char* const (&up)[NI], int nch, int lane, float (&act)[NI],
+                                              AfterIssue after_issue) {
+  Raw8<true> g[NI][4], u[NI][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const size_t c8 = (size_t)min(lane + kWave * j, nch - 1) * 8;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      g[i][j] = load_raw8_stream<true>(gate[i], c8);
+      u[i][j] = load_raw8_stream<true>(up[i], c8);
+    }
+  }
+  after_issue();
+  float acc[2 * NI];
+#pragma unroll
+  for (int i = 0; i < 2 * NI; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (lane + kWave * j < nch) {
+      float x8[8], w8[8];
+      raw8_to_f32<BFX>(xt[j], x8);
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        raw8_to_f32<true>(g[i][j], w8);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[2 * i] = fmaf(w8[q], x8[q], acc[2 * i]);
+        raw8_to_f32<true>(u[i][j], w8);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[2 * i + 1] = fmaf(w8[q], x8[q], acc[2 * i + 1]);
+      }
+    }
+  }
+  // the 2 NI sums at once (rows4_sum: lanes 16 r hold sum r; rows8_sum:
+  // lanes 8 r)
+  if constexpr (NI <= 2) {
+    float d[4] = {acc[0], acc[1], NI > 1 ? acc[2] : 0.f, NI > 1 ? acc[3] : 0.f};
+    const float rs = rows4_sum(d);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const float gs = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 32 * i));
+      const float us = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 32 * i + 16));
+      act[i] = silu(gs) * us;
+    }
+  } else {
+    static_assert(NI <= 4, "at most four intermediates per call");
+    float d[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) d[i] = i < 2 * NI ? acc[i] : 0.f;
+    const float rs = rows8_sum(d);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const float gs = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 16 * i));
+      const float us = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 16 * i + 8));
+      act[i] = silu(gs) * us;
+    }
+  }
+}
+
+// Eight down rows (one 16-byte chunk of each in this lane) against the
+// lane's 8 activation columns, read once from LDS; d[j] is row j's partial.
+__device__ __forceinline__ void dot8x8_act_lds(const Raw8<true> (&w)[8], const float* act_row, int lane, int I,
+                                               float (&d)[8]) {
+  float a8[8];
+  const float4* p = reinterpret_cast<const float4*>(act_row + min(lane * 8, I - 8));
+  const float4 lo = p[0], hi = p[1];
+  a8[0] = lo.x; a8[1] = lo.y; a8[2] = lo.z; a8[3] = lo.w;
+  a8[4] = hi.x; a8[5] = hi.y; a8[6] = hi.z; a8[7] = hi.w;
+  const bool in = lane * 8 < I;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float w8[8];
+    raw8_to_f32<true>(w[j], w8);
+    float acc = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc = fmaf(w8[q], a8[q], acc);
+    d[j] = in ? acc : 0.f;
+  }
+}
+
 FK_TIMELINE_BUFFER(moe_fused)
 
-template <bool BFX>
+// FAST: the host has checked that the grid has one workgroup per gate/up
+// block, per down item and per output row group (the model's shape on a
+// full MI355X): straight-line code for that case.
+template <bool BFX, bool FAST>
 __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
-  constexpr int NPF = 8;  // prefetched down rows per wavefront: one per routed expert
-  __shared__ __align__(16) int s_ids[kFusedMaxPairs];
-  __shared__ float s_w[kFusedMaxPairs];
-  __shared__ int s_active[kFusedMaxPairs];      // routed experts, selection order
-  __shared__ int s_nact;
+  constexpr int RG = kFusedWaves;       // output rows per final row group (one per wavefront)
+  constexpr int DR = RG * kFusedWaves;  // rows per down item (8 per wavefront)
+  __shared__ int s_active[kFusedMaxPairs];  // routed experts, selection order
+  __shared__ float s_wpos[kFusedMaxPairs];  // routing weight of each slot
   __shared__ int s_fail;
   __shared__ uint32_t s_wtag[kFusedWaves];
-  __shared__ float s_chunk[kFusedMaxTokens][kFusedChunk];
-  __shared__ float s_wpos[kFusedMaxPairs];      // permuted position -> routing weight
-  extern __shared__ float4 s_act_v[];  // [(P + T) * I] activations, then [T] shared gates
-  float* s_act = reinterpret_cast<float*>(s_act_v);
+  __shared__ __align__(16) TopkLds s_topk;
+  __shared__ __align__(16) float s_sha[512];  // shared activations
+  __shared__ __align__(16) float s_ra[512];   // activations of the down item's slot
+  __shared__ float s_sg;                      // shared gate
+  __shared__ float s_yk[kFusedMaxPairs * RG];  // final: y[slot][row] of the row group
+  __shared__ float s_act16[kFusedChunk];       // the gate/up block's activations
+  __shared__ float s_ystage[DR];               // the down item's outputs
+  __shared__ float s_sh[RG];                   // final: shared down rows of the row group
   const RouterArgs& a = f.r;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = gridDim.x, b = blockIdx.x;
   const int NW = G * kFusedWaves;
   const int q0 = wave * G + b;
-  const int T = 1, H = a.H, E = a.E, K = a.K, I = f.I, P = K;
+  const int H = a.H, E = a.E, K = a.K, I = f.I, P = K;
   const int nch = H >> 3;
   uint32_t* err = &a.ws.tickets[kTicketError];
   // The launch tag (epoch + 1) is loaded after the wavefront's P1 weight
@@ -1343,24 +1539,34 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   __syncthreads();
   FK_TIMELINE_DECL;
   FK_MARK(0);  // (timeline markers: diagnostic builds only)
+  // The fast path's item indices (block b: slot f_ub, intermediates f_i0..;
+  // down item b: slot f_ud, rows f_rr0..), computed here, where the scalar
+  // divisions overlap the first loads' latency instead of delaying the
+  // routed gate/up rows.
+  int f_ub = 0, f_i0 = 0, f_ud = 0, f_rr0 = 0;
+  if constexpr (FAST) {
+    const int bpe_ = I / kFusedChunk, cpe_ = (H + DR - 1) / DR;
+    f_ub = b / bpe_;
+    f_i0 = (b - f_ub * bpe_) * kFusedChunk;
+    f_ud = b / cpe_;
+    f_rr0 = (b - f_ud * cpe_) * DR;
+    asm volatile("" : "+s"(f_ub), "+s"(f_i0), "+s"(f_ud), "+s"(f_rr0));
+  }
 
   // ---------------- P1: router rows, shared gate/up, shared gate -----------
-  // Item q (router rows 0..E-1, shared intermediates E..E+I-1, then the
-  // shared gate) goes to wavefront q / G of workgroup q % G: every workgroup
-  // holds one router row (its wavefront 0 at E <= G), so the logits land one
-  // row's latency after launch instead of behind rows queued on a few CUs.
-  // Each wavefront publishes its own result as one tagged word.
+  // Item q: router rows 0..E-1, shared intermediates E..E+I-1, then the
+  // shared gate.  Each wavefront publishes its result as one tagged word.
   const int nitems = E + I + 1;
   for (int q = q0; q < nitems; q += NW) {
     if (q < E) {
       const int e = q;
-      // All loads of the row (weights, token 0, the bf16 norm weight) are
+      // All loads of the row (weights, the token, the bf16 norm weight) are
       // issued before the first use: indices are clamped in range and
       // out-of-range chunks are zeroed afterwards, so there is no branch
       // between them (a load whose dtype is tested at run time would wait
       // for every load before it).
       Raw8<true> wr[4], nr[4];
-      Raw8<BFX> xr[4];  // the token rides with the weights
+      Raw8<BFX> xr[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int cc = min(lane + kWave * j, nch - 1);
@@ -1407,29 +1613,24 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       }
     } else if (q < E + I) {
       const int i = q - E;
-      Raw8<true> wg[4], wu[4];
+      Raw8<BFX> xt[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = lane + kWave * j;
-        if (c < nch) {
-          wg[j] = load_raw8_stream<true>(f.sgu, (size_t)i * H + (size_t)c * 8);
-          wu[j] = load_raw8_stream<true>(f.sgu, (size_t)(I + i) * H + (size_t)c * 8);
-        }
-      }
-      {
+      for (int j = 0; j < 4; ++j) xt[j] = load_raw8<BFX>(a.x, (size_t)min(lane + kWave * j, nch - 1) * 8);
+      const char* sgu = reinterpret_cast<const char*>(f.sgu);
+      const char* g[1] = {sgu + (size_t)i * H * 2};
+      const char* u[1] = {sgu + (size_t)(I + i) * H * 2};
+      float act[1];
+      fused_gu_rows<BFX, 1>(xt, g, u, nch, lane, act, [&]() {
         const WaitLimits wl = wait_limits(a.ws.tickets, kTicketEpoch);
         tag = wl.tag;
         plim = wl.poll;
-      }
+      });
       have_tag = true;
-      // (lane 0 writes the value to its wavefront's LDS slot and reads it back)
-      fused_gateup_item<BFX>(wg, wu, a.x, H, lane, T, nullptr, &s_chunk[0][wave]);
-      if (lane == 0) store_tagged(a.ws.f_act + (size_t)P * I + i, s_chunk[0][wave], tag);
+      if (lane == 0) store_tagged(a.ws.f_act + (size_t)P * I + i, act[0], tag);
     } else {
-      // Shared-expert gate of the token: one row like the router's, loads
-      // issued together as there.
-      // (the gate weight is bf16 here; a NULL gate reads the norm weight, a
-      // valid address, and the products are dropped)
+      // Shared-expert gate of the token: one row like the router's.  (The
+      // gate weight is bf16 here; a NULL gate reads the norm weight, a valid
+      // address, and the products are dropped.)
       Raw8<BFX> xr[4];
       Raw8<true> gr[4];
       const void* gsrc = f.sg ? f.sg : a.nw;
@@ -1445,21 +1646,15 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
         plim = wl.poll;
       }
       have_tag = true;
-      float g8[4][8];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int c = lane + kWave * j;
-        raw8_to_f32<true>(gr[j], g8[j]);
-#pragma unroll
-        for (int qq = 0; qq < 8; ++qq) g8[j][qq] = (f.sg && c < nch) ? g8[j][qq] : 0.f;
-      }
       float d = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float x8[8];
+        const int c = lane + kWave * j;
+        float x8[8], g8[8];
         raw8_to_f32<BFX>(xr[j], x8);
+        raw8_to_f32<true>(gr[j], g8);
 #pragma unroll
-        for (int qq = 0; qq < 8; ++qq) d = fmaf(x8[qq], g8[j][qq], d);
+        for (int qq = 0; qq < 8; ++qq) d = fmaf(x8[qq], (f.sg && c < nch) ? g8[qq] : 0.f, d);
       }
       d = wave_sum(d);
       if (lane == 0) store_tagged(a.ws.f_sgate, f.sg ? sigmoid(d) : 1.f, tag);
@@ -1477,51 +1672,36 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   if (lane == 0) s_wtag[wave] = tag;
   __syncthreads();
   if (tid == 0) store_tagged(a.ws.f_started + b, __uint_as_float(s_wtag[kFusedWaves - 1]), tag);
-  // This wavefront's first down row (shared expert part) and residual inputs,
-  // fetched early.
-  const int r_first = q0;
-  Raw8<true> sdr;
-  if (r_first < H && lane * 8 < I) sdr = load_raw8_stream<true>(f.sdn, (size_t)r_first * I + (size_t)lane * 8);
-  // (raw bits, converted where used: a conversion here would wait for the
-  // down-row load above)
-  uint32_t x_first_raw[1];
-  gather_raw<BFX>(a.x, f.layer_out && r_first < H && lane < T ? (size_t)lane * H + r_first : 0, 0, 1, x_first_raw);
 
-  // ---------------- P2: top-k of every token, routing tables in LDS --------
-  int tk_id = 0;
-  float tk_w = 0.f;
-  if (wave < T) {
+  // ---------------- P2: top-k, routing table in LDS ------------------------
+  if (wave == 0) {
     constexpr int NJE = kFusedMaxExperts / kWave;
-    const int t = wave;
     uint64_t w[NJE];
     const uint64_t* srcs[NJE];
 #pragma unroll
     for (int j = 0; j < NJE; ++j) {
       const int ex = lane + kWave * j;
-      srcs[j] = ex < E ? a.ws.f_logits + (size_t)t * E + ex : nullptr;
+      srcs[j] = ex < E ? a.ws.f_logits + ex : nullptr;
       w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
     }
     const bool ok = poll_tagged<NJE>(w, srcs, tag, plim);
     if (!ok) s_fail = 1;
     FK_MARK(2);
-    float p[NJE];
+    float l[NJE];
 #pragma unroll
-    for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
-    topk_select_regs<NJE>(p, E, K, lane, tk_id, tk_w);
+    for (int j = 0; j < NJE; ++j) l[j] = value_of(w[j]);
+    // One token: the K selections are distinct experts, so the routing
+    // table is the selection itself (slot u = selection u) with no sort.
+    // (After a failed wait the logits may be stale: the ids are in range
+    // and every output of this workgroup is poisoned below.)
+    topk_select_ranked(l, E, K, lane, &s_topk, s_active, s_wpos);
     FK_MARK(3);
-    // (after a failed wait the logits may be stale: ids stay in range and
-    // every output of this workgroup is poisoned below)
-    if (!ok) tk_id = min(max(tk_id, 0), E - 1);
-    if (lane < K) {
-      s_ids[t * K + lane] = tk_id;
-      s_w[t * K + lane] = tk_w;
-    }
-  } else if (b == 0 && wave >= kFusedMaxTokens) {
+  } else if (b == 0) {
     // Workgroup 0 checks that every wavefront of this launch has read the
     // epoch (its started record carries the tag) before advancing it.
     constexpr int kChunk = 4;
-    const int nthr = (kFusedWaves - kFusedMaxTokens) * kWave;
-    for (int base = tid - kFusedMaxTokens * kWave; base < G; base += kChunk * nthr) {
+    const int nthr = (kFusedWaves - 1) * kWave;
+    for (int base = tid - kWave; base < G; base += kChunk * nthr) {
       uint64_t w[kChunk];
       const uint64_t* srcs[kChunk];
 #pragma unroll
@@ -1533,16 +1713,6 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
       if (!poll_tagged<kChunk>(w, srcs, tag, plim)) s_fail = 1;
     }
   }
-  // One token: the top-k wavefront holds the K pairs in its lanes, each a
-  // distinct expert, so the tables are the selection itself (expert u at
-  // permuted position u, selection order) with no sort.
-  if (wave == 0) {
-    if (lane < K) {
-      s_active[lane] = tk_id;
-      s_wpos[lane] = tk_w;
-    }
-    if (lane == 0) s_nact = K;
-  }
   __syncthreads();
   // A failed wait poisons every later output of the workgroup.  Workgroup 0
   // advances the epoch only when every workgroup has read it (all started
@@ -1550,635 +1720,251 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
   // the next launch's tag and publish words that launch reads as its own.
   const bool bad = s_fail;
   if (b == 0 && tid == 0 && !bad) store_coherent(&a.ws.tickets[kTicketEpoch], tag);
-  const int U = s_nact;
   FK_MARK(4);
-  if (b == 0) {
-    for (int j = tid; j < P; j += 512) {
-      a.ids_out[j] = s_ids[j];
-      a.w_out[j] = poison_if(bad, s_w[j]);
-    }
+  if (b == 0 && tid < P) {
+    a.ids_out[tid] = s_active[tid];
+    a.w_out[tid] = poison_if(bad, s_wpos[tid]);
   }
 
-  // ---------------- P3: routed gate/up (+ down-row prefetch) ---------------
-  // Blocks of kFusedChunk consecutive intermediates of one expert per
-  // workgroup, two per wavefront; each block leaves as one 128-byte line per
-  // routed token.
-  const int bpe = I / kFusedChunk, nblk = U * bpe;
-  // (wave-uniform: the down code branches on it and reduces across lanes
-  // with lane swaps, which read inactive lanes' stale registers)
-  const bool prefetch = U <= NPF && r_first < H;
-  Raw8<true> dr[NPF];
-  {
-    // One token: each routed expert holds one pair (expert u at permuted
-    // position u).  The token's chunks and the first block's gate/up rows are
-    // issued first; this wavefront's 8 down rows only once the block's
-    // activations are stored.  Loads in flight together are served
-    // interleaved, whatever their issue order: with the down rows (16 MB
-    // over the grid) issued right behind the gate/up rows (32 MB), gate/up
-    // completed ~1 us later, and the activation hand-off that follows it is
-    // on the critical path while the down stream is not (it overlaps the
-    // hand-off).  Every load is unconditional (clamped in range; unused lanes and slots
-    // are dropped where the values are used), so no branch makes the
-    // compiler wait for the loads before it.
+  // ---------------- P3..P5 ------------------------------------------------
+  const int bpe = I / kFusedChunk, nblk = K * bpe;
+  const int cpe = (H + DR - 1) / DR, ndn = K * cpe;  // down items: (slot, 64-row chunk)
+  const int ngrp = H / RG;                            // final row groups
+  const int r0 = b * RG;  // this workgroup's first final row group (if b < ngrp)
+  const size_t dcol = (size_t)min(lane * 8, I - 8);
+  const char* gu = reinterpret_cast<const char*>(f.gu);
+  const size_t rowb = (size_t)H * 2, expb = (size_t)2 * I * rowb;
+  // The residual input of the workgroup's rows (raw bits; converted where
+  // used, since a conversion here would wait for it).
+  uint32_t x_raw[1];
+  gather_raw<BFX>(a.x, (size_t)min(r0 + lane, H - 1), 0, 1, x_raw);
+  if constexpr (FAST) {
+    // The model's shape on a full grid: workgroup b takes gate/up block b,
+    // down item b and output rows r0 .. r0 + 7, in straight-line code with
+    // unconditional (clamped) loads, so the compiler's waits are exact.
+    // Stores go out through one wavefront (7) and the polls through others:
+    // a wavefront's loads retire in order behind its stores, so a poll
+    // behind a store would wait for the store's acknowledgement.
+    const int ub = f_ub, i0 = f_i0, ia = i0 + 2 * wave;
+    const int ud = f_ud, rr0 = f_rr0, rw = rr0 + wave * RG;
+    const char* we = gu + (size_t)s_active[ub] * expb;
+    const char* g2[2] = {we + (size_t)ia * rowb, we + (size_t)(ia + 1) * rowb};
+    const char* u2[2] = {we + (size_t)(I + ia) * rowb, we + (size_t)(I + ia + 1) * rowb};
+    const uint16_t* dnb = reinterpret_cast<const uint16_t*>(f.dn) + (size_t)s_active[ud] * H * I;
+    const uint16_t* sdb = reinterpret_cast<const uint16_t*>(f.sdn);
+    const uint64_t* sh_src = a.ws.f_act + (size_t)P * I + min(tid, I - 1);
+    const uint64_t* ra_src0 = a.ws.f_act + (size_t)ud * I + min(tid, I - 1);
+    const uint64_t* ra_src1 = a.ws.f_act + (size_t)ud * I + min(tid + 256, I - 1);
+    const uint64_t* y_src = a.ws.f_y + (size_t)min(lane >> 3, K - 1) * H + r0 + (lane & 7);
     Raw8<BFX> xt[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) xt[j] = load_raw8<BFX>(a.x, (size_t)min(lane + kWave * j, nch - 1) * 8);
-    const size_t dcol = (size_t)min(lane * 8, I - 8), drow = (size_t)min(r_first, H - 1);
-    auto issue_down = [&]() {
-#pragma unroll
-      for (int u = 0; u < NPF; ++u)
-        dr[u] = load_raw8_stream<true>(f.dn, ((size_t)s_active[min(u, U - 1)] * H + drow) * I + dcol);
-    };
-    // one block: its gate/up rows, then (first block only) the down rows
-    auto block = [&](int blk, bool first_blk) {
-      const int u = blk / bpe, i0 = (blk - u * bpe) * kFusedChunk;
-      const int ia = i0 + 2 * wave;
-      const char* we = reinterpret_cast<const char*>(f.gu) + (size_t)s_active[u] * 2 * I * H * 2;
-      Raw8<true> ga[4], ua8[4], gb[4], ub8[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const size_t c8 = (size_t)min(lane + kWave * j, nch - 1) * 8;
-        ga[j] = load_raw8_stream<true>(we, (size_t)ia * H + c8);
-        gb[j] = load_raw8_stream<true>(we, (size_t)(ia + 1) * H + c8);
-        ua8[j] = load_raw8_stream<true>(we, (size_t)(I + ia) * H + c8);
-        ub8[j] = load_raw8_stream<true>(we, (size_t)(I + ia + 1) * H + c8);
-      }
-      float acc[4] = {0.f, 0.f, 0.f, 0.f};  // gate ia, up ia, gate ia + 1, up ia + 1
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (lane + kWave * j < nch) {
-          float x8[8], w8[8];
-          raw8_to_f32<BFX>(xt[j], x8);
-          raw8_to_f32<true>(ga[j], w8);
-#pragma unroll
-          for (int q = 0; q < 8; ++q) acc[0] = fmaf(w8[q], x8[q], acc[0]);
-          raw8_to_f32<true>(ua8[j], w8);
-#pragma unroll
-          for (int q = 0; q < 8; ++q) acc[1] = fmaf(w8[q], x8[q], acc[1]);
-          raw8_to_f32<true>(gb[j], w8);
-#pragma unroll
-          for (int q = 0; q < 8; ++q) acc[2] = fmaf(w8[q], x8[q], acc[2]);
-          raw8_to_f32<true>(ub8[j], w8);
-#pragma unroll
-          for (int q = 0; q < 8; ++q) acc[3] = fmaf(w8[q], x8[q], acc[3]);
-        }
-      }
-      // the four sums at once (lanes 16r ..: sum r)
-      const float rs = rows4_sum(acc);
-      const float g0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 0));
-      const float u0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 16));
-      const float g1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 32));
-      const float u1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 48));
-      if (lane == 0) {
-        s_chunk[0][2 * wave] = silu(g0) * u0;
-        s_chunk[0][2 * wave + 1] = silu(g1) * u1;
-      }
-      __syncthreads();
-      if (tid < kFusedChunk) store_tagged(a.ws.f_act + (size_t)u * I + i0 + tid, poison_if(bad, s_chunk[0][tid]), tag);
-      if (first_blk) issue_down();
-      __syncthreads();
-    };
-    if (b < nblk) {
-      block(b, true);
-      for (int blk = b + G; blk < nblk; blk += G) block(blk, false);
-    } else {
-      issue_down();  // a workgroup without a gate/up block
-    }
-  }
-
-  FK_MARK(5);
-  // ---------------- P4: stage activations, down rows, combine --------------
-  // Every workgroup polls all activations (and the shared gates) into LDS,
-  // kFusedStage tagged loads in flight per thread.
-  const int n_act = (P + T) * I, n_stage = n_act + T;
-  bool stage_ok = true;
-  for (int base = tid; base < n_stage; base += 512 * kFusedStage) {
-    uint64_t w[kFusedStage];
-    const uint64_t* srcs[kFusedStage];
-#pragma unroll
-    for (int j = 0; j < kFusedStage; ++j) {
-      const int idx = base + j * 512;
-      srcs[j] = idx < n_act ? a.ws.f_act + idx : idx < n_stage ? a.ws.f_sgate + (idx - n_act) : nullptr;
-      w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
-    }
-    stage_ok = poll_tagged<kFusedStage>(w, srcs, tag, plim) && stage_ok;
-#pragma unroll
-    for (int j = 0; j < kFusedStage; ++j)
-      if (srcs[j]) s_act[base + j * 512] = value_of(w[j]);
-  }
-  if (!stage_ok) s_fail = 1;
-  __syncthreads();
-  const bool bad_out = s_fail;
-  if (tid == 0 && bad_out) __hip_atomic_fetch_or(err, FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  FK_MARK(6);
-
-  // Down rows: each lane accumulates the gate- and routing-weighted partial
-  // dots of the shared and every routed expert on its 8 columns (shared
-  // first, then the routed experts in selection order, as the multi-launch
-  // combine); one wave sum gives out[r].
-  const float* s_sg = s_act + n_act;
-  for (int r = q0; r < H; r += NW) {
-    const bool first = r == r_first;
-    float acc;
-    if (first && prefetch) {
-      // Down rows prefetched: expert u sits at permuted position u; the code
-      // has no branches and every LDS read can be issued at once.
-      acc = s_sg[0] * dot8_act_lds(sdr, s_act + (size_t)P * I, lane, I);
-#pragma unroll
-      for (int u = 0; u < NPF; ++u) {
-        // (slots past U hold a repeated row: dropped, not multiplied by 0)
-        const float d = dot8_act_lds(dr[u], s_act + (size_t)(u < U ? u : 0) * I, lane, I);
-        acc = u < U ? fmaf(s_wpos[u], d, acc) : acc;
-      }
-    } else {
-      Raw8<true> w;
-      if (first) w = sdr;
-      else if (lane * 8 < I) w = load_raw8_stream<true>(f.sdn, (size_t)r * I + (size_t)lane * 8);
-      acc = s_sg[0] * dot8_act_lds(w, s_act + (size_t)P * I, lane, I);
-      for (int u0 = 0; u0 < U; u0 += 8) {
-        Raw8<true> wb8[8];
-#pragma unroll
-        for (int v = 0; v < 8; ++v)
-          if (u0 + v < U && lane * 8 < I)
-            wb8[v] = load_raw8_stream<true>(f.dn, ((size_t)s_active[u0 + v] * H + r) * I + (size_t)lane * 8);
-#pragma unroll
-        for (int v = 0; v < 8; ++v)
-          if (u0 + v < U) acc = fmaf(s_wpos[u0 + v], dot8_act_lds(wb8[v], s_act + (size_t)(u0 + v) * I, lane, I), acc);
-      }
-    }
-    const float o = poison_if(bad_out, wave_sum(acc));
+    uint64_t shw = 0, sgw = 0;
+    float act[2];
+    // gate/up rows, then the shared activation word and gate (stored in P1)
+    FK_MARK(9);
+    fused_gu_rows<BFX, 2>(xt, g2, u2, nch, lane, act, [&]() {
+      shw = load_tagged(sh_src);
+      sgw = load_tagged(a.ws.f_sgate);
+      FK_MARK(10);
+    });
+    FK_MARK(11);
     if (lane == 0) {
-      f.out[r] = o;
-      if (f.layer_out)
-        f.layer_out[r] = (first ? raw_value<BFX>(x_first_raw[0]) : load_scalar(a.x, BFX ? FK_DTYPE_BF16 : FK_DTYPE_F32, r)) + o;
+      s_act16[2 * wave] = act[0];
+      s_act16[2 * wave + 1] = act[1];
     }
-  }
-  FK_MARK(7);
-  FK_TIMELINE_COMMIT(moe_fused, blockIdx.x);
-}
-
-// ---------------------------------------------------------------------------
-// A run of MoE layers at one token in one launch (fk_moe_stack_decode): layer
-// l's input is layer l-1's layer_out, as in the resident layer stack.  Each
-// layer runs the phases of moe_fused_kernel with the same arithmetic in the
-// same order, so its outputs equal a chain of fk_moe_layer calls bit for bit:
-//   X   the layer's input in LDS (fp32): layer 0's converted from the
-//       caller's tokens, a later layer's polled from the previous layer's
-//       tagged outputs by every workgroup
-//   P1  router rows, shared gate/up rows and the shared gate, in units of 8
-//       rows (one per wavefront), at most one unit per workgroup; a unit's
-//       weight rows for layer l + 1 are fetched during layer l's down phase
-//   P2  every workgroup polls the logits and selects the top-k itself
-//   P3  routed gate/up blocks, the wavefront's 8 down rows fetched behind them
-//   P4  activations polled into LDS, down rows, combine and residual; the
-//       layer output also leaves as tagged words for the next layer
-// The launch epoch is kept as in the single-launch layer (once per launch).
-// Per-layer tagged words: logits [E], activations [(K + 1) I], the shared
-// gate [1], the layer output [H] (kStackLayerWords per layer).
-// ---------------------------------------------------------------------------
-constexpr int kStackMaxH = 2048;
-constexpr int kStackMaxLayers = 64;  // layers per launch (descriptors staged in LDS)
-static_assert(sizeof(fk_moe_stack_layer) == 13 * 8, "descriptor: 13 pointers");
-constexpr size_t kStackLayerWords = 256 + 9 * 512 + 64 + kStackMaxH;  // logits, activations, gate (padded), output
-constexpr size_t kStackMaxDynLds = ((size_t)kStackMaxH + 9 * 512 + 4) * sizeof(float);
-
-struct StackArgs {
-  const void* x0;
-  const fk_moe_stack_layer* layers;
-  int L, bias_dt, H, I, E, K;
-  float eps, off;
-  uint32_t* tickets;   // workspace header (epoch, poll bound, error word)
-  uint64_t* started;   // [kFusedMaxGrid]
-  uint64_t* words;     // [L][kStackLayerWords]
-};
-
-// The layer descriptors live in device memory, so the compiler cannot tell
-// that their pointers address global memory: without these casts every
-// access through them would be a flat access (which also counts against the
-// LDS wait counter).  Elements are bf16 unless stated.
-typedef const __attribute__((address_space(1))) u32x4 g_u32x4;
-__device__ __forceinline__ u32x4 g_row16(const void* base, size_t elem) {
-  return *(g_u32x4*)((const __attribute__((address_space(1))) char*)base + elem * 2);
-}
-__device__ __forceinline__ u32x4 g_row16_nt(const void* base, size_t elem) {
-  return __builtin_nontemporal_load((g_u32x4*)((const __attribute__((address_space(1))) char*)base + elem * 2));
-}
-__device__ __forceinline__ float g_scalar(const void* p, int dtype, size_t i) {
-  const __attribute__((address_space(1))) char* c = (const __attribute__((address_space(1))) char*)p;
-  return dtype == FK_DTYPE_BF16 ? __uint_as_float((uint32_t)((const __attribute__((address_space(1))) uint16_t*)c)[i] << 16)
-                                : ((const __attribute__((address_space(1))) float*)c)[i];
-}
-template <class T>
-__device__ __forceinline__ void g_store(T* p, size_t i, T v) {
-  ((__attribute__((address_space(1))) T*)p)[i] = v;
-}
-__device__ __forceinline__ void bf16x8_to_f32(const u32x4& v, float out[8]) {
-  Raw8<true> r;
-  r.a = v;
-  r.b = u32x4{0, 0, 0, 0};
-  raw8_to_f32<true>(r, out);
-}
-
-FK_TIMELINE_BUFFER(moe_stack)
-
-template <bool BFX0>
-__global__ __launch_bounds__(512) void moe_stack_kernel(StackArgs sa) {
-  constexpr int NPF = 8;  // prefetched down rows per wavefront: one per routed expert
-  __shared__ int s_ids[8];
-  __shared__ float s_w[8];
-  __shared__ int s_active[8];  // routed experts, selection order
-  __shared__ float s_wpos[8];  // their routing weights
-  __shared__ int s_fail;
-  __shared__ uint32_t s_wtag[kFusedWaves];
-  __shared__ float s_chunk[kFusedChunk];
-  __shared__ uint64_t s_desc_w[kStackMaxLayers * 13];  // the layer descriptors
-  extern __shared__ float4 s_dyn_v[];
-  float* s_x = reinterpret_cast<float*>(s_dyn_v);  // [H] the layer's input
-  float* s_act = s_x + kStackMaxH;                  // [(K + 1) I] activations, then the shared gate
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int G = gridDim.x, b = blockIdx.x;
-  const int NW = G * kFusedWaves;  // (>= H, the host checks: one down row per wavefront)
-  const int H = sa.H, E = sa.E, K = sa.K, I = sa.I, L = sa.L, P = K;
-  const int nch = H >> 3;
-  const int nrb = (E + 7) / 8, nsb = I / 8, nunits = nrb + nsb + 1;
-  const bool has_unit = b < nunits;
-  const int unit = b;
-  uint32_t* err = &sa.tickets[kTicketError];
-  WaitHeader hdr = load_wait_header(sa.tickets, kTicketEpoch);
-  if (tid == 0) s_fail = 0;
-  FK_TIMELINE_DECL;
-  FK_MARK(0);  // (timeline markers: diagnostic builds only)
-
-  // P1 weight rows of this workgroup's unit: router row (pa) + norm weight
-  // (pb), or shared gate row (pa) + up row (pb), or the shared gate (pa; the
-  // norm weight when there is none: a valid address, products dropped).
-  // Clamped in range and unconditional within the unit's kind.
-  u32x4 pa[4], pb[4];
-  auto issue_unit = [&](const fk_moe_stack_layer& lyr) {
-    // one source and row per kind, then the same eight loads for every kind
-    const void* src_a;
-    const void* src_b;
-    size_t row_a, row_b;
-    if (unit < nrb) {
-      src_a = lyr.router_weight;
-      row_a = (size_t)min(unit * 8 + wave, E - 1) * H;
-      src_b = lyr.norm_weight;
-      row_b = 0;
-    } else if (unit < nrb + nsb) {
-      const int i = (unit - nrb) * 8 + wave;
-      src_a = src_b = lyr.shared_gate_up;
-      row_a = (size_t)i * H;
-      row_b = (size_t)(I + i) * H;
-    } else {
-      src_a = src_b = lyr.shared_gate ? lyr.shared_gate : lyr.norm_weight;
-      row_a = row_b = 0;
+    // Down rows of the item and the shared down row, issued only now: loads
+    // in flight together are served interleaved whatever their issue order,
+    // and the hand-off waits for the gate/up rows, not for these.
+    Raw8<true> dr[RG];
+#pragma unroll
+    for (int j = 0; j < RG; ++j) dr[j] = load_raw8_stream<true>(dnb, (size_t)(uint32_t)(min(rw + j, H - 1) * I) + dcol);
+    const Raw8<true> sdr = load_raw8_stream<true>(sdb, (size_t)(uint32_t)((r0 + wave) * I) + dcol);
+    // the slot's activations: 512 words over wavefronts 0-3, two per lane
+    uint64_t raw0 = 0, raw1 = 0;
+    if (wave < 4) {
+      raw0 = load_tagged(ra_src0);
+      raw1 = load_tagged(ra_src1);
     }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const size_t cc = (size_t)min(lane + kWave * j, nch - 1) * 8;
-      pa[j] = g_row16(src_a, row_a + cc);
-      pb[j] = g_row16(src_b, row_b + cc);
+    bool ok = true;
+    const float shv = settle_tagged(shw, sh_src, tag, plim, ok);
+    const float sgv = settle_tagged(sgw, a.ws.f_sgate, tag, plim, ok);
+    if (tid < I) s_sha[tid] = shv;
+    if (tid == 0) s_sg = sgv;
+    lds_barrier();
+    FK_MARK(5);
+    if (wave == kFusedWaves - 1 && lane < kFusedChunk)
+      store_tagged(a.ws.f_act + (size_t)ub * I + i0 + lane, poison_if(bad, s_act16[lane]), tag);
+    if (wave < 4) {
+      const float v0 = settle_tagged(raw0, ra_src0, tag, plim, ok);
+      const float v1 = settle_tagged(raw1, ra_src1, tag, plim, ok);
+      if (tid < I) s_ra[tid] = v0;
+      if (tid + 256 < I) s_ra[tid + 256] = v1;
     }
-  };
-  // The descriptors are read once into LDS: read from global memory where a
-  // phase needs them, they would be vector loads (the kernel writes global
-  // memory, so the compiler cannot serve them from the scalar cache), each
-  // waited for on the spot.
-  {
-    const __attribute__((address_space(1))) uint64_t* gd = (const __attribute__((address_space(1))) uint64_t*)sa.layers;
-    for (int w = tid; w < L * 13; w += 512) s_desc_w[w] = gd[w];
-  }
-  __syncthreads();
-  const fk_moe_stack_layer* s_desc = reinterpret_cast<const fk_moe_stack_layer*>(s_desc_w);
-  if (has_unit) issue_unit(s_desc[0]);
-  // layer 0's input into LDS (chunk tid of the H / 8, threads tid < nch)
-  {
-    const Raw8<BFX0> x0r = load_raw8<BFX0>(sa.x0, (size_t)min(tid, nch - 1) * 8);
-    if (tid < nch) {
-      float x8[8];
-      raw8_to_f32<BFX0>(x0r, x8);
-      float4* d = reinterpret_cast<float4*>(s_x + tid * 8);
-      d[0] = make_float4(x8[0], x8[1], x8[2], x8[3]);
-      d[1] = make_float4(x8[4], x8[5], x8[6], x8[7]);
-    }
-  }
-  const WaitLimits wl = hdr.limits();
-  const uint32_t tag = wl.tag, plim = wl.poll;
-
-  for (int l = 0; l < L; ++l) {
-    // The thread index, made opaque once per layer: per-lane addresses
-    // derived from it are recomputed in each layer instead of being hoisted
-    // out of the loop and held in registers across all of it.
-    int tid_l = threadIdx.x;
-    asm volatile("" : "+v"(tid_l));
-    const int tid = tid_l, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int q0 = wave * G + b;
-    FK_MARK(1);
-    const fk_moe_stack_layer& ly = s_desc[l];
-    uint64_t* f_logits = sa.words + (size_t)l * kStackLayerWords;
-    uint64_t* f_act = f_logits + 256;
-    uint64_t* f_sgate = f_act + 9 * 512;
-    uint64_t* f_x = f_sgate + 64;
-    // ---- X: the layer's input into LDS (layer 0's: before the loop) -------
-    if (l > 0) {
-      const uint64_t* px = sa.words + (size_t)(l - 1) * kStackLayerWords + 256 + 9 * 512 + 64;
-      uint64_t w[kStackMaxH / 512];
-      if (!poll_run<kStackMaxH / 512>(w, px, tid, 512, H, tag, plim)) s_fail = 1;
-#pragma unroll
-      for (int j = 0; j < kStackMaxH / 512; ++j)
-        if (tid + 512 * j < H) s_x[tid + 512 * j] = value_of(w[j]);
-    }
-    __syncthreads();
-    FK_MARK(2);
-
-    // ---- P1: this workgroup's unit (as moe_fused_kernel, x from LDS) -----
-    if (has_unit) {
-      float mine = 0.f;
-      if (unit < nrb) {
-        const int e = unit * 8 + wave;
-        if (e < E) {
-          float wn[4][8];
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int c = lane + kWave * j;
-            float w8[8], n8[8];
-            bf16x8_to_f32(pb[j], n8);
-            bf16x8_to_f32(pa[j], w8);
-#pragma unroll
-            for (int qq = 0; qq < 8; ++qq) wn[j][qq] = c < nch ? w8[qq] * (sa.off + n8[qq]) : 0.f;
-          }
-          const float bias = ly.router_bias ? g_scalar(ly.router_bias, sa.bias_dt, e) : 0.f;
-          float ss = 0.f, d = 0.f;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int c = lane + kWave * j;
-            const bool in = c < nch;
-            const float4* xp = reinterpret_cast<const float4*>(s_x + (size_t)min(c, nch - 1) * 8);
-            const float4 xa = xp[0], xb = xp[1];
-            const float x8[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-#pragma unroll
-            for (int qq = 0; qq < 8; ++qq) {
-              const float xv = in ? x8[qq] : 0.f;
-              ss = fmaf(xv, xv, ss);
-              d = fmaf(xv, wn[j][qq], d);
-            }
-          }
-          ss = wave_sum(ss);
-          d = wave_sum(d);
-          mine = d * rsqrtf(ss / (float)H + sa.eps) + bias;
-        }
-      } else if (unit < nrb + nsb) {
-        float g = 0.f, u = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int c = lane + kWave * j;
-          if (c < nch) {
-            float a8[8], b8[8];
-            const float4* xp = reinterpret_cast<const float4*>(s_x + (size_t)c * 8);
-            const float4 xa = xp[0], xb = xp[1];
-            const float x8[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-            bf16x8_to_f32(pa[j], a8);
-            bf16x8_to_f32(pb[j], b8);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-              g = fmaf(a8[q], x8[q], g);
-              u = fmaf(b8[q], x8[q], u);
-            }
-          }
-        }
-        g = wave_sum(g);
-        u = wave_sum(u);
-        mine = silu(g) * u;
-      } else if (wave == 0) {
-        float g8[4][8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int c = lane + kWave * j;
-          bf16x8_to_f32(pa[j], g8[j]);
-#pragma unroll
-          for (int qq = 0; qq < 8; ++qq) g8[j][qq] = (ly.shared_gate && c < nch) ? g8[j][qq] : 0.f;
-        }
-        float d = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float4* xp = reinterpret_cast<const float4*>(s_x + (size_t)min(lane + kWave * j, nch - 1) * 8);
-          const float4 xa = xp[0], xb = xp[1];
-          const float x8[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-#pragma unroll
-          for (int qq = 0; qq < 8; ++qq) d = fmaf(x8[qq], g8[j][qq], d);
-        }
-        d = wave_sum(d);
-        mine = ly.shared_gate ? sigmoid(d) : 1.f;
-      }
-      if (lane == 0) s_chunk[wave] = mine;
-      __syncthreads();
-      if (tid < 8) {
-        const float v = s_chunk[tid];
-        if (unit < nrb) {
-          const int e = unit * 8 + tid;
-          if (e < E) {
-            g_store(ly.logits, (size_t)e, v);
-            store_tagged(f_logits + e, v, tag);
-          }
-        } else if (unit < nrb + nsb) {
-          store_tagged(f_act + (size_t)P * I + (unit - nrb) * 8 + tid, v, tag);
-        } else if (tid == 0) {
-          store_tagged(f_sgate, v, tag);
-        }
-      }
-    }
-    if (l == 0) {
-      // started record (every wavefront has used the epoch it read)
-      if (lane == 0) s_wtag[wave] = tag;
-      __syncthreads();
-      if (tid == 0) store_tagged(sa.started + b, __uint_as_float(s_wtag[kFusedWaves - 1]), tag);
-    }
-    FK_MARK(3);
-    // this wavefront's shared down row
-    const int r_first = q0;
-    Raw8<true> sdr;
-    sdr.a = g_row16_nt(ly.shared_down, (size_t)min(r_first, H - 1) * I + (size_t)min(lane * 8, I - 8));
-    sdr.b = u32x4{0, 0, 0, 0};
-
-    // ---- P2: top-k in every workgroup ------------------------------------
-    if (wave == 0) {
-      constexpr int NJE = kFusedMaxExperts / kWave;
-      uint64_t w[NJE];
-      const uint64_t* srcs[NJE];
-#pragma unroll
-      for (int j = 0; j < NJE; ++j) {
-        const int ex = lane + kWave * j;
-        srcs[j] = ex < E ? f_logits + ex : nullptr;
-        w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
-      }
-      const bool ok = poll_tagged<NJE>(w, srcs, tag, plim);
-      if (!ok) s_fail = 1;
-      float p[NJE];
-#pragma unroll
-      for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
-      int tk_id = 0;
-      float tk_w = 0.f;
-      topk_select_regs<NJE>(p, E, K, lane, tk_id, tk_w);
-      if (!ok) tk_id = min(max(tk_id, 0), E - 1);
-      if (lane < K) {
-        s_ids[lane] = tk_id;
-        s_w[lane] = tk_w;
-        s_active[lane] = tk_id;
-        s_wpos[lane] = tk_w;
-      }
-    } else if (l == 0 && b == 0) {
-      // workgroup 0: every workgroup of the launch has read the epoch
-      constexpr int kChunk = 4;
-      const int nthr = (kFusedWaves - 1) * kWave;
-      for (int base = tid - kWave; base < G; base += kChunk * nthr) {
-        uint64_t w[kChunk];
-        const uint64_t* srcs[kChunk];
-#pragma unroll
-        for (int j = 0; j < kChunk; ++j) {
-          const int r = base + j * nthr;
-          srcs[j] = r < G ? sa.started + r : nullptr;
-          w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
-        }
-        if (!poll_tagged<kChunk>(w, srcs, tag, plim)) s_fail = 1;
-      }
-    }
-    __syncthreads();
-    const bool bad = s_fail;
-    if (l == 0 && b == 0 && tid == 0 && !bad) store_coherent(&sa.tickets[kTicketEpoch], tag);
-    if (b == 0 && tid < K) {
-      g_store(ly.topk_ids, (size_t)tid, (int64_t)s_ids[tid]);
-      g_store(ly.topk_weights, (size_t)tid, poison_if(bad, s_w[tid]));
-    }
-    FK_MARK(4);
-
-    // ---- P3: routed gate/up (+ down-row prefetch) --------------------------
-    const int U = K, bpe = I / kFusedChunk, nblk = U * bpe;
-    const bool prefetch = r_first < H;
-    Raw8<true> dr[NPF];
-#pragma unroll
-    for (int u = 0; u < NPF; ++u) dr[u].b = u32x4{0, 0, 0, 0};
+    if (!ok) s_fail = 1;
+    lds_barrier();
+    FK_MARK(6);
+    // down: 8 rows per wavefront (lanes 8 j .. 8 j + 7 end with row j), and
+    // one shared row
     {
-      const void* gu = ly.gate_up;
-      const void* dn = ly.down;
-      const size_t dcol = (size_t)min(lane * 8, I - 8), drow = (size_t)min(r_first, H - 1);
-      auto issue_down = [&]() {
+      float dd[RG];
+      dot8x8_act_lds(dr, s_ra, lane, I, dd);
+      const float v = rows8_sum(dd);
+      if ((lane & 7) == 0) s_ystage[wave * RG + (lane >> 3)] = v;
+    }
+    {
+      const float sh = wave_sum(dot8_act_lds(sdr, s_sha, lane, I));
+      if (lane == 0) s_sh[wave] = sh;
+    }
+    uint64_t yw = 0;
+    if (wave == 0) yw = load_tagged(y_src);
+    lds_barrier();
+    if (wave == kFusedWaves - 1 && rr0 + lane < H)
+      store_tagged(a.ws.f_y + (size_t)ud * H + rr0 + lane, poison_if(s_fail, s_ystage[lane]), tag);
+    FK_MARK(7);
+    if (wave == 0) {
+      bool yok = true;
+      const float yv = settle_tagged(yw, y_src, tag, plim, yok);
+      s_yk[lane] = yv;
+      if (!yok) s_fail = 1;
+    }
+    lds_barrier();
+    if (wave == 0 && lane < RG) {
+      const bool bad_out = s_fail;
+      float acc = 0.f;
 #pragma unroll
-        for (int u = 0; u < NPF; ++u)
-          dr[u].a = g_row16_nt(dn, ((size_t)s_active[min(u, U - 1)] * H + drow) * I + dcol);
+      for (int k = 0; k < kFusedMaxPairs; ++k)
+        if (k < K) acc += s_wpos[k] * s_yk[k * RG + lane];
+      acc += s_sg * s_sh[lane];
+      const float o = poison_if(bad_out, acc);
+      f.out[r0 + lane] = o;
+      if (f.layer_out) f.layer_out[r0 + lane] = raw_value<BFX>(x_raw[0]) + o;
+    }
+  } else {
+    // The shared activations and gate, one word per thread: stored in P1, so
+    // the first read finds them; issued behind the first gate/up rows.
+    uint64_t shw[2];
+    const uint64_t* shs[2] = {tid < I ? a.ws.f_act + (size_t)P * I + tid : nullptr, tid == 0 ? a.ws.f_sgate : nullptr};
+    {
+      Raw8<BFX> xt[4];
+  #pragma unroll
+      for (int j = 0; j < 4; ++j) xt[j] = load_raw8<BFX>(a.x, (size_t)min(lane + kWave * j, nch - 1) * 8);
+      bool first = true;
+      auto issue_shared = [&]() {
+        if (first) {
+  #pragma unroll
+          for (int j = 0; j < 2; ++j) shw[j] = shs[j] ? load_tagged(shs[j]) : 0ull;
+        }
       };
-      auto block = [&](int blk, bool first_blk) {
-        const int u = blk / bpe, i0 = (blk - u * bpe) * kFusedChunk;
-        const int ia = i0 + 2 * wave;
-        const size_t we = (size_t)s_active[u] * 2 * I * H;  // (elements)
-        u32x4 ga[4], ua8[4], gb[4], ub8[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const size_t c8 = (size_t)min(lane + kWave * j, nch - 1) * 8;
-          ga[j] = g_row16_nt(gu, we + (size_t)ia * H + c8);
-          gb[j] = g_row16_nt(gu, we + (size_t)(ia + 1) * H + c8);
-          ua8[j] = g_row16_nt(gu, we + (size_t)(I + ia) * H + c8);
-          ub8[j] = g_row16_nt(gu, we + (size_t)(I + ia + 1) * H + c8);
-        }
-        float acc[4] = {0.f, 0.f, 0.f, 0.f};  // gate ia, up ia, gate ia + 1, up ia + 1
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int c = lane + kWave * j;
-          if (c < nch) {
-            float w8[8];
-            const float4* xp = reinterpret_cast<const float4*>(s_x + (size_t)c * 8);
-            const float4 xa = xp[0], xb = xp[1];
-            const float x8[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-            bf16x8_to_f32(ga[j], w8);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) acc[0] = fmaf(w8[q], x8[q], acc[0]);
-            bf16x8_to_f32(ua8[j], w8);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) acc[1] = fmaf(w8[q], x8[q], acc[1]);
-            bf16x8_to_f32(gb[j], w8);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) acc[2] = fmaf(w8[q], x8[q], acc[2]);
-            bf16x8_to_f32(ub8[j], w8);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) acc[3] = fmaf(w8[q], x8[q], acc[3]);
-          }
-        }
-        const float rs = rows4_sum(acc);
-        const float g0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 0));
-        const float u0 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 16));
-        const float g1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 32));
-        const float u1 = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(rs), 48));
-        if (lane == 0) {
-          s_chunk[2 * wave] = silu(g0) * u0;
-          s_chunk[2 * wave + 1] = silu(g1) * u1;
-        }
-        __syncthreads();
-        if (tid < kFusedChunk) store_tagged(f_act + (size_t)u * I + i0 + tid, poison_if(bad, s_chunk[tid]), tag);
-        if (first_blk) issue_down();  // (after the gate/up rows are in, as in moe_fused_kernel)
-        __syncthreads();
-      };
-      if (b < nblk) {
-        block(b, true);
-        for (int blk = b + G; blk < nblk; blk += G) block(blk, false);
-      } else {
-        issue_down();
+      if (b >= nblk) {
+        issue_shared();
+      }
+      for (int blk = b; blk < nblk; blk += G) {
+        // intermediates ia, ia + 1 of slot u in this wavefront
+        const int u_ = blk / bpe, ia = (blk - u_ * bpe) * kFusedChunk + 2 * wave;
+        const char* we = gu + (size_t)s_active[u_] * expb;
+        const char* g[2] = {we + (size_t)ia * rowb, we + (size_t)(ia + 1) * rowb};
+        const char* u[2] = {we + (size_t)(I + ia) * rowb, we + (size_t)(I + ia + 1) * rowb};
+        float act[2];
+        fused_gu_rows<BFX, 2>(xt, g, u, nch, lane, act, issue_shared);
+        first = false;
+        if (lane < 2) store_tagged(a.ws.f_act + (size_t)u_ * I + ia + lane, poison_if(bad, lane ? act[1] : act[0]), tag);
       }
     }
+    // The first down item's rows and the shared down row of the first row
+    // group, issued only now: loads in flight together are served interleaved
+    // whatever their issue order, and the hand-off waits for the gate/up rows,
+    // not for these.  (wave-uniform: the down code reduces across lanes with
+    // lane swaps, which read inactive lanes' stale registers)
+    const bool dn0 = b < ndn, grp0 = r0 < H;
+    Raw8<true> dr[RG], sdr;
+    auto issue_down = [&](int d, Raw8<true> (&w)[RG]) {
+      const int u_ = d / cpe, rr = (d - u_ * cpe) * DR + wave * RG;
+      const size_t ex = (size_t)s_active[u_];
+  #pragma unroll
+      for (int j = 0; j < RG; ++j) w[j] = load_raw8_stream<true>(f.dn, (ex * H + min(rr + j, H - 1)) * I + dcol);
+    };
+    if (dn0) issue_down(b, dr);
+    if (grp0) sdr = load_raw8_stream<true>(f.sdn, (size_t)(r0 + wave) * I + dcol);
+    // the shared words
+    if (!poll_tagged<2>(shw, shs, tag, plim)) s_fail = 1;
+    if (tid < I) s_sha[tid] = value_of(shw[0]);
+    if (tid == 0) s_sg = value_of(shw[1]);
+    lds_barrier();
     FK_MARK(5);
 
-    // ---- P4: activations, next layer's unit rows, down rows, combine -----
-    // ((K + 1) I <= 9 * 512 activations: 9 words per thread; the shared gate
-    // by thread 0)
-    const int n_act = (P + 1) * I;
-    bool stage_ok;
-    {
-      uint64_t w[9];
-      stage_ok = poll_run<9>(w, f_act, tid, 512, n_act, tag, plim);
-#pragma unroll
-      for (int j = 0; j < 9; ++j)
-        if (tid + 512 * j < n_act) s_act[tid + 512 * j] = value_of(w[j]);
-      if (tid == 0) {
-        uint64_t g[1];
-        stage_ok = poll_run<1>(g, f_sgate, 0, 1, 1, tag, plim) && stage_ok;
-        s_act[n_act] = value_of(g[0]);
+    // ---------------- P4: down items -----------------------------------------
+    // The item's slot activations, one word per thread, then its 64 rows.
+    auto down_item = [&](int d, const Raw8<true> (&w)[RG]) {
+      const int u_ = d / cpe, rr = (d - u_ * cpe) * DR + wave * RG;
+      {
+        uint64_t aw[1];
+        const uint64_t* as[1] = {tid < I ? a.ws.f_act + (size_t)u_ * I + tid : nullptr};
+        aw[0] = as[0] ? load_tagged(as[0]) : 0ull;
+        if (!poll_tagged<1>(aw, as, tag, plim)) s_fail = 1;
+        if (tid < I) s_ra[tid] = value_of(aw[0]);
       }
+      lds_barrier();
+      float dd[RG];
+  #pragma unroll
+      for (int j = 0; j < RG; ++j) dd[j] = dot8_act_lds(w[j], s_ra, lane, I);
+      const float v = rows8_sum(dd);
+      const int row = rr + (lane >> 3);
+      if ((lane & 7) == 0 && row < H) store_tagged(a.ws.f_y + (size_t)u_ * H + row, poison_if(s_fail, v), tag);
+      lds_barrier();  // s_ra is rewritten by the next item
+    };
+    if (dn0) down_item(b, dr);
+    for (int d = b + G; d < ndn; d += G) {
+      Raw8<true> w[RG];
+      issue_down(d, w);
+      down_item(d, w);
     }
-    if (!stage_ok) s_fail = 1;
-    __syncthreads();
-    const bool bad_out = s_fail;
-    // the next layer's unit rows: issued after the activation polls (a
-    // wavefront's loads retire in order, so rows issued before them would
-    // hold the polls back); they arrive during the down rows and the next
-    // layer's input hand-off
-    if (l + 1 < L && has_unit) issue_unit(s_desc[l + 1]);
     FK_MARK(6);
-    const float* s_sg = s_act + n_act;
-    for (int r = q0; r < H; r += NW) {
-      const bool first = r == r_first;
-      float acc;
-      if (first && prefetch) {
-        acc = s_sg[0] * dot8_act_lds(sdr, s_act + (size_t)P * I, lane, I);
-#pragma unroll
-        for (int u = 0; u < NPF; ++u) {
-          const float d = dot8_act_lds(dr[u], s_act + (size_t)(u < U ? u : 0) * I, lane, I);
-          acc = u < U ? fmaf(s_wpos[u], d, acc) : acc;
-        }
-      } else {
-        // (not reached at the host-checked shapes: every row is a first row)
-        acc = 0.f;
+
+    // ---------------- P5: combine of the workgroup's output rows -------------
+    auto final_group = [&](int rg0, const Raw8<true>& ws) {
+      const float sh = wave_sum(dot8_act_lds(ws, s_sha, lane, I));
+      if (lane == 0) s_sh[wave] = sh;
+      if (wave == 0) {
+        // lane (k, j) = (l / 8, l % 8): y of slot k at row rg0 + j
+        const int k = lane >> 3, j = lane & 7;
+        uint64_t yw[1];
+        const uint64_t* ys[1] = {k < K ? a.ws.f_y + (size_t)k * H + rg0 + j : nullptr};
+        yw[0] = ys[0] ? load_tagged(ys[0]) : 0ull;
+        if (!poll_tagged<1>(yw, ys, tag, plim)) s_fail = 1;
+        s_yk[lane] = value_of(yw[0]);
       }
-      const float o = poison_if(bad_out, wave_sum(acc));
-      if (lane == 0) {
-        const float lo = s_x[r] + o;
-        g_store(ly.moe_out, (size_t)r, o);
-        g_store(ly.layer_out, (size_t)r, lo);
-        store_tagged(f_x + r, lo, tag);
+      lds_barrier();
+      if (wave == 0 && lane < RG) {
+        const bool bad_out = s_fail;
+        float acc = 0.f;
+  #pragma unroll
+        for (int k = 0; k < kFusedMaxPairs; ++k)
+          if (k < K) acc += s_wpos[k] * s_yk[k * RG + lane];
+        acc += s_sg * s_sh[lane];
+        const float o = poison_if(bad_out, acc);
+        const int r = rg0 + lane;
+        f.out[r] = o;
+        if (f.layer_out)
+          f.layer_out[r] = (rg0 == r0 ? raw_value<BFX>(x_raw[0]) : load_scalar(a.x, BFX ? FK_DTYPE_BF16 : FK_DTYPE_F32, r)) + o;
       }
+      lds_barrier();
+    };
+    if (grp0) {
+      FK_MARK(7);
+      final_group(r0, sdr);
     }
-    __syncthreads();  // s_x and s_act are reused by the next layer
-    FK_MARK(7);
+    for (int grp = b + G; grp < ngrp; grp += G) {
+      const int rg0 = grp * RG;
+      const Raw8<true> ws = load_raw8_stream<true>(f.sdn, (size_t)(rg0 + wave) * I + dcol);
+      final_group(rg0, ws);
+    }
   }
+  // A failed wait anywhere in the workgroup sets the workspace's error word.
+  lds_barrier();
   if (tid == 0 && s_fail) __hip_atomic_fetch_or(err, FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  FK_TIMELINE_COMMIT(moe_stack, blockIdx.x);
+  FK_MARK(8);
+  FK_TIMELINE_COMMIT(moe_fused, blockIdx.x);
 }
 
 // ---------------------------------------------------------------------------
@@ -2614,64 +2400,26 @@ static int check_ws(void* ws, size_t bytes, int T, int K, int E, int I, int H, M
 // when there is no gate weight).
 static bool fused_eligible(int T, int H, int I, int E, int K, int router_dt, int expert_dt, bool has_shared, int norm_dt,
                            bool has_gate, int gate_dt) {
-  return T >= 1 && T <= kFusedMaxTokens && H <= 2048 && I <= 512 && I % kFusedChunk == 0 && E <= kFusedMaxExperts && K <= 8 &&
+  return T >= 1 && T <= kFusedMaxTokens && H <= 2048 && H % 8 == 0 && I <= 512 && I % kFusedChunk == 0 && E <= kFusedMaxExperts && K <= 8 &&
          router_dt == FK_DTYPE_BF16 && expert_dt == FK_DTYPE_BF16 && has_shared && norm_dt == FK_DTYPE_BF16 &&
          (!has_gate || gate_dt == FK_DTYPE_BF16);
 }
 
-constexpr size_t kFusedMaxDynLds = ((size_t)(kFusedMaxPairs + kFusedMaxTokens) * 512 + kFusedMaxTokens) * sizeof(float);
-
 template <bool BX>
 static int launch_fused_t(const FusedArgs& fa, hipStream_t stream) {
   static int cap_cache[64] = {0};
-  static bool attr_set[64] = {false};
-  auto kernel = moe_fused_kernel<BX>;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(FK_ERR_LAUNCH, "no current HIP device");
-  if (!attr_set[dev]) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)kFusedMaxDynLds) != hipSuccess)
-      return fail(FK_ERR_LAUNCH, "cannot reserve %zu bytes of LDS for the fused MoE kernel", kFusedMaxDynLds);
-    attr_set[dev] = true;
-  }
-  const size_t shm = ((size_t)(fa.r.T * fa.r.K + fa.r.T) * fa.I + fa.r.T) * sizeof(float);
-  const int cap = resident_capacity(kernel, 512, kFusedMaxDynLds, cap_cache);
+  const int cap = resident_capacity(moe_fused_kernel<BX, false>, 512, 0, cap_cache);
   const int cus = device_cus();
   const int G = cap < cus ? cap : cus;  // one workgroup per CU
   if (G < 1) return fail(FK_ERR_UNSUPPORTED, "fused MoE kernel does not fit on this device");
   if (G > kFusedMaxGrid) return fail(FK_ERR_UNSUPPORTED, "fused MoE grid %d exceeds %d workgroups", G, kFusedMaxGrid);
-  hipLaunchKernelGGL(kernel, dim3(G), dim3(512), shm, stream, fa);
+  // one workgroup per gate/up block (16 intermediates of a slot), per down
+  // item (64 rows of a slot) and per row group (8 output rows)
+  const int K = fa.r.K, H = fa.r.H, I = fa.I;
+  const bool fast = G == K * (I / kFusedChunk) && G == K * ((H + 63) / 64) && G * 8 == H;
+  if (fast) hipLaunchKernelGGL((moe_fused_kernel<BX, true>), dim3(G), dim3(512), 0, stream, fa);
+  else hipLaunchKernelGGL((moe_fused_kernel<BX, false>), dim3(G), dim3(512), 0, stream, fa);
   return check_launch("moe_fused_kernel");
-}
-
-// Single-launch run of layers (T = 1): shapes the kernel handles on a grid
-// of G workgroups (every P1 unit on its own workgroup, one down row per
-// wavefront).
-static bool stack_eligible(int H, int I, int E, int K, int G) {
-  const int nunits = (E + 7) / 8 + I / 8 + 1;
-  return H >= 8 && H <= kStackMaxH && H % 8 == 0 && I >= kFusedChunk && I <= 512 && I % kFusedChunk == 0 && E >= 1 &&
-         E <= kFusedMaxExperts && K >= 1 && K <= 8 && K <= E && nunits <= G && G * kFusedWaves >= H && G <= kFusedMaxGrid;
-}
-
-template <bool BX>
-static int stack_grid() {
-  static int cap_cache[64] = {0};
-  const int cap = resident_capacity(moe_stack_kernel<BX>, 512, kStackMaxDynLds, cap_cache);
-  const int cus = device_cus();
-  return cap < cus ? cap : cus;  // one workgroup per CU
-}
-
-static size_t stack_ws_layout(int L, char* base, uint32_t** tickets, uint64_t** started, uint64_t** words) {
-  size_t off = 0;
-  auto take = [&](size_t bytes) {
-    size_t at = off;
-    off = align_up(off + bytes, 256);
-    return base ? base + at : nullptr;
-  };
-  *tickets = reinterpret_cast<uint32_t*>(take(16 * sizeof(uint32_t)));
-  *started = reinterpret_cast<uint64_t*>(take((size_t)kFusedMaxGrid * 8));
-  *words = reinterpret_cast<uint64_t*>(take((size_t)L * kStackLayerWords * 8));
-  return off;
 }
 
 template <bool BW, bool BX, int NJ, int NJE>
@@ -3071,53 +2819,6 @@ int fk_moe_layer(const void* hidden, int hidden_dtype, const void* norm_weight, 
                                    shared_gate_dtype, tokens, hidden_size, intermediate, num_experts, top_k,
                                    moe_out, layer_out, ws);
   return launch_experts(ea, expert_dtype, as_stream(stream));
-}
-
-size_t fk_moe_stack_workspace_bytes(int num_layers, int num_experts, int top_k, int intermediate, int hidden_size) {
-  if (num_layers < 1 || num_experts < 1 || top_k < 1 || intermediate < 1 || hidden_size < 1) return 0;
-  uint32_t* t;
-  uint64_t *s, *w;
-  return stack_ws_layout(num_layers, nullptr, &t, &s, &w);
-}
-
-int fk_moe_stack_decode(const void* hidden, int hidden_dtype, const fk_moe_stack_layer* layers, int num_layers,
-                        int bias_dtype, int hidden_size, int intermediate, int num_experts, int top_k, float eps,
-                        float norm_offset, void* workspace, size_t workspace_bytes, void* stream) {
-  if (num_layers < 1) return fail(FK_ERR_INVALID, "num_layers must be positive");
-  if (num_layers > kStackMaxLayers)
-    return fail(FK_ERR_UNSUPPORTED, "num_layers must be <= %d per call (chain longer runs through layer_out)",
-                kStackMaxLayers);
-  if (!hidden || !layers) return fail(FK_ERR_INVALID, "hidden and layers must be non-NULL");
-  if (!is_float_dtype(hidden_dtype) || !is_float_dtype(bias_dtype))
-    return fail(FK_ERR_DTYPE, "hidden and router bias must be f32 or bf16");
-  if (!aligned16(hidden)) return fail(FK_ERR_ALIGNMENT, "hidden must be 16-byte aligned");
-  const bool bx = hidden_dtype == FK_DTYPE_BF16;
-  const int G = bx ? stack_grid<true>() : stack_grid<false>();
-  if (!stack_eligible(hidden_size, intermediate, num_experts, top_k, G))
-    return fail(FK_ERR_UNSUPPORTED,
-                "fk_moe_stack_decode: hidden_size <= %d (multiple of 8), intermediate <= 512 (multiple of %d), "
-                "num_experts <= %d, top_k <= 8 on a grid of %d workgroups",
-                kStackMaxH, kFusedChunk, kFusedMaxExperts, G);
-  StackArgs sa;
-  const size_t need = stack_ws_layout(num_layers, nullptr, &sa.tickets, &sa.started, &sa.words);
-  if (!workspace || workspace_bytes < need)
-    return fail(FK_ERR_WORKSPACE, "stack workspace needs %zu bytes (got %zu)", need, workspace_bytes);
-  stack_ws_layout(num_layers, reinterpret_cast<char*>(workspace), &sa.tickets, &sa.started, &sa.words);
-  sa.x0 = hidden;
-  sa.layers = layers;
-  sa.L = num_layers;
-  sa.bias_dt = bias_dtype;
-  sa.H = hidden_size;
-  sa.I = intermediate;
-  sa.E = num_experts;
-  sa.K = top_k;
-  sa.eps = eps;
-  sa.off = norm_offset;
-  const size_t shm = kStackMaxDynLds;
-  const hipStream_t s = as_stream(stream);
-  if (bx) hipLaunchKernelGGL(moe_stack_kernel<true>, dim3(G), dim3(512), shm, s, sa);
-  else hipLaunchKernelGGL(moe_stack_kernel<false>, dim3(G), dim3(512), shm, s, sa);
-  return check_launch("moe_stack_kernel");
 }
 
 int fk_moe_layer_noalloc(const void* hidden, int hidden_dtype, const void* norm_weight, int norm_dtype,

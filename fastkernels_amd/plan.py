@@ -10,10 +10,6 @@ graph (torch.cuda.CUDAGraph), which is how bench.py times them.
   DeltaNetStepPlan  projections + conv -> recurrent/gated-norm -> out-proj
                     (+ residual) through fk_deltanet_step, writing the next
                     conv / recurrent states.
-  MoeStackPlan      a run of MoE layers at one token, each layer's input the
-                    previous layer's output, as ONE launch
-                    (fk_moe_stack_decode); outputs equal a chain of
-                    MoeLayerPlans bit for bit.
   AttentionStepPlan gated full attention (+ residual) through
                     fk_attention_decode at a device-held position that the
                     step advances itself, with the KV
@@ -147,102 +143,6 @@ class MoeLayerPlan:
             self.tokens, self.hidden_size, self.intermediate, self.num_experts, self.top_k,
             self.moe_out.data_ptr(), self.layer_out.data_ptr(),
             self.workspace.data_ptr(), self.workspace.numel(), _stream_handle(stream, self.device),
-        )
-
-    def check_device(self, stream: torch.cuda.Stream | None = None) -> None:
-        _check_device(self.workspace, self.device, stream)
-
-    def set_poll_limit(self, limit: int | None, stream: torch.cuda.Stream | None = None) -> None:
-        _set_poll_limit(self.workspace, self.device, limit, stream)
-
-
-class MoeStackPlan:
-    """A run of MoE layers at one token in one launch (fk_moe_stack_decode).
-
-    Layer 0 reads `hidden` ([1, H], bf16 or f32); layer l > 0 reads layer
-    l-1's `layer_out[l-1]` (f32), as a chain of MoeLayerPlans with
-    `hidden=prev.layer_out` does, and every output equals that chain's bit
-    for bit.  Per layer: `logits[l]` [1, E], `ids[l]` / `weights[l]` [1, K],
-    `moe_out[l]` and `layer_out[l]` [1, H].  The layer descriptors (device
-    pointers of the weights and outputs) live in a device tensor the plan
-    owns, so a captured step replays with no host work.  At most 64 layers
-    per plan (chain plans for longer runs through `hidden=`).
-    """
-
-    def __init__(
-        self,
-        layer_weights: list[dict[str, Any]],
-        *,
-        top_k: int = 8,
-        eps: float = 1e-6,
-        norm_offset: float = 1.0,
-        router_biases: list[Any] | None = None,
-        hidden: torch.Tensor | None = None,
-        hidden_dtype: torch.dtype = torch.bfloat16,
-    ) -> None:
-        self.lib = _lib.load()
-        if not layer_weights:
-            raise ValueError("at least one layer is needed")
-        ws = []
-        for w in layer_weights:
-            if hasattr(w, "as_dict"):
-                w = w.as_dict()
-            ws.append({k: (None if v is None else _dense(v)) for k, v in w.items()})
-        self.w = ws
-        gu = ws[0]["expert_gate_up_weight"]
-        self.device = dev = gu.device
-        self.num_experts, two_i, self.hidden_size = gu.shape
-        self.intermediate = two_i // 2
-        self.num_layers = L = len(ws)
-        self.top_k = top_k
-        self.eps = float(eps)
-        self.norm_offset = float(norm_offset)
-        H, E, K = self.hidden_size, self.num_experts, top_k
-        for w in ws:
-            for name in ("norm_weight", "router_weight", "expert_gate_up_weight", "expert_down_weight",
-                         "shared_gate_up_weight", "shared_down_weight"):
-                if w[name].dtype != torch.bfloat16:
-                    raise ValueError(f"{name} must be bfloat16 for the single-launch layer run")
-            sg = w.get("shared_expert_gate_weight")
-            if sg is not None and sg.dtype != torch.bfloat16:
-                raise ValueError("shared_expert_gate_weight must be bfloat16 for the single-launch layer run")
-            if w["expert_gate_up_weight"].shape != gu.shape:
-                raise ValueError("every layer of a run needs the same shapes")
-        self.router_biases = [None if b is None else _dense(b) for b in (router_biases or [None] * L)]
-        if len(self.router_biases) != L:
-            raise ValueError("router_biases needs one entry per layer")
-        codes = {_fcode(b, "router_bias") for b in self.router_biases if b is not None}
-        if len(codes) > 1:
-            raise ValueError("the router biases of a run must share one dtype")
-        self.bias_code = codes.pop() if codes else _lib.FK_DTYPE_F32
-        self.hidden = hidden if hidden is not None else torch.zeros((1, H), dtype=hidden_dtype, device=dev)
-        self.logits = torch.empty((L, 1, E), dtype=torch.float32, device=dev)
-        self.ids = torch.empty((L, 1, K), dtype=torch.int64, device=dev)
-        self.weights = torch.empty((L, 1, K), dtype=torch.float32, device=dev)
-        self.moe_out = torch.empty((L, 1, H), dtype=torch.float32, device=dev)
-        self.layer_out = torch.empty((L, 1, H), dtype=torch.float32, device=dev)
-        rows = []
-        for l, w in enumerate(ws):
-            sg = w.get("shared_expert_gate_weight")
-            b = self.router_biases[l]
-            rows.append([
-                w["norm_weight"].data_ptr(), w["router_weight"].data_ptr(), 0 if b is None else b.data_ptr(),
-                w["expert_gate_up_weight"].data_ptr(), w["expert_down_weight"].data_ptr(),
-                w["shared_gate_up_weight"].data_ptr(), w["shared_down_weight"].data_ptr(),
-                0 if sg is None else sg.data_ptr(),
-                self.logits[l].data_ptr(), self.ids[l].data_ptr(), self.weights[l].data_ptr(),
-                self.moe_out[l].data_ptr(), self.layer_out[l].data_ptr(),
-            ])
-        self.descriptors = torch.tensor(rows, dtype=torch.int64).to(dev)
-        nbytes = self.lib.fk_moe_stack_workspace_bytes(L, E, K, self.intermediate, H)
-        self.workspace = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
-
-    def run(self, stream: torch.cuda.Stream | None = None) -> None:
-        _lib.call(
-            "fk_moe_stack_decode",
-            self.hidden.data_ptr(), _fcode(self.hidden, "hidden"), self.descriptors.data_ptr(), self.num_layers,
-            self.bias_code, self.hidden_size, self.intermediate, self.num_experts, self.top_k, self.eps,
-            self.norm_offset, self.workspace.data_ptr(), self.workspace.numel(), _stream_handle(stream, self.device),
         )
 
     def check_device(self, stream: torch.cuda.Stream | None = None) -> None:

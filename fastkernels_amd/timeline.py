@@ -6,15 +6,12 @@ Usage, on a GPU, after ``python -m fastkernels_amd.build --timeline``::
     python -m fastkernels_amd.timeline deltanet --tokens 8
     python -m fastkernels_amd.timeline router --tokens 128 --zipf
     python -m fastkernels_amd.timeline attention --tokens 1 --context 1024
-    python -m fastkernels_amd.timeline stack --layers 8
 
 It loads ``libfastkernels_hip_timeline.so``: the same kernels compiled with
 ``-DFK_TIMELINE``, in which thread 0 of every workgroup of
 ``moe_fused_kernel`` (the MoE layer at T = 1), ``moe_router_tagged_kernel``
 (the router stage from two tokens on; the layer's router stage alone is
-timed), ``moe_stack_kernel`` (a run of ``--layers`` MoE layers in one launch;
-the markers after the first keep the last layer's times),
-``deltanet_step_kernel`` and ``attn_step_kernel`` (the attention step
+timed), ``deltanet_step_kernel`` and ``attn_step_kernel`` (the attention step
 after ``--context`` cached positions) keeps the wall clock (100 MHz) at each
 phase boundary.  Steps run in steady
 state: 16 back-to-back steps over 4 weight sets are captured as one HIP graph
@@ -40,13 +37,17 @@ MARKERS = {
         "moe_fused",
         [
             "workgroup start",
-            "router rows, shared gate/up and gate done (logits stored)",
+            "P1 item done (router row, shared intermediate or gate stored)",
             "logits of the token polled",
             "top-k selected",
-            "routing tables built",
-            "routed gate/up done (activations stored)",
-            "activations staged in LDS",
-            "down rows and combine written (end)",
+            "routing table in LDS",
+            "routed gate/up block done, down rows issued, shared activations in LDS",
+            "the down item's slot activations in LDS",
+            "down rows applied, y stored (wavefront 7)",
+            "end: y of the K slots polled, rows written",
+            "fast path: wavefront 0 issues its gate/up rows",
+            "fast path: wavefront 0's gate/up rows issued",
+            "fast path: wavefront 0's gate/up products done",
         ],
     ),
     "router": (
@@ -58,19 +59,6 @@ MARKERS = {
             "top-k done, ids published (workgroups < T; the others end here)",
             "workgroup 0: every id polled, epoch advanced",
             "workgroup 0: routing tables built",
-        ],
-    ),
-    "stack": (
-        "moe_stack",
-        [
-            "workgroup start",
-            "last layer: start (previous layer written)",
-            "last layer: input staged",
-            "last layer: P1 unit done",
-            "last layer: top-k selected, ids written",
-            "last layer: routed gate/up done",
-            "last layer: activations staged",
-            "last layer: down rows and combine written",
         ],
     ),
     "attention": (
@@ -119,7 +107,6 @@ def parse_args(argv=None) -> argparse.Namespace:
     p.add_argument("--weight-sets", type=int, default=4)
     p.add_argument("--zipf", action="store_true", help="router: the config-2 Zipf router bias")
     p.add_argument("--context", type=int, default=1024, help="attention: cached positions before the step")
-    p.add_argument("--layers", type=int, default=8, help="stack: layers per run")
     p.add_argument("--dump", default=None, help="also write every workgroup's marker times (µs) to this CSV file")
     return p.parse_args(argv)
 
@@ -138,7 +125,7 @@ def main(argv=None) -> int:
     import torch
 
     from fastkernels_amd import workloads as wl
-    from fastkernels_amd.plan import AttentionStepPlan, DeltaNetStepPlan, MoeLayerPlan, MoeStackPlan
+    from fastkernels_amd.plan import AttentionStepPlan, DeltaNetStepPlan, MoeLayerPlan
     from fastkernels_amd.spec import qwen36_35b_a3b_spec
 
     if not torch.cuda.is_available():
@@ -152,8 +139,6 @@ def main(argv=None) -> int:
     dev = torch.device("cuda", 0)
     spec = qwen36_35b_a3b_spec()
     T, R = args.tokens, max(1, args.weight_sets)
-    if args.kernel == "stack":
-        T = 1
     H, E, I = spec.hidden_size, spec.num_experts, spec.expert_intermediate_size
 
     def moe_set(r: int) -> dict:
@@ -183,9 +168,6 @@ def main(argv=None) -> int:
     for r in range(R):
         if args.kernel in ("moe", "router"):
             p = MoeLayerPlan(moe_set(r), T, top_k=spec.num_routed_experts, router_bias=bias)
-        elif args.kernel == "stack":
-            # a run of args.layers layers per weight set (the markers keep the last layer's times)
-            p = MoeStackPlan([moe_set(r * 64 + l) for l in range(args.layers)], top_k=spec.num_routed_experts)
         elif args.kernel == "attention":
             # room for every run of the warmup, the capture's replays and the marked replay
             p = AttentionStepPlan(wl.make_attention_weights(spec, seed=3000 + r, device=dev), T, spec,

@@ -162,53 +162,6 @@ int fk_moe_layer(const void* hidden, int hidden_dtype,
                  float* moe_out, float* layer_out,
                  void* workspace, size_t workspace_bytes, void* stream);
 
-/* One MoE layer of a run decoded in one launch by fk_moe_stack_decode:
- * fk_moe_layer's weights and outputs for that layer.  bf16 norm, router,
- * expert and shared-expert weights (shared_gate nullable, bf16); router_bias
- * nullable (dtype: the call's bias_dtype).  Outputs as fk_moe_layer's at
- * tokens = 1: logits [E], topk_ids / topk_weights [K], moe_out and
- * layer_out [H] (fp32); layer_out is also the next layer's input. */
-typedef struct fk_moe_stack_layer {
-  const void* norm_weight;
-  const void* router_weight;
-  const void* router_bias;
-  const void* gate_up;
-  const void* down;
-  const void* shared_gate_up;
-  const void* shared_down;
-  const void* shared_gate;
-  float* logits;
-  int64_t* topk_ids;
-  float* topk_weights;
-  float* moe_out;
-  float* layer_out;
-} fk_moe_stack_layer;
-
-/* Bytes of workspace for fk_moe_stack_decode. */
-size_t fk_moe_stack_workspace_bytes(int num_layers, int num_experts, int top_k, int intermediate,
-                                    int hidden_size);
-
-/* A run of num_layers MoE layers at one token in one launch: layer 0 takes
- * `hidden` (f32 or bf16 [1, H]), layer l > 0 takes layer l-1's layer_out.
- * Each layer's outputs equal those of fk_moe_layer on the same inputs bit
- * for bit (the same arithmetic in the same order), written into the
- * caller's buffers named by `layers`, a DEVICE array of num_layers
- * descriptors that stays valid while the call runs (a captured graph reads
- * it at every replay).  H <= 2048 and a multiple of 8, I <= 512 and a
- * multiple of 16, E <= 256, K <= 8, one workgroup per CU holding the
- * layer's units.  The workgroups hand values to each other (logits,
- * activations, each layer's output), so the workspace is polled like
- * fk_moe_layer's (fk_workspace_status); zero-fill it once.
- * No counterpart in the reference: its 40-layer stack
- * is 40 calls of triton_qwen36_batched_moe_layer_decode
- * (qwen36_expert.py:1312-1350), which this replaces for T = 1.  On MI355X
- * it measures slower than one fk_moe_layer launch per layer (every
- * workgroup reads each layer's outputs before the next layer starts). */
-int fk_moe_stack_decode(const void* hidden, int hidden_dtype, const fk_moe_stack_layer* layers,
-                        int num_layers, int bias_dtype, int hidden_size, int intermediate,
-                        int num_experts, int top_k, float eps, float norm_offset,
-                        void* workspace, size_t workspace_bytes, void* stream);
-
 /* fk_moe_layer without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.

@@ -34,14 +34,14 @@ def test_library_loads_and_exports_every_declared_symbol():
 def test_product_library_carries_no_timeline_markers():
     # the per-phase timeline exists only in the -DFK_TIMELINE diagnostic build
     lib = _lib.load()
-    for unit in ("moe_fused", "moe_router", "deltanet_step", "attn_step", "moe_stack"):
+    for unit in ("moe_fused", "moe_router", "deltanet_step", "attn_step"):
         assert not hasattr(lib, f"fk_timeline_read_{unit}"), unit
 
 
 def test_timeline_markers_have_names():
     from fastkernels_amd import timeline
 
-    assert {k: len(v[1]) for k, v in timeline.MARKERS.items()} == {"moe": 8, "router": 6, "deltanet": 10, "attention": 15, "stack": 8}
+    assert {k: len(v[1]) for k, v in timeline.MARKERS.items()} == {"moe": 12, "router": 6, "deltanet": 10, "attention": 15}
     assert all(len(names) <= 16 for _, names in timeline.MARKERS.values())  # kTimelineMarks
 
 
