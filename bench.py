@@ -12,7 +12,9 @@ to layer (config 4; cache-cold by construction).
 Method: every step is one MoE layer (router + top-k + routing tables +
 experts + residual) issued through the C ABI from a preallocated plan.  K
 steps are captured in one HIP graph and replayed once between two HIP events
-on the capture stream, after W eager warmup steps and one untimed replay.
+on the capture stream, after W eager warmup steps and untimed replays (the
+last of them still running when the timed one is enqueued, so the GPU does
+not idle while the host submits the graph).
 Steps cycle through R independent weight sets (each 1.6 GB) so one step's
 57.7 MB does not stay in the 256 MB last-level cache.  The expert stage
 (gate/up + down kernels, 98% of the bytes) is timed the same way on its own
@@ -33,7 +35,8 @@ import time
 
 METRIC = "µs per MoE layer decode step at batch 1/16/128; achieved HBM TB/s vs peak"
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
-GRAPH_WARM_REPLAYS = 2  # untimed replays of each captured graph before the timed one
+GRAPH_WARM_REPLAYS = 2  # untimed replays of each captured graph before the timed one, at least
+GRAPH_WARM_STEPS = 256  # ... and at least this many untimed steps (the memory system warms over ~100-200 steps)
 REFERENCE_A100_T1_US = 181.5  # real_moe_ms 0.1815 ms, A100 (reference docs/modal.md:1053)
 
 
@@ -239,6 +242,9 @@ def main() -> int:
     sets = [] if args.only in ("deltanet", "stack", "attention", "model") else [moe_set(r) for r in range(R)]
     torch.cuda.synchronize()
 
+    def warm_replays(steps: int) -> int:
+        return max(GRAPH_WARM_REPLAYS, -(-GRAPH_WARM_STEPS // steps))
+
     def timed_graph(fns, steps: int, warmup: int) -> float:
         """ms per step over exactly `steps` graph-captured steps."""
 
@@ -253,14 +259,18 @@ def main() -> int:
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         # replay() launches on the current stream: make it the timed stream.
-        # Two untimed replays first (the first uploads the graph; the one
-        # after it still runs ~3% slow at T=16 while the 13 GB of rotating
-        # weight sets are first touched through the graph), then exactly
-        # `steps` steps timed in one replay.
+        # Untimed replays first, at least GRAPH_WARM_STEPS steps of them: the
+        # first uploads the graph, and a T=16 step over the 13 GB of rotating
+        # weight sets runs ~4% slow until ~100-200 steps have run (measured:
+        # 20-step replays after 65 steps 114.3 us, after 200 steps 108.4 us,
+        # as 64-step ones), then exactly `steps` steps timed in one replay.
+        # The timed replay is enqueued while one more untimed replay runs, so
+        # the GPU does not wait for the host to submit the graph.
         with torch.cuda.stream(stream):
-            for _ in range(GRAPH_WARM_REPLAYS):
+            for _ in range(warm_replays(steps)):
                 graph.replay()
             stream.synchronize()
+            graph.replay()
             start.record(stream)
             graph.replay()
             end.record(stream)
@@ -342,7 +352,7 @@ def main() -> int:
             w = wl.make_attention_weights(spec, seed=3000 + r, device=dev)
             # every run advances the position: room for the warmup, untimed and timed replays
             ap = AttentionStepPlan(w, tokens, spec,
-                                   max_positions=context + (args.warmup + (GRAPH_WARM_REPLAYS + 1) * steps + 8) * tokens,
+                                   max_positions=context + (args.warmup + (warm_replays(steps) + 2) * steps + 8) * tokens,
                                    start_position=context)
             ap.hidden.copy_(wl.make_hidden(tokens, H, seed=70 + r).to(dev))
             aplans.append(ap)
@@ -373,15 +383,17 @@ def main() -> int:
             else:
                 mixer = wl.make_attention_weights(spec, seed=4000 + l, device=dev)
             layers.append((kind, mixer, lsets[l % len(lsets)]))
-        runner = ResidentDecodeRunner(layers, tokens, spec, max_positions=(steps + 8) * tokens)
+        warm = 8  # decode steps (320 layer steps) before the timed ones
+        runner = ResidentDecodeRunner(layers, tokens, spec, max_positions=(steps + warm + 8) * tokens)
         runner.hidden.copy_(wl.make_hidden(tokens, H, seed=8).to(dev))
         runner.capture(stream)
         with torch.cuda.stream(stream):
-            runner.replay()
-            runner.replay()
+            for _ in range(warm - 1):
+                runner.replay()
             stream.synchronize()
             start = torch.cuda.Event(enable_timing=True)
             end = torch.cuda.Event(enable_timing=True)
+            runner.replay()  # (the timed replays are enqueued while this one runs)
             start.record(stream)
             for _ in range(steps):
                 runner.replay()
@@ -588,6 +600,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "graph_warm_replays": GRAPH_WARM_REPLAYS,
+        "graph_warm_steps": GRAPH_WARM_STEPS,
         "ms_per_step": round(ms_per_step, 6),
         "higher_is_better": False,
         "scaling": "weak",

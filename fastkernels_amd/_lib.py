@@ -52,6 +52,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [P, I, P, I, P, I, P, I, P, P, I, P, P, P, I, I, I, I, I, I, c_float, c_float, P, P, P, P, P, P, c_size_t, P],
     ),
+    "fk_moe_noalloc_workspace": (c_int, [P, P, P]),
     "fk_moe_layer_noalloc": (
         c_int,
         [P, I, P, I, P, I, P, I, P, P, I, P, P, P, I, I, I, I, I, I, c_float, c_float, P, P, P, P, P, P],

@@ -1,4 +1,5 @@
 // Library-level C-ABI functions: version, status strings, last-error text.
+#include "fk_common.h"
 #include "fk_host.h"
 
 namespace fk {
@@ -64,7 +65,9 @@ int fk_workspace_status(const void* workspace, size_t workspace_bytes, int clear
     if (err == hipSuccess) err = hipStreamSynchronize(s);
   }
   if (err != hipSuccess) return fail(FK_ERR_LAUNCH, "fk_workspace_status: %s", hipGetErrorString(err));
-  if (v != 0) return fail(FK_ERR_DEVICE, "a kernel's bounded wait ran out (device flags 0x%x)", v);
+  if (v != 0)
+    return fail(FK_ERR_DEVICE, "device flags 0x%x:%s%s", v, (v & FK_DEVICE_ERR_BARRIER) ? " a kernel's bounded wait ran out;" : "",
+                (v & FK_DEVICE_ERR_POSITION) ? " an attention step's device-held position would pass the cache;" : "");
   return FK_OK;
 }
 
@@ -72,7 +75,10 @@ int fk_workspace_set_poll_limit(void* workspace, size_t workspace_bytes, long lo
   using namespace fk;
   if (!workspace || workspace_bytes < (kWorkspaceErrorWord + 1) * sizeof(uint32_t))
     return fail(FK_ERR_WORKSPACE, "fk_workspace_set_poll_limit: workspace missing or smaller than its header");
-  if (limit > (long long)0x7fffffff) return fail(FK_ERR_INVALID, "poll limit must be < 2^31 (got %lld)", limit);
+  // A round is one coherent read of the words not yet in (0.1-1 us), so the
+  // cap keeps a wait that fails within a few seconds, like the built-in bound.
+  if (limit > kMaxPollLimit)
+    return fail(FK_ERR_INVALID, "poll limit must be at most %lld rounds (got %lld)", (long long)kMaxPollLimit, limit);
   const uint32_t value = limit < 0 ? 0u : (uint32_t)limit + 1u;
   hipLaunchKernelGGL(ws_set_word_kernel, dim3(1), dim3(1), 0, as_stream(stream), reinterpret_cast<uint32_t*>(workspace),
                      kWorkspacePollWord, value);

@@ -562,6 +562,8 @@ struct AttnOutArgs {
   float* update;
   float* hidden_out;
   int* advance;  // nullable: *advance += T at the end of the step (device-held position)
+  int max_pos;   // the cache length: a position whose step would pass it is not advanced
+  uint32_t* err; // the workspace's error word (FK_DEVICE_ERR_POSITION)
 };
 
 // 4 rows of Wo per workgroup (1 per wavefront), K <= 4096, loaded once and
@@ -610,8 +612,13 @@ __global__ __launch_bounds__(256) void attn_out_kernel(AttnOutArgs a) {
       if (a.hidden_out) a.hidden_out[o] = load_scalar(a.x, a.x_dt, o) + u;
     }
   }
-  // the attention launch before this one has read the position
-  if (a.advance && blockIdx.x == 0 && threadIdx.x == 0) *a.advance += a.T;
+  // the attention launch before this one has read the position; one whose
+  // step would pass the cache (NaN update) stays, and the error word says so
+  if (a.advance && blockIdx.x == 0 && threadIdx.x == 0) {
+    const int s0 = *a.advance;
+    if (s0 >= 0 && s0 + a.T <= a.max_pos) *a.advance = s0 + a.T;
+    else __hip_atomic_fetch_or(a.err, FK_DEVICE_ERR_POSITION, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1321,12 +1328,16 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
     // later launches)
     if (tid == 0 && !s_kfail) {
       store_coherent(&a.tw.tickets[kWorkspaceEpochWord], tag);
-      if (a.start_dev) store_coherent(a.start_dev, start + T);
+      // (a position whose step would pass the cache stays where it is)
+      if (a.start_dev && !bad_pos) store_coherent(a.start_dev, start + T);
     }
   }
   lds_barrier();
   if (tid == 0 && (s_fail || s_kfail))
     __hip_atomic_fetch_or(&a.tw.tickets[kWorkspaceErrorWord], FK_DEVICE_ERR_BARRIER, __ATOMIC_RELAXED,
+                          __HIP_MEMORY_SCOPE_AGENT);
+  if (b == 0 && tid == 0 && bad_pos)
+    __hip_atomic_fetch_or(&a.tw.tickets[kWorkspaceErrorWord], FK_DEVICE_ERR_POSITION, __ATOMIC_RELAXED,
                           __HIP_MEMORY_SCOPE_AGENT);
   FK_MARK(9);
   FK_TIMELINE_COMMIT(attn_step, blockIdx.x);
@@ -1639,6 +1650,8 @@ int fk_attention_decode(const void* hidden, int hidden_dtype, const void* norm_w
   o.update = update;
   o.hidden_out = hidden_out;
   o.advance = const_cast<int*>(start_position_device);
+  o.max_pos = max_positions;
+  o.err = ws.tw.tickets + kWorkspaceErrorWord;
   const dim3 ogrid((unsigned)((hidden_size + kAttnOutRows - 1) / kAttnOutRows));
   if (weight_dtype == FK_DTYPE_BF16) hipLaunchKernelGGL(attn_out_kernel<true>, ogrid, dim3(256), 0, s, o);
   else hipLaunchKernelGGL(attn_out_kernel<false>, ogrid, dim3(256), 0, s, o);

@@ -438,6 +438,9 @@ __device__ __forceinline__ bool poll_run(uint64_t (&w)[N], const uint64_t* base,
 // configuration gives flagged, poisoned results but never a hang.
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr uint32_t FK_DEVICE_ERR_BARRIER = 1u;
+// A device-held attention position whose step would pass the cache: the
+// step's update is NaN and the position is left where it is.
+constexpr uint32_t FK_DEVICE_ERR_POSITION = 2u;
 
 __device__ __forceinline__ bool grid_arrive_and_wait(uint32_t* counter, uint32_t target, uint32_t* error,
                                                      uint32_t limit) {

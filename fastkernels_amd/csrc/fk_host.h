@@ -25,6 +25,8 @@ int fail(int status, const char* fmt, ...);
 constexpr int kWorkspaceEpochWord = 8;
 constexpr int kWorkspacePollWord = 14;
 constexpr int kWorkspaceErrorWord = 15;
+// Largest host-set wait bound (poll rounds), fk_workspace_set_poll_limit.
+constexpr long long kMaxPollLimit = 1ll << 22;
 
 // Normalized multi-matrix projection (fk_deltanet.hip), shared by the mixers.
 int launch_norm_projection(const void* x, int x_dt, const void* nw, int nw_dt, const void* const (&w)[4],

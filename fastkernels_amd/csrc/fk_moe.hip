@@ -2634,8 +2634,9 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(u32x4* p, size_t n16) {
 // device (with that device current) the address is taken with
 // hipGetSymbolAddress -- the array's name is only a host-side stand-in --
 // and the array is zero-filled on `stream` (the workspace contract: zero
-// once, then self-resetting).  That first call must not be under graph
-// capture: a captured fill would re-zero the launch epoch on every replay.
+// once, then self-resetting), and waited for.  That first call must not be
+// under graph capture: a captured fill would re-zero the launch epoch on
+// every replay.
 static int noalloc_scratch(hipStream_t stream, void** out) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(FK_ERR_LAUNCH, "no current HIP device");
@@ -2653,6 +2654,10 @@ static int noalloc_scratch(hipStream_t stream, void** out) {
                        kNoAllocScratchBytes / 16);
     const int st = check_launch("zero_fill_kernel");
     if (st) return st;
+    // Wait for the fill: a first call from another stream (or thread, once
+    // the lock is released) must find the array cleared.
+    const hipError_t se = hipStreamSynchronize(stream);
+    if (se != hipSuccess) return fail(FK_ERR_LAUNCH, "clearing the scratch array: %s", hipGetErrorString(se));
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
@@ -2845,6 +2850,16 @@ int fk_moe_layer_noalloc(const void* hidden, int hidden_dtype, const void* norm_
                       bias_dtype, gate_up, down, expert_dtype, shared_gate_up, shared_down, shared_gate,
                       shared_gate_dtype, tokens, hidden_size, intermediate, num_experts, top_k, eps, norm_offset,
                       logits, topk_ids, topk_weights, moe_out, layer_out, ptr, kNoAllocScratchBytes, stream);
+}
+
+int fk_moe_noalloc_workspace(void** workspace, size_t* workspace_bytes, void* stream) {
+  if (!workspace || !workspace_bytes) return fail(FK_ERR_INVALID, "workspace and workspace_bytes must be non-NULL");
+  void* p = nullptr;
+  const int st = noalloc_scratch(as_stream(stream), &p);
+  if (st) return st;
+  *workspace = p;
+  *workspace_bytes = kNoAllocScratchBytes;
+  return FK_OK;
 }
 
 }  // extern "C"

@@ -66,20 +66,26 @@ const char* fk_last_error_detail(void);
  * from incomplete inputs are NaN (routing weights, MoE outputs, DeltaNet
  * update and recurrent state, attention update and the step's cache rows).
  * While the word stays set, every later call on the workspace gives NaN
- * outputs.  This call synchronises `stream`, then returns FK_OK
- * or FK_ERR_DEVICE; `clear` != 0 also resets the word (stream-ordered),
- * after which calls give valid outputs again.
+ * outputs.  fk_attention_decode also sets it (another bit) when a
+ * device-held position would take the step past the cache: the update is
+ * NaN, the caches are untouched and the position is not advanced.  This
+ * call synchronises `stream`, then returns FK_OK or FK_ERR_DEVICE (with the
+ * flags in fk_last_error_detail); `clear` != 0 also resets the word
+ * (stream-ordered), after which calls give valid outputs again.
  * No counterpart in the reference: its Triton kernels never wait on another
  * program.  For callers that validate a run (tests, benchmarks). */
 int fk_workspace_status(const void* workspace, size_t workspace_bytes, int clear, void* stream);
 
 /* Bound on every in-kernel wait of the calls on `workspace` (same
- * workspaces as fk_workspace_status), stream-ordered: `limit` poll rounds
- * (0: each wait gives up at once, so every such call flags FK_ERR_DEVICE
- * and gives NaN outputs, and every kernel still ends); a negative `limit`
- * restores the built-in bound.  No counterpart in the reference: a test
- * hook for the failure path, and a knob for callers that prefer an early
- * flagged failure to a long wait. */
+ * workspaces as fk_workspace_status), stream-ordered: `limit` poll rounds,
+ * each one coherent read of the words not yet in (roughly 0.1-1 us), at
+ * most FK_MAX_POLL_LIMIT (FK_ERR_INVALID above it: a wait that fails still
+ * ends within seconds); 0: each wait gives up at once, so every such call
+ * flags FK_ERR_DEVICE and gives NaN outputs, and every kernel still ends; a
+ * negative `limit` restores the built-in bound (2^16 rounds).  No
+ * counterpart in the reference: a test hook for the failure path, and a
+ * knob for callers that prefer an early flagged failure to a long wait. */
+#define FK_MAX_POLL_LIMIT (1ll << 22)
 int fk_workspace_set_poll_limit(void* workspace, size_t workspace_bytes, long long limit, void* stream);
 
 /* ------------------------------------------------------------------------ */
@@ -166,17 +172,20 @@ int fk_moe_layer(const void* hidden, int hidden_dtype,
  * allocate device memory (code under HIP graph capture, tight serving
  * loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
  * The workspace is a file-scope device array of FK_MOE_NOALLOC_SCRATCH_BYTES
- * (16 MiB) that each GPU the library runs on holds until the process ends;
+ * (16 MiB) that each GPU holds from the moment a process loads this library
+ * until the process ends, whether or not it ever calls this function;
  * a problem whose fk_moe_workspace_bytes exceeds it returns
  * FK_ERR_UNSUPPORTED (at the model's shape: up to 174 tokens).  The call
  * allocates nothing.  The first call on a device zero-fills the array on
- * `stream` and must not be under graph capture; later calls may be.  Every
- * call on a GPU shares that GPU's array, so calls that overlap on one GPU
- * (on different streams, or from several threads) race and give wrong
- * results; serialise them.  A bounded in-kernel wait that runs out gives
- * NaN outputs for this call and every later one on the GPU (the array keeps
- * the flag; callers that need to recover use fk_moe_layer with their own
- * workspace and fk_workspace_status). */
+ * `stream` and waits for that fill (so a first call from another stream or
+ * thread cannot see an uncleared array); it must not be under graph capture,
+ * later calls may be.  Every call on a GPU shares that GPU's array, so calls
+ * that overlap on one GPU (on different streams, or from several threads)
+ * race and give wrong results; serialise them.  A bounded in-kernel wait
+ * that runs out gives NaN outputs for this call and every later one on the
+ * GPU until the array's error word is cleared: fk_moe_noalloc_workspace
+ * gives the array's device address, for fk_workspace_status and
+ * fk_workspace_set_poll_limit. */
 #define FK_MOE_NOALLOC_SCRATCH_BYTES (16u << 20)
 int fk_moe_layer_noalloc(const void* hidden, int hidden_dtype,
                          const void* norm_weight, int norm_dtype,
@@ -189,6 +198,12 @@ int fk_moe_layer_noalloc(const void* hidden, int hidden_dtype,
                          int num_experts, int top_k, float eps, float norm_offset,
                          float* logits, int64_t* topk_ids, float* topk_weights,
                          float* moe_out, float* layer_out, void* stream);
+
+/* The current device's fk_moe_layer_noalloc array: its device address and
+ * size, for fk_workspace_status (read and clear its error word) and
+ * fk_workspace_set_poll_limit.  Allocates nothing; the first use on a device
+ * clears the array as fk_moe_layer_noalloc's first call does (same rules). */
+int fk_moe_noalloc_workspace(void** workspace, size_t* workspace_bytes, void* stream);
 
 /* counts[e] = #{i : ids[i] == e} over n ids (int32 or int64); ids outside
  * [0, num_experts) are ignored.  counts is overwritten.

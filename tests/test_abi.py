@@ -227,3 +227,13 @@ def test_product_package_does_not_import_oracle():
     for path in (ROOT / "fastkernels_amd").rglob("*.py"):
         text = path.read_text()
         assert "import oracle" not in text and "from oracle" not in text, path
+
+
+def test_poll_limit_above_the_cap_is_refused_before_any_launch():
+    # refused on the host (no launch, so no GPU is needed): a failed wait must
+    # still end within seconds
+    lib = _lib.load()
+    buf = ctypes.create_string_buffer(64)
+    status = lib.fk_workspace_set_poll_limit(ctypes.addressof(buf), 64, (1 << 22) + 1, None)
+    assert status == _lib.FK_ERR_INVALID
+    assert "at most" in lib.fk_last_error_detail().decode()

@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import oracle
+from fastkernels_amd import _lib
 from fastkernels_amd.kernels import hip
 from tests.parity import assert_routing_parity, tol
 
@@ -208,21 +209,29 @@ def test_attention_plan_graph_replays_decode_successive_positions(device, attn_c
     graphed.check_device()
 
 
-def test_attention_plan_position_past_the_cache_gives_nan(device, attn_gpu):
-    # a device-held position whose step would pass the cache: NaN update,
-    # caches untouched, no wait flagged; a valid position afterwards decodes
-    plan = _plan(attn_gpu, 2, 8, 7)
+@pytest.mark.parametrize("tokens", [2, 5])
+def test_attention_plan_position_past_the_cache_gives_nan(device, attn_gpu, tokens):
+    # a device-held position whose step would pass the cache (T = 2: the
+    # single launch, T = 5: the four launches): NaN update, caches untouched,
+    # the position left where it is and the error word set (reported, then
+    # cleared); a valid position afterwards decodes
+    plan = _plan(attn_gpu, tokens, 8, 7)
     g = torch.Generator().manual_seed(29)
     plan.key_cache.copy_(torch.randn(8, KVH, HD, generator=g).to(device))
     plan.value_cache.copy_(torch.randn(8, KVH, HD, generator=g).to(device))
-    plan.hidden.copy_(torch.randn(2, H, generator=g).to(torch.bfloat16).to(device))
+    plan.hidden.copy_(torch.randn(tokens, H, generator=g).to(torch.bfloat16).to(device))
     kc, vc = plan.key_cache.clone(), plan.value_cache.clone()
     plan.run()
     torch.cuda.synchronize()
     assert bool(torch.isnan(plan.update).all())
     assert torch.equal(plan.key_cache, kc) and torch.equal(plan.value_cache, vc)
-    plan.check_device()
-    plan.set_position(6)
+    assert int(plan.position.item()) == 7
+    with pytest.raises(_lib.FastKernelsError) as info:
+        plan.check_device()
+    assert info.value.status == _lib.FK_ERR_DEVICE
+    assert "position" in str(info.value)
+    plan.check_device()  # cleared
+    plan.set_position(8 - tokens)
     plan.run()
     torch.cuda.synchronize()
     assert bool(torch.isfinite(plan.update).all())

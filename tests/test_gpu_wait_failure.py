@@ -35,6 +35,11 @@ def small_moe(device):
 
 
 @pytest.fixture(scope="module")
+def model_moe(device):
+    return wl.make_moe_weights(SPEC, seed=36, device=device)
+
+
+@pytest.fixture(scope="module")
 def dn_weights(device):
     return wl.make_deltanet_weights(SPEC, seed=32, device=device)
 
@@ -82,6 +87,15 @@ def test_moe_layer_wait_failure_is_poisoned_and_flagged(device, small_moe, token
     print(f"moe wait failure tokens={tokens}", flush=True)
     plan = MoeLayerPlan(small_moe, tokens)
     plan.hidden.copy_(wl.make_hidden(tokens, SMALL.hidden_size, seed=33).to(device))
+    _exercise(plan)
+
+
+def test_moe_layer_model_shape_t1_wait_failure_is_poisoned_and_flagged(device, model_moe):
+    # the model's shape at T = 1 takes the single launch's straight-line
+    # variant (one workgroup per gate/up block, down item and row group)
+    print("moe wait failure model shape T=1", flush=True)
+    plan = MoeLayerPlan(model_moe, 1)
+    plan.hidden.copy_(wl.make_hidden(1, SPEC.hidden_size, seed=37).to(device))
     _exercise(plan)
 
 

@@ -6,11 +6,15 @@ workspace on the same inputs: two calls in a row, the second with fewer
 tokens (the shared array keeps the first call's contents), across the
 single-launch (T = 1), GEMV (T < 64) and MFMA (T >= 64) paths; the
 results must be identical bit for bit (same kernels, same arithmetic).
-Sizes beyond the array are refused before anything is launched.
+Sizes beyond the array are refused before anything is launched.  The
+array's error word, reached through fk_moe_noalloc_workspace, reports a
+wait that ran out (forced with a wait bound of 0) and clears, after which
+the results are identical again.
 """
 
 from __future__ import annotations
 
+import ctypes
 import dataclasses
 
 import pytest
@@ -106,3 +110,28 @@ def test_noalloc_rejects_sizes_beyond_its_scratch(device, weights):
     status = _lib.load().fk_moe_layer_noalloc(*head, torch.cuda.current_stream(device).cuda_stream)
     assert status == _lib.FK_ERR_UNSUPPORTED
     assert "scratch" in _lib.load().fk_last_error_detail().decode()
+
+
+def test_noalloc_failed_wait_is_flagged_and_clears(device, weights):
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(device).cuda_stream
+    ptr, nbytes = ctypes.c_void_p(), ctypes.c_size_t()
+    _lib.call("fk_moe_noalloc_workspace", ctypes.byref(ptr), ctypes.byref(nbytes), stream)
+    assert ptr.value and nbytes.value == 16 << 20
+    for tokens in (1, 4):
+        print(f"noalloc forced wait failure T={tokens}", flush=True)
+        x = wl.make_hidden(tokens, SMALL.hidden_size, seed=70 + tokens).to(device)
+        try:
+            _lib.call("fk_workspace_set_poll_limit", ptr, nbytes, 0, stream)
+            a = _noalloc(weights, x)
+            assert bool(torch.isnan(a["layer"]).all()) and bool(torch.isnan(a["moe"]).all())
+        finally:
+            _lib.call("fk_workspace_set_poll_limit", ptr, nbytes, -1, stream)
+        assert lib.fk_workspace_status(ptr, nbytes, 1, stream) == _lib.FK_ERR_DEVICE
+        assert lib.fk_workspace_status(ptr, nbytes, 0, stream) == _lib.FK_OK
+        a = _noalloc(weights, x)
+        b = _with_workspace(weights, x)
+        torch.cuda.synchronize()
+        assert torch.equal(a["ids"], b["ids"])
+        for k in ("logits", "w", "moe", "layer"):
+            assert torch.equal(a[k], b[k]), k
