@@ -85,6 +85,29 @@ class Qwen36A3BSpec:
             "expert_down_weight": (self.num_experts, self.hidden_size, self.expert_intermediate_size),
         }
 
+    def summary_lines(self, token_counts=(1, 16, 128)) -> list[str]:
+        """A text summary of the spec, one "key: value" line per field group,
+        then the routed (token, expert) rows of each token count (reference
+        models/qwen36.py:97-114, same lines)."""
+
+        counts = self.layer_counts()
+        kinds = self.layer_kinds()
+        fields = [
+            ("model", self.name),
+            ("layers", self.num_layers),
+            ("hidden_size", self.hidden_size),
+            ("layer pattern", f"{', '.join(kinds[:4])} x {self.num_layers // 4}"),
+            ("deltanet/attention layers", f"{counts['deltanet_moe']}/{counts['attention_moe']}"),
+            ("deltanet qk/value heads", f"{self.deltanet_qk_heads}/{self.deltanet_value_heads}"),
+            ("attention q/kv heads", f"{self.attention_heads}/{self.attention_kv_heads}"),
+            ("experts", self.num_experts),
+            ("routed/shared active experts", f"{self.num_routed_experts}/{self.num_shared_experts}"),
+            ("expert_intermediate_size", self.expert_intermediate_size),
+        ]
+        return [f"{k}: {v}" for k, v in fields] + [
+            f"tokens={t}: routed_expert_rows={t * self.num_routed_experts}" for t in token_counts
+        ]
+
     @classmethod
     def from_hf_config(cls, config: dict, name: str = "hf-config") -> "Qwen36A3BSpec":
         """Spec from a Hugging Face config dict (its `text_config` when

@@ -322,3 +322,19 @@ def test_initial_decode_state_shapes():
     assert st.deltanet_recurrent_states[0].shape == (32, 128, 128)
     assert st.attention_key_cache[0].shape == (64, 2, 256) and st.position == 0
     assert all(float(t.abs().sum()) == 0.0 for t in st.deltanet_conv_states + st.attention_value_cache)
+
+
+def test_spec_summary_lines():
+    # reference models/qwen36.py:97-114: the field lines, then one line per
+    # token count with its routed (token, expert) rows
+    from fastkernels_amd.spec import qwen36_35b_a3b_spec
+
+    lines = qwen36_35b_a3b_spec().summary_lines()
+    assert lines[0] == "model: Qwen3.6-35B-A3B"
+    assert "layers: 40" in lines and "hidden_size: 2048" in lines and "experts: 256" in lines
+    assert "layer pattern: deltanet_moe, deltanet_moe, deltanet_moe, attention_moe x 10" in lines
+    assert "deltanet/attention layers: 30/10" in lines
+    assert "routed/shared active experts: 8/1" in lines
+    assert lines[-3:] == ["tokens=1: routed_expert_rows=8", "tokens=16: routed_expert_rows=128",
+                          "tokens=128: routed_expert_rows=1024"]
+    assert qwen36_35b_a3b_spec().summary_lines([4])[-1] == "tokens=4: routed_expert_rows=32"
