@@ -1985,16 +1985,18 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
 // words; workgroup 0 polls the T*K ids.  Either way workgroup 0 then
 // advances the epoch (the words it polled carry this launch's tag, so every
 // workgroup has written logits with it and has read the epoch) and builds
-// the routing tables for the expert stage.  Same arithmetic as
-// moe_router_kernel, so both give identical logits and ids.
+// the routing tables for the expert stage.  The logits are moe_router_kernel's
+// (same arithmetic); the selection is the ranked one of the single-launch
+// layer (topk_select_ranked): the same ids, weights equal to rounding.
 // ---------------------------------------------------------------------------
 constexpr int kTagRouterMaxTokens = 256;
 constexpr int kTagRouterTile = 4;       // tokens per tile of the logits loop
 constexpr int kTagRouterMaxPerWg = 32;  // most tokens per workgroup
 // Up to this many tokens workgroup 0 selects them all, one token per
-// wavefront.  (Two per wavefront, up to 16 tokens, measured no faster at
-// T = 16 than the selections spread over 16 workgroups: a selection is
-// VALU-bound, and eight wavefronts share one CU's four SIMDs.)
+// wavefront.  (Two per wavefront, up to 16 tokens, measured 0.4-0.8 us
+// slower at 12-16 tokens than the selections spread over one workgroup per
+// token: a selection is VALU-bound, and eight wavefronts share one CU's
+// four SIMDs.)
 constexpr int kTagRouterSelfTokens = kFusedWaves;
 constexpr int kMaskWords = kTagRouterMaxTokens / 32;
 static_assert(kFusedSelWords >= (size_t)kTagRouterMaxTokens * 8, "router selection region too small");
@@ -2077,6 +2079,9 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   __shared__ float s_chunk[TU][8];
   __shared__ float s_ss[TU];
   __shared__ int s_fail;
+  __shared__ __align__(16) TopkLds s_topk[kFusedWaves];
+  __shared__ float s_selw[kTagRouterSelfTokens * 8];  // selected weights (ids: s_ids, or s_sel_id)
+  __shared__ int s_sel_id[8];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int T = a.T, H = a.H, E = a.E, K = a.K, nch = H >> 3;
   const int nrb = (E + 7) / 8, tu = a.tu;
@@ -2244,39 +2249,43 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
       return;
     }
     for (int i = tid; i < E * nmw; i += kFusedWaves * kWave) s_mask[i] = 0u;
-    constexpr int NJE = kFusedMaxExperts / kWave;
-    const int t = wave;
-    uint64_t w[NJE];
-    const uint64_t* srcs[NJE];
+    // Wavefront w: token w (tokens w + 8 s with more per wavefront); the
+    // ranked selections write ids and weights to LDS.
+    constexpr int S = kTagRouterSelfTokens / kFusedWaves;
+    uint64_t w[S * 4];
+    const uint64_t* srcs[S * 4];
 #pragma unroll
-    for (int j = 0; j < NJE; ++j) {
-      const int ex = lane + kWave * j;
-      srcs[j] = t < T && ex < E ? a.ws.f_logits + (size_t)t * E + ex : nullptr;
-      w[j] = srcs[j] ? load_tagged(srcs[j]) : 0ull;
-    }
-    const bool ok = poll_tagged<NJE>(w, srcs, tag, wl.poll);
-    int id = 0;
-    float wt = 0.f;
-    if (t < T) {
-      float p[NJE];
+    for (int s = 0; s < S; ++s)
 #pragma unroll
-      for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
-      topk_select_regs<NJE>(p, E, K, lane, id, wt);
+      for (int j = 0; j < 4; ++j) {
+        const int t = wave + kFusedWaves * s, ex = lane + kWave * j;
+        srcs[s * 4 + j] = t < T && ex < E ? a.ws.f_logits + (size_t)t * E + ex : nullptr;
+        w[s * 4 + j] = srcs[s * 4 + j] ? load_tagged(srcs[s * 4 + j]) : 0ull;
+      }
+    const bool ok = poll_tagged<S * 4>(w, srcs, tag, wl.poll);
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int t = wave + kFusedWaves * s;
+      if (t < T) {
+        float l[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) l[j] = srcs[s * 4 + j] ? value_of(w[s * 4 + j]) : -INFINITY;
+        topk_select_ranked(l, E, K, lane, &s_topk[wave], s_ids + t * K, s_selw + t * K);
+      }
     }
-    __syncthreads();  // s_mask cleared
-    if (t < T && lane < K) {
-      // (after a failed wait: stale logits, ids kept in range, weights poisoned)
-      const int sid = ok ? id : min(max(id, 0), E - 1);
-      const float swt = poison_if(!ok, wt);
-      const int j = t * K + lane;
+    if (!ok) s_fail = 1;
+    __syncthreads();  // s_mask cleared, selections and s_fail in LDS
+    const bool bad = s_fail != 0;
+    for (int j = tid; j < T * K; j += kFusedWaves * kWave) {
+      // (after a failed wait: stale logits, ids in range, weights poisoned)
+      const int sid = s_ids[j], t = j / K;
+      const float swt = poison_if(bad, s_selw[j]);
       a.ids_out[j] = sid;
       a.w_out[j] = swt;
       a.ws.ids32[j] = sid;
       a.ws.wts[j] = swt;
-      s_ids[j] = sid;
       atomicOr(&s_mask[sid * nmw + (t >> 5)], 1u << (t & 31));
     }
-    if (!ok) s_fail = 1;
     __syncthreads();
     if (tid == 0) {
       if (!s_fail) store_coherent(&a.ws.tickets[kTicketEpoch], tag);
@@ -2303,17 +2312,16 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
       }
       const bool ok = poll_tagged<NJE>(w, srcs, tag, wl.poll);
       if (!ok) s_fail = 1;
-      float p[NJE];
+      float l[NJE];
 #pragma unroll
-      for (int j = 0; j < NJE; ++j) p[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
-      int id;
-      float wt;
-      topk_select_regs<NJE>(p, E, K, lane, id, wt);
-      if (!ok) {  // stale logits: ids kept in range, weights poisoned
-        id = min(max(id, 0), E - 1);
-        wt = poison_if(true, wt);
-      }
+      for (int j = 0; j < NJE; ++j) l[j] = srcs[j] ? value_of(w[j]) : -INFINITY;
+      topk_select_ranked(l, E, K, lane, &s_topk[0], s_sel_id, s_selw);
+      // (one wavefront: its LDS writes are done once the count drains)
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       if (lane < K) {
+        // (stale logits after a failed wait: ids in range, weights poisoned)
+        const int id = s_sel_id[lane];
+        const float wt = poison_if(!ok, s_selw[lane]);
         const int j = t * K + lane;
         a.ids_out[j] = id;
         a.w_out[j] = wt;

@@ -92,7 +92,7 @@ def test_router_real_shape(device, dtype):
     torch.testing.assert_close(w.cpu(), o_w[0], atol=1e-4, rtol=1e-4)
 
 
-@pytest.mark.parametrize("tokens", [1, 2, 4, 5, 8, 9, 16, 37, 128, 256])
+@pytest.mark.parametrize("tokens", [1, 2, 4, 5, 8, 9, 12, 16, 17, 37, 128, 256])
 def test_batched_router_and_tables(device, tokens):
     g = torch.Generator().manual_seed(2 + tokens)
     x = (0.02 * torch.randn(tokens, H, generator=g)).bfloat16()
@@ -126,7 +126,7 @@ def test_router_exact_ties_go_to_lower_id(device):
     assert_routing_parity(logits, ids, w, o_logits, 4)
 
 
-@pytest.mark.parametrize("tokens", [2, 5, 8, 9, 16])
+@pytest.mark.parametrize("tokens", [2, 5, 9, 12, 16, 17, 24])
 def test_batched_router_exact_ties_go_to_lower_id(device, tokens):
     # Per token, three identical router rows give identical logits at the top
     # (the lower id first) whichever path selects: workgroup 0 for every token
@@ -177,6 +177,22 @@ def test_single_expert_mlp(device, real_cpu):
     dn = real_cpu["expert_down_weight"][7]
     out = hip.hip_qwen36_single_expert_mlp_decode(x.to(device), gu.to(device), dn.to(device))
     torch.testing.assert_close(out.cpu(), oracle.expert_mlp(x, gu, dn), **tol(torch.bfloat16))
+
+
+def test_expert_stage_after_other_tables_on_one_workspace(device, real_cpu):
+    # The stream's workspace keeps what earlier calls of other shapes left:
+    # tables of a large alignment, small integers, where a small expert
+    # stage's tagged down outputs lie.  Its combine must not take them for
+    # this launch's outputs.
+    rng = np.random.default_rng(11)
+    ids = np.stack([rng.choice(1024, size=8, replace=False) for _ in range(512)])
+    hip.hip_qwen36_moe_align(torch.from_numpy(ids).to(device), 1024)
+    x = wl.make_hidden(1, H, seed=5)[0]
+    for e in (7, 8, 7):
+        gu = real_cpu["expert_gate_up_weight"][e]
+        dn = real_cpu["expert_down_weight"][e]
+        out = hip.hip_qwen36_single_expert_mlp_decode(x.to(device), gu.to(device), dn.to(device))
+        torch.testing.assert_close(out.cpu(), oracle.expert_mlp(x, gu, dn), **tol(torch.bfloat16))
 
 
 def test_routed_shared_fixed_ids(device, real_cpu, real_gpu):
