@@ -1999,6 +1999,9 @@ constexpr int kTagRouterMaxPerWg = 32;  // most tokens per workgroup
 // four SIMDs.)
 constexpr int kTagRouterSelfTokens = kFusedWaves;
 constexpr int kMaskWords = kTagRouterMaxTokens / 32;
+// From this many tokens on the tagged router computes its logits on MFMA
+// (moe_router_tagged_kernel<.., MF = true>) when the shapes allow.
+constexpr int kRouterMfmaMinTokens = 33;
 static_assert(kFusedSelWords >= (size_t)kTagRouterMaxTokens * 8, "router selection region too small");
 static_assert(kFusedLogitWords >= (size_t)kTagRouterMaxTokens * kFusedMaxExperts, "router logit region too small");
 
@@ -2071,7 +2074,16 @@ __device__ void build_routing_tables_masks(const int* s_ids, const uint32_t* s_m
 // masks [E * ceil(T/32)] (sized by the host for this T).
 FK_TIMELINE_BUFFER(moe_router)
 
-template <bool BFW, bool BFX, bool BFN, bool TILED, int TU>
+// MF: the logits as v_mfma_f32_16x16x32_bf16 tiles instead (bf16 router
+// weight, H a multiple of 256 up to 2048, E a multiple of 16; the host picks
+// it from kRouterMfmaMinTokens tokens on).  Workgroup (ue, ut) takes experts
+// 16 ue .. + 15 and tokens 16 ut .. + 15; wavefront w multiplies the K range
+// w H/8 .. + H/8: A = the 16 weight rows, B = the tokens x * (off + w_norm)
+// as bf16 hi + lo columns (~16 mantissa bits, as the expert stage's
+// activations), accumulated in fp32; each lane also sums its x^2 for the
+// token's RMSNorm.  The eight partial tiles and sums meet in LDS in wave
+// order; the logit is sum * rsqrt(mean(x^2) + eps) + bias.
+template <bool BFW, bool BFX, bool BFN, bool TILED, int TU, bool MF = false>
 __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   static_assert(TU <= kTagRouterTile && (!TILED || TU == kTagRouterTile), "tile of tokens");
   extern __shared__ int s_dyn_ids[];
@@ -2092,144 +2104,221 @@ __global__ __launch_bounds__(512) void moe_router_tagged_kernel(RouterArgs a) {
   FK_TIMELINE_DECL;
   FK_MARK(0);  // (timeline markers: diagnostic builds only)
 
-  // ---- logits of rows 8ub.. for tokens t0 .. t0 + ntok - 1 ----------------
-  // Every load of the row is issued with the first tile's tokens, before the
-  // first use (the norm weight with a compile-time dtype: a run-time dtype
-  // test would wait for every load before it); token indices past this
-  // workgroup's last token repeat it (cache hits, not other tokens' lines).
-  const int tlast = t0 + ntok - 1;
-  const bool row = e < E;
-  const int erow = row ? e : 0;
-  Raw8<BFX> xr[TU][4];
-  float wn[4][8];
-  // bias of the row whose logits this thread applies it to: the wavefront's
-  // row, or (tiled) the row this thread stores (thread t*8 + l: row 8ub + l);
-  // its word is loaded after the rows (unconditionally: a missing bias reads
-  // the router weight and is dropped), decoded where it is added
-  const int brow = TILED ? min(ub * 8 + (tid & 7), E - 1) : erow;
-  const void* bsrc = a.bias ? a.bias : a.W;
-  const int bdt = a.bias ? a.bias_dt : FK_DTYPE_F32;
-  uint32_t bias_word;
-  {
-    Raw8<BFW> wr[4];
-    Raw8<BFN> nr[4];
+  WaitLimits wl{};
+  uint32_t tag = 0;
+  if constexpr (MF) {
+    static_assert(BFW, "the MFMA logits take a bf16 router weight");
+    __shared__ float s_macc[kFusedWaves][16][17];
+    __shared__ float s_mss[kFusedWaves][16];
+    const int nue = E >> 4, ue = blockIdx.x % nue, ut = blockIdx.x / nue;
+    const int e0 = ue * 16, tm0 = ut * 16;
+    const int kw = H >> 3, ks = kw >> 5;  // K range per wavefront, its 32-wide steps (<= 8)
+    const int n = lane & 15, g4 = lane >> 4;
+    const int tok = min(tm0 + n, T - 1);  // (columns past the last token repeat it; not stored)
+    // every load first: the weight rows (A operands), the token chunks and
+    // the norm weight of this lane's k groups, then the bias word
+    u32x4 wa[8];
+    Raw8<BFX> xb[8];
+    Raw8<BFN> nb[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int cc = min(lane + kWave * j, nch - 1);
-      wr[j] = load_raw8<BFW>(a.W, (size_t)erow * H + (size_t)cc * 8);
-#pragma unroll
-      for (int t = 0; t < TU; ++t)
-        xr[t][j] = load_raw8<BFX>(a.x, (size_t)min(t0 + t, tlast) * H + (size_t)cc * 8);
-      nr[j] = load_raw8<BFN>(a.nw, (size_t)cc * 8);
-    }
-    bias_word = elem_word(bsrc, bdt, brow);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = lane + kWave * j;
-      float w8[8], n8[8];
-      raw8_to_f32<BFN>(nr[j], n8);
-      raw8_to_f32<BFW>(wr[j], w8);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) wn[j][q] = c < nch ? w8[q] * (a.off + n8[q]) : 0.f;
-    }
-  }
-  const bool bias_on = a.bias && (TILED ? tid < 8 * TU && ub * 8 + (tid & 7) < E : row);
-  const float bias = bias_on ? elem_value(bias_word, bsrc, bdt, brow) : 0.f;
-  const WaitLimits wl = hdr.limits();
-  const uint32_t tag = wl.tag;
-  for (int tt = 0; tt < ntok; tt += TU) {
-    const int nt = min(TU, ntok - tt);
-    // next tile's tokens, fetched while this tile is computed (bf16 tokens;
-    // fp32 ones are fetched after it, which keeps the registers in budget)
-    constexpr bool PF = BFX && TILED;
-    Raw8<BFX> xn[PF ? TU : 1][4];
-    const bool more = TILED && tt + TU < ntok;
-    if (PF && more) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int cc = min(lane + kWave * j, nch - 1);
-#pragma unroll
-        for (int t = 0; t < (PF ? TU : 1); ++t)
-          xn[t][j] = load_raw8<BFX>(a.x, (size_t)min(t0 + tt + TU + t, tlast) * H + (size_t)cc * 8);
+    for (int s = 0; s < 8; ++s) {
+      if (s < ks) {
+        const int k = wave * kw + s * 32 + g4 * 8;
+        wa[s] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(a.W) + (size_t)(e0 + n) * H + k);
+        xb[s] = load_raw8<BFX>(a.x, (size_t)tok * H + k);
+        nb[s] = load_raw8<BFN>(a.nw, (size_t)k);
       }
     }
-    // Wavefront t < TU also sums the squares of token t (the RMSNorm scale
-    // is shared by every row); the storing threads apply it.
-    float mine = 0.f;  // lane t < nt: dot of token t0 + tt + t with the row
+    const int brow = min(e0 + (tid & 15), E - 1);
+    const void* bsrc = a.bias ? a.bias : a.W;
+    const int bdt = a.bias ? a.bias_dt : FK_DTYPE_F32;
+    const uint32_t bias_word = elem_word(bsrc, bdt, brow);
+    wl = hdr.limits();
+    tag = wl.tag;
+    f32x4_t acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float ss = 0.f;
 #pragma unroll
-    for (int t = 0; t < TU; ++t) {
-      if (t < nt) {
-        if constexpr (!TILED) {
-          float ss = 0.f, d = 0.f;
+    for (int s = 0; s < 8; ++s) {
+      if (s < ks) {
+        float x8[8], n8[8], y[8];
+        raw8_to_f32<BFX>(xb[s], x8);
+        raw8_to_f32<BFN>(nb[s], n8);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const bool in = lane + kWave * j < nch;
-            float x8[8];
-            raw8_to_f32<BFX>(xr[t][j], x8);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-              const float xv = in ? x8[q] : 0.f;
-              ss = fmaf(xv, xv, ss);
-              d = fmaf(xv, wn[j][q], d);
-            }
-          }
-          ss = wave_sum(ss);
-          d = wave_sum(d);
-          mine = lane == t ? d * rsqrtf(ss / (float)H + a.eps) + bias : mine;
-          continue;
+        for (int q = 0; q < 8; ++q) {
+          ss = fmaf(x8[q], x8[q], ss);
+          y[q] = x8[q] * (a.off + n8[q]);
         }
-        float d = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bool in = lane + kWave * j < nch;
-          float x8[8];
-          raw8_to_f32<BFX>(xr[t][j], x8);
-#pragma unroll
-          for (int q = 0; q < 8; ++q) d = fmaf(in ? x8[q] : 0.f, wn[j][q], d);
-        }
-        d = wave_sum(d);
-        mine = lane == t ? d : mine;
-        if (wave == t) {  // (a branch of its own: a per-element test costs every wavefront)
-          float ss = 0.f;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const bool in = lane + kWave * j < nch;
-            float x8[8];
-            raw8_to_f32<BFX>(xr[t][j], x8);
-#pragma unroll
-            for (int q = 0; q < 8; ++q) {
-              const float xv = in ? x8[q] : 0.f;
-              ss = fmaf(xv, xv, ss);
-            }
-          }
-          ss = wave_sum(ss);
-          if (lane == 0) s_ss[t] = ss;
-        }
+        u32x4 vh, vl;
+        split_hi_lo8(y, vh, vl);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wa[s]), __builtin_bit_cast(bf16x8_t, vh), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, wa[s]), __builtin_bit_cast(bf16x8_t, vl), acc, 0, 0, 0);
       }
     }
-    if (lane < nt) s_chunk[lane][wave] = mine;
+    // lanes n, n + 16, n + 32, n + 48 hold token n's k groups
+    ss += __shfl_xor(ss, 16);
+    ss += __shfl_xor(ss, 32);
+    if (g4 == 0) s_mss[wave][n] = ss;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) s_macc[wave][g4 * 4 + q][n] = acc[q];  // row (expert) g4*4+q, column (token) n
     __syncthreads();
-    if (tid < 8 * nt) {
-      const int t = tid >> 3, l = tid & 7, ee = ub * 8 + l;
-      if (ee < E) {
-        const float v = TILED ? s_chunk[t][l] * rsqrtf(s_ss[t] / (float)H + a.eps) + bias : s_chunk[t][l];
-        const size_t o = (size_t)(t0 + tt + t) * E + ee;
+    if (tid < 256) {
+      const int r = tid & 15, c = tid >> 4, t = tm0 + c, ee = e0 + r;
+      float d = 0.f, st = 0.f;
+#pragma unroll
+      for (int w = 0; w < kFusedWaves; ++w) {
+        d += s_macc[w][r][c];
+        st += s_mss[w][c];
+      }
+      const float bias = a.bias ? elem_value(bias_word, bsrc, bdt, brow) : 0.f;
+      const float v = d * rsqrtf(st / (float)H + a.eps) + bias;
+      if (t < T && ee < E) {
+        const size_t o = (size_t)t * E + ee;
         a.logits[o] = v;
         store_tagged(a.ws.f_logits + o, v, tag);
       }
     }
-    __syncthreads();  // s_chunk is rewritten by the next tile
-    if (tt == 0) FK_MARK(1);
-    if (more) {
-#pragma unroll
-      for (int t = 0; t < TU; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          if constexpr (PF) xr[t][j] = xn[t][j];
-          else xr[t][j] = load_raw8<BFX>(a.x, (size_t)min(t0 + tt + TU + t, tlast) * H +
-                                                  (size_t)min(lane + kWave * j, nch - 1) * 8);
-        }
+    FK_MARK(1);
+  } else {
+    // ---- logits of rows 8ub.. for tokens t0 .. t0 + ntok - 1 ----------------
+    // Every load of the row is issued with the first tile's tokens, before the
+    // first use (the norm weight with a compile-time dtype: a run-time dtype
+    // test would wait for every load before it); token indices past this
+    // workgroup's last token repeat it (cache hits, not other tokens' lines).
+    const int tlast = t0 + ntok - 1;
+    const bool row = e < E;
+    const int erow = row ? e : 0;
+    Raw8<BFX> xr[TU][4];
+    float wn[4][8];
+    // bias of the row whose logits this thread applies it to: the wavefront's
+    // row, or (tiled) the row this thread stores (thread t*8 + l: row 8ub + l);
+    // its word is loaded after the rows (unconditionally: a missing bias reads
+    // the router weight and is dropped), decoded where it is added
+    const int brow = TILED ? min(ub * 8 + (tid & 7), E - 1) : erow;
+    const void* bsrc = a.bias ? a.bias : a.W;
+    const int bdt = a.bias ? a.bias_dt : FK_DTYPE_F32;
+    uint32_t bias_word;
+    {
+      Raw8<BFW> wr[4];
+      Raw8<BFN> nr[4];
+  #pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int cc = min(lane + kWave * j, nch - 1);
+        wr[j] = load_raw8<BFW>(a.W, (size_t)erow * H + (size_t)cc * 8);
+  #pragma unroll
+        for (int t = 0; t < TU; ++t)
+          xr[t][j] = load_raw8<BFX>(a.x, (size_t)min(t0 + t, tlast) * H + (size_t)cc * 8);
+        nr[j] = load_raw8<BFN>(a.nw, (size_t)cc * 8);
+      }
+      bias_word = elem_word(bsrc, bdt, brow);
+  #pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = lane + kWave * j;
+        float w8[8], n8[8];
+        raw8_to_f32<BFN>(nr[j], n8);
+        raw8_to_f32<BFW>(wr[j], w8);
+  #pragma unroll
+        for (int q = 0; q < 8; ++q) wn[j][q] = c < nch ? w8[q] * (a.off + n8[q]) : 0.f;
+      }
     }
+    const bool bias_on = a.bias && (TILED ? tid < 8 * TU && ub * 8 + (tid & 7) < E : row);
+    const float bias = bias_on ? elem_value(bias_word, bsrc, bdt, brow) : 0.f;
+    wl = hdr.limits();
+    tag = wl.tag;
+    for (int tt = 0; tt < ntok; tt += TU) {
+      const int nt = min(TU, ntok - tt);
+      // next tile's tokens, fetched while this tile is computed (bf16 tokens;
+      // fp32 ones are fetched after it, which keeps the registers in budget)
+      constexpr bool PF = BFX && TILED;
+      Raw8<BFX> xn[PF ? TU : 1][4];
+      const bool more = TILED && tt + TU < ntok;
+      if (PF && more) {
+  #pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int cc = min(lane + kWave * j, nch - 1);
+  #pragma unroll
+          for (int t = 0; t < (PF ? TU : 1); ++t)
+            xn[t][j] = load_raw8<BFX>(a.x, (size_t)min(t0 + tt + TU + t, tlast) * H + (size_t)cc * 8);
+        }
+      }
+      // Wavefront t < TU also sums the squares of token t (the RMSNorm scale
+      // is shared by every row); the storing threads apply it.
+      float mine = 0.f;  // lane t < nt: dot of token t0 + tt + t with the row
+  #pragma unroll
+      for (int t = 0; t < TU; ++t) {
+        if (t < nt) {
+          if constexpr (!TILED) {
+            float ss = 0.f, d = 0.f;
+  #pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const bool in = lane + kWave * j < nch;
+              float x8[8];
+              raw8_to_f32<BFX>(xr[t][j], x8);
+  #pragma unroll
+              for (int q = 0; q < 8; ++q) {
+                const float xv = in ? x8[q] : 0.f;
+                ss = fmaf(xv, xv, ss);
+                d = fmaf(xv, wn[j][q], d);
+              }
+            }
+            ss = wave_sum(ss);
+            d = wave_sum(d);
+            mine = lane == t ? d * rsqrtf(ss / (float)H + a.eps) + bias : mine;
+            continue;
+          }
+          float d = 0.f;
+  #pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bool in = lane + kWave * j < nch;
+            float x8[8];
+            raw8_to_f32<BFX>(xr[t][j], x8);
+  #pragma unroll
+            for (int q = 0; q < 8; ++q) d = fmaf(in ? x8[q] : 0.f, wn[j][q], d);
+          }
+          d = wave_sum(d);
+          mine = lane == t ? d : mine;
+          if (wave == t) {  // (a branch of its own: a per-element test costs every wavefront)
+            float ss = 0.f;
+  #pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const bool in = lane + kWave * j < nch;
+              float x8[8];
+              raw8_to_f32<BFX>(xr[t][j], x8);
+  #pragma unroll
+              for (int q = 0; q < 8; ++q) {
+                const float xv = in ? x8[q] : 0.f;
+                ss = fmaf(xv, xv, ss);
+              }
+            }
+            ss = wave_sum(ss);
+            if (lane == 0) s_ss[t] = ss;
+          }
+        }
+      }
+      if (lane < nt) s_chunk[lane][wave] = mine;
+      __syncthreads();
+      if (tid < 8 * nt) {
+        const int t = tid >> 3, l = tid & 7, ee = ub * 8 + l;
+        if (ee < E) {
+          const float v = TILED ? s_chunk[t][l] * rsqrtf(s_ss[t] / (float)H + a.eps) + bias : s_chunk[t][l];
+          const size_t o = (size_t)(t0 + tt + t) * E + ee;
+          a.logits[o] = v;
+          store_tagged(a.ws.f_logits + o, v, tag);
+        }
+      }
+      __syncthreads();  // s_chunk is rewritten by the next tile
+      if (tt == 0) FK_MARK(1);
+      if (more) {
+  #pragma unroll
+        for (int t = 0; t < TU; ++t)
+  #pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            if constexpr (PF) xr[t][j] = xn[t][j];
+            else xr[t][j] = load_raw8<BFX>(a.x, (size_t)min(t0 + tt + TU + t, tlast) * H +
+                                                    (size_t)min(lane + kWave * j, nch - 1) * 8);
+          }
+      }
+    }
+  
   }
 
   FK_MARK(2);
@@ -2450,7 +2539,21 @@ static bool tagged_router_eligible(const RouterArgs& ra) {
 
 template <bool BW, bool BX, bool BN>
 static int launch_router_tagged_t(const RouterArgs& ra_in, hipStream_t stream) {
-  static int cap_cache[2][64] = {{0}};
+  static int cap_cache[3][64] = {{0}};
+  constexpr size_t kMaxShmAll = ((size_t)kTagRouterMaxTokens * 8 + (size_t)kFusedMaxExperts * kMaskWords) * 4;
+  if constexpr (BW) {
+    // MFMA logits: one workgroup per 16 experts x 16 tokens
+    if (ra_in.T >= kRouterMfmaMinTokens && ra_in.H % 256 == 0 && ra_in.H <= 2048 && ra_in.E % 16 == 0) {
+      auto kernel = moe_router_tagged_kernel<true, BX, BN, false, 2, true>;
+      const int units = (ra_in.E / 16) * ((ra_in.T + 15) / 16);
+      const int cap = resident_capacity(kernel, 512, kMaxShmAll, cap_cache[2]);
+      if (units <= cap) {
+        const size_t shm = ((size_t)ra_in.T * ra_in.K + (size_t)ra_in.E * ((ra_in.T + 31) / 32)) * 4;
+        hipLaunchKernelGGL(kernel, dim3(units), dim3(512), shm, stream, ra_in);
+        return check_launch("moe_router_tagged_kernel");
+      }
+    }
+  }
   // Workgroup 0 waits for every other workgroup's logits: all must be
   // resident.  The fewest tokens per workgroup (2, 4, 8, .. 32) whose grid
   // is co-resident; one tile per workgroup (tu <= 4) takes the single-tile

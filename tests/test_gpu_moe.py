@@ -126,23 +126,29 @@ def test_router_exact_ties_go_to_lower_id(device):
     assert_routing_parity(logits, ids, w, o_logits, 4)
 
 
-@pytest.mark.parametrize("tokens", [2, 5, 9, 12, 16, 17, 24])
-def test_batched_router_exact_ties_go_to_lower_id(device, tokens):
+@pytest.mark.parametrize("tokens,hidden", [(2, 64), (5, 64), (9, 64), (12, 64), (16, 64), (17, 64), (24, 64),
+                                           (40, 256), (70, 512)])
+def test_batched_router_exact_ties_go_to_lower_id(device, tokens, hidden):
     # Per token, three identical router rows give identical logits at the top
     # (the lower id first) whichever path selects: workgroup 0 for every token
-    # up to 8 tokens, one workgroup per token from 9 on.
+    # up to 8 tokens, one workgroup per token from 9 on; from 33 tokens at a
+    # hidden size that is a multiple of 256 the logits come from MFMA tiles
+    # (rows 5 and 11 in one tile, 17 in the next).
     g = torch.Generator().manual_seed(30 + tokens)
-    x = torch.randn(64, generator=g) + 0.3 * torch.randn(tokens, 64, generator=g)  # tokens near one direction
-    nw = torch.zeros(64)
-    rw = 0.05 * torch.randn(24, 64, generator=g)
+    x = torch.randn(hidden, generator=g) + 0.3 * torch.randn(tokens, hidden, generator=g)  # tokens near one direction
+    nw = torch.zeros(hidden)
+    rw = 0.05 * torch.randn(32, hidden, generator=g)
     n = oracle.rms_norm(x, nw)
     # a row along the tokens' mean direction: the largest logit of every token
     d = n.mean(0)
     rw[5] = 4.0 * d / d.norm()
     rw[11] = rw[5]
     rw[17] = rw[5]
+    # (a bf16 router weight at the MFMA shapes: the path takes bf16 rows)
+    rw_dev = rw.bfloat16() if hidden % 256 == 0 else rw
+    rw = rw_dev.float()
     assert bool(((n @ rw[5]) > 0.5).all())
-    logits, ids, w = hip.hip_qwen36_batched_moe_router_decode(x.to(device), nw.to(device), rw.to(device), top_k=4)
+    logits, ids, w = hip.hip_qwen36_batched_moe_router_decode(x.to(device), nw.to(device), rw_dev.to(device), top_k=4)
     o_logits, o_ids, _ = oracle.router(x, nw, rw, 4)
     for t in range(tokens):
         assert logits[t, 5].item() == logits[t, 11].item() == logits[t, 17].item()
