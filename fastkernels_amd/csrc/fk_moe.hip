@@ -2000,8 +2000,11 @@ constexpr int kTagRouterMaxPerWg = 32;  // most tokens per workgroup
 constexpr int kTagRouterSelfTokens = kFusedWaves;
 constexpr int kMaskWords = kTagRouterMaxTokens / 32;
 // From this many tokens on the tagged router computes its logits on MFMA
-// (moe_router_tagged_kernel<.., MF = true>) when the shapes allow.
-constexpr int kRouterMfmaMinTokens = 33;
+// (moe_router_tagged_kernel<.., MF = true>) when the shapes allow: at the
+// model's shapes 11.4-11.6 us from 33 to 48 tokens, where the register tiles
+// take 11.0 us at 33 tokens and 12.0-12.3 us from 36 on (18.4 against
+// 12.6 us at 128).
+constexpr int kRouterMfmaMinTokens = 36;
 static_assert(kFusedSelWords >= (size_t)kTagRouterMaxTokens * 8, "router selection region too small");
 static_assert(kFusedLogitWords >= (size_t)kTagRouterMaxTokens * kFusedMaxExperts, "router logit region too small");
 

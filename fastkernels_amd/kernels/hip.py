@@ -261,6 +261,22 @@ def _router_bias_checks(router_bias: Any | None, num_experts: int) -> None:
         raise ValueError("router_bias must have num_experts elements")
 
 
+# The C ABI routes at most 4096 (token, expert) pairs per call (fk_moe.hip
+# kMaxPairs: one workgroup builds the routing tables in LDS).  Longer batches
+# go through in consecutive calls of whole tokens on the same stream and
+# workspace: every token is routed, and its experts combined, on its own, so
+# the split changes no token's result beyond the kernel choice that the
+# batch size makes anyway.
+_MAX_PAIRS = 4096
+
+
+def _token_chunks(tokens: int, top_k: int) -> list[tuple[int, int]]:
+    if tokens < 1:
+        return [(0, tokens)]  # (the C ABI reports the bad size)
+    step = max(1, _MAX_PAIRS // top_k)
+    return [(s, min(tokens, s + step)) for s in range(0, tokens, step)]
+
+
 def _run_router(hidden2d, norm_weight, router_weight, top_k, eps, norm_offset, router_bias, ws):
     tokens, hidden_size = hidden2d.shape
     num_experts = router_weight.shape[0]
@@ -270,15 +286,16 @@ def _run_router(hidden2d, norm_weight, router_weight, top_k, eps, norm_offset, r
     weights = torch.empty((tokens, top_k), device=dev, dtype=torch.float32)
     nw = _dense(norm_weight)
     rb = None if router_bias is None else _dense(router_bias)
-    _lib.call(
-        "fk_moe_router",
-        hidden2d.data_ptr(), _fcode(hidden2d, "hidden"),
-        nw.data_ptr(), _fcode(nw, "norm_weight"),
-        router_weight.data_ptr(), _fcode(router_weight, "router_weight"),
-        _ptr(rb), _fcode(rb, "router_bias") if rb is not None else 0,
-        tokens, hidden_size, num_experts, top_k, float(eps), float(norm_offset),
-        logits.data_ptr(), ids.data_ptr(), weights.data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev),
-    )
+    for s, e in _token_chunks(tokens, top_k):
+        _lib.call(
+            "fk_moe_router",
+            hidden2d[s:e].data_ptr(), _fcode(hidden2d, "hidden"),
+            nw.data_ptr(), _fcode(nw, "norm_weight"),
+            router_weight.data_ptr(), _fcode(router_weight, "router_weight"),
+            _ptr(rb), _fcode(rb, "router_bias") if rb is not None else 0,
+            e - s, hidden_size, num_experts, top_k, float(eps), float(norm_offset),
+            logits[s:e].data_ptr(), ids[s:e].data_ptr(), weights[s:e].data_ptr(), ws.data_ptr(), ws.numel(), _stream(dev),
+        )
     return logits, ids, weights
 
 
@@ -327,7 +344,8 @@ def hip_qwen36_batched_moe_router_decode(
     _router_bias_checks(router_bias, router_weight.shape[0])
     x = _dense(hidden)
     rw = _dense(router_weight)
-    ws = _workspace("moe", x.device, _lib.load().fk_moe_workspace_bytes(x.shape[0], top_k, rw.shape[0], 8, 8))
+    cmax = max(e - s for s, e in _token_chunks(x.shape[0], top_k))
+    ws = _workspace("moe", x.device, _lib.load().fk_moe_workspace_bytes(cmax, top_k, rw.shape[0], 8, 8))
     return _run_router(x, norm_weight, rw, top_k, eps, norm_offset, router_bias, ws)
 
 
@@ -371,11 +389,9 @@ def _shared_checks(shared_gate_up_weight, shared_down_weight, shared_expert_gate
             raise ValueError("shared_expert_gate_weight must have hidden_size elements")
 
 
-def _run_experts(
-    hidden2d, gu, dn, sgu, sdn, sg, ids2d, w2d, *, layer_out=False, ws=None, aligned=False
-):
-    """Expert stage for `[T,H]` hidden; routing given by ids/weights (aligned here)
-    or already in `ws` (aligned=True, written by the router)."""
+def _run_experts(hidden2d, gu, dn, sgu, sdn, sg, ids2d, w2d, *, layer_out=False):
+    """Expert stage for `[T,H]` hidden, routing given by ids/weights (aligned
+    here, in calls of at most 4096 pairs)."""
 
     tokens, hidden_size = hidden2d.shape
     num_experts, two_i, _ = gu.shape
@@ -383,27 +399,28 @@ def _run_experts(
     top_k = ids2d.shape[1]
     dev = hidden2d.device
     lib = _lib.load()
-    if ws is None:
-        ws = _workspace("moe", dev, lib.fk_moe_workspace_bytes(tokens, top_k, num_experts, intermediate, hidden_size))
+    chunks = _token_chunks(tokens, top_k)
+    cmax = max(e - s for s, e in chunks)
+    ws = _workspace("moe", dev, lib.fk_moe_workspace_bytes(cmax, top_k, num_experts, intermediate, hidden_size))
     stream = _stream(dev)
-    if not aligned:
-        ids = _dense(ids2d)
-        w = _dense(w2d)
-        _lib.call(
-            "fk_moe_align", ids.data_ptr(), _icode(ids, "topk_ids"), w.data_ptr(), _fcode(w, "topk_weights"),
-            tokens, top_k, num_experts, ws.data_ptr(), ws.numel(), None, None, None, None, stream,
-        )
+    ids = _dense(ids2d)
+    w = _dense(w2d)
     out = torch.empty((tokens, hidden_size), device=dev, dtype=torch.float32)
     lo = torch.empty_like(out) if layer_out else None
     sgp = None if sg is None else _dense(sg)
-    _lib.call(
-        "fk_moe_experts",
-        hidden2d.data_ptr(), _fcode(hidden2d, "hidden"),
-        gu.data_ptr(), dn.data_ptr(), _fcode(gu, "expert weights"),
-        _ptr(sgu), _ptr(sdn), _ptr(sgp), _fcode(sgp, "shared_expert_gate_weight") if sgp is not None else 0,
-        tokens, hidden_size, intermediate, num_experts, top_k,
-        out.data_ptr(), _ptr(lo), ws.data_ptr(), ws.numel(), stream,
-    )
+    for s, e in chunks:
+        _lib.call(
+            "fk_moe_align", ids[s:e].data_ptr(), _icode(ids, "topk_ids"), w[s:e].data_ptr(), _fcode(w, "topk_weights"),
+            e - s, top_k, num_experts, ws.data_ptr(), ws.numel(), None, None, None, None, stream,
+        )
+        _lib.call(
+            "fk_moe_experts",
+            hidden2d[s:e].data_ptr(), _fcode(hidden2d, "hidden"),
+            gu.data_ptr(), dn.data_ptr(), _fcode(gu, "expert weights"),
+            _ptr(sgu), _ptr(sdn), _ptr(sgp), _fcode(sgp, "shared_expert_gate_weight") if sgp is not None else 0,
+            e - s, hidden_size, intermediate, num_experts, top_k,
+            out[s:e].data_ptr(), _ptr(lo[s:e] if lo is not None else None), ws.data_ptr(), ws.numel(), stream,
+        )
     return out, lo
 
 
@@ -554,7 +571,9 @@ def _moe_full(hidden2d, norm_weight, router_weight, gu_w, dn_w, sgu_w, sdn_w, sg
     num_experts = gu_w.shape[0]
     dev = x.device
     lib = _lib.load()
-    ws = _workspace("moe", dev, lib.fk_moe_workspace_bytes(tokens, top_k, num_experts, intermediate, hidden_size))
+    chunks = _token_chunks(tokens, top_k)
+    cmax = max(e - s for s, e in chunks)
+    ws = _workspace("moe", dev, lib.fk_moe_workspace_bytes(cmax, top_k, num_experts, intermediate, hidden_size))
     rw = _dense(router_weight)
     gu, dn, sgu, sdn = _dense(gu_w), _dense(dn_w), _dense(sgu_w), _dense(sdn_w)
     nw = _dense(norm_weight)
@@ -565,16 +584,17 @@ def _moe_full(hidden2d, norm_weight, router_weight, gu_w, dn_w, sgu_w, sdn_w, sg
     weights = torch.empty((tokens, top_k), device=dev, dtype=torch.float32)
     out = torch.empty((tokens, hidden_size), device=dev, dtype=torch.float32)
     lo = torch.empty_like(out) if layer_out else None
-    _lib.call(
-        "fk_moe_layer",
-        x.data_ptr(), _fcode(x, "hidden"), nw.data_ptr(), _fcode(nw, "norm_weight"),
-        rw.data_ptr(), _fcode(rw, "router_weight"), _ptr(rb), _fcode(rb, "router_bias") if rb is not None else 0,
-        gu.data_ptr(), dn.data_ptr(), _fcode(gu, "expert weights"),
-        sgu.data_ptr(), sdn.data_ptr(), _ptr(sg), _fcode(sg, "shared_expert_gate_weight") if sg is not None else 0,
-        tokens, hidden_size, intermediate, num_experts, top_k, float(eps), float(norm_offset),
-        logits.data_ptr(), ids.data_ptr(), weights.data_ptr(), out.data_ptr(), _ptr(lo),
-        ws.data_ptr(), ws.numel(), _stream(dev),
-    )
+    for s, e in chunks:
+        _lib.call(
+            "fk_moe_layer",
+            x[s:e].data_ptr(), _fcode(x, "hidden"), nw.data_ptr(), _fcode(nw, "norm_weight"),
+            rw.data_ptr(), _fcode(rw, "router_weight"), _ptr(rb), _fcode(rb, "router_bias") if rb is not None else 0,
+            gu.data_ptr(), dn.data_ptr(), _fcode(gu, "expert weights"),
+            sgu.data_ptr(), sdn.data_ptr(), _ptr(sg), _fcode(sg, "shared_expert_gate_weight") if sg is not None else 0,
+            e - s, hidden_size, intermediate, num_experts, top_k, float(eps), float(norm_offset),
+            logits[s:e].data_ptr(), ids[s:e].data_ptr(), weights[s:e].data_ptr(), out[s:e].data_ptr(),
+            _ptr(lo[s:e] if lo is not None else None), ws.data_ptr(), ws.numel(), _stream(dev),
+        )
     return out, lo, logits, ids, weights
 
 
@@ -941,6 +961,9 @@ def hip_qwen36_batched_attention_project(
     return q, k, v
 
 
+_MAX_ATTN_ROWS = 32  # rows per fk_attention_decode call (fk_attention.hip kAttnMaxTokens)
+
+
 def _attention(hidden, key_cache, value_cache, norm_weight, q_proj_weight, k_proj_weight, v_proj_weight,
                out_proj_weight, q_norm_weight, k_norm_weight, start_position, attention_heads, kv_heads, head_dim,
                rope_dim, rope_theta, eps, qk_norm_eps, copy_cache, rope_interleaved, residual):
@@ -985,18 +1008,25 @@ def _attention(hidden, key_cache, value_cache, norm_weight, q_proj_weight, k_pro
     dev = x.device
     update = torch.empty((tokens, hidden_size), device=dev, dtype=torch.float32)
     out = torch.empty_like(update) if residual else None
-    nbytes = _lib.load().fk_attention_workspace_bytes(tokens, attention_heads, kv_heads, head_dim)
+    # The C ABI decodes at most _MAX_ATTN_ROWS rows per call (their new keys
+    # sit in LDS); longer batches go through in consecutive calls: each call
+    # writes its rows' keys and values into the cache before the next one
+    # reads them, which is the causal order one call keeps.
+    step = _MAX_ATTN_ROWS
+    nbytes = _lib.load().fk_attention_workspace_bytes(min(tokens, step), attention_heads, kv_heads, head_dim)
     ws = _workspace("attention", dev, nbytes)
-    _lib.call(
-        "fk_attention_decode",
-        x.data_ptr(), _fcode(x, "hidden"), nw.data_ptr(), _fcode(nw, "norm_weight"),
-        wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), wo.data_ptr(), _fcode(wq, "projection weights"),
-        qn.data_ptr(), kn.data_ptr(), _fcode(qn, "q_norm_weight"),
-        kc.data_ptr(), vc.data_ptr(), _fcode(kc, "key_cache"), kc.shape[0], int(start_position), None,
-        tokens, hidden_size, attention_heads, kv_heads, head_dim, int(rope_dim), float(rope_theta),
-        1 if rope_interleaved else 0, float(eps), float(qk_norm_eps),
-        update.data_ptr(), _ptr(out), ws.data_ptr(), ws.numel(), _stream(dev),
-    )
+    for s in range(0, max(tokens, 1), step):
+        e = min(tokens, s + step)
+        _lib.call(
+            "fk_attention_decode",
+            x[s:e].data_ptr(), _fcode(x, "hidden"), nw.data_ptr(), _fcode(nw, "norm_weight"),
+            wq.data_ptr(), wk.data_ptr(), wv.data_ptr(), wo.data_ptr(), _fcode(wq, "projection weights"),
+            qn.data_ptr(), kn.data_ptr(), _fcode(qn, "q_norm_weight"),
+            kc.data_ptr(), vc.data_ptr(), _fcode(kc, "key_cache"), kc.shape[0], int(start_position) + s, None,
+            e - s, hidden_size, attention_heads, kv_heads, head_dim, int(rope_dim), float(rope_theta),
+            1 if rope_interleaved else 0, float(eps), float(qk_norm_eps),
+            update[s:e].data_ptr(), _ptr(out[s:e] if out is not None else None), ws.data_ptr(), ws.numel(), _stream(dev),
+        )
     return update, out, kc, vc
 
 

@@ -96,6 +96,26 @@ def test_attention_steps_chain_through_the_cache(device, attn_gpu):
     torch.testing.assert_close(v2, v1, atol=1e-6, rtol=1e-6)
 
 
+@pytest.mark.parametrize("copy_cache", [True, False])
+def test_attention_decode_more_than_32_rows(device, attn_cpu, attn_gpu, copy_cache):
+    # 40 rows: two calls of the C ABI (32 + 8), the second reading the first
+    # one's keys and values from the cache, against the oracle's single pass
+    tokens, start = 40, 11
+    x, kc, vc = _inputs(tokens, start, torch.bfloat16, seed=17)
+    kd, vd = kc.to(device), vc.to(device)
+    upd, nkc, nvc = hip.hip_qwen36_batched_attention_decode(
+        x.to(device), kd, vd, *_args(attn_gpu), start_position=start, copy_cache=copy_cache, **KW)
+    o_upd, o_kc, o_vc = oracle.attention_update(
+        x, kc, vc, *_args(attn_cpu), start_position=start, heads=HEADS, kv_heads=KVH, head_dim=HD, rope_dim=RD,
+        rope_theta=THETA, interleaved=True)
+    torch.testing.assert_close(upd.cpu(), o_upd, **tol(torch.bfloat16))
+    new = slice(start, start + tokens)
+    torch.testing.assert_close(nkc[new].float().cpu(), o_kc[new].float(), **tol(torch.bfloat16))
+    torch.testing.assert_close(nvc[new].float().cpu(), o_vc[new].float(), **tol(torch.bfloat16))
+    assert (nkc is kd) == (not copy_cache)
+    assert torch.equal(nkc[:start].cpu(), kc[:start]) and torch.equal(nvc[:start].cpu(), vc[:start])
+
+
 def test_attention_moe_layer_matches_oracle(device, attn_cpu, attn_gpu):
     g = torch.Generator().manual_seed(12)
     r = lambda *s, sc=0.02: (torch.randn(*s, generator=g) * sc).to(torch.bfloat16)  # noqa: E731

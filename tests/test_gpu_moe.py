@@ -131,7 +131,7 @@ def test_router_exact_ties_go_to_lower_id(device):
 def test_batched_router_exact_ties_go_to_lower_id(device, tokens, hidden):
     # Per token, three identical router rows give identical logits at the top
     # (the lower id first) whichever path selects: workgroup 0 for every token
-    # up to 8 tokens, one workgroup per token from 9 on; from 33 tokens at a
+    # up to 8 tokens, one workgroup per token from 9 on; from 36 tokens at a
     # hidden size that is a multiple of 256 the logits come from MFMA tiles
     # (rows 5 and 11 in one tile, 17 in the next).
     g = torch.Generator().manual_seed(30 + tokens)

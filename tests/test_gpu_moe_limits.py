@@ -74,6 +74,7 @@ def _check(device, e, h, i, tokens, seed):
         (64, 3072, 128, 5),     # H > 2048: 8 chunks per lane in router and gate/up
         (16, 4096, 1024, 2),    # the hidden and intermediate limits together
         (64, 1024, 1024, 1),    # I > 512 at one token: tagged router, 2 chunks per lane in down
+        (64, 256, 128, 600),    # 4800 (token, expert) pairs: two calls of the C ABI (512 + 88 tokens)
     ],
 )
 def test_moe_layer_at_operator_limits(device, e, h, i, tokens):
@@ -110,3 +111,17 @@ def test_router_bias_bf16_and_misaligned(device, tokens):
         o_logits, _, _ = oracle.router(x, w[0], w[1], K, router_bias=bias16)
         torch.testing.assert_close(logits.cpu(), o_logits, atol=1e-4, rtol=1e-4)
         assert_routing_parity(logits, ids, wt, o_logits, K)
+
+
+def test_batched_routed_experts_over_4096_pairs(device):
+    # the fixed-ids expert path in calls of at most 4096 pairs (512 + 88 tokens)
+    e, h, i, tokens = 32, 256, 64, 600
+    w = _weights(e, h, i, seed=77)
+    x = wl.make_hidden(tokens, h, seed=78)
+    g = torch.Generator().manual_seed(79)
+    ids = torch.stack([torch.randperm(e, generator=g)[:K] for _ in range(tokens)])
+    wt = torch.softmax(torch.randn(tokens, K, generator=g), -1)
+    out = hip.hip_qwen36_batched_routed_shared_experts_decode(
+        x.to(device), ids.to(device), wt.to(device), *[t.to(device) for t in w[2:7]])
+    ref = oracle.routed_experts(x, ids, wt, w[2], w[3]) + oracle.shared_expert(x, w[4], w[5], w[6])
+    torch.testing.assert_close(out.cpu(), ref, **tol(torch.bfloat16))
