@@ -266,15 +266,18 @@ def _router_bias_checks(router_bias: Any | None, num_experts: int) -> None:
 # go through in consecutive calls of whole tokens on the same stream and
 # workspace: every token is routed, and its experts combined, on its own, so
 # the split changes no token's result beyond the kernel choice that the
-# batch size makes anyway.
+# batch size makes anyway.  A batch of no tokens makes no call and returns
+# empty outputs, as the reference's zero-sized launch grids do.
 _MAX_PAIRS = 4096
 
 
 def _token_chunks(tokens: int, top_k: int) -> list[tuple[int, int]]:
-    if tokens < 1:
-        return [(0, tokens)]  # (the C ABI reports the bad size)
     step = max(1, _MAX_PAIRS // top_k)
     return [(s, min(tokens, s + step)) for s in range(0, tokens, step)]
+
+
+def _chunk_max(chunks: list[tuple[int, int]]) -> int:
+    return max((e - s for s, e in chunks), default=1)
 
 
 def _run_router(hidden2d, norm_weight, router_weight, top_k, eps, norm_offset, router_bias, ws):
@@ -344,7 +347,7 @@ def hip_qwen36_batched_moe_router_decode(
     _router_bias_checks(router_bias, router_weight.shape[0])
     x = _dense(hidden)
     rw = _dense(router_weight)
-    cmax = max(e - s for s, e in _token_chunks(x.shape[0], top_k))
+    cmax = _chunk_max(_token_chunks(x.shape[0], top_k))
     ws = _workspace("moe", x.device, _lib.load().fk_moe_workspace_bytes(cmax, top_k, rw.shape[0], 8, 8))
     return _run_router(x, norm_weight, rw, top_k, eps, norm_offset, router_bias, ws)
 
@@ -400,7 +403,7 @@ def _run_experts(hidden2d, gu, dn, sgu, sdn, sg, ids2d, w2d, *, layer_out=False)
     dev = hidden2d.device
     lib = _lib.load()
     chunks = _token_chunks(tokens, top_k)
-    cmax = max(e - s for s, e in chunks)
+    cmax = _chunk_max(chunks)
     ws = _workspace("moe", dev, lib.fk_moe_workspace_bytes(cmax, top_k, num_experts, intermediate, hidden_size))
     stream = _stream(dev)
     ids = _dense(ids2d)
@@ -572,7 +575,7 @@ def _moe_full(hidden2d, norm_weight, router_weight, gu_w, dn_w, sgu_w, sdn_w, sg
     dev = x.device
     lib = _lib.load()
     chunks = _token_chunks(tokens, top_k)
-    cmax = max(e - s for s, e in chunks)
+    cmax = _chunk_max(chunks)
     ws = _workspace("moe", dev, lib.fk_moe_workspace_bytes(cmax, top_k, num_experts, intermediate, hidden_size))
     rw = _dense(router_weight)
     gu, dn, sgu, sdn = _dense(gu_w), _dense(dn_w), _dense(sgu_w), _dense(sdn_w)
@@ -688,6 +691,8 @@ def hip_qwen36_batched_deltanet_project(
     z = torch.empty((tokens, wz.shape[0]), device=dev, dtype=torch.float32)
     a = torch.empty((tokens, wa.shape[0]), device=dev, dtype=torch.float32)
     b = torch.empty((tokens, wb.shape[0]), device=dev, dtype=torch.float32)
+    if tokens == 0:
+        return mixed, z, a, b
     _lib.call(
         "fk_deltanet_project",
         x.data_ptr(), _fcode(x, "hidden"), nw.data_ptr(), _fcode(nw, "norm_weight"),
@@ -951,6 +956,8 @@ def hip_qwen36_batched_attention_project(
     q = torch.empty((tokens, wq.shape[0]), device=dev, dtype=torch.float32)
     k = torch.empty((tokens, wk.shape[0]), device=dev, dtype=torch.float32)
     v = torch.empty((tokens, wv.shape[0]), device=dev, dtype=torch.float32)
+    if tokens == 0:
+        return q, k, v
     _lib.call(
         "fk_attention_project",
         x.data_ptr(), _fcode(x, "hidden"), nw.data_ptr(), _fcode(nw, "norm_weight"),
@@ -1012,10 +1019,11 @@ def _attention(hidden, key_cache, value_cache, norm_weight, q_proj_weight, k_pro
     # sit in LDS); longer batches go through in consecutive calls: each call
     # writes its rows' keys and values into the cache before the next one
     # reads them, which is the causal order one call keeps.
+    # No rows: no call (the caches are returned as given, or copied).
     step = _MAX_ATTN_ROWS
-    nbytes = _lib.load().fk_attention_workspace_bytes(min(tokens, step), attention_heads, kv_heads, head_dim)
+    nbytes = _lib.load().fk_attention_workspace_bytes(min(max(tokens, 1), step), attention_heads, kv_heads, head_dim)
     ws = _workspace("attention", dev, nbytes)
-    for s in range(0, max(tokens, 1), step):
+    for s in range(0, tokens, step):
         e = min(tokens, s + step)
         _lib.call(
             "fk_attention_decode",
