@@ -1068,13 +1068,21 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(ExpertArgs a) {
 //   gate/up: work item (slot, 16 intermediates) = 16 gate + 16 up rows, 512
 //            threads, K = H split over the 8 wavefronts; the tokens are the
 //            bf16 hidden states themselves (exact products).
-//   down:    work item (slot, 64 output rows), 256 threads, K = I split over
+//   down:    work item (slot, 32 or 64 output rows), 256 threads, K = I split over
 //            the 4 wavefronts; fp32 activations enter as bf16 hi + lo
 //            columns (8 pairs per tile, ~16 mantissa bits).
 // ---------------------------------------------------------------------------
 constexpr int kMfmaMinTokens = 64;
 constexpr int kGuMfmaRows = 16;   // intermediates per gate/up work item
-constexpr int kDnMfmaRows = 64;   // output rows per down work item
+// Output rows per down work item: 32 while the routed experts average at
+// most kDnMfmaSmallPairs pairs (one tile of 8 pairs for most of them), else
+// 64.  Smaller items stream their 32 KB sooner (T=64 76.6 -> 71.3 us, T=128
+// 88.8 -> 85.7 us at the model's shapes); with more tiles per item the
+// per-tile reduction and the activation reads, which grow with the number
+// of items, cost more (T=256 99.8 -> 106.2 us), so 64 rows stay there.
+constexpr int kDnMfmaRowsSmall = 32;
+constexpr int kDnMfmaRows = 64;
+constexpr int kDnMfmaSmallPairs = 4;
 constexpr int kGuMfmaWaves = 8;
 constexpr int kDnMfmaWaves = 4;
 
@@ -1229,15 +1237,17 @@ __global__ __launch_bounds__(512) void moe_gateup_mfma_kernel(ExpertArgs a) {
   }
 }
 
-// KS = I / 128: MFMA steps per wavefront (I = 256, 512 -> 2, 4).
-template <int KS>
+// KS = I / 128: MFMA steps per wavefront (I = 256, 512 -> 2, 4); RT: row
+// tiles of 16 output rows per work item.
+template <int KS, int RT>
 __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertArgs a) {
   extern __shared__ float4 s_dn_v[];
   char* s_lds = reinterpret_cast<char*>(s_dn_v);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int H = a.H, I = a.I;
-  const int rbn = H / kDnMfmaRows;
-  const int rb = blockIdx.x % rbn, r0 = rb * kDnMfmaRows;
+  constexpr int NR = RT * 16;  // output rows per work item
+  const int rbn = H / NR;
+  const int rb = blockIdx.x % rbn, r0 = rb * NR;
   const char* W;
   int pos0, npairs;
   bool shared;
@@ -1267,18 +1277,18 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertArgs a) {
   };
   load_act(0);
 
-  // rows r0 + 16 rt .. of this wavefront's K range (4 row tiles)
+  // rows r0 + 16 rt .. of this wavefront's K range (RT row tiles)
   const uint32_t lane_off = (uint32_t)((((lane >> lpr_sh) << li) + wave * kw + ((lane & ((1 << lpr_sh) - 1)) << 3)) << 1);
-  u32x4 av[4][KS];
+  u32x4 av[RT][KS];
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt)
+  for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
     for (int s = 0; s < KS; ++s)
       av[rt][s] = __builtin_nontemporal_load(
           reinterpret_cast<const u32x4*>(W + ((size_t)(r0 + rt * 16 + s * rpi) << (li + 1)) + lane_off));
   char* area = s_lds + (size_t)wave * 16 * pitch;
 #pragma unroll
-  for (int rt = 0; rt < 4; ++rt) rows_to_mfma_a<KS>(av[rt], area, pitch, lpr_sh, lane);
+  for (int rt = 0; rt < RT; ++rt) rows_to_mfma_a<KS>(av[rt], area, pitch, lpr_sh, lane);
   __syncthreads();  // the partial tiles below overlap other wavefronts' areas
 
   float* s_part = reinterpret_cast<float*>(s_lds);  // [wave][row tile][16 rows][16 columns]
@@ -1299,9 +1309,9 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertArgs a) {
       bv[s] = u32x4{h[0], h[1], h[2], h[3]};
     }
     if ((tile + 1) * 8 < npairs) load_act(tile + 1);
-    f32x4_t acc[4];
+    f32x4_t acc[RT];
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       acc[rt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < KS; ++s)
@@ -1309,22 +1319,25 @@ __global__ __launch_bounds__(256) void moe_down_mfma_kernel(ExpertArgs a) {
                                                           __builtin_bit_cast(bf16x8_t, bv[s]), acc[rt], 0, 0, 0);
     }
     if (tile > 0) __syncthreads();  // the previous tile's sums are read
-    float* pw = s_part + (size_t)wave * 1024;
+    float* pw = s_part + (size_t)wave * RT * 256;
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int q = 0; q < 4; ++q) pw[rt * 256 + (g4 * 4 + q) * 16 + n] = acc[rt][q];
     __syncthreads();
-    // thread: output row R = tid % 64 (tile R / 16, row R % 16), pairs j and j + 4
+    // thread: output row R = tid % NR (tile R / 16, row R % 16), pairs
+    // j = tid / NR + jj * (256 / NR) (NR = 16: threads past 128 idle)
     {
-      const int R = tid & 63, rt = R >> 4, r = R & 15;
+      constexpr int JS = 256 / NR < 8 ? 256 / NR : 8;
+      const int R = tid % NR, rt = R >> 4, r = R & 15;
 #pragma unroll
-      for (int jj = 0; jj < 2; ++jj) {
-        const int j = (tid >> 6) + jj * 4;
+      for (int jj = 0; jj < 8 / JS; ++jj) {
+        const int j = tid / NR + jj * JS;
+        if (j >= 8) break;
         float y = 0.f;
 #pragma unroll
         for (int w = 0; w < kDnMfmaWaves; ++w)
-          y += s_part[w * 1024 + rt * 256 + r * 16 + 2 * j] + s_part[w * 1024 + rt * 256 + r * 16 + 2 * j + 1];
+          y += s_part[w * RT * 256 + rt * 256 + r * 16 + 2 * j] + s_part[w * RT * 256 + rt * 256 + r * 16 + 2 * j + 1];
         if (tile * 8 + j < npairs) a.ws.y[(size_t)(pos0 + tile * 8 + j) * H + r0 + R] = y;
       }
     }
@@ -2612,8 +2625,10 @@ static int launch_router(const RouterArgs& ra, int router_dt, int hidden_dt, hip
 static int launch_experts_mfma(const ExpertArgs& ea, int slots, hipStream_t stream) {
   static bool attr_set[64] = {false};
   const size_t gu_shm = std::max((size_t)16 * ((size_t)ea.H * 2 + 16), (size_t)kGuMfmaWaves * 512 * sizeof(float));
+  const bool dn_small = (long long)ea.T * ea.K <= (long long)kDnMfmaSmallPairs * ea.E;
+  const int dn_rows = dn_small ? kDnMfmaRowsSmall : kDnMfmaRows;
   const size_t dn_shm = std::max((size_t)16 * kDnMfmaWaves * ((size_t)ea.I / kDnMfmaWaves * 2 + 16),
-                                 (size_t)kDnMfmaWaves * 1024 * sizeof(float));
+                                 (size_t)kDnMfmaWaves * dn_rows * 16 * sizeof(float));
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return fail(FK_ERR_LAUNCH, "no current HIP device");
   if (!attr_set[dev]) {
@@ -2632,9 +2647,14 @@ static int launch_experts_mfma(const ExpertArgs& ea, int slots, hipStream_t stre
   else hipLaunchKernelGGL(moe_gateup_mfma_kernel<2>, gu_grid, gu_block, gu_shm, stream, ea);
   int st = check_launch("moe_gateup_mfma_kernel");
   if (st) return st;
-  const dim3 dn_grid(slots * (ea.H / kDnMfmaRows)), dn_block(kDnMfmaWaves * kWave);
-  if (ea.I == 512) hipLaunchKernelGGL(moe_down_mfma_kernel<4>, dn_grid, dn_block, dn_shm, stream, ea);
-  else hipLaunchKernelGGL(moe_down_mfma_kernel<2>, dn_grid, dn_block, dn_shm, stream, ea);
+  const dim3 dn_grid(slots * (ea.H / dn_rows)), dn_block(kDnMfmaWaves * kWave);
+  if (dn_small) {
+    if (ea.I == 512) hipLaunchKernelGGL((moe_down_mfma_kernel<4, kDnMfmaRowsSmall / 16>), dn_grid, dn_block, dn_shm, stream, ea);
+    else hipLaunchKernelGGL((moe_down_mfma_kernel<2, kDnMfmaRowsSmall / 16>), dn_grid, dn_block, dn_shm, stream, ea);
+  } else {
+    if (ea.I == 512) hipLaunchKernelGGL((moe_down_mfma_kernel<4, kDnMfmaRows / 16>), dn_grid, dn_block, dn_shm, stream, ea);
+    else hipLaunchKernelGGL((moe_down_mfma_kernel<2, kDnMfmaRows / 16>), dn_grid, dn_block, dn_shm, stream, ea);
+  }
   return check_launch("moe_down_mfma_kernel");
 }
 
