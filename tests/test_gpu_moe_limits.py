@@ -11,7 +11,8 @@ never run:
   * the gate/up GEMV with eight 8-element chunks per lane (H > 2048);
   * the down GEMV with two chunks per lane (I > 512);
   * hidden sizes that are multiples of 8 but not of 16 (odd chunk counts),
-    through the single-launch layer, the tagged router and the GEMV experts.
+    through the single-launch layer, the tagged router and the GEMV experts;
+  * both work-item sizes of the MFMA down kernel with both K splits.
 Weights are reduced in the other dimensions so the oracle stays quick.
 """
 
@@ -86,6 +87,20 @@ def test_moe_layer_beyond_256_tokens(device, e, h, i, tokens):
     # grid-barrier router for T > 256; GEMV experts (I = 64) and MFMA experts
     # (I = 256) after it; T * K = 4096 is the routing-table limit
     _check(device, e, h, i, tokens, seed=200 + tokens + i)
+
+
+@pytest.mark.parametrize(
+    "e,h,i,tokens",
+    [
+        (256, 2048, 512, 192),  # the model's shapes past 4 pairs per expert: 64-row MFMA down items
+        (256, 512, 256, 100),   # I = 256 at <= 4 pairs per expert: 32-row MFMA down items, 2 steps per wavefront
+    ],
+)
+def test_moe_layer_mfma_down_item_sizes(device, e, h, i, tokens):
+    # the MFMA down kernel takes 32 output rows per work item while
+    # T * K <= 4 E and 64 above; config 2 (T = 128, E = 256) covers the
+    # 32-row items at the model's I = 512
+    _check(device, e, h, i, tokens, seed=400 + tokens + i)
 
 
 @pytest.mark.parametrize("tokens", [1, 2, 16, 64])
