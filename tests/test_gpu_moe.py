@@ -321,7 +321,8 @@ def test_moe_layer_deterministic(device, real_gpu):
 def test_moe_layer_fp32_hidden(device, real_cpu, real_gpu, tokens):
     # the real-weight runner feeds fp32 hidden (bench/qwen36_full_decode.py:152),
     # and a layer stack feeds each layer the previous layer's fp32 output:
-    # single-launch (T = 1), GEMV (T = 8) and T >= 64 expert paths
+    # single-launch (T = 1) and GEMV (T = 8, and T = 64: the MFMA experts take
+    # bf16 hidden states only) expert paths
     x = wl.make_hidden(tokens, H, seed=9, dtype=torch.float32)
     lh, moe, logits, ids, w = hip.hip_qwen36_batched_moe_layer_decode(x.to(device), *_moe_args(real_gpu), top_k=K)
     ref = oracle.routed_experts(x, ids.cpu(), w.cpu(), real_cpu["expert_gate_up_weight"], real_cpu["expert_down_weight"])

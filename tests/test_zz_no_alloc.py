@@ -4,7 +4,7 @@ It runs fk_moe_layer's kernels with the workspace in a file-scope device
 array.  Checked through the C ABI against fk_moe_layer with a caller-owned
 workspace on the same inputs: two calls in a row, the second with fewer
 tokens (the shared array keeps the first call's contents), across the
-single-launch (T = 1), GEMV (T < 64) and MFMA (T >= 64) paths; the
+single-launch (T = 1), GEMV (T < 44) and MFMA (T >= 44) paths; the
 results must be identical bit for bit (same kernels, same arithmetic).
 Sizes beyond the array are refused before anything is launched.  The
 array's error word, reached through fk_moe_noalloc_workspace, reports a
