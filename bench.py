@@ -98,8 +98,9 @@ def copy_bandwidth_tbs(torch, dev) -> float:
 
 
 def read_bandwidth_tbs(torch, dev) -> float:
-    """TB/s of fk_stream_read over 4 GiB (16-byte non-temporal loads, as the
-    weight streams use), 8 timed passes after one warm pass."""
+    """TB/s of fk_stream_read over 4 GiB (16-byte non-temporal loads in
+    one-shot 16 KiB workgroups, the fastest read shape measured on this
+    part), 8 timed passes after one warm pass."""
 
     from fastkernels_amd import _lib
 
@@ -637,7 +638,7 @@ def main() -> int:
         "copy_bandwidth_tbs": copy_tbs,
         "read_bandwidth_tbs": read_tbs,
         "measured_bandwidth_note": "copy: torch device-to-device copy of 1 GiB, read + write bytes; read: "
-                                   "fk_stream_read over 4 GiB, 16-byte non-temporal loads like the weight streams",
+                                   "fk_stream_read over 4 GiB, 16-byte non-temporal loads in one-shot 16 KiB workgroups",
         "layer": main_res,
         "sub_results": sub,
         "cpu_baseline": cpu,

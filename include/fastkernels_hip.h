@@ -222,10 +222,10 @@ int fk_residual_add(const void* hidden, int hidden_dtype, const float* update,
                     int64_t n, float* out, void* stream);
 
 /* Reads `bytes` (a multiple of 16) at `src` once, as the weight streams do
- * (16-byte non-temporal loads), and writes nothing (`sink`, one word, is
- * only a guard).  A bandwidth probe: the read ceiling bench.py reports the
- * kernels' fractions against, beside the published peak.  No counterpart
- * in the reference. */
+ * (16-byte non-temporal loads, one-shot 16 KiB per workgroup), and writes
+ * nothing (`sink`, one word, is only a guard).  A bandwidth probe: the read
+ * ceiling bench.py reports the kernels' fractions against, beside the
+ * published peak.  No counterpart in the reference. */
 int fk_stream_read(const void* src, size_t bytes, uint32_t* sink, void* stream);
 
 /* ------------------------------------------------------------------------ */
