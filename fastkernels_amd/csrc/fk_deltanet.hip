@@ -564,15 +564,6 @@ struct StepTagWs {
   uint64_t* z;        // [T, V]
   uint64_t* norm;     // [T, V] gated values o * w * silu(z), before the RMSNorm scale
   uint64_t* started;  // [grid]
-  // Polling hints (from three tokens on; at one or two tokens the consumers
-  // poll the outputs directly and no tile hint is stored): a tile's (a
-  // head's) tag is stored once its outputs are stored.  A consumer waits on
-  // the few hints of its producers before it reads their outputs, instead of
-  // spinning on every output word (which floods the memory system while the
-  // producers still stream).  The outputs still carry their own tags and are
-  // re-read until they do.
-  uint64_t* hint_tile;  // [kStepTilesPerWG * kStepMaxGrid]
-  uint64_t* hint_head;  // [64 * kStepHeadWGs] per head workgroup
   uint64_t* hss;        // [kStepMaxTokens][kStepHssPitch] head quarters' sums of squares
   uint64_t* part;       // [V / 512][T][H] phase C partial sums
 };
@@ -1010,7 +1001,6 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       }
       if (i + kStepTilesAhead < kStepTilesPerWG) issue_tile(i + kStepTilesAhead);
     }
-    // (no tile hints: at T <= 2 the heads poll their inputs directly)
     if (o_kind == 1) {
 #pragma unroll
       for (int t = 0; t < NT; ++t)
@@ -1117,8 +1107,6 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       }
     }
     __syncthreads();  // phases B and C reuse the dynamic LDS
-    // every thread's stores of the tiles are issued before these hints
-    if (tid < ntl) store_tagged(a.tw.hint_tile + b + tid * G, 0.f, tag);
   }
   }
 
@@ -1177,25 +1165,9 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     float* s_o = s_in + (size_t)T * kStepInPitch;
     const int hq = head / (Hv / a.Hk);
     bool ok = true;
-    // From three tokens on: hints of the 20 tiles holding this quarter's q,
-    // k, v and z rows (one load per lane), then one read of the inputs.  At
-    // one or two tokens the inputs are polled directly (a round trip fewer;
-    // the few words re-read while the last tiles stream cost less than it).
-    if (NT > 2 && wave == 0) {
-      constexpr int TPB = kStepD / 16, TPQ = kStepQCols / 16;  // tiles per 128 rows, per quarter's 32 rows
-      int tl = -1;
-      if (lane < 2 * TPB) {
-        tl = ((lane < TPB ? hq : a.Hk + hq) * kStepD) / 16 + lane % TPB;
-      } else if (lane < 2 * TPB + 2 * TPQ) {
-        const int l = lane - 2 * TPB;
-        const int row0 = (l < TPQ ? 2 * a.Hk * kStepD : C) + head * kStepD + quarter * kStepQCols;
-        tl = row0 / 16 + l % TPQ;
-      }
-      uint64_t hw[1];
-      const uint64_t* hs[1] = {tl >= 0 ? a.tw.hint_tile + tl : nullptr};
-      hw[0] = hs[0] ? load_tagged(hs[0]) : 0ull;
-      if (!poll_tagged<1>(hw, hs, tag, plim)) s_fail = 1;
-    }
+    // The consumers poll their inputs directly (tagged words re-read until
+    // they carry this launch's tag): with hint words per tile first, a round
+    // trip more, the step took 0.3-0.4 us longer at 3-8 tokens.
     __syncthreads();
     // Wavefront t < T reads token t's inputs (lane: q and k rows lane and
     // lane + 64, and v (lanes < 32) or z of this quarter's columns), l2-
@@ -1312,8 +1284,11 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
                      poison_if(bad_in, o * raw_value<true>(lnw1[0]) * silu(zz)), tag);
       }
     }
+    // (a full barrier: it waits until the gated values and sums above are
+    // acknowledged before the state write-back below is issued, so the 16 KB
+    // of state stores do not sit between them and the units that poll them;
+    // without it the step took 0.2-0.9 us longer)
     __syncthreads();
-    if (tid == 0) store_tagged(a.tw.hint_head + qb, 0.f, tag);
     FK_MARK(5);
     {
       const size_t base = ((size_t)head * kStepD + (size_t)sgr * 8) * kStepD + jcol;
@@ -1328,16 +1303,8 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     uint16_t* s_nb = reinterpret_cast<uint16_t*>(s_dyn);  // [kcu/8][NCP][8] bf16 (bcol_slot)
     const int h0 = uks * (kcu / kStepD), nh = kcu / kStepD;  // heads of the unit's columns
     bool ok = true;
-    // From three tokens on, the hints of the head workgroups of those heads
-    // first; at one or two tokens the inputs are polled directly (-0.45 us
-    // at T = 1; at T = 8 the units re-read 8x the words while the heads
-    // still run, +0.65 us).
-    if (NT > 2 && wave == 0) {
-      uint64_t hw[1];
-      const uint64_t* hs[1] = {lane < nh * kStepHeadWGs ? a.tw.hint_head + h0 * kStepHeadWGs + lane : nullptr};
-      hw[0] = hs[0] ? load_tagged(hs[0]) : 0ull;
-      if (!poll_tagged<1>(hw, hs, tag, plim)) s_fail = 1;
-    }
+    // (the heads' values polled directly, as the heads poll theirs: with
+    // head hint words first the step took 0.6 us longer at 3-8 tokens)
     __syncthreads();
     // The T * kcu inputs, read coalesced (thread tid: words tid + 512 j of
     // the unit's [T][kcu] block) with the quarter sums of squares of its
@@ -1414,7 +1381,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   FK_MARK(7);
   // ---- phase C2: rows 16b..16b+15 = sum of the nks unit partials ----------
   if (is_out) {
-    // (nks partials per thread: polled directly, few enough not to need hints)
+    // (nks partials per thread, polled directly)
     if (tid < 16 * T) {
       const int r = tid & 15, t = tid >> 4;
       uint64_t w[8];
@@ -1547,8 +1514,6 @@ static size_t step_tag_layout(char* base, StepTagWs* tw) {
   tw->z = reinterpret_cast<uint64_t*>(take(kStepVWords * 8));
   tw->norm = reinterpret_cast<uint64_t*>(take(kStepVWords * 8));
   tw->started = reinterpret_cast<uint64_t*>(take((size_t)kStepMaxGrid * 8));
-  tw->hint_tile = reinterpret_cast<uint64_t*>(take((size_t)kStepTilesPerWG * kStepMaxGrid * 8));
-  tw->hint_head = reinterpret_cast<uint64_t*>(take((size_t)64 * kStepHeadWGs * 8));
   tw->hss = reinterpret_cast<uint64_t*>(take((size_t)kStepMaxTokens * kStepHssPitch * 8));
   tw->part = reinterpret_cast<uint64_t*>(take(kStepPartWords * 8));
   return off;

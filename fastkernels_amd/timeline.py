@@ -86,10 +86,10 @@ MARKERS = {
         [
             "workgroup start",
             "tokens normalised and staged",
-            "A: projection tiles done (stored, hints set)",
+            "A: projection tiles done (stored)",
             "B: head inputs read and normalised",
             "B: recurrence done",
-            "B: gated values and sums of squares stored, hint set",
+            "B: gated values and sums of squares stored",
             "C1: unit inputs staged",
             "C1: unit partial sums stored",
             "C2: output rows written",
