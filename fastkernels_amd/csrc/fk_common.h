@@ -491,12 +491,14 @@ __device__ __forceinline__ WaitLimits wait_limits(const uint32_t* header, int ep
   return load_wait_header(header, epoch_word).limits();
 }
 
-// Workgroup barrier for hand-offs through LDS only: waits for the
-// wavefront's LDS operations, not for its global stores (__syncthreads()
-// also waits until every global store of the wavefront is acknowledged, a
-// memory round trip).  For kernels whose wavefronts exchange data through
-// LDS alone while their global words go to other workgroups, which read
-// them by their launch tags.
+// Workgroup barrier for hand-offs through LDS only: its fences cover LDS
+// alone, so it waits for the wavefront's LDS operations and never for its
+// global stores.  (On gfx950 without threadgroup split, __syncthreads()
+// compiles to the same s_barrier behind an LDS wait; its workgroup-scope
+// global fence would wait for the stores' acknowledgements only in a
+// threadgroup-split build.)  For kernels whose wavefronts exchange data
+// through LDS alone while their global words go to other workgroups, which
+// read them by their launch tags.
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
   __builtin_amdgcn_s_barrier();

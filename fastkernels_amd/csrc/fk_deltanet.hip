@@ -1284,10 +1284,12 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
                      poison_if(bad_in, o * raw_value<true>(lnw1[0]) * silu(zz)), tag);
       }
     }
-    // (a full barrier: it waits until the gated values and sums above are
-    // acknowledged before the state write-back below is issued, so the 16 KB
-    // of state stores do not sit between them and the units that poll them;
-    // without it the step took 0.2-0.9 us longer)
+    // (a barrier: every wavefront has issued its gated values and sums
+    // above before any of the 16 KB of state stores below is issued, so
+    // those stores do not sit in the CU's memory pipeline ahead of them;
+    // without it the step took 0.2-0.9 us longer.  It does not wait for the
+    // stores to be acknowledged: __syncthreads() compiles to s_barrier with
+    // an LDS wait only on gfx950)
     __syncthreads();
     FK_MARK(5);
     {
