@@ -788,19 +788,23 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
   __shared__ float s_L;
   __shared__ float s_mo[kAsWaves][kAsMDims];
   __shared__ int s_fail, s_kfail;
+  __shared__ uint32_t s_hdr[4];  // header words and position, as wavefront 0 loaded them
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, b = blockIdx.x;
   const int T = a.T, H = a.H, hd = a.hd, heads = a.heads, kvh = a.kvh, Gq = heads / kvh;
   const int K = heads * hd, Rq = 2 * K, Rk = kvh * hd, R = Rq + 2 * Rk;
   const int nch = a.nch, nds = hd / kAsMDims, nks = K / kAsKcu, nchk = H >> 3;
   const int hd_sh = 31 - __builtin_clz(hd);  // (hd is a power of two: the host checks)
-  // The workspace header and the position are loaded first.  The position
-  // stays in a vector register (a scalar copy would make the compiler wait
-  // for it at once); its first use, the cached-row addresses, comes after
-  // the weight rows are issued, and the loads retire in order, so that wait
-  // holds back nothing else.
-  WaitHeader hdr = load_wait_header(a.tw.tickets, kWorkspaceEpochWord);
-  int start_ld = a.start_dev ? load_coherent(a.start_dev) : a.start;
+  // The workspace header and the device-held position are loaded first, by
+  // wavefront 0 alone, and shared through LDS at the staging barrier: the
+  // words are read past the caches (coherent loads), and the same lines
+  // read by every wavefront of the grid at once queue behind each other.
+  WaitHeader hdr{0u, 0u, 0u};
+  int start_ld = a.start;
+  if (wave == 0) {
+    hdr = load_wait_header(a.tw.tickets, kWorkspaceEpochWord);
+    if (a.start_dev) start_ld = load_coherent(a.start_dev);
+  }
 
   // Roles: attention units and merge units on the last workgroups (at the
   // model shape every workgroup is an attention unit), C1 units and C2 rows
@@ -854,13 +858,10 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) wt[i][j] = load_raw8_stream<true>(wp, (size_t)min(lane + kWave * j, nchk - 1) * 8);
   }
-  // the unit's chunk (its first tile of cached rows is issued in phase B)
-  asm volatile("" : "+v"(start_ld));  // (the position's wait: here, not at its load)
-  const int start = start_ld;
-  const bool bad_pos = start < 0 || start + T > a.max_pos;
-  const int apos = start + at, an = bad_pos ? 0 : apos + 1;  // positions 0 .. apos
-  const int aC = (an + nch - 1) / nch;
-  const int p_lo = min(ac * aC, an), p_hi = min(p_lo + aC, an);
+  // the unit's chunk (set at the staging, once the position is shared; its
+  // first tile of cached rows is issued in phase B)
+  int start = 0, apos = 0, an = 0, p_lo = 0, p_hi = 0;  // positions 0 .. apos of the token
+  bool bad_pos = false;
   // Cached rows of an attention unit, a tile of kAsTile positions from pt at
   // a time: load u = tid + 512 i covers 4 dims (quad u % (hd / 4)) of row
   // u / (hd / 4) of [k rows | v rows]; positions past the chunk repeat its
@@ -887,8 +888,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
   FK_MARK(1);
 
   // ---- stage the tokens: s_x[t][c] = x * (1 + w), s_rs[t] -----------------
-  const WaitLimits wl = hdr.limits();
-  const uint32_t tag = wl.tag, plim = wl.poll;
+  uint32_t tag = 0u, plim = 0u;
   float* s_x = s_dyn;
   {
     float ssp[kAsMaxTokens] = {0.f, 0.f, 0.f, 0.f};
@@ -922,8 +922,25 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
     if (tid == 0) {
       s_fail = 0;
       s_kfail = 0;
+      s_hdr[0] = hdr.epoch;
+      s_hdr[1] = hdr.set;
+      s_hdr[2] = hdr.err;
+      s_hdr[3] = (uint32_t)start_ld;
     }
     lds_barrier();
+    {
+      WaitHeader h{s_hdr[0], s_hdr[1], s_hdr[2]};
+      const WaitLimits wl = h.limits();
+      tag = wl.tag;
+      plim = wl.poll;
+      start = (int)s_hdr[3];
+      bad_pos = start < 0 || start + T > a.max_pos;
+      apos = start + at;
+      an = bad_pos ? 0 : apos + 1;
+      const int aC = (an + nch - 1) / nch;
+      p_lo = min(ac * aC, an);
+      p_hi = min(p_lo + aC, an);
+    }
     if (tid < T) {
       float tot = 0.f;
 #pragma unroll
