@@ -699,8 +699,9 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   // a/b and state loads towards their use, behind the tiles, and the waits
   // for them would then wait for the tiles too)
   __builtin_amdgcn_sched_barrier(0);
+  FK_MARK(10);
 
-  // The first weight tiles are issued right behind the token chunks: the
+  // The first weight tile is issued right behind the token chunks: the
   // staging below waits for the chunks only (loads retire in order), so the
   // weight stream runs while the tokens are normalised and staged.
   // Conv taps (state and weights) of this workgroup's qkv rows, needed by
@@ -764,9 +765,18 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   // LDS staging and MFMAs) runs under the stream: issued all at once, a
   // wavefront's first tile completes about as late as its last, and the
   // wavefront cannot even issue the rest until the memory pipeline drains.
-#pragma unroll
-  for (int i = 0; i < kStepTilesPerWG; ++i)
-    if (i < kStepTilesAhead) issue_tile(i);
+  // Only the first tile is issued before the staging, the next one right
+  // after it: issuing a tile's loads takes each wavefront about a
+  // microsecond (the CU's memory pipeline backpressures), and the staging's
+  // barriers wait for the last wavefront to finish issuing, so with two
+  // tiles ahead the tokens were staged 1.3-1.6 us later (T = 1 20.05 ->
+  // 19.27 us, T = 8 24.97 -> 24.66 us).  (Every load of the tile goes out
+  // before the staging: left to itself, the scheduler hoists the staging's
+  // first token conversions between them, and the wait for the tokens then
+  // holds back the rest of the tile.)
+  issue_tile(0);
+  __builtin_amdgcn_sched_barrier(0);
+  FK_MARK(11);
 
 
   // ---- stage the normalised tokens -----------------------------------------
@@ -808,6 +818,7 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
         }
       }
     }
+    FK_MARK(12);
     if (tid == 0) {
       s_fail = 0;
       s_hdr[0] = hdr.epoch;
@@ -891,6 +902,9 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     __syncthreads();
   }
   FK_MARK(1);
+#pragma unroll
+  for (int i = 1; i < kStepTilesPerWG; ++i)
+    if (i < kStepTilesAhead) issue_tile(i);  // the rest of the tiles ahead
 
   if constexpr (VALU_A) {
     // ---- phase A (T <= 2): whole-row dot products on the VALU --------------

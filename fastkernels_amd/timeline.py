@@ -94,6 +94,9 @@ MARKERS = {
             "C1: unit partial sums stored",
             "C2: output rows written",
             "end",
+            "A: first loads issued (tokens, norm and a/b rows, state, conv taps)",
+            "A: first weight tiles issued",
+            "tokens in (wavefront 0's sums of squares done)",
         ],
     ),
 }
