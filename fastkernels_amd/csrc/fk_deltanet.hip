@@ -553,6 +553,7 @@ constexpr int kStepHeadWGs = 4;  // workgroups per value head (value columns spl
 constexpr int kStepQCols = kStepD / kStepHeadWGs;  // value columns per head workgroup
 constexpr int kStepInPitch = 2 * kStepD + 2 * kStepQCols + 4;  // head workgroup inputs per token (q, k, v, z, a, b, pad)
 constexpr int kStepHssPitch = 64 * kStepHeadWGs;  // (head, quarter) words per token
+constexpr int kStepStPitch = kStepD + 4;  // LDS pitch of a state column in phase B (floats)
 constexpr int kStepTilesAhead = 2;  // phase A weight tiles in flight per wavefront
 constexpr int kStepTicketEpoch = kWorkspaceEpochWord;
 constexpr int kStepTicketError = kWorkspaceErrorWord;
@@ -684,17 +685,40 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
   }
   // Small operands of phase B, fetched with the tokens, ahead of the weight
   // tiles: the head's norm weight and decay parameters, and (head
-  // workgroups) the head quarter's state: thread (jl, g) holds rows
-  // 8g .. 8g + 7 of value column jcol = quarter * 32 + jl.  Issued after the
-  // staging instead, they sat between the tiles' loads, and the waits for
-  // the tiles (counted over both paths) waited for them too.
+  // workgroups) the head quarter's state, [128 rows][32 columns] fp32, for
+  // the recurrence's layout (thread (jl, g): rows 8g .. 8g + 7 of value
+  // column jcol = quarter * 32 + jl).  T > 2 (MFMA path): read coalesced,
+  // thread tid loading columns 4 (tid % 8) .. + 3 of rows tid / 8 and
+  // tid / 8 + 64 (two 16-byte loads, eight threads per 128-byte row), and
+  // handed over through LDS in phase B.  T <= 2: gathered in the layout
+  // directly, one float per row (1,024 line requests per workgroup instead
+  // of 128).  The coalesced read lets the head workgroups finish issuing
+  // their first tile ~1 us sooner, which at T = 8 brings the heads' inputs
+  // 1.5 us earlier (24.6 -> 23.2 us); at T = 1 the heads are not on the
+  // critical path but the W_out blocks of the other workgroups are, and
+  // the head workgroups' faster start took HBM share from those workgroups'
+  // projection tiles, so their W_out blocks came later (19.3 -> 19.9 us).
+  // Issued after the staging instead, these loads sat between the tiles'
+  // loads, and the waits for the tiles (counted over both paths) waited for
+  // them too.
   uint32_t lnw1[1], alog[1], dtb1[1];
   gather_raw<true>(a.lnw, quarter * kStepQCols + (lane & (kStepQCols - 1)), 0, 1, lnw1);
   gather_raw<true>(a.a_log, is_head ? head : 0, 0, 1, alog);
   gather_raw<true>(a.dt_bias, is_head ? head : 0, 0, 1, dtb1);
   const int sjl = tid >> 4, sgr = tid & 15, jcol = quarter * kStepQCols + sjl;
-  uint32_t S_raw[8];
-  if (is_head) gather_raw<false>(a.rec_state, ((size_t)head * kStepD + (size_t)sgr * 8) * kStepD + jcol, kStepD, 8, S_raw);
+  u32x4 S_ld[2];       // T > 2
+  uint32_t S_raw[8];   // T <= 2
+  if (is_head) {
+    if constexpr (VALU_A) {
+      gather_raw<false>(a.rec_state, ((size_t)head * kStepD + (size_t)sgr * 8) * kStepD + jcol, kStepD, 8, S_raw);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        S_ld[j] = *reinterpret_cast<const u32x4*>(reinterpret_cast<const float*>(a.rec_state) +
+                                                  ((size_t)head * kStepD + (size_t)(tid >> 3) + 64 * j) * kStepD +
+                                                  quarter * kStepQCols + (tid & 7) * 4);
+    }
+  }
   // (kept ahead of the weight tiles: the scheduler would otherwise sink the
   // a/b and state loads towards their use, behind the tiles, and the waits
   // for them would then wait for the tiles too)
@@ -1193,6 +1217,10 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     // workgroup's own (s_abp).
     float* s_in = reinterpret_cast<float*>(s_dyn);
     float* s_o = s_in + (size_t)T * kStepInPitch;
+    // the state quarter, column-major [32][kStepStPitch] (rows padded by 4:
+    // the transposing writes of one wavefront fall in two banks' worth of
+    // distinct rows)
+    float* s_st = s_o + (size_t)T * kStepQCols;
     const int hq = head / (Hv / a.Hk);
     bool ok = true;
     // The consumers poll their inputs directly (tagged words re-read until
@@ -1239,6 +1267,15 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
       }
     }
     if (!ok) s_fail = 1;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if constexpr (VALU_A) break;
+      const int r = (tid >> 3) + 64 * j, c0 = (tid & 7) * 4;
+      s_st[(c0 + 0) * kStepStPitch + r] = __uint_as_float(S_ld[j][0]);
+      s_st[(c0 + 1) * kStepStPitch + r] = __uint_as_float(S_ld[j][1]);
+      s_st[(c0 + 2) * kStepStPitch + r] = __uint_as_float(S_ld[j][2]);
+      s_st[(c0 + 3) * kStepStPitch + r] = __uint_as_float(S_ld[j][3]);
+    }
     __syncthreads();
     FK_MARK(3);
     // inputs incomplete (a failed wait): the head's outputs and state are NaN
@@ -1248,8 +1285,15 @@ __global__ __launch_bounds__(512) void deltanet_step_kernel(StepArgs a) {
     // the 16 lanes.  The next token's q, k and v are read from LDS while the
     // current one runs.
     float S[8];
+    if constexpr (VALU_A) {
 #pragma unroll
-    for (int m = 0; m < 8; ++m) S[m] = raw_value<false>(S_raw[m]);
+      for (int m = 0; m < 8; ++m) S[m] = raw_value<false>(S_raw[m]);
+    } else {
+      const float4* sp = reinterpret_cast<const float4*>(s_st + (size_t)sjl * kStepStPitch + sgr * 8);
+      const float4 s0 = sp[0], s1 = sp[1];
+      S[0] = s0.x; S[1] = s0.y; S[2] = s0.z; S[3] = s0.w;
+      S[4] = s1.x; S[5] = s1.y; S[6] = s1.z; S[7] = s1.w;
+    }
     auto load_tok = [&](int t, float (&k8)[8], float (&q8)[8], float& v) {
       const float* tin = s_in + (size_t)t * kStepInPitch;
       const float4* k4 = reinterpret_cast<const float4*>(tin + kStepD + sgr * 8);
@@ -1587,7 +1631,7 @@ static size_t step_fused_lds(int T, int H, int V) {
   const size_t tile = (size_t)16 * (2 * (size_t)H + 16),
                red = ((size_t)kStepWaves * kStepTilesPerWG * 16 * nc + kStepTilesPerWG * 16 * 16) * 4;
   const size_t pa = T <= 2 ? (size_t)T * H * 4 : (size_t)H * ncp * 2 + (tile > red ? tile : red);
-  const size_t pb = ((size_t)T * kStepInPitch + (size_t)T * kStepQCols) * 4;
+  const size_t pb = ((size_t)T * kStepInPitch + (size_t)T * kStepQCols + (size_t)kStepQCols * kStepStPitch) * 4;
   const size_t kcu = V < 512 ? V : 512;
   // phase C: the unit's staging [kcu/8][ncp][8] bf16, values [T][kcu], sums of squares [T][16]
   const size_t pc = kcu * ncp * 2 + ((size_t)T * kcu + (size_t)T * 4 * kStepHeadWGs) * 4;
@@ -1824,7 +1868,8 @@ int fk_deltanet_step(const void* hidden, const void* input_norm_weight, const vo
   const bool bx = dtypes[0] == FK_DTYPE_BF16, few = tokens <= 2 && hidden_size == 2048;
   const int G = bx ? (few ? step_grid<true, 2>() : step_grid<true, 8>())
                    : (few ? step_grid<false, 2>() : step_grid<false, 8>());
-  if (G > 0 && step_fused_eligible(tokens, hidden_size, qk_heads, value_heads, head_dim, dtypes, G)) {
+  // (the single launch reads the state 16 bytes at a time on its MFMA path)
+  if (G > 0 && (few || aligned16(recurrent_state)) && step_fused_eligible(tokens, hidden_size, qk_heads, value_heads, head_dim, dtypes, G)) {
     StepArgs sa;
     sa.x = hidden;
     sa.nw = input_norm_weight;
