@@ -1681,6 +1681,16 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
     tag = wl.tag;
     plim = wl.poll;
   }
+  // Fast path: wavefronts 1-7 fetch their shared down row (routing-
+  // independent, used at the very end) while wavefront 0 selects the top-k,
+  // when the HBM is otherwise nearly idle; wavefront 0 fetches its own after
+  // the selection (before it, the row would sit ahead of the logit polls in
+  // the wavefront's in-order load queue).
+  Raw8<true> sdr_early;
+  if constexpr (FAST) {
+    if (wave != 0)
+      sdr_early = load_raw8_stream<true>(f.sdn, (size_t)(uint32_t)((b * RG + wave) * I) + (size_t)min(lane * 8, I - 8));
+  }
   // Started record of this workgroup: every wavefront has used the epoch it
   // read (its LDS write needs the loaded value), so the epoch may advance
   // once all records of this launch are there.
@@ -1794,7 +1804,8 @@ __global__ __launch_bounds__(512) void moe_fused_kernel(FusedArgs f) {
     Raw8<true> dr[RG];
 #pragma unroll
     for (int j = 0; j < RG; ++j) dr[j] = load_raw8_stream<true>(dnb, (size_t)(uint32_t)(min(rw + j, H - 1) * I) + dcol);
-    const Raw8<true> sdr = load_raw8_stream<true>(sdb, (size_t)(uint32_t)((r0 + wave) * I) + dcol);
+    Raw8<true> sdr = sdr_early;
+    if (wave == 0) sdr = load_raw8_stream<true>(sdb, (size_t)(uint32_t)((r0 + wave) * I) + dcol);
     // the slot's activations: 512 words over wavefronts 0-3, two per lane
     uint64_t raw0 = 0, raw1 = 0;
     if (wave < 4) {
