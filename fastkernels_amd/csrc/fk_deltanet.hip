@@ -1627,10 +1627,13 @@ static bool step_fused_eligible(int T, int H, int Hk, int Hv, int D, const int* 
 }
 
 static size_t step_fused_lds(int T, int H, int V) {
+  // (the VALU projection runs at T <= 2 only with H = 2048, as the launch
+  // selects it; other hidden sizes stage through the MFMA path's tile)
+  const bool valu_a = T <= 2 && H == 2048;
   const size_t nc = 2 * (size_t)T, ncp = nc <= 2 ? 2 : nc <= 4 ? 4 : nc <= 8 ? 8 : 16;
   const size_t tile = (size_t)16 * (2 * (size_t)H + 16),
                red = ((size_t)kStepWaves * kStepTilesPerWG * 16 * nc + kStepTilesPerWG * 16 * 16) * 4;
-  const size_t pa = T <= 2 ? (size_t)T * H * 4 : (size_t)H * ncp * 2 + (tile > red ? tile : red);
+  const size_t pa = valu_a ? (size_t)T * H * 4 : (size_t)H * ncp * 2 + (tile > red ? tile : red);
   const size_t pb = ((size_t)T * kStepInPitch + (size_t)T * kStepQCols + (size_t)kStepQCols * kStepStPitch) * 4;
   const size_t kcu = V < 512 ? V : 512;
   // phase C: the unit's staging [kcu/8][ncp][8] bf16, values [T][kcu], sums of squares [T][16]

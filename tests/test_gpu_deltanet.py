@@ -210,6 +210,32 @@ def test_step_single_launch_matches_staged_kernels(device, real_dn, tokens):
     torch.testing.assert_close(plan.next_conv_state.float(), conv.float(), atol=1e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("tokens", [1, 2, 3])
+def test_step_single_launch_narrower_hidden(device, tokens):
+    # H = 1024: the single launch stages its projection tiles through the
+    # MFMA path at every token count (the VALU path needs H = 2048), and its
+    # LDS must be sized for that path at T <= 2 too.
+    from fastkernels_amd.plan import DeltaNetStepPlan
+
+    spec = dataclasses.replace(REAL, hidden_size=1024)
+    wd = _to(wl.make_deltanet_weights(spec, seed=11), device)
+    x = wl.make_hidden(tokens, spec.hidden_size, seed=75 + tokens).to(device)
+    plan = DeltaNetStepPlan(wd, tokens, spec)
+    plan.hidden.copy_(x)
+    plan.run()
+    mixed, z, a, b = hip.hip_qwen36_batched_deltanet_project(
+        x, wd["input_norm_weight"], wd["in_proj_qkv_weight"], wd["in_proj_z_weight"],
+        wd["in_proj_a_weight"], wd["in_proj_b_weight"])
+    mixed, conv = hip.hip_qwen36_batched_deltanet_conv(mixed, wd["conv_state"], wd["conv1d_weight"])
+    update, state = hip.hip_qwen36_batched_deltanet_recurrent_output(
+        mixed, z, a, b, wd["recurrent_state"], wd["out_proj_weight"], wd["linear_norm_weight"], wd["a_log"],
+        wd["dt_bias"], **_dims(spec))
+    torch.cuda.synchronize()
+    torch.testing.assert_close(plan.update, update, atol=1e-4, rtol=1e-3)
+    torch.testing.assert_close(plan.next_recurrent_state, state, atol=1e-5, rtol=1e-4)
+    torch.testing.assert_close(plan.next_conv_state.float(), conv.float(), atol=1e-2, rtol=1e-2)
+
+
 def test_step_single_launch_repeated_calls_stay_consistent(device, real_dn):
     # The launch tag advances every launch: cycling inputs through one
     # workspace must keep reproducing each input's first result bit for bit.
