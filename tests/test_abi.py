@@ -41,7 +41,7 @@ def test_product_library_carries_no_timeline_markers():
 def test_timeline_markers_have_names():
     from fastkernels_amd import timeline
 
-    assert {k: len(v[1]) for k, v in timeline.MARKERS.items()} == {"moe": 12, "router": 6, "deltanet": 10, "attention": 15}
+    assert {k: len(v[1]) for k, v in timeline.MARKERS.items()} == {"moe": 12, "router": 6, "deltanet": 13, "attention": 15}
     assert all(len(names) <= 16 for _, names in timeline.MARKERS.values())  # kTimelineMarks
 
 
