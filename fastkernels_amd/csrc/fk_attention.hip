@@ -670,16 +670,14 @@ constexpr int kAsMDims = 64;       // head dims per merge unit
 constexpr int kAsKcu = 512;        // Wo columns per C1 unit
 constexpr int kAsRb = 128;         // Wo rows per C1 unit (16 per wavefront)
 constexpr int kAsTile = 24;        // cached positions per LDS tile of an attention unit
-constexpr int kAsKvLoads = 2 * kAsTile * (kAttnMaxHeadDim / 4) / kAsThreads;  // 4-element loads per thread per tile
 constexpr int kAsMaxH = 2048;
 constexpr int kAsMaxG = 8;         // query heads per kv head
 constexpr int kAsGu = 4;           // query heads per attention unit
 // dynamic LDS: phase B's [4][hd] x 2 (queries), [4][hd] x 3 (own keys raw
-// and final, own values) and a tile of cached rows [kAsTile][hd] x 2 (k, v;
-// the softmax states [8 wavefronts][4][hd] reuse it); phase A's [T][H] and
-// C1's [T][512] are smaller
-constexpr size_t kAsMaxLds = (size_t)(2 * kAsGu + 3 * kAsMaxTokens + 2 * kAsTile) * kAttnMaxHeadDim * 4;
-static_assert(kAsWaves * kAsGu <= 2 * kAsTile, "the softmax states must fit in the row tile");
+// and final, own values) and the softmax states [8 wavefronts][4][hd] (the
+// cached rows go straight to registers); phase A's [T][H] and C1's
+// [T][512] are smaller
+constexpr size_t kAsMaxLds = (size_t)(2 * kAsGu + 3 * kAsMaxTokens + kAsWaves * kAsGu) * kAttnMaxHeadDim * 4;
 static_assert(kAsMaxTokens * kAsMaxH * 4 <= kAsMaxLds, "phase A's tokens must fit in the LDS");
 
 struct AttnTagWs {
@@ -863,26 +861,22 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
   int start = 0, apos = 0, an = 0, p_lo = 0, p_hi = 0;  // positions 0 .. apos of the token
   bool bad_pos = false;
   // Cached rows of an attention unit, a tile of kAsTile positions from pt at
-  // a time: load u = tid + 512 i covers 4 dims (quad u % (hd / 4)) of row
-  // u / (hd / 4) of [k rows | v rows]; positions past the chunk repeat its
-  // last one (clamped in range).
-  const int qsh = hd_sh - 2;
-  Row4<CBF> kvr[kAsKvLoads];
+  // a time, read straight into the registers of the wavefront that scores
+  // them: wavefront w the positions pt + w + 8 bb (bb < kAsTile / 8), lane
+  // l dims 4 l .. 4 l + 3 of their k and v rows (no LDS staging, no
+  // barrier); positions past the chunk repeat its last one (clamped in
+  // range, never scored).  Staged through LDS by every thread instead, the
+  // step took 0.5-0.6 us longer (the staging and its barrier sat between
+  // the RoPE and the softmax).
+  constexpr int PPW = kAsTile / kAsWaves;  // positions per wavefront per tile
+  Row4<CBF> ckr[PPW], cvr[PPW];
   auto issue_tile = [&](int pt) {
 #pragma unroll
-    for (int i = 0; i < kAsKvLoads; ++i) {
-      const int u = tid + i * kAsThreads, row = u >> qsh, qd = u & ((1 << qsh) - 1);
-      const bool isv = row >= kAsTile;
-      const int p = max(min(pt + (isv ? row - kAsTile : row), p_hi - 1), 0);
-      const size_t cr = ((size_t)p * kvh + aj) * hd + 4 * qd;
-      kvr[i] = load_row4<CBF>(isv ? a.vc : a.kc, row < 2 * kAsTile ? cr : 0);
-    }
-  };
-  auto stage_tile = [&](float* s_kt) {  // [2 * kAsTile][hd] as fp32: k rows, then v rows
-#pragma unroll
-    for (int i = 0; i < kAsKvLoads; ++i) {
-      const int u = tid + i * kAsThreads;
-      if ((u >> qsh) < 2 * kAsTile) *reinterpret_cast<float4*>(s_kt + 4 * u) = kvr[i].f4();
+    for (int bb = 0; bb < PPW; ++bb) {
+      const int p = max(min(pt + wave + kAsWaves * bb, p_hi - 1), 0);
+      const size_t cr = ((size_t)p * kvh + aj) * hd + dl;
+      ckr[bb] = load_row4<CBF>(a.kc, cr);
+      cvr[bb] = load_row4<CBF>(a.vc, cr);
     }
   };
   FK_MARK(1);
@@ -988,8 +982,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
     float* s_kr = s_qf + kAsGu * hd;               // [4][hd] own keys raw, then normalised
     float* s_kf = s_kr + kAsMaxTokens * hd;        // [4][hd] own keys rotated
     float* s_vn = s_kf + kAsMaxTokens * hd;        // [4][hd] own values
-    float* s_kt = s_vn + kAsMaxTokens * hd;        // [2][kAsTile][hd] cached k, v rows of a tile
-    float* s_acc = s_kt;                           // [waves][Gu][hd] after the last tile
+    float* s_acc = s_vn + kAsMaxTokens * hd;       // [waves][Gu][hd] wavefront states after the last tile
     // own positions of the chunk: o_lo .. p_hi - 1, tokens u_lo ..
     const int o_lo = max(p_lo, start), n_own = p_hi > o_lo ? p_hi - o_lo : 0, u_lo = o_lo - start;
     // token at's queries of heads hb .. (word e = g * hd + d), the own
@@ -1071,27 +1064,19 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
       m[g] = -INFINITY;
       l[g] = 0.f;
     }
-    // tiles of kAsTile positions (the first fetched before phase A): staged
-    // in LDS, then wavefront w takes positions pt + w, + 8, ..; per head one
-    // softmax step over its positions of the tile.  The step's own
+    // tiles of kAsTile positions (the first issued with the inputs):
+    // wavefront w takes positions pt + w, + 8, .. from its registers; per
+    // head one softmax step over its positions of the tile.  The step's own
     // positions read the recomputed keys and the values from v.
-    constexpr int PPW = kAsTile / kAsWaves;  // positions per wavefront per tile
     for (int pt = p_lo; pt < p_hi; pt += kAsTile) {
-      if (pt != p_lo) {
-        lds_barrier();  // every wavefront is done with the previous tile
-        issue_tile(pt);
-      }
-      stage_tile(s_kt);
-      lds_barrier();
+      if (pt != p_lo) issue_tile(pt);
       FK_MARK(12);
-      const float* s_vt = s_kt + kAsTile * hd;
       const int pend = min(pt + kAsTile, p_hi);
       float sr[PPW];  // lanes 16g ..: head g's score at position pt + w + 8 bb
 #pragma unroll
       for (int bb = 0; bb < PPW; ++bb) {
         const int p = min(pt + wave + kAsWaves * bb, pend - 1);  // (positions past the tile: scored -inf below)
-        const float* kp = p >= o_lo ? s_kf + (p - o_lo) * hd : s_kt + (p - pt) * hd;  // (uniform)
-        const float4 k4 = *reinterpret_cast<const float4*>(kp + dl);
+        const float4 k4 = p >= o_lo ? *reinterpret_cast<const float4*>(s_kf + (p - o_lo) * hd + dl) : ckr[bb].f4();  // (uniform)
         float d[kAsGu];
 #pragma unroll
         for (int g = 0; g < kAsGu; ++g) d[g] = q4[g].x * k4.x + q4[g].y * k4.y + q4[g].z * k4.z + q4[g].w * k4.w;
@@ -1117,8 +1102,7 @@ __global__ __launch_bounds__(kAsThreads) void attn_step_kernel(AttnStepArgs a) {
         for (int bb = 0; bb < PPW; ++bb) {
           const int p = min(pt + wave + kAsWaves * bb, pend - 1);
           const float e = __expf(sc[bb] - mx);
-          const float* vp = p >= o_lo ? s_vn + (p - o_lo) * hd : s_vt + (p - pt) * hd;  // (uniform)
-          const float4 v4 = *reinterpret_cast<const float4*>(vp + dl);
+          const float4 v4 = p >= o_lo ? *reinterpret_cast<const float4*>(s_vn + (p - o_lo) * hd + dl) : cvr[bb].f4();  // (uniform)
           es += e;
           av.x = fmaf(e, v4.x, av.x);
           av.y = fmaf(e, v4.y, av.y);

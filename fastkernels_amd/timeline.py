@@ -76,7 +76,7 @@ MARKERS = {
             "end",
             "B: q and own-key norms",
             "B: RoPE",
-            "B: row tile staged",
+            "B: tile of cached rows issued (loop entered)",
             "B: softmax over the chunk done",
             "B: wavefronts merged, partials stored",
         ],
